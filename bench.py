@@ -1,0 +1,195 @@
+#!/usr/bin/env python3
+"""bench.py -- MoE expert path throughput on one MI355X (gfx950).
+
+Default workload: one M=1 INT8 MoE decode step over 48
+distinct synthetic layers (H=2048, I=512, 512 routed experts, top-10 + 1
+gated shared expert, ~78 GB of weights resident in HBM so every layer is
+streamed). A step is the 48-layer pass; the step is captured once in a HIP
+graph and replayed. Reported value: microseconds per token per MoE layer
+(lower is better), with the layer's algorithmic HBM bytes over that time as
+the roofline figure, and the CPU oracle timed on a bounded sample of the same
+workload as the CPU baseline.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qwen-3-ocho_amd"))
+
+H, I, E, K = 2048, 512, 512, 10
+EXPERT_BYTES = 3 * H * I + (I + I + H) * 4            # int8 gate/up/down + fp32 row scales
+ROUTER_BYTES = E * H * 4
+ACT_BYTES = 2 * H * 2                                  # x in, y out (bf16)
+GATE_VEC_BYTES = H * 4                                 # shared-expert sigmoid gate vector
+LAYER_BYTES_M1 = (K + 1) * EXPERT_BYTES + ROUTER_BYTES + ACT_BYTES + GATE_VEC_BYTES
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(n_layers, seconds, threads):
+    """Time the oracle's fp32 CPU path on n_layers x 1 token of the same workload."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import _oracle as orc
+    lib = orc.load()
+    seed = 0
+    layers = []
+    for l in range(n_layers):
+        router = orc.fill("gauss", seed, l, orc.T_ROUTER, 0, E * H, 0.02)
+        x = orc.fill("gauss_bf16", seed, 1000 + l, orc.T_X, 0, H)
+        sel, _, _ = orc.topk(orc.router_logits(router.reshape(E, H), x.reshape(1, H)), K)
+        # host arena: [E+1] experts, only the routed ones and the shared one are filled
+        qg = np.empty((E + 1) * I * H, np.int8); qu = np.empty_like(qg); qd = np.empty_like(qg)
+        sg = np.empty((E + 1) * I, np.float32); su = np.empty_like(sg); sd = np.empty((E + 1) * H, np.float32)
+        for e in list(sel[0]) + [E]:
+            e = int(e)
+            lib.orc_fill_i8(seed, l, orc.T_QG, e * I * H, I * H, qg[e * I * H:].ctypes.data)
+            lib.orc_fill_i8(seed, l, orc.T_QU, e * I * H, I * H, qu[e * I * H:].ctypes.data)
+            lib.orc_fill_i8(seed, l, orc.T_QD, e * H * I, H * I, qd[e * H * I:].ctypes.data)
+            lib.orc_fill_rowscale(seed, l, orc.T_SG, e * I, I, sg[e * I:].ctypes.data)
+            lib.orc_fill_rowscale(seed, l, orc.T_SU, e * I, I, su[e * I:].ctypes.data)
+            lib.orc_fill_rowscale(seed, l, orc.T_SD, e * H, H, sd[e * H:].ctypes.data)
+        g = orc.fill("gauss", seed, l, orc.T_SHGATE, 0, H, 0.02)
+        hl = orc.HostLayer(router.ctypes.data, qg.ctypes.data, qu.ctypes.data, qd.ctypes.data,
+                           sg.ctypes.data, su.ctypes.data, sd.ctypes.data, g.ctypes.data)
+        layers.append((hl, x, (router, qg, qu, qd, sg, su, sd, g)))
+    y = np.empty(H, np.float32)
+    for hl, x, _ in layers[:1]:
+        lib.orc_cpu_moe_layer_fast(C.byref(hl), H, I, E, K, x.ctypes.data, 1, y.ctypes.data, threads)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        for hl, x, _ in layers:
+            lib.orc_cpu_moe_layer_fast(C.byref(hl), H, I, E, K, x.ctypes.data, 1, y.ctypes.data, threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 1000:
+            break
+    us = el * 1e6 / (reps * n_layers)
+    return {"value": round(us, 2), "unit": "us/token/layer", "cores": threads, "kind": "port",
+            "sample": f"{n_layers} distinct layers x 1 token (config-1 shapes), {reps} passes, "
+                      f"fp32-accumulate oracle path, OpenMP {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-layers", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+    ws_env = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or ws_env != 1:
+        print("bench.py: this build runs on one GPU only (single-GPU box; the multi-GPU "
+              "sharding is a design in DESIGN.md, not a measured path). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import qfm
+    lib = qfm.load()
+    info = qfm.device_info()
+    log("device", info)
+    qfm.init(H, I, E, K, 1, 1)
+    st = qfm.Stream()
+    nl = args.layers
+    t0 = time.time()
+    layers = []
+    for l in range(nl):
+        layers.append(qfm.SynthLayer(qfm.QFM_FMT_INT8, 0, l, stream=st))
+        if (l + 1) % 8 == 0:
+            st.sync()
+            log(f"generated {l + 1}/{nl} layers ({time.time() - t0:.1f}s)")
+    arr = (qfm.QfmLayer * nl)(*[L.s.layer for L in layers])
+    x = qfm.DevBuf(nl * H * 2)
+    y = qfm.DevBuf(nl * H * 2)
+    for l in range(nl):
+        qfm.check(lib.qfm_gen_input_rows(x.ptr + l * H * 2, 1, 0, 1000 + l, 0, st.h), "x")
+    wsb = lib.qfm_workspace_bytes(1)
+    ws = qfm.DevBuf(wsb)
+    st.sync()
+
+    def enqueue_step():
+        qfm.check(lib.qfm_moe_forward_layers(arr, nl, x.ptr, H, 1, y.ptr, H, ws.ptr, wsb, st.h), "forward")
+
+    graph = None
+    if not args.no_graph:
+        qfm.check(lib.qfm_graph_capture_begin(st.h), "capture")
+        enqueue_step()
+        graph = lib.qfm_graph_capture_end(st.h)
+        if not graph:
+            raise qfm.QfmError(lib.qfm_last_error().decode())
+
+    def step():
+        if graph:
+            qfm.check(lib.qfm_graph_launch(graph, st.h), "graph launch")
+        else:
+            enqueue_step()
+
+    for _ in range(args.warmup):
+        step()
+    st.sync()
+    qfm.check(lib.qfm_device_sync(), "sync")
+    e0, e1 = qfm.Event(), qfm.Event()
+    e0.record(st)
+    t_host = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    e1.record(st)
+    st.sync()
+    qfm.check(lib.qfm_device_sync(), "sync")
+    t_host = time.perf_counter() - t_host
+    ms_step = e0.elapsed_ms(e1) / args.steps
+    us_layer = ms_step * 1000.0 / nl
+    gbs = LAYER_BYTES_M1 / (us_layer * 1e-6) / 1e9
+    log(f"step {ms_step:.3f} ms ({us_layer:.2f} us/layer, {gbs:.0f} GB/s), host wall {t_host:.2f}s")
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        log(f"cpu baseline: {args.cpu_layers} layers, ~{args.cpu_seconds}s, {threads} threads")
+        cpu = cpu_baseline(args.cpu_layers, args.cpu_seconds, threads)
+        log("cpu baseline", cpu)
+
+    out = {
+        "metric": "MoE-layer us/token at M=1 & M=8 (HBM GB/s, % peak); prefill MoE tok/s",
+        "value": round(us_layer, 3),
+        "unit": "us/token/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic (Philox-generated weights and inputs, generated on device)",
+        "config": {"workload": "BASELINE config 1: M=1 INT8 MoE decode step, 48 distinct layers",
+                   "hidden": H, "inter": I, "experts": E, "top_k": K, "shared_experts": 1,
+                   "layers": nl, "rows": 1, "graph": graph is not None},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole MoE layer (router, top-k, gate/up, down launches)",
+                     "algorithmic_bytes_per_layer": LAYER_BYTES_M1},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    if graph:
+        lib.qfm_graph_destroy(graph)
+    for L in layers:
+        L.destroy()
+
+
+if __name__ == "__main__":
+    main()

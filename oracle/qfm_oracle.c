@@ -1,0 +1,482 @@
+/*
+ * qfm_oracle.c -- CPU restatement of the quantized MoE expert path.
+ * TEST INFRASTRUCTURE ONLY (see qfm_oracle.h): the checker, never the product.
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off -fopenmp).
+ */
+#include "qfm_oracle.h"
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Philox-4x32-10 (Salmon et al., SC'11), as frozen in the reference:
+   stoch/include/philox.cuh:17-35 -- multipliers 0xD2511F53 / 0xCD9E8D57,
+   Weyl bumps 0x9E3779B9 / 0xBB67AE85 after every round but the last. */
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; r++) {
+        const uint64_t p0 = (uint64_t)c0 * 0xD2511F53ull;
+        const uint64_t p1 = (uint64_t)c2 * 0xCD9E8D57ull;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+        const uint32_t n1 = (uint32_t)p1;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        const uint32_t n3 = (uint32_t)p0;
+        c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+        if (r != 9) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+/* Word j of the stream (seed, layer, tensor): block j/4 of Philox with
+   counter (lo32(j/4), hi32(j/4), tensor, layer) and key (seed, 0). */
+uint32_t orc_word(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t j) {
+    const uint64_t b = j >> 2;
+    const uint32_t ctr[4] = {(uint32_t)b, (uint32_t)(b >> 32), tensor, layer};
+    const uint32_t key[2] = {seed, 0u};
+    uint32_t o[4];
+    orc_philox4x32_10(ctr, key, o);
+    return o[j & 3];
+}
+
+/* int8 code uniform over [-127, 127]: floor(w * 255 / 2^32) - 127 */
+int8_t orc_gen_i8(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t n) {
+    const uint32_t w = orc_word(seed, layer, tensor, n);
+    return (int8_t)((int)(((uint64_t)w * 255u) >> 32) - 127);
+}
+
+/* 24-bit uniform u = (w >> 8) * 2^-24, the reference's frozen extractor
+   (stoch/include/philox.cuh:57-60). Row scale = (0.5 + u) * 0.02/127,
+   evaluated as one fused multiply-add: fma(u, C, C/2). */
+#define ORC_ROWSCALE_C  0x1.4a429ap-13f   /* float(0.02f / 127.0f) */
+#define ORC_ROWSCALE_CH 0x1.4a429ap-14f   /* C / 2 (exact) */
+float orc_gen_rowscale(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t n) {
+    const uint32_t w = orc_word(seed, layer, tensor, n);
+    const float u = (float)(w >> 8) * 0x1p-24f;
+    return fmaf(u, ORC_ROWSCALE_C, ORC_ROWSCALE_CH);
+}
+
+/* Gaussian by Irwin-Hall: sum of 12 24-bit uniforms (words 12n..12n+11,
+   three whole Philox blocks), integer-exact, centred, one int->float rounding. */
+float orc_gen_gauss(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t n) {
+    const uint64_t b0 = n * 3u;
+    uint32_t s = 0;
+    for (int i = 0; i < 3; i++) {
+        const uint64_t b = b0 + (uint64_t)i;
+        const uint32_t ctr[4] = {(uint32_t)b, (uint32_t)(b >> 32), tensor, layer};
+        const uint32_t key[2] = {seed, 0u};
+        uint32_t o[4];
+        orc_philox4x32_10(ctr, key, o);
+        s += (o[0] >> 8) + (o[1] >> 8) + (o[2] >> 8) + (o[3] >> 8);
+    }
+    const int32_t c = (int32_t)s - (int32_t)(6u << 24);
+    return (float)c * 0x1p-24f;
+}
+
+/* packed e2m1 byte: two codes uniform over all 16 (low nibble = element 2i,
+   high nibble = element 2i+1, the adjacent-pair order of
+   qf_nvfp4_wave64.hip:75-101). */
+uint8_t orc_gen_fp4byte(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t n) {
+    return (uint8_t)(orc_word(seed, layer, tensor, n) >> 24);
+}
+
+/* e4m3 block scale: nearest e4m3 of v = 0.25 + 1.75 u, v in [0.25, 2). */
+uint8_t orc_gen_e4m3scale(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t n) {
+    const uint32_t w = orc_word(seed, layer, tensor, n);
+    const float u = (float)(w >> 8) * 0x1p-24f;
+    return orc_e4m3_encode(fmaf(1.75f, u, 0.25f));
+}
+
+void orc_fill_i8(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t n0, uint64_t cnt, int8_t *out) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)cnt; i++) out[i] = orc_gen_i8(seed, layer, tensor, n0 + (uint64_t)i);
+}
+void orc_fill_rowscale(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t n0, uint64_t cnt, float *out) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)cnt; i++) out[i] = orc_gen_rowscale(seed, layer, tensor, n0 + (uint64_t)i);
+}
+void orc_fill_gauss(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t n0, uint64_t cnt, float scale, float *out) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)cnt; i++) out[i] = orc_gen_gauss(seed, layer, tensor, n0 + (uint64_t)i) * scale;
+}
+void orc_fill_gauss_bf16(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t n0, uint64_t cnt, uint16_t *out) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)cnt; i++) out[i] = orc_bf16_rne(orc_gen_gauss(seed, layer, tensor, n0 + (uint64_t)i));
+}
+void orc_fill_fp4byte(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t n0, uint64_t cnt, uint8_t *out) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)cnt; i++) out[i] = orc_gen_fp4byte(seed, layer, tensor, n0 + (uint64_t)i);
+}
+void orc_fill_e4m3scale(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t n0, uint64_t cnt, uint8_t *out) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)cnt; i++) out[i] = orc_gen_e4m3scale(seed, layer, tensor, n0 + (uint64_t)i);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Number formats. E2M1: +-{0, .5, 1, 1.5, 2, 3, 4, 6}[n & 7], sign bit 3
+   (qf_nvfp4_wave64.hip:62-67). E4M3: e = b >> 3, m = b & 7; e == 0 ->
+   m * 2^-9, else (1 + m/8) * 2^(e-7); 0x7F -> +inf as in the reference
+   (qf_nvfp4_wave64.hip:68-73). Written from the closed forms with ldexp. */
+float orc_e2m1(uint32_t nib) {
+    const uint32_t mag = nib & 7u, e = mag >> 1, m = mag & 1u;
+    const float v = e ? ldexpf(1.0f + 0.5f * (float)m, (int)e - 1) : 0.5f * (float)m;
+    return (nib & 8u) ? -v : v;
+}
+float orc_e4m3(uint32_t b) {
+    const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+    if (e == 0) return ldexpf((float)m, -9);
+    if (e == 15 && m == 7) return INFINITY;
+    return ldexpf(1.0f + (float)m / 8.0f, (int)e - 7);
+}
+uint8_t orc_e4m3_encode(float v) {
+    uint32_t bits; memcpy(&bits, &v, 4);
+    int e = (int)((bits >> 23) & 0xFF) - 127;
+    uint32_t mant = bits & 0x7FFFFFu;
+    uint32_t m3 = mant >> 20, rem = mant & 0xFFFFFu;
+    if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) m3++;
+    if (m3 == 8u) { m3 = 0; e++; }
+    return (uint8_t)(((uint32_t)(e + 7) << 3) | m3);
+}
+uint16_t orc_bf16_rne(float f) {
+    uint32_t u; memcpy(&u, &f, 4);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);   /* quiet NaN */
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+float orc_bf16_to_f32(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f; memcpy(&f, &u, 4);
+    return f;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Router logits in the canonical fp32 order (the order the HIP router
+   kernels execute): 64 lane partials, partial l = sequential fma over
+   k = j*256 + 4l + c for j = 0..H/256-1, c = 0..3; then a butterfly
+   p[l] = p[l] + p[l ^ m] for m = 32, 16, 8, 4, 2, 1. H % 256 == 0.
+   Bias (prefill skew) is added last with one rounding. The reference's
+   router is a plain fp32 dot (qf_router_wave64.hip:42-51); the order is
+   fixed here so that GPU and CPU logits are bit-identical. */
+static float canon_dot(const float *w, const float *xf, int H) {
+    float p[64], q[64];
+    for (int l = 0; l < 64; l++) {
+        float a = 0.0f;
+        for (int j = 0; j < H / 256; j++)
+            for (int c = 0; c < 4; c++) {
+                const int k = j * 256 + l * 4 + c;
+                a = fmaf(w[k], xf[k], a);
+            }
+        p[l] = a;
+    }
+    for (int s = 32; s >= 1; s >>= 1) {
+        for (int l = 0; l < 64; l++) q[l] = p[l] + p[l ^ s];
+        memcpy(p, q, sizeof p);
+    }
+    return p[0];
+}
+void orc_router_logits(const float *W, const uint16_t *x, const float *bias,
+                       int M, int E, int H, float *logits) {
+    float *xf = (float *)malloc(sizeof(float) * (size_t)H);
+    for (int m = 0; m < M; m++) {
+        for (int k = 0; k < H; k++) xf[k] = orc_bf16_to_f32(x[(size_t)m * H + k]);
+        for (int e = 0; e < E; e++) {
+            float v = canon_dot(W + (size_t)e * H, xf, H);
+            if (bias) v = v + bias[e];
+            logits[(size_t)m * E + e] = v;
+        }
+    }
+    free(xf);
+}
+
+/* Top-K by descending logit, ties -> lower index (qf.cu:1230-1255 ranks
+   logits; qf_router_wave64.hip:120-147 the same tie rule). Weights:
+   p_e = exp(l_e - max) / sum_all (qf_router_wave64.hip:100-116), then
+   renormalized over the selected K (qf_router_wave64.hip:149-154). */
+void orc_topk(const float *logits, int M, int E, int K, int renorm,
+              int *sel, double *w64, float *w32) {
+    unsigned char *taken = (unsigned char *)malloc((size_t)E);
+    for (int m = 0; m < M; m++) {
+        const float *l = logits + (size_t)m * E;
+        memset(taken, 0, (size_t)E);
+        for (int k = 0; k < K; k++) {
+            int bi = -1;
+            for (int e = 0; e < E; e++) {
+                if (taken[e]) continue;
+                if (bi < 0 || l[e] > l[bi]) bi = e;   /* strict: the lower index wins a tie */
+            }
+            taken[bi] = 1;
+            sel[(size_t)m * K + k] = bi;
+        }
+        const double mx = (double)l[sel[(size_t)m * K]];
+        double denom = 0.0, wsum = 0.0;
+        for (int e = 0; e < E; e++) denom += exp((double)l[e] - mx);
+        double p[64];
+        for (int k = 0; k < K; k++) {
+            p[k] = exp((double)l[sel[(size_t)m * K + k]] - mx) / denom;
+            wsum += p[k];
+        }
+        for (int k = 0; k < K; k++) {
+            const double w = renorm ? p[k] / wsum : p[k];
+            if (w64) w64[(size_t)m * K + k] = w;
+            if (w32) w32[(size_t)m * K + k] = (float)w;
+        }
+    }
+    free(taken);
+}
+
+/* ------------------------------------------------------------------------ */
+/* INT8 expert, exact dequant-matmul in fp64 (SURVEY Appendix A.2;
+   reference structure qf8_moe_i8.hip:72-144 with exact activations):
+   silu(g) = g / (1 + e^-g) as at qf8_moe_i8.hip:105. */
+void orc_i8_expert(const double *x, const int8_t *Qg, const float *sg,
+                   const int8_t *Qu, const float *su, const int8_t *Qd, const float *sd,
+                   int H, int I, double *h, double *y) {
+    for (int r = 0; r < I; r++) {
+        double ag = 0.0, au = 0.0;
+        const int8_t *wg = Qg + (size_t)r * H, *wu = Qu + (size_t)r * H;
+        for (int k = 0; k < H; k++) { ag += (double)wg[k] * x[k]; au += (double)wu[k] * x[k]; }
+        const double g = ag * (double)sg[r], u = au * (double)su[r];
+        h[r] = g / (1.0 + exp(-g)) * u;
+    }
+    for (int c = 0; c < H; c++) {
+        double a = 0.0;
+        const int8_t *wd = Qd + (size_t)c * I;
+        for (int r = 0; r < I; r++) a += (double)wd[r] * h[r];
+        y[c] = a * (double)sd[c];
+    }
+}
+
+/* NVFP4: w[r][k] = E2M1(nib(r,k)) * E4M3(S[r][k/16]) * s2, nib(r,k) = low
+   nibble of byte k/2 for even k, high nibble for odd k (qf8_moe_i8.hip:170-174). */
+void orc_nvfp4_dequant(const uint8_t *F, const uint8_t *S, float s2, int rows, int K, double *out) {
+    for (int r = 0; r < rows; r++)
+        for (int k = 0; k < K; k++) {
+            const uint8_t b = F[(size_t)r * (K / 2) + k / 2];
+            const uint32_t nib = (k & 1) ? (uint32_t)(b >> 4) : (uint32_t)(b & 15u);
+            out[(size_t)r * K + k] = (double)orc_e2m1(nib) * (double)orc_e4m3(S[(size_t)r * (K / 16) + k / 16]) * (double)s2;
+        }
+}
+void orc_nvfp4_expert(const double *x, const uint8_t *Fg, const uint8_t *Sg, float s2g,
+                      const uint8_t *Fu, const uint8_t *Su, float s2u,
+                      const uint8_t *Fd, const uint8_t *Sd, float s2d,
+                      int H, int I, double *h, double *y) {
+    double *wg = (double *)malloc(sizeof(double) * (size_t)I * H);
+    double *wu = (double *)malloc(sizeof(double) * (size_t)I * H);
+    double *wd = (double *)malloc(sizeof(double) * (size_t)I * H);
+    orc_nvfp4_dequant(Fg, Sg, s2g, I, H, wg);
+    orc_nvfp4_dequant(Fu, Su, s2u, I, H, wu);
+    orc_nvfp4_dequant(Fd, Sd, s2d, H, I, wd);
+    for (int r = 0; r < I; r++) {
+        double ag = 0.0, au = 0.0;
+        for (int k = 0; k < H; k++) { ag += wg[(size_t)r * H + k] * x[k]; au += wu[(size_t)r * H + k] * x[k]; }
+        h[r] = ag / (1.0 + exp(-ag)) * au;
+    }
+    for (int c = 0; c < H; c++) {
+        double a = 0.0;
+        for (int r = 0; r < I; r++) a += wd[(size_t)c * I + r] * h[r];
+        y[c] = a;
+    }
+    free(wg); free(wu); free(wd);
+}
+
+/* X8: per 32-block s = absmax/127 (1 if absmax == 0), q = clamp(rint(v/s), +-127)
+   (qf8_moe_i8.hip:58-70). */
+void orc_x8_quant(const float *v, int n, int8_t *q, float *s) {
+    for (int b = 0; b < n / 32; b++) {
+        float mx = 0.0f;
+        for (int i = 0; i < 32; i++) mx = fmaxf(mx, fabsf(v[b * 32 + i]));
+        const float sc = mx > 0.0f ? mx * (1.0f / 127.0f) : 1.0f;
+        for (int i = 0; i < 32; i++) {
+            int qi = (int)rintf(v[b * 32 + i] / sc);
+            qi = qi > 127 ? 127 : (qi < -127 ? -127 : qi);
+            q[b * 32 + i] = (int8_t)qi;
+        }
+        s[b] = sc;
+    }
+}
+
+/* Routing inversion: experts ascending; within an expert, pairs in (token, k)
+   order (qf8_moe_i8.hip:323-358; qf_moe_m8_wave64.hip:261-299). */
+int orc_csr_build(const int *sel, const float *wt, int T, int K, int E,
+                  int *exp_ids, int *exp_ptr, int *pair_tok, int *pair_k, float *pair_wt,
+                  int *n_pairs) {
+    int *cnt = (int *)calloc((size_t)E, sizeof(int));
+    for (int p = 0; p < T * K; p++) {
+        const int e = sel[p];
+        if (e < 0 || e >= E) { free(cnt); return -1; }
+        cnt[e]++;
+    }
+    int n = 0, off = 0;
+    int *start = (int *)malloc(sizeof(int) * (size_t)E);
+    for (int e = 0; e < E; e++) {
+        start[e] = off;
+        if (cnt[e]) { exp_ids[n] = e; exp_ptr[n] = off; n++; }
+        off += cnt[e];
+    }
+    exp_ptr[n] = off;
+    for (int t = 0; t < T; t++)
+        for (int k = 0; k < K; k++) {
+            const int e = sel[t * K + k], w = start[e]++;
+            pair_tok[w] = t; pair_k[w] = k; pair_wt[w] = wt[t * K + k];
+        }
+    *n_pairs = off;
+    free(cnt); free(start);
+    return n;
+}
+
+/* ------------------------------------------------------------------------ */
+static void gen_i8_expert(const orc_layer_cfg *c, int e, int8_t *qg, float *sg,
+                          int8_t *qu, float *su, int8_t *qd, float *sd) {
+    const uint64_t H = (uint64_t)c->H, I = (uint64_t)c->I;
+    orc_fill_i8(c->seed, c->layer, ORC_T_QG, (uint64_t)e * I * H, I * H, qg);
+    orc_fill_i8(c->seed, c->layer, ORC_T_QU, (uint64_t)e * I * H, I * H, qu);
+    orc_fill_i8(c->seed, c->layer, ORC_T_QD, (uint64_t)e * H * I, H * I, qd);
+    orc_fill_rowscale(c->seed, c->layer, ORC_T_SG, (uint64_t)e * I, I, sg);
+    orc_fill_rowscale(c->seed, c->layer, ORC_T_SU, (uint64_t)e * I, I, su);
+    orc_fill_rowscale(c->seed, c->layer, ORC_T_SD, (uint64_t)e * H, H, sd);
+}
+
+int orc_moe_layer(const orc_layer_cfg *c, int M, uint16_t *x_out, float *logits,
+                  int *sel, double *w64, double *y64, uint16_t *ybf16) {
+    const int H = c->H, I = c->I, E = c->E, K = c->K;
+    if (H % 256 || I % 32 || K > 64 || K > E) return -1;
+    uint16_t *x = x_out ? x_out : (uint16_t *)malloc(sizeof(uint16_t) * (size_t)M * H);
+    orc_fill_gauss_bf16(c->seed, c->x_layer, ORC_T_X, (uint64_t)c->x_row0 * H, (uint64_t)M * H, x);
+    float *W = (float *)malloc(sizeof(float) * (size_t)E * H);
+    orc_fill_gauss(c->seed, c->layer, ORC_T_ROUTER, 0, (uint64_t)E * H, 0.02f, W);
+    float *bias = NULL;
+    if (c->use_bias) {
+        bias = (float *)malloc(sizeof(float) * (size_t)E);
+        orc_fill_gauss(c->seed, c->layer, ORC_T_BIAS, 0, (uint64_t)E, 1.5f, bias);
+    }
+    float *lg = logits ? logits : (float *)malloc(sizeof(float) * (size_t)M * E);
+    orc_router_logits(W, x, bias, M, E, H, lg);
+    orc_topk(lg, M, E, K, c->renorm, sel, w64, NULL);
+
+    float *g = (float *)malloc(sizeof(float) * (size_t)H);
+    orc_fill_gauss(c->seed, c->layer, ORC_T_SHGATE, 0, (uint64_t)H, 0.02f, g);
+    int8_t *qg = (int8_t *)malloc((size_t)I * H), *qu = (int8_t *)malloc((size_t)I * H), *qd = (int8_t *)malloc((size_t)I * H);
+    float *sg = (float *)malloc(4 * (size_t)I), *su = (float *)malloc(4 * (size_t)I), *sd = (float *)malloc(4 * (size_t)H);
+    uint8_t *fg = NULL, *fu = NULL, *fd = NULL, *fsg = NULL, *fsu = NULL, *fsd = NULL;
+    if (c->fmt == 1) {
+        fg = (uint8_t *)malloc((size_t)I * H / 2); fu = (uint8_t *)malloc((size_t)I * H / 2); fd = (uint8_t *)malloc((size_t)I * H / 2);
+        fsg = (uint8_t *)malloc((size_t)I * H / 16); fsu = (uint8_t *)malloc((size_t)I * H / 16); fsd = (uint8_t *)malloc((size_t)I * H / 16);
+    }
+    double *xd = (double *)malloc(sizeof(double) * (size_t)H), *h = (double *)malloc(sizeof(double) * (size_t)I);
+    double *ye = (double *)malloc(sizeof(double) * (size_t)H);
+    for (int m = 0; m < M; m++)
+        for (int k = 0; k < H; k++) y64[(size_t)m * H + k] = 0.0;
+
+    /* routed experts: visit each distinct expert once, in ascending order */
+    unsigned char *used = (unsigned char *)calloc((size_t)E, 1);
+    for (int p = 0; p < M * K; p++) used[sel[p]] = 1;
+    for (int e = 0; e < E; e++) {
+        if (!used[e]) continue;
+        const uint64_t IH = (uint64_t)I * H;
+        if (c->fmt == 0) {
+            gen_i8_expert(c, e, qg, sg, qu, su, qd, sd);
+        } else {
+            orc_fill_fp4byte(c->seed, c->layer, ORC_T_FG, (uint64_t)e * IH / 2, IH / 2, fg);
+            orc_fill_fp4byte(c->seed, c->layer, ORC_T_FU, (uint64_t)e * IH / 2, IH / 2, fu);
+            orc_fill_fp4byte(c->seed, c->layer, ORC_T_FD, (uint64_t)e * IH / 2, IH / 2, fd);
+            orc_fill_e4m3scale(c->seed, c->layer, ORC_T_FSG, (uint64_t)e * IH / 16, IH / 16, fsg);
+            orc_fill_e4m3scale(c->seed, c->layer, ORC_T_FSU, (uint64_t)e * IH / 16, IH / 16, fsu);
+            orc_fill_e4m3scale(c->seed, c->layer, ORC_T_FSD, (uint64_t)e * IH / 16, IH / 16, fsd);
+        }
+        for (int m = 0; m < M; m++)
+            for (int k = 0; k < K; k++) {
+                if (sel[m * K + k] != e) continue;
+                for (int i = 0; i < H; i++) xd[i] = (double)orc_bf16_to_f32(x[(size_t)m * H + i]);
+                if (c->fmt == 0) orc_i8_expert(xd, qg, sg, qu, su, qd, sd, H, I, h, ye);
+                else orc_nvfp4_expert(xd, fg, fsg, 0.01f, fu, fsu, 0.01f, fd, fsd, 0.01f, H, I, h, ye);
+                const double w = w64[m * K + k];
+                for (int i = 0; i < H; i++) y64[(size_t)m * H + i] += w * ye[i];
+            }
+    }
+    /* shared expert (index E of the generator), always INT8 */
+    gen_i8_expert(c, E, qg, sg, qu, su, qd, sd);
+    for (int m = 0; m < M; m++) {
+        double gx = 0.0;
+        for (int i = 0; i < H; i++) {
+            xd[i] = (double)orc_bf16_to_f32(x[(size_t)m * H + i]);
+            gx += (double)g[i] * xd[i];
+        }
+        orc_i8_expert(xd, qg, sg, qu, su, qd, sd, H, I, h, ye);
+        const double gam = c->gated ? 1.0 / (1.0 + exp(-gx)) : 1.0;
+        for (int i = 0; i < H; i++) y64[(size_t)m * H + i] += gam * ye[i];
+    }
+    if (ybf16)
+        for (size_t i = 0; i < (size_t)M * H; i++) ybf16[i] = orc_bf16_rne((float)y64[i]);
+
+    free(used); free(xd); free(h); free(ye); free(g);
+    free(qg); free(qu); free(qd); free(sg); free(su); free(sd);
+    free(fg); free(fu); free(fd); free(fsg); free(fsu); free(fsd);
+    if (!logits) free(lg);
+    free(bias); free(W);
+    if (!x_out) free(x);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* CPU baseline: the same layer in fp32 accumulate over a resident host
+   arena, parallel over output rows. Router in the canonical order. */
+static float silu_f(float g) { return g / (1.0f + expf(-g)); }
+void orc_cpu_moe_layer_fast(const orc_host_layer *L, int H, int I, int E, int K,
+                            const uint16_t *x, int M, float *y, int nthreads) {
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+    (void)nthreads;
+#endif
+    float *lg = (float *)malloc(sizeof(float) * (size_t)M * E);
+    float *xf = (float *)malloc(sizeof(float) * (size_t)M * H);
+    for (size_t i = 0; i < (size_t)M * H; i++) xf[i] = orc_bf16_to_f32(x[i]);
+    #pragma omp parallel for schedule(static)
+    for (int me = 0; me < M * E; me++) {
+        const int m = me / E, e = me % E;
+        lg[me] = canon_dot(L->router + (size_t)e * H, xf + (size_t)m * H, H);
+    }
+    int *sel = (int *)malloc(sizeof(int) * (size_t)M * (K + 1));
+    float *wt = (float *)malloc(sizeof(float) * (size_t)M * (K + 1));
+    int *selk = (int *)malloc(sizeof(int) * (size_t)M * K);
+    float *wk = (float *)malloc(sizeof(float) * (size_t)M * K);
+    orc_topk(lg, M, E, K, 1, selk, NULL, wk);
+    for (int m = 0; m < M; m++) {
+        float gx = 0.0f;
+        for (int i = 0; i < H; i++) gx += L->shgate[i] * xf[(size_t)m * H + i];
+        for (int k = 0; k < K; k++) { sel[m * (K + 1) + k] = selk[m * K + k]; wt[m * (K + 1) + k] = wk[m * K + k]; }
+        sel[m * (K + 1) + K] = E;
+        wt[m * (K + 1) + K] = 1.0f / (1.0f + expf(-gx));
+    }
+    const int NE = K + 1;
+    float *h = (float *)malloc(sizeof(float) * (size_t)M * NE * I);
+    #pragma omp parallel for schedule(static)
+    for (int idx = 0; idx < M * NE * I; idx++) {
+        const int r = idx % I, mk = idx / I, m = mk / NE;
+        const int e = sel[mk];
+        const int8_t *wg = L->qg + ((size_t)e * I + r) * H, *wu = L->qu + ((size_t)e * I + r) * H;
+        const float *xv = xf + (size_t)m * H;
+        float ag = 0.0f, au = 0.0f;
+        for (int k = 0; k < H; k++) { ag += (float)wg[k] * xv[k]; au += (float)wu[k] * xv[k]; }
+        const float g = ag * L->sg[(size_t)e * I + r], u = au * L->su[(size_t)e * I + r];
+        h[idx] = silu_f(g) * u;
+    }
+    #pragma omp parallel for schedule(static)
+    for (int mc = 0; mc < M * H; mc++) {
+        const int m = mc / H, c = mc % H;
+        float tot = 0.0f;
+        for (int k = 0; k < NE; k++) {
+            const int e = sel[m * NE + k];
+            const int8_t *wd = L->qd + ((size_t)e * H + c) * I;
+            const float *hv = h + ((size_t)m * NE + k) * I;
+            float a = 0.0f;
+            for (int r = 0; r < I; r++) a += (float)wd[r] * hv[r];
+            tot += wt[m * NE + k] * a * L->sd[(size_t)e * H + c];
+        }
+        y[mc] = tot;
+    }
+    free(h); free(sel); free(wt); free(selk); free(wk); free(lg); free(xf);
+}

@@ -1,0 +1,313 @@
+// qfm_api.cpp -- extern "C" boundary: configuration, error latch, the
+// reference-named launchers, the fused per-layer forward and the harness
+// utilities. Host code only; every kernel lives in the .hip files.
+#include "qfm_internal.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstddef>
+#include <cstring>
+
+namespace qfm {
+
+Cfg g_cfg;
+
+static thread_local int t_err_code = 0;
+static thread_local char t_err_msg[512] = {0};
+
+void set_error(int code, const char *fmt, ...) {
+    if (t_err_code) return;   // keep the first error until it is read
+    t_err_code = code;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_err_msg, sizeof t_err_msg, fmt, ap);
+    va_end(ap);
+}
+
+int check_launch(const char *what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error(-100 - (int)e, "%s: launch failed: %s", what, hipGetErrorString(e));
+        return -3;
+    }
+    return 0;
+}
+
+// The arena struct must stay byte-compatible with the reference's Qf4ExpCache
+// (ocho/amd_server/qf_nvfp4_wave64.h:133-173) on LP64.
+static_assert(offsetof(Qf4ExpCache, w_gate) == 8, "Qf4ExpCache layout");
+static_assert(offsetof(Qf4ExpCache, i8_gate) == 80, "Qf4ExpCache layout");
+static_assert(offsetof(Qf4ExpCache, nv_ring) == 128, "Qf4ExpCache layout");
+static_assert(offsetof(Qf4ExpCache, s_gate) == 136, "Qf4ExpCache layout");
+static_assert(offsetof(Qf4ExpCache, clock) == 184, "Qf4ExpCache layout");
+static_assert(offsetof(Qf4ExpCache, fully_resident) == 216, "Qf4ExpCache layout");
+static_assert(offsetof(Qf4ExpCache, s2g_dev) == 256, "Qf4ExpCache layout");
+static_assert(offsetof(Qf4ExpCache, mb_dev) == 296, "Qf4ExpCache layout");
+static_assert(sizeof(Qf4ExpCache) == 312, "Qf4ExpCache layout");
+static_assert(sizeof(Qf8I8Mat) == 24, "Qf8I8Mat layout");
+static_assert(sizeof(Qf5M8Route) == 56, "Qf5M8Route layout");
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct WsLayout {
+    size_t logits, sel, wts, hidden, total;
+};
+static WsLayout ws_layout(int M) {
+    const Cfg &c = g_cfg;
+    WsLayout w{};
+    size_t off = 0;
+    w.logits = off; off += align256((size_t)M * (c.E + 1) * sizeof(float));
+    w.sel = off;    off += align256((size_t)M * c.K * sizeof(int));
+    w.wts = off;    off += align256((size_t)M * c.K * sizeof(float));
+    w.hidden = off; off += align256((size_t)M * (c.K + 1) * c.I * sizeof(float));
+    w.total = off;
+    return w;
+}
+
+static bool layer_ok(const qfm_layer *L) {
+    if (!L || !L->arena || !L->router) return false;
+    if (L->fmt == QFM_FMT_INT8) {
+        const Qf4ExpCache *a = L->arena;
+        if (!a->i8_gate || !a->i8_up || !a->i8_down || !a->i8s_gate || !a->i8s_up || !a->i8s_down) return false;
+    } else {
+        return false;
+    }
+    if (L->sh_gate.w) {
+        if (!L->sh_up.w || !L->sh_down.w || !L->sh_gate.s || !L->sh_up.s || !L->sh_down.s) return false;
+        if (L->sh_gate.rows != g_cfg.I || L->sh_gate.K != g_cfg.H || L->sh_up.rows != g_cfg.I ||
+            L->sh_up.K != g_cfg.H || L->sh_down.rows != g_cfg.H || L->sh_down.K != g_cfg.I)
+            return false;
+    }
+    return true;
+}
+
+}  // namespace qfm
+
+using namespace qfm;
+
+extern "C" {
+
+int qfm_init(const qfm_config *cfg) {
+    if (!cfg) { set_error(-1, "qfm_init: null config"); return -1; }
+    const bool shape = (cfg->hidden == 2048 && cfg->inter == 512) || (cfg->hidden == 2560 && cfg->inter == 640);
+    const int E = cfg->n_experts;
+    const bool e_ok = E == 64 || E == 128 || E == 256 || E == 512 || E == 1024;
+    if (!shape || !e_ok || cfg->top_k < 1 || cfg->top_k > 16 || cfg->top_k > E) {
+        set_error(-1, "qfm_init: unsupported configuration H=%d I=%d E=%d K=%d", cfg->hidden, cfg->inter, E, cfg->top_k);
+        return -1;
+    }
+    g_cfg.H = cfg->hidden; g_cfg.I = cfg->inter; g_cfg.E = E; g_cfg.K = cfg->top_k;
+    g_cfg.renorm = cfg->renorm ? 1 : 0; g_cfg.gated = cfg->shared_gated ? 1 : 0;
+    return 0;
+}
+
+int qfm_get_config(qfm_config *cfg) {
+    if (!cfg) return -1;
+    cfg->hidden = g_cfg.H; cfg->inter = g_cfg.I; cfg->n_experts = g_cfg.E; cfg->top_k = g_cfg.K;
+    cfg->renorm = g_cfg.renorm; cfg->shared_gated = g_cfg.gated;
+    return 0;
+}
+
+const char *qfm_last_error(void) {
+    static thread_local char out[512];
+    std::strncpy(out, t_err_msg, sizeof out - 1);
+    out[sizeof out - 1] = 0;
+    t_err_code = 0; t_err_msg[0] = 0;
+    return out;
+}
+
+int qfm_status(void) {
+    check_launch("qfm_status");
+    return t_err_code;
+}
+
+const char *qfm_version(void) { return "qfm 0.1 gfx950"; }
+
+size_t qfm_sizeof(int which) {
+    switch (which) {
+    case 0: return sizeof(Qf4ExpCache);
+    case 1: return sizeof(qfm_layer);
+    case 2: return sizeof(qfm_synth_layer);
+    case 3: return sizeof(Qf8I8Mat);
+    case 4: return sizeof(Qf5M8Route);
+    case 5: return sizeof(qfm_config);
+    case 6: return sizeof(qfm_ws_view);
+    default: return 0;
+    }
+}
+
+// ---- router ----------------------------------------------------------------
+void qf_rtr_gemv_launch(const uint16_t *router, const float *x, float *logits, hipStream_t s) {
+    if (!router || !x || !logits) { set_error(-1, "qf_rtr_gemv_launch: null pointer"); return; }
+    launch_router_bf16w(router, x, logits, s);
+}
+void qf_rtr_topk10_launch(const float *logits, int *sel_ids, float *wts, hipStream_t s) {
+    if (!logits || !sel_ids || !wts) { set_error(-1, "qf_rtr_topk10_launch: null pointer"); return; }
+    launch_topk(logits, g_cfg.E, 1, sel_ids, wts, s);
+}
+void qf_rtr_topk10_rows_launch(const float *logits, int *sel_ids, float *wts, int T, hipStream_t s) {
+    if (!logits || !sel_ids || !wts || T < 1) { set_error(-1, "qf_rtr_topk10_rows_launch: bad arguments"); return; }
+    launch_topk(logits, g_cfg.E, T, sel_ids, wts, s);
+}
+int qfm_router_logits(const float *W, const float *bias, const uint16_t *x, int M, float *logits, hipStream_t s) {
+    if (!W || !x || !logits || M < 1) { set_error(-1, "qfm_router_logits: bad arguments"); return -1; }
+    return launch_router_f32w(W, bias, nullptr, x, M, logits, g_cfg.E, s);
+}
+int qfm_topk(const float *logits, int M, int *sel, float *wts, hipStream_t s) {
+    if (!logits || !sel || !wts || M < 1) { set_error(-1, "qfm_topk: bad arguments"); return -1; }
+    return launch_topk(logits, g_cfg.E, M, sel, wts, s);
+}
+
+// ---- INT8 M=1 (reference signatures) ------------------------------------------
+void qf8_i8_gateup_m1(const Qf4ExpCache *c, const float *x, int8_t *x8q, float *x8s, float *hidden,
+                      const int *sel_ids, int nexp, int quant_x, hipStream_t s) {
+    (void)x8q; (void)x8s; (void)quant_x;
+    if (!x) { set_error(-1, "qf8_i8_gateup_m1: null x"); return; }
+    launch_i8_gateup_m1(c, nullptr, x, sel_ids, nexp, nullptr, hidden, s);
+}
+void qf8_i8_down_m1(const Qf4ExpCache *c, const float *hidden, int8_t *h8q, float *h8s, const float *wts,
+                    const int *sel_ids, float *y, int nexp, hipStream_t s) {
+    (void)h8q; (void)h8s;
+    launch_i8_down_m1(c, hidden, wts, sel_ids, nexp, nullptr, nullptr, y, nullptr, s);
+}
+
+// ---- fused layer ---------------------------------------------------------------
+size_t qfm_workspace_bytes(int M) { return M < 1 ? 0 : ws_layout(M).total; }
+
+int qfm_workspace_view(void *ws, int M, qfm_ws_view *v) {
+    if (!ws || !v || M < 1) return -1;
+    const WsLayout w = ws_layout(M);
+    char *b = static_cast<char *>(ws);
+    v->logits = reinterpret_cast<float *>(b + w.logits);
+    v->sel = reinterpret_cast<int *>(b + w.sel);
+    v->wts = reinterpret_cast<float *>(b + w.wts);
+    v->hidden = reinterpret_cast<float *>(b + w.hidden);
+    return 0;
+}
+
+int qfm_moe_forward(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
+                    hipStream_t s) {
+    if (!layer_ok(L) || !x || !y || !ws || M < 1) { set_error(-1, "qfm_moe_forward: bad arguments"); return -1; }
+    if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) { set_error(-1, "qfm_moe_forward: workspace not 256-byte aligned"); return -1; }
+    const WsLayout w = ws_layout(M);
+    if (ws_bytes < w.total) { set_error(-1, "qfm_moe_forward: workspace too small (%zu < %zu)", ws_bytes, w.total); return -1; }
+    const Cfg &c = g_cfg;
+    char *b = static_cast<char *>(ws);
+    float *logits = reinterpret_cast<float *>(b + w.logits);
+    int *sel = reinterpret_cast<int *>(b + w.sel);
+    float *wts = reinterpret_cast<float *>(b + w.wts);
+    float *hidden = reinterpret_cast<float *>(b + w.hidden);
+    const bool has_sh = L->sh_gate.w != nullptr;
+    const float *g = (has_sh && c.gated && L->sh_gate_inp) ? L->sh_gate_inp : nullptr;
+    if (has_sh && c.gated && !g) { set_error(-1, "qfm_moe_forward: gated shared expert needs sh_gate_inp"); return -1; }
+    I8Shared shp{};
+    if (has_sh) {
+        shp.qg = L->sh_gate.w; shp.qu = L->sh_up.w; shp.qd = L->sh_down.w;
+        shp.sg = L->sh_gate.s; shp.su = L->sh_up.s; shp.sd = L->sh_down.s;
+    }
+    int rc = launch_router_f32w(L->router, L->router_bias, g, x, M, logits, c.E + 1, s);
+    if (!rc) rc = launch_topk(logits, c.E + 1, M, sel, wts, s);
+    for (int m = 0; m < M && !rc; m++) {
+        float *hm = hidden + (size_t)m * (c.K + 1) * c.I;
+        rc = launch_i8_gateup_m1(L->arena, x + (size_t)m * c.H, nullptr, sel + m * c.K, c.K, has_sh ? &shp : nullptr, hm, s);
+        if (!rc) rc = launch_i8_down_m1(L->arena, hm, wts + m * c.K, sel + m * c.K, c.K, has_sh ? &shp : nullptr,
+                                        g ? logits + (size_t)m * (c.E + 1) + c.E : nullptr, nullptr, y + (size_t)m * c.H, s);
+    }
+    return rc;
+}
+
+int qfm_moe_forward_layers(const qfm_layer *layers, int nl, const uint16_t *x, long x_stride, int M, uint16_t *y,
+                           long y_stride, void *ws, size_t ws_bytes, hipStream_t s) {
+    if (!layers || nl < 1 || x_stride < 0 || y_stride < 0) { set_error(-1, "qfm_moe_forward_layers: bad arguments"); return -1; }
+    for (int l = 0; l < nl; l++) {
+        const int rc = qfm_moe_forward(&layers[l], x + (size_t)l * x_stride, M, y + (size_t)l * y_stride, ws, ws_bytes, s);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+// ---- graphs ----------------------------------------------------------------------
+int qfm_graph_capture_begin(void *stream) {
+    const hipError_t e = hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeGlobal);
+    if (e != hipSuccess) { set_error(-5, "hipStreamBeginCapture: %s", hipGetErrorString(e)); return -5; }
+    return 0;
+}
+void *qfm_graph_capture_end(void *stream) {
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(static_cast<hipStream_t>(stream), &g);
+    if (e != hipSuccess || !g) { set_error(-5, "hipStreamEndCapture: %s", hipGetErrorString(e)); return nullptr; }
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) { set_error(-5, "hipGraphInstantiate: %s", hipGetErrorString(e)); return nullptr; }
+    return x;
+}
+int qfm_graph_launch(void *graph_exec, void *stream) {
+    const hipError_t e = hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) { set_error(-5, "hipGraphLaunch: %s", hipGetErrorString(e)); return -5; }
+    return 0;
+}
+int qfm_graph_destroy(void *graph_exec) {
+    return hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)) == hipSuccess ? 0 : -1;
+}
+
+// ---- generator -------------------------------------------------------------------
+int qfm_gen_fill(void *out, int kind, uint64_t n0, uint64_t cnt, uint32_t seed, uint32_t layer, uint32_t tensor,
+                 float scale, hipStream_t s) {
+    return launch_gen_fill(out, kind, n0, cnt, seed, layer, tensor, scale, s);
+}
+int qfm_fill_f32(float *out, uint64_t cnt, float value, hipStream_t s) { return launch_fill_f32(out, cnt, value, s); }
+
+// ---- harness utilities -------------------------------------------------------------
+void *qfm_dev_malloc(size_t bytes) {
+    void *p = nullptr;
+    const hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) { set_error(-4, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e)); return nullptr; }
+    return p;
+}
+int qfm_dev_free(void *p) { return hipFree(p) == hipSuccess ? 0 : -1; }
+int qfm_memcpy_h2d(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1; }
+int qfm_memcpy_d2h(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1; }
+int qfm_memset(void *dst, int v, size_t n) { return hipMemset(dst, v, n) == hipSuccess ? 0 : -1; }
+void *qfm_stream_create(void) {
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    return s;
+}
+int qfm_stream_destroy(void *s) { return hipStreamDestroy(static_cast<hipStream_t>(s)) == hipSuccess ? 0 : -1; }
+int qfm_stream_sync(void *s) {
+    const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(s));
+    if (e != hipSuccess) { set_error(-100 - (int)e, "hipStreamSynchronize: %s", hipGetErrorString(e)); return -1; }
+    return 0;
+}
+int qfm_device_sync(void) {
+    const hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) { set_error(-100 - (int)e, "hipDeviceSynchronize: %s", hipGetErrorString(e)); return -1; }
+    return 0;
+}
+void *qfm_event_create(void) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+int qfm_event_destroy(void *e) { return hipEventDestroy(static_cast<hipEvent_t>(e)) == hipSuccess ? 0 : -1; }
+int qfm_event_record(void *e, void *s) {
+    return hipEventRecord(static_cast<hipEvent_t>(e), static_cast<hipStream_t>(s)) == hipSuccess ? 0 : -1;
+}
+float qfm_event_elapsed_ms(void *e0, void *e1) {
+    float ms = -1.0f;
+    if (hipEventElapsedTime(&ms, static_cast<hipEvent_t>(e0), static_cast<hipEvent_t>(e1)) != hipSuccess) return -1.0f;
+    return ms;
+}
+int qfm_device_info(char *name, int name_len, int *n_cu, size_t *mem_bytes, int *arch_major, int *arch_minor) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, 0) != hipSuccess) return -1;
+    if (name && name_len > 0) { std::strncpy(name, p.gcnArchName, (size_t)name_len - 1); name[name_len - 1] = 0; }
+    if (n_cu) *n_cu = p.multiProcessorCount;
+    if (mem_bytes) *mem_bytes = p.totalGlobalMem;
+    if (arch_major) *arch_major = p.major;
+    if (arch_minor) *arch_minor = p.minor;
+    return 0;
+}
+
+}  // extern "C"

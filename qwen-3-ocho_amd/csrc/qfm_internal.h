@@ -1,0 +1,45 @@
+// qfm_internal.h -- host-side internals shared by the translation units.
+#pragma once
+#include "../../include/qf_moe.h"
+#include <hip/hip_runtime.h>
+
+namespace qfm {
+
+// Active shape configuration (set by qfm_init; defaults to the BASELINE shape).
+struct Cfg {
+    int H = 2048, I = 512, E = 512, K = 10, renorm = 1, gated = 1;
+};
+extern Cfg g_cfg;
+
+// Error latch: the first error since the last read is kept.
+void set_error(int code, const char *fmt, ...);
+int  check_launch(const char *what);   // polls hipGetLastError after a launch
+
+// shape dispatch helpers
+inline bool shape_2048() { return g_cfg.H == 2048 && g_cfg.I == 512; }
+inline bool shape_2560() { return g_cfg.H == 2560 && g_cfg.I == 640; }
+
+// ---- launchers (defined in the .hip files) ----------------------------------
+// generator
+int launch_gen_fill(void *out, int kind, uint64_t n0, uint64_t cnt, uint32_t seed,
+                    uint32_t layer, uint32_t tensor, float scale, hipStream_t s);
+int launch_fill_f32(float *out, uint64_t cnt, float value, hipStream_t s);
+
+// router: W_f32 [E][H] (+extra row g [H] written at column E when g != nullptr)
+int launch_router_f32w(const float *W, const float *bias, const float *g,
+                       const uint16_t *x, int M, float *logits, int ld_logits, hipStream_t s);
+int launch_router_bf16w(const uint16_t *W, const float *x, float *logits, hipStream_t s);
+int launch_topk(const float *logits, int ld_logits, int M, int *sel, float *wts, hipStream_t s);
+
+// INT8 M=1 experts. Job list: nexp routed experts from sel (device), plus the
+// shared expert when sh != nullptr. x is bf16 (xb) or fp32 (xf).
+struct I8Shared { const int8_t *qg, *qu, *qd; const float *sg, *su, *sd; };
+int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *xf,
+                        const int *sel, int nexp, const I8Shared *sh, float *hidden, hipStream_t s);
+// y = sum_k wts[k] * down_k(hidden_k) (+ gamma * shared_down(hidden_K)), gamma =
+// sigmoid(*gdot) when gdot != nullptr, 1 otherwise. Writes y32 and/or ybf.
+int launch_i8_down_m1(const Qf4ExpCache *c, const float *hidden, const float *wts, const int *sel,
+                      int nexp, const I8Shared *sh, const float *gdot, float *y32, uint16_t *ybf,
+                      hipStream_t s);
+
+}  // namespace qfm

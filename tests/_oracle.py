@@ -1,0 +1,212 @@
+"""ctypes binding of the CPU oracle (oracle/_build/libqfm_oracle.so).
+
+Test infrastructure: the checker the HIP path is compared against. Builds
+the oracle with make on first use when the shared object is absent.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+ORACLE_SO = os.path.join(ORACLE_DIR, "_build", "libqfm_oracle.so")
+
+T_QG, T_QU, T_QD, T_SG, T_SU, T_SD = 1, 2, 3, 4, 5, 6
+T_ROUTER, T_X, T_SHGATE, T_BIAS = 7, 8, 9, 10
+T_FG, T_FU, T_FD, T_FSG, T_FSU, T_FSD = 11, 12, 13, 14, 15, 16
+
+vp = C.c_void_p
+u32, u64 = C.c_uint32, C.c_uint64
+
+
+class LayerCfg(C.Structure):
+    _fields_ = [("H", C.c_int), ("I", C.c_int), ("E", C.c_int), ("K", C.c_int),
+                ("fmt", C.c_int), ("gated", C.c_int), ("renorm", C.c_int), ("use_bias", C.c_int),
+                ("seed", u32), ("layer", u32), ("x_layer", u32), ("x_row0", C.c_int)]
+
+
+class HostLayer(C.Structure):
+    _fields_ = [("router", vp), ("qg", vp), ("qu", vp), ("qd", vp),
+                ("sg", vp), ("su", vp), ("sd", vp), ("shgate", vp)]
+
+
+_SIGS = {
+    "orc_philox4x32_10": (None, [vp, vp, vp]),
+    "orc_word": (u32, [u32, u32, u32, u64]),
+    "orc_gen_i8": (C.c_int8, [u32, u32, u32, u64]),
+    "orc_gen_rowscale": (C.c_float, [u32, u32, u32, u64]),
+    "orc_gen_gauss": (C.c_float, [u32, u32, u32, u64]),
+    "orc_gen_fp4byte": (C.c_uint8, [u32, u32, u32, u64]),
+    "orc_gen_e4m3scale": (C.c_uint8, [u32, u32, u32, u64]),
+    "orc_fill_i8": (None, [u32, u32, u32, u64, u64, vp]),
+    "orc_fill_rowscale": (None, [u32, u32, u32, u64, u64, vp]),
+    "orc_fill_gauss": (None, [u32, u32, u32, u64, u64, C.c_float, vp]),
+    "orc_fill_gauss_bf16": (None, [u32, u32, u32, u64, u64, vp]),
+    "orc_fill_fp4byte": (None, [u32, u32, u32, u64, u64, vp]),
+    "orc_fill_e4m3scale": (None, [u32, u32, u32, u64, u64, vp]),
+    "orc_e2m1": (C.c_float, [u32]),
+    "orc_e4m3": (C.c_float, [u32]),
+    "orc_e4m3_encode": (C.c_uint8, [C.c_float]),
+    "orc_bf16_rne": (C.c_uint16, [C.c_float]),
+    "orc_bf16_to_f32": (C.c_float, [C.c_uint16]),
+    "orc_router_logits": (None, [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
+    "orc_topk": (None, [vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, vp]),
+    "orc_i8_expert": (None, [vp, vp, vp, vp, vp, vp, vp, C.c_int, C.c_int, vp, vp]),
+    "orc_nvfp4_expert": (None, [vp, vp, vp, C.c_float, vp, vp, C.c_float, vp, vp, C.c_float,
+                                C.c_int, C.c_int, vp, vp]),
+    "orc_nvfp4_dequant": (None, [vp, vp, C.c_float, C.c_int, C.c_int, vp]),
+    "orc_x8_quant": (None, [vp, C.c_int, vp, vp]),
+    "orc_csr_build": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp, vp]),
+    "orc_moe_layer": (C.c_int, [C.POINTER(LayerCfg), C.c_int, vp, vp, vp, vp, vp, vp]),
+    "orc_cpu_moe_layer_fast": (None, [C.POINTER(HostLayer), C.c_int, C.c_int, C.c_int, C.c_int,
+                                      vp, C.c_int, vp, C.c_int]),
+}
+
+_lib = None
+
+
+def load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(ORACLE_SO):
+        subprocess.run(["make", "-C", ORACLE_DIR], check=True, capture_output=True)
+    lib = C.CDLL(ORACLE_SO)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def ptr(a):
+    return a.ctypes.data if a is not None else None
+
+
+# ---- numpy-facing helpers -------------------------------------------------
+def philox(ctr, key):
+    lib = load()
+    c = np.array(ctr, dtype=np.uint32)
+    k = np.array(key, dtype=np.uint32)
+    o = np.zeros(4, dtype=np.uint32)
+    lib.orc_philox4x32_10(ptr(c), ptr(k), ptr(o))
+    return o
+
+
+def fill(kind, seed, layer, tensor, n0, cnt, scale=1.0):
+    lib = load()
+    if kind == "i8":
+        out = np.empty(cnt, np.int8); lib.orc_fill_i8(seed, layer, tensor, n0, cnt, ptr(out))
+    elif kind == "rowscale":
+        out = np.empty(cnt, np.float32); lib.orc_fill_rowscale(seed, layer, tensor, n0, cnt, ptr(out))
+    elif kind == "gauss":
+        out = np.empty(cnt, np.float32); lib.orc_fill_gauss(seed, layer, tensor, n0, cnt, scale, ptr(out))
+    elif kind == "gauss_bf16":
+        out = np.empty(cnt, np.uint16); lib.orc_fill_gauss_bf16(seed, layer, tensor, n0, cnt, ptr(out))
+    elif kind == "fp4byte":
+        out = np.empty(cnt, np.uint8); lib.orc_fill_fp4byte(seed, layer, tensor, n0, cnt, ptr(out))
+    elif kind == "e4m3scale":
+        out = np.empty(cnt, np.uint8); lib.orc_fill_e4m3scale(seed, layer, tensor, n0, cnt, ptr(out))
+    else:
+        raise ValueError(kind)
+    return out
+
+
+def bf16_to_f32(h):
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def router_logits(W, x_bf16, bias=None):
+    lib = load()
+    W = np.ascontiguousarray(W, np.float32)
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    E, H = W.shape
+    M = x.shape[0]
+    out = np.empty((M, E), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib.orc_router_logits(ptr(W), ptr(x), ptr(b), M, E, H, ptr(out))
+    return out
+
+
+def topk(logits, K, renorm=1):
+    lib = load()
+    lg = np.ascontiguousarray(logits, np.float32)
+    M, E = lg.shape
+    sel = np.empty((M, K), np.int32)
+    w64 = np.empty((M, K), np.float64)
+    w32 = np.empty((M, K), np.float32)
+    lib.orc_topk(ptr(lg), M, E, K, renorm, ptr(sel), ptr(w64), ptr(w32))
+    return sel, w64, w32
+
+
+def i8_expert(x, Qg, sg, Qu, su, Qd, sd):
+    lib = load()
+    I, H = Qg.shape
+    xd = np.ascontiguousarray(x, np.float64)
+    h = np.empty(I, np.float64)
+    y = np.empty(H, np.float64)
+    args = [np.ascontiguousarray(a) for a in (Qg, sg, Qu, su, Qd, sd)]
+    lib.orc_i8_expert(ptr(xd), *[ptr(a) for a in args], H, I, ptr(h), ptr(y))
+    return h, y
+
+
+def nvfp4_dequant(F, S, s2, rows, K):
+    lib = load()
+    out = np.empty((rows, K), np.float64)
+    lib.orc_nvfp4_dequant(ptr(np.ascontiguousarray(F)), ptr(np.ascontiguousarray(S)), s2, rows, K, ptr(out))
+    return out
+
+
+def nvfp4_expert(x, Fg, Sg, s2g, Fu, Su, s2u, Fd, Sd, s2d, H, I):
+    lib = load()
+    xd = np.ascontiguousarray(x, np.float64)
+    h = np.empty(I, np.float64)
+    y = np.empty(H, np.float64)
+    c = np.ascontiguousarray
+    lib.orc_nvfp4_expert(ptr(xd), ptr(c(Fg)), ptr(c(Sg)), s2g, ptr(c(Fu)), ptr(c(Su)), s2u,
+                         ptr(c(Fd)), ptr(c(Sd)), s2d, H, I, ptr(h), ptr(y))
+    return h, y
+
+
+def x8_quant(v):
+    lib = load()
+    v = np.ascontiguousarray(v, np.float32)
+    q = np.empty(v.shape[0], np.int8)
+    s = np.empty(v.shape[0] // 32, np.float32)
+    lib.orc_x8_quant(ptr(v), v.shape[0], ptr(q), ptr(s))
+    return q, s
+
+
+def csr_build(sel, wt, E):
+    lib = load()
+    sel = np.ascontiguousarray(sel, np.int32)
+    wt = np.ascontiguousarray(wt, np.float32)
+    T, K = sel.shape
+    exp_ids = np.empty(T * K, np.int32)
+    exp_ptr = np.empty(T * K + 1, np.int32)
+    pair_tok = np.empty(T * K, np.int32)
+    pair_k = np.empty(T * K, np.int32)
+    pair_wt = np.empty(T * K, np.float32)
+    npairs = C.c_int()
+    n = lib.orc_csr_build(ptr(sel), ptr(wt), T, K, E, ptr(exp_ids), ptr(exp_ptr), ptr(pair_tok),
+                          ptr(pair_k), ptr(pair_wt), C.byref(npairs))
+    if n < 0:
+        raise ValueError("bad expert id")
+    return exp_ids[:n], exp_ptr[:n + 1], pair_tok[:npairs.value], pair_k[:npairs.value], pair_wt[:npairs.value]
+
+
+def moe_layer(H, I, E, K, M, seed, layer, x_layer, x_row0=0, fmt=0, gated=1, renorm=1, use_bias=0):
+    lib = load()
+    cfg = LayerCfg(H, I, E, K, fmt, gated, renorm, use_bias, seed, layer, x_layer, x_row0)
+    x = np.empty((M, H), np.uint16)
+    logits = np.empty((M, E), np.float32)
+    sel = np.empty((M, K), np.int32)
+    w64 = np.empty((M, K), np.float64)
+    y64 = np.empty((M, H), np.float64)
+    ybf = np.empty((M, H), np.uint16)
+    rc = lib.orc_moe_layer(C.byref(cfg), M, ptr(x), ptr(logits), ptr(sel), ptr(w64), ptr(y64), ptr(ybf))
+    assert rc == 0
+    return dict(x=x, logits=logits, sel=sel, w=w64, y=y64, ybf=ybf)

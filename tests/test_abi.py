@@ -1,0 +1,105 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry
+point include/qf_moe.h declares, and the FFI struct layouts agree."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qf_moe.h")
+LIB = os.path.join(ROOT, "qwen-3-ocho_amd", "libqfm.so")
+
+
+def _declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    src = re.sub(r"//[^\n]*", "", src)
+    names = set()
+    for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b([a-z_][a-z0-9_]*)\s*\(", src, flags=re.M):
+        name = m.group(1)
+        if name not in ("if", "while", "for", "sizeof", "typedef"):
+            names.add(name)
+    return names
+
+
+def _exported():
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB], check=True, capture_output=True, text=True).stdout
+    return {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+
+
+@pytest.fixture(scope="module")
+def built():
+    if not os.path.exists(LIB):
+        pytest.fail("libqfm.so not built: run __graft_entry__.build()")
+    return LIB
+
+
+def test_header_declares_expected_reference_entry_points():
+    names = _declared_functions()
+    for ref_name in ["qf_rtr_gemv_launch", "qf_rtr_topk10_launch", "qf_rtr_topk10_rows_launch",
+                     "qf8_i8_gateup_m1", "qf8_i8_down_m1"]:
+        assert ref_name in names
+
+
+def test_every_declared_symbol_is_exported(built):
+    declared = _declared_functions()
+    exported = _exported()
+    missing = sorted(declared - exported)
+    assert not missing, f"declared but not exported: {missing}"
+    # nothing beyond the header leaks out of the library
+    extra = sorted(n for n in exported - declared if not n.startswith("_"))
+    assert not extra, f"exported but not declared: {extra}"
+
+
+def test_python_binding_covers_the_header(built):
+    import qfm
+    assert set(qfm.exported_symbols()) == _declared_functions()
+
+
+def test_library_loads_without_gpu_and_struct_sizes_match(built):
+    import qfm
+    lib = qfm.load()
+    assert lib.qfm_version().startswith(b"qfm")
+    assert lib.qfm_sizeof(0) == C.sizeof(qfm.Qf4ExpCache) == 312
+    assert lib.qfm_sizeof(1) == C.sizeof(qfm.QfmLayer)
+    assert lib.qfm_sizeof(2) == C.sizeof(qfm.QfmSynthLayer)
+    assert lib.qfm_sizeof(3) == C.sizeof(qfm.Qf8I8Mat) == 24
+    assert lib.qfm_sizeof(4) == C.sizeof(qfm.Qf5M8Route) == 56
+    assert lib.qfm_sizeof(5) == C.sizeof(qfm.QfmConfig)
+    assert lib.qfm_sizeof(6) == C.sizeof(qfm.QfmWsView)
+    # reference field offsets of the arena (qf_nvfp4_wave64.h:133-173 on LP64)
+    assert qfm.Qf4ExpCache.i8_gate.offset == 80 and qfm.Qf4ExpCache.s_gate.offset == 136
+    assert qfm.Qf4ExpCache.s2g_dev.offset == 256 and qfm.Qf4ExpCache.expected_seq.offset == 304
+
+
+def test_config_validation_without_gpu(built):
+    import qfm
+    lib = qfm.load()
+    bad = qfm.QfmConfig(2048, 640, 512, 10, 1, 1)
+    assert lib.qfm_init(C.byref(bad)) != 0
+    assert b"unsupported" in lib.qfm_last_error()
+    assert lib.qfm_last_error() == b""              # reading clears the latch
+    for cfg in [(2048, 512, 512, 10, 1, 1), (2560, 640, 512, 10, 1, 1), (2048, 512, 64, 4, 0, 0)]:
+        c = qfm.QfmConfig(*cfg)
+        assert lib.qfm_init(C.byref(c)) == 0
+        out = qfm.QfmConfig()
+        lib.qfm_get_config(C.byref(out))
+        assert (out.hidden, out.inter, out.n_experts, out.top_k) == cfg[:4]
+    assert lib.qfm_init(C.byref(qfm.QfmConfig(2048, 512, 512, 17, 1, 1))) != 0
+    lib.qfm_last_error()
+    lib.qfm_init(C.byref(qfm.QfmConfig(2048, 512, 512, 10, 1, 1)))
+
+
+def test_argument_rejection_without_gpu(built):
+    import qfm
+    lib = qfm.load()
+    lib.qfm_init(C.byref(qfm.QfmConfig(2048, 512, 512, 10, 1, 1)))
+    assert lib.qfm_moe_forward(None, None, 1, None, None, 0, None) != 0
+    assert b"bad arguments" in lib.qfm_last_error()
+    assert lib.qfm_router_logits(None, None, None, 1, None, None) != 0
+    lib.qfm_last_error()
+    assert lib.qfm_gen_fill(None, 0, 0, 10, 0, 0, 1, 0.0, None) != 0
+    lib.qfm_last_error()
+    assert lib.qfm_workspace_bytes(1) > 0 and lib.qfm_workspace_bytes(0) == 0

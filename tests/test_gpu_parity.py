@@ -1,0 +1,248 @@
+"""GPU parity: the HIP library (through its C ABI) against the CPU oracle.
+
+Bars (from the task's north star): router top-k indices bit-exact (ties to
+the lower index); FFN outputs within max|y - r| / max|r| <= 1e-2 (bf16 out,
+fp32 accumulate); integer/byte data (generator output) bit-exact.
+"""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import _oracle as orc
+import qfm
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2          # max|y - r| / max|r| for FFN outputs (bf16 out)
+RNG = np.random.default_rng(7)
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def lib():
+    L = qfm.load()
+    qfm.init(2048, 512, 512, 10, 1, 1)
+    info = qfm.device_info()
+    _say("device", info)
+    assert info["arch"].startswith("gfx950"), info
+    return L
+
+
+def _cfg(lib, H=2048, I=512, E=512, K=10, renorm=1, gated=1):
+    qfm.init(H, I, E, K, renorm, gated)
+
+
+def _rel(y, r):
+    return float(np.abs(y - r).max() / np.abs(r).max())
+
+
+# ------------------------------------------------------------------ generator
+@pytest.mark.parametrize("kind,tensor,n0,cnt,scale", [
+    (qfm.GEN_I8, orc.T_QG, 37 * 512 * 2048 + 5, 4099, 0.0),
+    (qfm.GEN_ROWSCALE, orc.T_SD, 511 * 2048 + 1, 3001, 0.0),
+    (qfm.GEN_GAUSS_F32, orc.T_ROUTER, 12345, 2049, 0.02),
+    (qfm.GEN_GAUSS_BF16, orc.T_X, 7 * 2048, 4096, 0.0),
+    (qfm.GEN_FP4BYTE, orc.T_FD, 3 * 1024 + 3, 5003, 0.0),
+    (qfm.GEN_E4M3SCALE, orc.T_FSG, 77, 4100, 0.0),
+])
+def test_generator_bit_exact(lib, kind, tensor, n0, cnt, scale):
+    _say("gen kind", kind, "tensor", tensor)
+    width = {qfm.GEN_I8: 1, qfm.GEN_ROWSCALE: 4, qfm.GEN_GAUSS_F32: 4, qfm.GEN_GAUSS_BF16: 2,
+             qfm.GEN_FP4BYTE: 1, qfm.GEN_E4M3SCALE: 1}[kind]
+    buf = qfm.DevBuf(cnt * width)
+    qfm.check(lib.qfm_gen_fill(buf.ptr, kind, n0, cnt, 11, 3, tensor, scale, None), "gen")
+    qfm.check(lib.qfm_device_sync(), "sync")
+    if kind == qfm.GEN_I8:
+        got, ref = buf.download(np.int8, cnt), orc.fill("i8", 11, 3, tensor, n0, cnt)
+    elif kind == qfm.GEN_ROWSCALE:
+        got, ref = buf.download(np.float32, cnt), orc.fill("rowscale", 11, 3, tensor, n0, cnt)
+    elif kind == qfm.GEN_GAUSS_F32:
+        got, ref = buf.download(np.float32, cnt), orc.fill("gauss", 11, 3, tensor, n0, cnt, scale)
+    elif kind == qfm.GEN_GAUSS_BF16:
+        got, ref = buf.download(np.uint16, cnt), orc.fill("gauss_bf16", 11, 3, tensor, n0, cnt)
+    elif kind == qfm.GEN_FP4BYTE:
+        got, ref = buf.download(np.uint8, cnt), orc.fill("fp4byte", 11, 3, tensor, n0, cnt)
+    else:
+        got, ref = buf.download(np.uint8, cnt), orc.fill("e4m3scale", 11, 3, tensor, n0, cnt)
+    assert np.array_equal(got.view(np.uint8), ref.view(np.uint8))
+    buf.free()
+
+
+# ------------------------------------------------------------------ router
+@pytest.mark.parametrize("H,M,bias", [(2048, 1, False), (2048, 8, False), (2048, 37, True), (2560, 8, True)])
+def test_router_logits_bit_exact(lib, H, M, bias):
+    _say("router", H, M, bias)
+    _cfg(lib, H=H, I=512 if H == 2048 else 640)
+    E = 512
+    W = orc.fill("gauss", 0, 1, orc.T_ROUTER, 0, E * H, 0.02).reshape(E, H)
+    x = orc.fill("gauss_bf16", 0, 2, orc.T_X, 0, M * H).reshape(M, H)
+    b = orc.fill("gauss", 0, 1, orc.T_BIAS, 0, E, 1.5) if bias else None
+    dW, dx = qfm.DevBuf.from_array(W), qfm.DevBuf.from_array(x)
+    db = qfm.DevBuf.from_array(b) if bias else None
+    dl = qfm.DevBuf(M * E * 4)
+    qfm.check(lib.qfm_router_logits(dW.ptr, db.ptr if db else None, dx.ptr, M, dl.ptr, None), "router")
+    qfm.check(lib.qfm_device_sync(), "sync")
+    got = dl.download(np.float32, (M, E))
+    ref = orc.router_logits(W, x, b)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    _cfg(lib)
+
+
+def test_router_reference_form_bit_exact(lib):
+    # qf_rtr_gemv_launch: bf16 weights, fp32 activations (qf_router_wave64.h:81-84)
+    _cfg(lib)
+    E, H = 512, 2048
+    Wb = orc.fill("gauss_bf16", 4, 4, orc.T_ROUTER, 0, E * H).reshape(E, H)
+    x = (orc.fill("gauss", 4, 5, orc.T_X, 0, H, 1.0)).astype(np.float32)
+    dW, dx, dl = qfm.DevBuf.from_array(Wb), qfm.DevBuf.from_array(x), qfm.DevBuf(E * 4)
+    lib.qf_rtr_gemv_launch(dW.ptr, dx.ptr, dl.ptr, None)
+    qfm.status_check("qf_rtr_gemv_launch")
+    qfm.check(lib.qfm_device_sync(), "sync")
+    got = dl.download(np.float32, E)
+    # same canonical order with the operand roles swapped (fma is symmetric in its factors)
+    ref = orc.router_logits(x[None, :], Wb)[:, 0]
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------------------------ top-k
+def _tie_cases(E):
+    out = [np.zeros((1, E), np.float32)]
+    lg = (RNG.standard_normal((1, E)) * 0.1).astype(np.float32)
+    top = np.argsort(-lg[0])[:20]
+    lg[0, top[8:14]] = lg[0, top[8]]
+    out.append(lg)
+    lg = np.full((1, E), -1.0, np.float32)
+    lg[0, [500, 3, 250, 7]] = 2.0
+    lg[0, [9, 400, 1, 300, 100, 200, 2, 450]] = 1.0
+    out.append(lg)
+    out.append(RNG.integers(0, 4, (6, E)).astype(np.float32))
+    lg = np.full((1, E), -5.0, np.float32)
+    lg[0, [30, 10, 20]] = [-0.0, 0.0, -0.0]
+    out.append(lg)
+    out.append((RNG.standard_normal((300, E)) * 0.9).astype(np.float32))
+    return out
+
+
+@pytest.mark.parametrize("renorm", [1, 0])
+def test_topk_bit_exact_with_ties(lib, renorm):
+    _cfg(lib, renorm=renorm)
+    E, K = 512, 10
+    for i, lg in enumerate(_tie_cases(E)):
+        _say("topk case", i, "renorm", renorm)
+        M = lg.shape[0]
+        dl, ds, dw = qfm.DevBuf.from_array(lg), qfm.DevBuf(M * K * 4), qfm.DevBuf(M * K * 4)
+        qfm.check(lib.qfm_topk(dl.ptr, M, ds.ptr, dw.ptr, None), "topk")
+        qfm.check(lib.qfm_device_sync(), "sync")
+        sel = ds.download(np.int32, (M, K))
+        w = dw.download(np.float32, (M, K))
+        rs, rw, _ = orc.topk(lg, K, renorm)
+        assert np.array_equal(sel, rs), f"case {i}"
+        assert np.allclose(w, rw, rtol=2e-6, atol=1e-7), f"case {i}"
+        # reference rows launcher form
+        if renorm:
+            lib.qf_rtr_topk10_rows_launch(dl.ptr, ds.ptr, dw.ptr, M, None)
+            qfm.status_check("rows")
+            qfm.check(lib.qfm_device_sync(), "sync")
+            assert np.array_equal(ds.download(np.int32, (M, K)), rs)
+    _cfg(lib)
+
+
+# ------------------------------------------------------------------ experts (reference entry points)
+def _oracle_expert(seed, layer, e, H, I):
+    Qg = orc.fill("i8", seed, layer, orc.T_QG, e * I * H, I * H).reshape(I, H)
+    Qu = orc.fill("i8", seed, layer, orc.T_QU, e * I * H, I * H).reshape(I, H)
+    Qd = orc.fill("i8", seed, layer, orc.T_QD, e * H * I, H * I).reshape(H, I)
+    sg = orc.fill("rowscale", seed, layer, orc.T_SG, e * I, I)
+    su = orc.fill("rowscale", seed, layer, orc.T_SU, e * I, I)
+    sd = orc.fill("rowscale", seed, layer, orc.T_SD, e * H, H)
+    return Qg, sg, Qu, su, Qd, sd
+
+
+@pytest.mark.parametrize("H,I", [(2048, 512), (2560, 640)])
+def test_i8_m1_reference_entry_points(lib, H, I):
+    _say("i8 m1 ref entry", H, I)
+    _cfg(lib, H=H, I=I)
+    seed, layer = 5, 2
+    st = qfm.Stream()
+    arena = qfm.Qf4ExpCache()
+    qfm.check(lib.qfm_arena_init(C.byref(arena), qfm.QFM_FMT_INT8, layer), "arena init")
+    qfm.check(lib.qfm_arena_generate(C.byref(arena), seed, layer, st.h), "arena gen")
+    st.sync()
+    sel = np.array([511, 0, 77, 3, 300, 12, 499, 256, 1, 128], np.int32)
+    wts = RNG.random(10).astype(np.float32)
+    wts /= wts.sum()
+    x = orc.bf16_to_f32(orc.fill("gauss_bf16", seed, 9, orc.T_X, 0, H))
+    dx, dsel, dw = qfm.DevBuf.from_array(x), qfm.DevBuf.from_array(sel), qfm.DevBuf.from_array(wts)
+    dh, dy = qfm.DevBuf(10 * I * 4), qfm.DevBuf(H * 4)
+    lib.qf8_i8_gateup_m1(C.byref(arena), dx.ptr, None, None, dh.ptr, dsel.ptr, 10, 0, st.h)
+    lib.qf8_i8_down_m1(C.byref(arena), dh.ptr, None, None, dw.ptr, dsel.ptr, dy.ptr, 10, st.h)
+    qfm.status_check("i8 m1")
+    st.sync()
+    h = dh.download(np.float32, (10, I))
+    y = dy.download(np.float32, H)
+    yref = np.zeros(H)
+    for k, e in enumerate(sel):
+        href, ye = orc.i8_expert(x.astype(np.float64), *_oracle_expert(seed, layer, int(e), H, I))
+        assert _rel(h[k], href) < 1e-5, k
+        yref += float(wts[k]) * ye
+    assert _rel(y, yref) < 1e-5
+    lib.qfm_arena_free(C.byref(arena))
+    st.destroy()
+    _cfg(lib)
+
+
+# ------------------------------------------------------------------ fused layer
+def _run_layer(lib, M, seed, layer, x_layer, fmt=qfm.QFM_FMT_INT8, bias=False):
+    st = qfm.Stream()
+    L = qfm.SynthLayer(fmt, seed, layer, with_bias=bias, stream=st)
+    cfg = qfm.QfmConfig()
+    lib.qfm_get_config(C.byref(cfg))
+    H = cfg.hidden
+    dx, dy = qfm.DevBuf(M * H * 2), qfm.DevBuf(M * H * 2)
+    qfm.check(lib.qfm_gen_input_rows(dx.ptr, M, seed, x_layer, 0, st.h), "x")
+    wsb = lib.qfm_workspace_bytes(M)
+    ws = qfm.DevBuf(wsb)
+    qfm.check(lib.qfm_moe_forward(C.byref(L.s.layer), dx.ptr, M, dy.ptr, ws.ptr, wsb, st.h), "forward")
+    st.sync()
+    view = qfm.QfmWsView()
+    lib.qfm_workspace_view(ws.ptr, M, C.byref(view))
+    out = dict(y=orc.bf16_to_f32(dy.download(np.uint16, (M, H))),
+               sel=qfm.d2h(view.sel, np.int32, (M, cfg.top_k)),
+               wts=qfm.d2h(view.wts, np.float32, (M, cfg.top_k)),
+               logits=qfm.d2h(view.logits, np.float32, (M, cfg.n_experts + 1))[:, :cfg.n_experts],
+               x=dx.download(np.uint16, (M, H)))
+    L.destroy()
+    st.destroy()
+    return out
+
+
+@pytest.mark.parametrize("M,seed,layer", [(1, 0, 0), (1, 1, 17), (8, 0, 3)])
+def test_moe_layer_int8(lib, M, seed, layer):
+    _say("layer int8", M, seed, layer)
+    _cfg(lib)
+    g = _run_layer(lib, M, seed, layer, x_layer=100 + layer)
+    r = orc.moe_layer(2048, 512, 512, 10, M, seed, layer, 100 + layer)
+    assert np.array_equal(g["x"], r["x"])
+    assert np.array_equal(g["logits"].view(np.uint32), r["logits"].view(np.uint32))
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    for m in range(M):
+        rel = _rel(g["y"][m], r["y"][m])
+        _say("  row", m, "max rel err", rel)
+        assert rel <= TOL
+
+
+def test_moe_layer_int8_reference_shape_ungated(lib):
+    _say("layer int8 2560/640 ungated")
+    _cfg(lib, H=2560, I=640, gated=0)
+    g = _run_layer(lib, 1, 2, 4, x_layer=7)
+    r = orc.moe_layer(2560, 640, 512, 10, 1, 2, 4, 7, gated=0)
+    assert np.array_equal(g["sel"], r["sel"])
+    assert _rel(g["y"][0], r["y"][0]) <= TOL
+    _cfg(lib)
