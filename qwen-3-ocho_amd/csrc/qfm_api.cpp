@@ -151,7 +151,7 @@ void qf_rtr_topk10_rows_launch(const float *logits, int *sel_ids, float *wts, in
 }
 int qfm_router_logits(const float *W, const float *bias, const uint16_t *x, int M, float *logits, hipStream_t s) {
     if (!W || !x || !logits || M < 1) { set_error(-1, "qfm_router_logits: bad arguments"); return -1; }
-    return launch_router_f32w(W, bias, nullptr, x, M, logits, g_cfg.E, s);
+    return launch_router_shared(W, bias, nullptr, nullptr, x, M, logits, g_cfg.E, nullptr, 0, s);
 }
 int qfm_topk(const float *logits, int M, int *sel, float *wts, hipStream_t s) {
     if (!logits || !sel || !wts || M < 1) { set_error(-1, "qfm_topk: bad arguments"); return -1; }
@@ -163,7 +163,7 @@ void qf8_i8_gateup_m1(const Qf4ExpCache *c, const float *x, int8_t *x8q, float *
                       const int *sel_ids, int nexp, int quant_x, hipStream_t s) {
     (void)x8q; (void)x8s; (void)quant_x;
     if (!x) { set_error(-1, "qf8_i8_gateup_m1: null x"); return; }
-    launch_i8_gateup_m1(c, nullptr, x, sel_ids, nexp, nullptr, hidden, s);
+    launch_i8_gateup_m1(c, nullptr, x, nullptr, const_cast<int *>(sel_ids), nullptr, nexp, hidden, s);
 }
 void qf8_i8_down_m1(const Qf4ExpCache *c, const float *hidden, int8_t *h8q, float *h8s, const float *wts,
                     const int *sel_ids, float *y, int nexp, hipStream_t s) {
@@ -197,21 +197,33 @@ int qfm_moe_forward(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, v
     int *sel = reinterpret_cast<int *>(b + w.sel);
     float *wts = reinterpret_cast<float *>(b + w.wts);
     float *hidden = reinterpret_cast<float *>(b + w.hidden);
+    const size_t ldh = (size_t)(c.K + 1) * c.I;    // per row: K routed hidden vectors, then the shared one
+    float *hsh = hidden + (size_t)c.K * c.I;
     const bool has_sh = L->sh_gate.w != nullptr;
     const float *g = (has_sh && c.gated && L->sh_gate_inp) ? L->sh_gate_inp : nullptr;
     if (has_sh && c.gated && !g) { set_error(-1, "qfm_moe_forward: gated shared expert needs sh_gate_inp"); return -1; }
-    I8Shared shp{};
+    ShPtrs shp{};
     if (has_sh) {
         shp.qg = L->sh_gate.w; shp.qu = L->sh_up.w; shp.qd = L->sh_down.w;
         shp.sg = L->sh_gate.s; shp.su = L->sh_up.s; shp.sd = L->sh_down.s;
     }
-    int rc = launch_router_f32w(L->router, L->router_bias, g, x, M, logits, c.E + 1, s);
-    if (!rc) rc = launch_topk(logits, c.E + 1, M, sel, wts, s);
+    const ShPtrs *sp = has_sh ? &shp : nullptr;
+    const int ld = c.E + 1;
+    // 1. router logits (+ shared gate dot) and the shared expert's hidden: depend on x only
+    int rc = launch_router_shared(L->router, L->router_bias, g, sp, x, M, logits, ld, hsh, (int)ldh, s);
+    if (rc) return rc;
+    if (M == 1 && c.E == 512) {
+        // 2. top-K inside the gate/up kernel; 3. down + combine (+ shared) -> y bf16
+        rc = launch_i8_gateup_m1(L->arena, x, nullptr, logits, sel, wts, c.K, hidden, s);
+        if (!rc) rc = launch_i8_down_m1(L->arena, hidden, wts, sel, c.K, sp, g ? logits + c.E : nullptr, nullptr, y, s);
+        return rc;
+    }
+    rc = launch_topk(logits, ld, M, sel, wts, s);
     for (int m = 0; m < M && !rc; m++) {
-        float *hm = hidden + (size_t)m * (c.K + 1) * c.I;
-        rc = launch_i8_gateup_m1(L->arena, x + (size_t)m * c.H, nullptr, sel + m * c.K, c.K, has_sh ? &shp : nullptr, hm, s);
-        if (!rc) rc = launch_i8_down_m1(L->arena, hm, wts + m * c.K, sel + m * c.K, c.K, has_sh ? &shp : nullptr,
-                                        g ? logits + (size_t)m * (c.E + 1) + c.E : nullptr, nullptr, y + (size_t)m * c.H, s);
+        float *hm = hidden + (size_t)m * ldh;
+        rc = launch_i8_gateup_m1(L->arena, x + (size_t)m * c.H, nullptr, nullptr, sel + m * c.K, nullptr, c.K, hm, s);
+        if (!rc) rc = launch_i8_down_m1(L->arena, hm, wts + m * c.K, sel + m * c.K, c.K, sp,
+                                        g ? logits + (size_t)m * ld + c.E : nullptr, nullptr, y + (size_t)m * c.H, s);
     }
     return rc;
 }

@@ -20,22 +20,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 }
 
 // ---- int8 x fp32 dot of one 16-byte chunk ---------------------------------
-// w holds 16 signed int8 codes. Each code is widened exactly with a
-// sign-extending bit-field extract and an int->float conversion.
-__device__ __forceinline__ float i8x4_f(uint32_t d, int b) {
-    return (float)__builtin_amdgcn_sbfe((int)d, b * 8, 8);
-}
-__device__ __forceinline__ float dot16_i8(const uint4 w, const float *x, float acc) {
-    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-#pragma unroll
-        for (int b = 0; b < 4; b++) acc = fmaf(i8x4_f(d[q], b), x[q * 4 + b], acc);
-    return acc;
-}
-// Offset-binary form for the gate/up GEMVs: u = q ^ 0x80 = q + 128 is an
-// unsigned byte, converted by v_cvt_f32_ubyteN in one op; the caller seeds
-// the accumulator with -128 * sum(x) over the same elements.
+// Codes are consumed in offset-binary form: u = q ^ 0x80 = q + 128 is an
+// unsigned byte, widened exactly by v_cvt_f32_ubyteN (one op per code); the
+// caller seeds the accumulator with -128 * sum(x) over the same elements.
+// (A sign-extending extract followed by an int->float conversion is not
+// used: hipcc 7.2 folds that pair into v_cvt_f32_u32_sdwa with a sext
+// source, an unsigned conversion that turns negative codes into ~4e9.)
 __device__ __forceinline__ float dot16_u8(const uint4 w, const float *x, float acc) {
     const uint32_t d[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
 #pragma unroll
@@ -62,6 +52,127 @@ __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
     for (int m = G / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, WAVE);
     return v;
+}
+
+// ---- wave-wide reductions from the ROCm device library (ockl) -------------
+extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_max_u64(unsigned long long);
+extern "C" __device__ __attribute__((const)) float __ockl_wfred_add_f32(float);
+
+// Order-preserving 64-bit selection key of a logit: descending value, ties to
+// the lower index. -0.0 is folded onto +0.0 (they compare equal as floats).
+__device__ __forceinline__ unsigned long long topk_key(float v, int e) {
+    const uint32_t b = __float_as_uint(v + 0.0f);
+    const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+__device__ __forceinline__ int topk_key_index(unsigned long long key) {
+    return (int)(0xFFFFFFFFu - (uint32_t)key);
+}
+__device__ __forceinline__ float topk_key_value(unsigned long long key) {
+    const uint32_t k = (uint32_t)(key >> 32);
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// One wave selects the top-K (K <= 16) of E = 64*EPL logits lr[0..E):
+// descending value, ties to the lower index (64-bit keys, all distinct).
+// Lane k < K receives the k-th expert id and its weight exp(l_k - l_max) /
+// denom, denom = sum over the K selected (renorm) or over all E (plain
+// softmax). Wave-uniform control flow; lds: 16 + 16*EPL u64 of wave-private LDS.
+// Method: T = the K-th largest of the 64 lane maxima (rank counting over
+// broadcast lane values) bounds the K-th largest key from below, so the
+// elements >= T (at most 8K of them, typically ~K) contain the top-K; those
+// candidates are compacted to LDS and ranked against each other.
+template <int EPL>
+__device__ __forceinline__ void wave_topk(const float *lr, int K, int renorm, int lane,
+                                          unsigned long long *lds, int &my_i, float &my_w) {
+    unsigned long long key[EPL];
+    float v[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        v[i] = lr[i * 64 + lane];
+        key[i] = topk_key(v[i], i * 64 + lane);
+    }
+    unsigned long long mx = key[0];
+#pragma unroll
+    for (int i = 1; i < EPL; i++) mx = key[i] > mx ? key[i] : mx;
+    // rank of this lane's maximum among the 64 lane maxima
+    int rank = 0;
+    for (int j = 0; j < 64; j++) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mx, j);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(mx >> 32), j);
+        rank += ((((unsigned long long)hi << 32) | lo) > mx) ? 1 : 0;
+    }
+    const unsigned long long bal = __ballot(rank == K - 1);
+    const int tl = __builtin_ctzll(bal);
+    // (readlane returns a signed int: widen through uint32_t, never directly)
+    const uint32_t t_hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(mx >> 32), tl);
+    const uint32_t t_lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mx, tl);
+    const unsigned long long T = ((unsigned long long)t_hi << 32) | t_lo;
+    // compact the candidates (keys >= T) into lds[64 ..]
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < EPL; i++) cnt += key[i] >= T ? 1 : 0;
+    const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int off = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) off += __popcll(__ballot((cnt >> b) & 1) & lt) << b;
+    int total = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) total += __popcll(__ballot((cnt >> b) & 1)) << b;
+    unsigned long long *cand = lds + 16;
+#pragma unroll
+    for (int i = 0; i < EPL; i++)
+        if (key[i] >= T) cand[off++] = key[i];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    // rank the candidates against each other; the K best land in lds[0..K)
+    for (int j = lane; j < total; j += 64) {
+        const unsigned long long cj = cand[j];
+        int r = 0;
+        for (int i = 0; i < total; i++) r += cand[i] > cj ? 1 : 0;
+        if (r < K) lds[r] = cj;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const unsigned long long mine = lane < K ? lds[lane] : 0ull;
+    const unsigned long long first = lds[0];
+    const float mxv = topk_key_value(first);
+    const float ek = lane < K ? __expf(topk_key_value(mine) - mxv) : 0.0f;
+    float denom;
+    if (renorm) {
+        denom = __ockl_wfred_add_f32(ek);
+    } else {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < EPL; i++) t += __expf(v[i] - mxv);
+        denom = __ockl_wfred_add_f32(t);
+    }
+    my_i = lane < K ? topk_key_index(mine) : -1;
+    my_w = ek / denom;
+}
+
+// x slice of one 32-lane group: lane l holds x[st*512 + 16l + i], i < 16.
+template <int H>
+__device__ __forceinline__ void load_x_slice_bf16(const uint16_t *x, int l, float (&xs)[H / 512][16]) {
+#pragma unroll
+    for (int st = 0; st < H / 512; st++) {
+        const int k0 = st * 512 + l * 16;
+        const uint4 a = *reinterpret_cast<const uint4 *>(x + k0);
+        const uint4 b = *reinterpret_cast<const uint4 *>(x + k0 + 8);
+        const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int q = 0; q < 8; q++) { xs[st][2 * q] = bf16_lo(d[q]); xs[st][2 * q + 1] = bf16_hi(d[q]); }
+    }
+}
+template <int H>
+__device__ __forceinline__ void load_x_slice_f32(const float *x, int l, float (&xs)[H / 512][16]) {
+#pragma unroll
+    for (int st = 0; st < H / 512; st++) {
+        const int k0 = st * 512 + l * 16;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 f = *reinterpret_cast<const float4 *>(x + k0 + 4 * q);
+            xs[st][4 * q] = f.x; xs[st][4 * q + 1] = f.y; xs[st][4 * q + 2] = f.z; xs[st][4 * q + 3] = f.w;
+        }
+    }
 }
 
 // ---- silu / sigmoid ----------------------------------------------------------

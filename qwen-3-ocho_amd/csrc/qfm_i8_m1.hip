@@ -6,78 +6,72 @@
 // activations kept exact (bf16/fp32) instead of the reference's X8 int8
 // re-quantization.
 //
-// gate/up: grid (I/8, jobs), 256 threads; one 32-lane half-wave per weight
+// gate/up: grid (I/8, K), 256 threads; one 32-lane half-wave per weight
 // row. Lane l owns bytes [st*512 + 16l, +16) of the H-byte row for
 // st = 0..H/512-1, so a half-wave reads 512 contiguous bytes per step and
 // all H/256 weight loads of a row pair (gate + up) are in flight before the
 // first multiply. The activation slice a lane needs is the same for every
 // row, so it is held in registers as fp32 (no LDS). Each code q is used in
 // offset-binary form q + 128 (one v_cvt_f32_ubyte per code) and the
-// accumulator starts at -128 * sum(x_slice).
+// accumulator starts at -128 * sum(x_slice). When the launch carries the
+// router logits, wave 0 of every block runs the top-K selection itself (the
+// 2 KiB row of logits is L2-resident), which removes a dependent launch from
+// the decode chain; block (0, 0) publishes sel/wts for the down kernel.
 //
 // down: one LPR-lane group per output row (LPR = 32 for I = 512, 8 for
-// I = 640); the jobs' hidden vectors are staged once per block in LDS. Each
+// I = 640). Every weight load of the row is issued first (the 16-byte chunks
+// of all K + 1 expert rows), then the hidden vectors are staged in LDS with
+// the sum of every 16-element chunk (the offset-binary correction). Each
 // lane accumulates sum_j w_j * sd_j[c] * <Wd_j slice, h_j slice> across all
-// jobs and the group reduces once, so every output row has one writer and
-// a fixed summation order (deterministic; y is seeded, not accumulated).
+// jobs and the group reduces once, so every output row has one writer and a
+// fixed summation order (deterministic; y is seeded, not accumulated).
 #include "qfm_dev.h"
 #include "qfm_internal.h"
 
 namespace qfm {
 
-struct JobPtrs {
-    const int8_t *qg, *qu, *qd;
-    const float *sg, *su, *sd;
-};
-
-template <int H>
-__device__ __forceinline__ void load_x_slice(const uint16_t *xb, const float *xf, int l, float (&xs)[H / 512][16]) {
-#pragma unroll
-    for (int st = 0; st < H / 512; st++) {
-        const int k0 = st * 512 + l * 16;
-        if (xb) {
-            const uint4 a = *reinterpret_cast<const uint4 *>(xb + k0);
-            const uint4 b = *reinterpret_cast<const uint4 *>(xb + k0 + 8);
-            const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int q = 0; q < 8; q++) { xs[st][2 * q] = bf16_lo(d[q]); xs[st][2 * q + 1] = bf16_hi(d[q]); }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4 f = *reinterpret_cast<const float4 *>(xf + k0 + 4 * q);
-                xs[st][4 * q] = f.x; xs[st][4 * q + 1] = f.y; xs[st][4 * q + 2] = f.z; xs[st][4 * q + 3] = f.w;
-            }
-        }
-    }
-}
-
-template <int H, int I>
+template <int H, int I, int EPL>
 __global__ void __launch_bounds__(256)
 k_i8_gateup_m1(const int8_t *__restrict__ Qg, const int8_t *__restrict__ Qu,
                const float *__restrict__ Sg, const float *__restrict__ Su,
                const uint16_t *__restrict__ xb, const float *__restrict__ xf,
-               const int *__restrict__ sel, int nexp, JobPtrs sh, float *__restrict__ hidden) {
+               const float *__restrict__ logits, int *__restrict__ sel, float *__restrict__ wts,
+               int K, int renorm, float *__restrict__ hidden) {
     constexpr int NST = H / 512;
+    __shared__ int s_e;
+    __shared__ unsigned long long s_tk[272];
     const int job = blockIdx.y;
     const int l = threadIdx.x & 31;
     const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
-    const int8_t *qg, *qu;
-    const float *sg, *su;
-    if (job < nexp) {
-        const size_t e = (size_t)sel[job];
-        qg = Qg + e * ((size_t)I * H); qu = Qu + e * ((size_t)I * H);
-        sg = Sg + e * I; su = Su + e * I;
+    float xs[NST][16];
+    if (xb) load_x_slice_bf16<H>(xb, l, xs);
+    else load_x_slice_f32<H>(xf, l, xs);
+    int e;
+    if (logits) {
+        if (threadIdx.x < 64) {
+            int my_i;
+            float my_w;
+            wave_topk<EPL>(logits, K, renorm, threadIdx.x, s_tk, my_i, my_w);
+            if (threadIdx.x == job) s_e = my_i;
+            if (blockIdx.x == 0 && job == 0 && threadIdx.x < K) {
+                sel[threadIdx.x] = my_i;
+                wts[threadIdx.x] = my_w;
+            }
+        }
+        __syncthreads();
+        e = s_e;
     } else {
-        qg = sh.qg; qu = sh.qu; sg = sh.sg; su = sh.su;
+        e = sel[job];
     }
+    const int8_t *qg = Qg + (size_t)e * ((size_t)I * H) + (size_t)row * H + l * 16;
+    const int8_t *qu = Qu + (size_t)e * ((size_t)I * H) + (size_t)row * H + l * 16;
     uint4 wg[NST], wu[NST];
 #pragma unroll
     for (int st = 0; st < NST; st++) {
-        wg[st] = ld_nt16(qg + (size_t)row * H + st * 512 + l * 16);
-        wu[st] = ld_nt16(qu + (size_t)row * H + st * 512 + l * 16);
+        wg[st] = ld_nt16(qg + st * 512);
+        wu[st] = ld_nt16(qu + st * 512);
     }
-    float xs[NST][16];
-    load_x_slice<H>(xb, xf, l, xs);
+    const float sg = Sg[(size_t)e * I + row], su = Su[(size_t)e * I + row];
     float xsum = 0.0f;
 #pragma unroll
     for (int st = 0; st < NST; st++)
@@ -91,71 +85,96 @@ k_i8_gateup_m1(const int8_t *__restrict__ Qg, const int8_t *__restrict__ Qu,
     }
     ag = group_sum<32>(ag);
     au = group_sum<32>(au);
-    if (l == 0) {
-        const float gv = ag * sg[row], uv = au * su[row];
-        hidden[(size_t)job * I + row] = silu(gv) * uv;
-    }
+    if (l == 0) hidden[(size_t)job * I + row] = silu(ag * sg) * (au * su);
 }
 
 constexpr int kMaxJobs = 17;   // top_k <= 16 plus the shared expert
 
-template <int H, int I, int LPR>
+// NJ jobs (routed experts, then the shared one when HAS_SH) are a template
+// parameter so that every register array is indexed at compile time: no
+// branches around loads and no scratch, which keeps all loads of a batch in
+// flight together (memory-counter waits retire in issue order).
+template <int H, int I, int LPR, int NJ, bool HAS_SH, int CH>
 __global__ void __launch_bounds__(256)
 k_i8_down_m1(const int8_t *__restrict__ Qd, const float *__restrict__ Sd,
              const float *__restrict__ hidden, const float *__restrict__ wts,
-             const int *__restrict__ sel, int nexp, JobPtrs sh, const float *__restrict__ gdot,
-             float *__restrict__ y32, uint16_t *__restrict__ ybf) {
+             const int *__restrict__ sel, ShPtrs sh,
+             const float *__restrict__ gdot, float *__restrict__ y32, uint16_t *__restrict__ ybf) {
     constexpr int NST = I / (16 * LPR);
     constexpr int RPB = 256 / LPR;
-    __shared__ __align__(16) float sh_h[kMaxJobs * I];
-    __shared__ const int8_t *sh_q[kMaxJobs];
-    __shared__ const float *sh_s[kMaxJobs];
-    __shared__ float sh_w[kMaxJobs];
-    const int njobs = nexp + (sh.qd ? 1 : 0);
-    for (int i = threadIdx.x; i < njobs * I / 4; i += 256)
-        reinterpret_cast<float4 *>(sh_h)[i] = reinterpret_cast<const float4 *>(hidden)[i];
-    if (threadIdx.x < njobs) {
-        const int j = threadIdx.x;
-        if (j < nexp) {
-            const size_t e = (size_t)sel[j];
-            sh_q[j] = Qd + e * ((size_t)H * I);
-            sh_s[j] = Sd + e * H;
-            sh_w[j] = wts[j];
-        } else {
-            sh_q[j] = sh.qd;
-            sh_s[j] = sh.sd;
-            sh_w[j] = gdot ? sigmoid(gdot[0]) : 1.0f;
-        }
-    }
-    __syncthreads();
+    constexpr int NEXP = HAS_SH ? NJ - 1 : NJ;
+    constexpr int NH4 = NJ * I / 4;
+    constexpr int NSTG = (NH4 + 255) / 256;
+    __shared__ __align__(16) float sh_h[NSTG * 256 * 4];   // padded: the fill below is unconditional
+    __shared__ float sh_cs[NJ * I / 16];
     const int l = threadIdx.x % LPR;
     const int c = blockIdx.x * RPB + threadIdx.x / LPR;
-    float acc = 0.0f;
-    int j = 0;
-    for (; j + 4 <= njobs; j += 4) {
-        uint4 w[4][NST];
+    // batch 1: routing, router weights, shared gate, hidden vectors (to registers)
+    float4 stg[NSTG];
 #pragma unroll
-        for (int u = 0; u < 4; u++)
-#pragma unroll
-            for (int st = 0; st < NST; st++)
-                w[u][st] = ld_nt16(sh_q[j + u] + (size_t)c * I + (st * LPR + l) * 16);
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            float d = 0.0f;
-#pragma unroll
-            for (int st = 0; st < NST; st++)
-                d = dot16_i8(w[u][st], sh_h + (j + u) * I + (st * LPR + l) * 16, d);
-            acc = fmaf(sh_w[j + u] * sh_s[j + u][c], d, acc);
-        }
+    for (int q = 0; q < NSTG; q++) {
+        int i = threadIdx.x + q * 256;
+        i = i < NH4 ? i : NH4 - 1;
+        stg[q] = reinterpret_cast<const float4 *>(hidden)[i];   // shared hidden follows the routed ones
     }
-    for (; j < njobs; j++) {
-        uint4 w[NST];
+    int ex[NEXP > 0 ? NEXP : 1];
+    float wt[NEXP > 0 ? NEXP : 1];
 #pragma unroll
-        for (int st = 0; st < NST; st++) w[st] = ld_nt16(sh_q[j] + (size_t)c * I + (st * LPR + l) * 16);
-        float d = 0.0f;
+    for (int j = 0; j < NEXP; j++) { ex[j] = sel[j]; wt[j] = wts[j]; }
+    float sh_sd = 0.0f, gd = 0.0f;
+    if constexpr (HAS_SH) {
+        sh_sd = sh.sd[c];
+        if (gdot) gd = gdot[0];
+    }
+    // batch 2: weight chunks and row scales
+    float wsc[NJ];
 #pragma unroll
-        for (int st = 0; st < NST; st++) d = dot16_i8(w[st], sh_h + j * I + (st * LPR + l) * 16, d);
-        acc = fmaf(sh_w[j] * sh_s[j][c], d, acc);
+    for (int j = 0; j < NEXP; j++) wsc[j] = wt[j] * Sd[(size_t)ex[j] * H + c];
+    uint4 w[CH][NST];
+#pragma unroll
+    for (int u = 0; u < CH && u < NJ; u++) {
+        const int8_t *p = (u < NEXP ? Qd + (size_t)ex[u] * ((size_t)H * I) : sh.qd) + (size_t)c * I;
+#pragma unroll
+        for (int st = 0; st < NST; st++) w[u][st] = ld_nt16(p + (st * LPR + l) * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < NSTG; q++) reinterpret_cast<float4 *>(sh_h)[threadIdx.x + q * 256] = stg[q];
+    __syncthreads();
+    for (int i = threadIdx.x; i < NJ * I / 16; i += 256) {
+        float t = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; q++) t += sh_h[i * 16 + q];
+        sh_cs[i] = -128.0f * t;
+    }
+    __syncthreads();
+    if constexpr (HAS_SH) wsc[NJ - 1] = (gdot ? sigmoid(gd) : 1.0f) * sh_sd;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j0 = 0; j0 < NJ; j0 += CH) {
+        if (j0 > 0) {
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                const int j = j0 + u;
+                if (j < NJ) {
+                    const int8_t *p = (j < NEXP ? Qd + (size_t)ex[j < NEXP ? j : 0] * ((size_t)H * I) : sh.qd) + (size_t)c * I;
+#pragma unroll
+                    for (int st = 0; st < NST; st++) w[u][st] = ld_nt16(p + (st * LPR + l) * 16);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < CH; u++) {
+            const int j = j0 + u;
+            if (j < NJ) {
+                float d = 0.0f;
+#pragma unroll
+                for (int st = 0; st < NST; st++) {
+                    d += sh_cs[j * (I / 16) + st * LPR + l];
+                    d = dot16_u8(w[u][st], sh_h + j * I + (st * LPR + l) * 16, d);
+                }
+                acc = fmaf(wsc[j], d, acc);
+            }
+        }
     }
     acc = group_sum<LPR>(acc);
     if (l == 0) {
@@ -164,25 +183,48 @@ k_i8_down_m1(const int8_t *__restrict__ Qd, const float *__restrict__ Sd,
     }
 }
 
-int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *xf, const int *sel,
-                        int nexp, const I8Shared *sh, float *hidden, hipStream_t s) {
+template <int H, int I, int LPR, int NJ, bool HAS_SH, int CH>
+static void down_launch(const Qf4ExpCache *c, const float *hidden, const float *wts, const int *sel, ShPtrs sp,
+                        const float *gdot, float *y32, uint16_t *ybf, hipStream_t s) {
+    hipLaunchKernelGGL((k_i8_down_m1<H, I, LPR, NJ, HAS_SH, CH>), dim3(H / (256 / LPR)), dim3(256), 0, s,
+                       c->i8_down, c->i8s_down, hidden, wts, sel, sp, gdot, y32, ybf);
+}
+
+template <int H, int I, int LPR, int CH, int NJ>
+static bool down_dispatch_nj(int nj, bool has_sh, const Qf4ExpCache *c, const float *hidden, const float *wts,
+                             const int *sel, ShPtrs sp, const float *gdot, float *y32,
+                             uint16_t *ybf, hipStream_t s) {
+    if constexpr (NJ > kMaxJobs) {
+        return false;
+    } else {
+        if (nj == NJ) {
+            if (has_sh) down_launch<H, I, LPR, NJ, true, (CH < NJ ? CH : NJ)>(c, hidden, wts, sel, sp, gdot, y32, ybf, s);
+            else down_launch<H, I, LPR, NJ, false, (CH < NJ ? CH : NJ)>(c, hidden, wts, sel, sp, gdot, y32, ybf, s);
+            return true;
+        }
+        return down_dispatch_nj<H, I, LPR, CH, NJ + 1>(nj, has_sh, c, hidden, wts, sel, sp, gdot, y32, ybf, s);
+    }
+}
+
+int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *xf, const float *logits, int *sel,
+                        float *wts, int nexp, float *hidden, hipStream_t s) {
     if (!c || !c->i8_gate || !c->i8_up || !c->i8s_gate || !c->i8s_up) {
         set_error(-1, "i8_gateup_m1: arena has no INT8 gate/up"); return -1;
     }
-    if (nexp < 0 || nexp > 16 || (!xb && !xf) || !hidden || (nexp && !sel)) {
+    if (nexp < 1 || nexp > 16 || (!xb && !xf) || !hidden || !sel || (logits && !wts)) {
         set_error(-1, "i8_gateup_m1: bad arguments"); return -1;
     }
-    JobPtrs jp{};
-    if (sh) { jp.qg = sh->qg; jp.qu = sh->qu; jp.sg = sh->sg; jp.su = sh->su; }
-    const int jobs = nexp + (sh ? 1 : 0);
-    if (!jobs) return 0;
+    if (logits && (nexp != g_cfg.K || g_cfg.E != 512)) {
+        set_error(-2, "i8_gateup_m1: in-kernel selection needs nexp == top_k and 512 experts"); return -2;
+    }
     const dim3 block(256);
+    const int K = g_cfg.K, rn = g_cfg.renorm;
     if (shape_2048()) {
-        hipLaunchKernelGGL((k_i8_gateup_m1<2048, 512>), dim3(512 / 8, jobs), block, 0, s, c->i8_gate, c->i8_up,
-                           c->i8s_gate, c->i8s_up, xb, xf, sel, nexp, jp, hidden);
+        hipLaunchKernelGGL((k_i8_gateup_m1<2048, 512, 8>), dim3(512 / 8, nexp), block, 0, s, c->i8_gate, c->i8_up,
+                           c->i8s_gate, c->i8s_up, xb, xf, logits, sel, wts, K, rn, hidden);
     } else if (shape_2560()) {
-        hipLaunchKernelGGL((k_i8_gateup_m1<2560, 640>), dim3(640 / 8, jobs), block, 0, s, c->i8_gate, c->i8_up,
-                           c->i8s_gate, c->i8s_up, xb, xf, sel, nexp, jp, hidden);
+        hipLaunchKernelGGL((k_i8_gateup_m1<2560, 640, 8>), dim3(640 / 8, nexp), block, 0, s, c->i8_gate, c->i8_up,
+                           c->i8s_gate, c->i8s_up, xb, xf, logits, sel, wts, K, rn, hidden);
     } else {
         set_error(-2, "i8_gateup_m1: unsupported shape"); return -2;
     }
@@ -190,23 +232,24 @@ int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *x
 }
 
 int launch_i8_down_m1(const Qf4ExpCache *c, const float *hidden, const float *wts, const int *sel, int nexp,
-                      const I8Shared *sh, const float *gdot, float *y32, uint16_t *ybf, hipStream_t s) {
+                      const ShPtrs *sh, const float *gdot, float *y32, uint16_t *ybf, hipStream_t s) {
     if (!c || !c->i8_down || !c->i8s_down) { set_error(-1, "i8_down_m1: arena has no INT8 down"); return -1; }
-    if (nexp < 0 || nexp > 16 || !hidden || (!y32 && !ybf) || (nexp && (!sel || !wts))) {
+    if (nexp < 0 || nexp > 16 || (!y32 && !ybf) || !hidden || (nexp && (!sel || !wts))) {
         set_error(-1, "i8_down_m1: bad arguments"); return -1;
     }
-    JobPtrs jp{};
-    if (sh) { jp.qd = sh->qd; jp.sd = sh->sd; }
-    const dim3 block(256);
+    ShPtrs sp{};
+    if (sh) sp = *sh;
+    const int nj = nexp + (sh ? 1 : 0);
+    if (nj == 0) { set_error(-1, "i8_down_m1: nothing to do"); return -1; }
+    bool ok;
     if (shape_2048()) {
-        hipLaunchKernelGGL((k_i8_down_m1<2048, 512, 32>), dim3(2048 / 8), block, 0, s, c->i8_down, c->i8s_down,
-                           hidden, wts, sel, nexp, jp, gdot, y32, ybf);
+        ok = down_dispatch_nj<2048, 512, 32, kMaxJobs, 1>(nj, sh != nullptr, c, hidden, wts, sel, sp, gdot, y32, ybf, s);
     } else if (shape_2560()) {
-        hipLaunchKernelGGL((k_i8_down_m1<2560, 640, 8>), dim3(2560 / 32), block, 0, s, c->i8_down, c->i8s_down,
-                           hidden, wts, sel, nexp, jp, gdot, y32, ybf);
+        ok = down_dispatch_nj<2560, 640, 8, 3, 1>(nj, sh != nullptr, c, hidden, wts, sel, sp, gdot, y32, ybf, s);
     } else {
         set_error(-2, "i8_down_m1: unsupported shape"); return -2;
     }
+    if (!ok) { set_error(-2, "i8_down_m1: unsupported job count %d", nj); return -2; }
     return check_launch("i8_down_m1");
 }
 

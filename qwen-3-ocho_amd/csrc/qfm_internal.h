@@ -25,21 +25,27 @@ int launch_gen_fill(void *out, int kind, uint64_t n0, uint64_t cnt, uint32_t see
                     uint32_t layer, uint32_t tensor, float scale, hipStream_t s);
 int launch_fill_f32(float *out, uint64_t cnt, float value, hipStream_t s);
 
-// router: W_f32 [E][H] (+extra row g [H] written at column E when g != nullptr)
-int launch_router_f32w(const float *W, const float *bias, const float *g,
-                       const uint16_t *x, int M, float *logits, int ld_logits, hipStream_t s);
+// Shared-expert (or any single INT8 expert) pointers, passed by value to kernels.
+struct ShPtrs { const int8_t *qg, *qu, *qd; const float *sg, *su, *sd; };
+
+// router: W_f32 [E][H] (+ row g [H] written at column E when g != nullptr)
+// and, when sh != nullptr, the shared-expert hidden hsh[m * ld_hsh + r], in one launch.
+int launch_router_shared(const float *W, const float *bias, const float *g, const ShPtrs *sh,
+                         const uint16_t *x, int M, float *logits, int ld_logits, float *hsh, int ld_hsh,
+                         hipStream_t s);
 int launch_router_bf16w(const uint16_t *W, const float *x, float *logits, hipStream_t s);
 int launch_topk(const float *logits, int ld_logits, int M, int *sel, float *wts, hipStream_t s);
 
-// INT8 M=1 experts. Job list: nexp routed experts from sel (device), plus the
-// shared expert when sh != nullptr. x is bf16 (xb) or fp32 (xf).
-struct I8Shared { const int8_t *qg, *qu, *qd; const float *sg, *su, *sd; };
-int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *xf,
-                        const int *sel, int nexp, const I8Shared *sh, float *hidden, hipStream_t s);
-// y = sum_k wts[k] * down_k(hidden_k) (+ gamma * shared_down(hidden_K)), gamma =
-// sigmoid(*gdot) when gdot != nullptr, 1 otherwise. Writes y32 and/or ybf.
+// INT8 M=1 routed gate/up: hidden[k][I] for the nexp experts sel[0..nexp).
+// With logits != nullptr the selection is made inside the kernel (every block
+// runs the top-K of its row of logits) and block 0 writes sel/wts; otherwise
+// sel is an input. x is bf16 (xb) or fp32 (xf).
+int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *xf, const float *logits,
+                        int *sel, float *wts, int nexp, float *hidden, hipStream_t s);
+// y = sum_k wts[k] * down_k(hidden[k]) (+ gamma * shared_down(hidden[nexp]) when
+// sh != nullptr: the shared expert's hidden vector follows the routed ones),
+// gamma = sigmoid(*gdot) when gdot != nullptr, 1 otherwise. Writes y32 and/or ybf.
 int launch_i8_down_m1(const Qf4ExpCache *c, const float *hidden, const float *wts, const int *sel,
-                      int nexp, const I8Shared *sh, const float *gdot, float *y32, uint16_t *ybf,
-                      hipStream_t s);
+                      int nexp, const ShPtrs *sh, const float *gdot, float *y32, uint16_t *ybf, hipStream_t s);
 
 }  // namespace qfm

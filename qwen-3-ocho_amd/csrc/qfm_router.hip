@@ -36,44 +36,80 @@ __device__ __forceinline__ float canon_reduce_row(const float4 (&w)[NJ], const f
     return a;
 }
 
-// W fp32 [E][H]; x bf16 [M][H]; logits [M][ld]. Row E (when g != nullptr)
-// is the shared-expert gate vector g [H], written to column E without bias.
-template <int NJ>
-__global__ void __launch_bounds__(256)
-k_router_f32w(const float *__restrict__ W, const float *__restrict__ bias, const float *__restrict__ g,
-              const uint16_t *__restrict__ x, int M, int E, float *__restrict__ logits, int ld) {
+// One wave per block. Blocks [0, E): router rows of W fp32 [E][H]; block E
+// (when g != nullptr): the shared-expert gate vector g [H], written to
+// column E without bias; the remaining I/2 blocks (when sh.qg != nullptr):
+// two shared-expert gate/up rows each, one per half-wave, giving
+// hsh[m][r] = silu(sg_r <Qg_r, x_m>) * (su_r <Qu_r, x_m>). x is bf16 [M][H],
+// logits [M][ld]. Every output depends on x only, so one launch covers all.
+template <int NJ, int I>
+__global__ void __launch_bounds__(64)
+k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, const float *__restrict__ g,
+                ShPtrs sh, const uint16_t *__restrict__ x, int M, int E, float *__restrict__ logits, int ld,
+                float *__restrict__ hsh, int ldh) {
     constexpr int H = NJ * 256;
-    const int lane = threadIdx.x & 63;
-    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const bool is_g = (g != nullptr) && e == E;
-    if (e > E || (e == E && !is_g)) return;
-    const float *wr = is_g ? g : W + (size_t)e * H;
-    float4 w[NJ];
+    const int lane = threadIdx.x;
+    const int b = blockIdx.x;
+    const int ng = g ? 1 : 0;
+    if (b < E + ng) {
+        const bool is_g = b == E;
+        const float *wr = is_g ? g : W + (size_t)b * H;
+        float4 w[NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; j++) w[j] = *reinterpret_cast<const float4 *>(wr + j * 256 + lane * 4);
-    const float b = (!is_g && bias) ? bias[e] : 0.0f;
-    const int m0 = blockIdx.y * 8, m1 = min(M, m0 + 8);
-    for (int m = m0; m < m1; m++) {
-        float xv[NJ][4];
+        for (int j = 0; j < NJ; j++) w[j] = *reinterpret_cast<const float4 *>(wr + j * 256 + lane * 4);
+        const float bb = (!is_g && bias) ? bias[b] : 0.0f;
+        for (int m = 0; m < M; m++) {
+            float xv[NJ][4];
 #pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const uint2 p = *reinterpret_cast<const uint2 *>(x + (size_t)m * H + j * 256 + lane * 4);
-            xv[j][0] = bf16_lo(p.x); xv[j][1] = bf16_hi(p.x);
-            xv[j][2] = bf16_lo(p.y); xv[j][3] = bf16_hi(p.y);
+            for (int j = 0; j < NJ; j++) {
+                const uint2 p = *reinterpret_cast<const uint2 *>(x + (size_t)m * H + j * 256 + lane * 4);
+                xv[j][0] = bf16_lo(p.x); xv[j][1] = bf16_hi(p.x);
+                xv[j][2] = bf16_lo(p.y); xv[j][3] = bf16_hi(p.y);
+            }
+            float a = canon_reduce_row<NJ>(w, xv);
+            if (bias && !is_g) a = __fadd_rn(a, bb);
+            if (lane == 0) logits[(size_t)m * ld + b] = a;
         }
-        float a = canon_reduce_row<NJ>(w, xv);
-        if (bias && !is_g) a = __fadd_rn(a, b);
-        if (lane == 0) logits[(size_t)m * ld + e] = a;
+        return;
+    }
+    // shared-expert gate/up rows
+    constexpr int NST = H / 512;
+    const int l = lane & 31;
+    const int r = (b - E - ng) * 2 + (lane >> 5);
+    uint4 wg[NST], wu[NST];
+#pragma unroll
+    for (int st = 0; st < NST; st++) {
+        wg[st] = ld_nt16(sh.qg + (size_t)r * H + st * 512 + l * 16);
+        wu[st] = ld_nt16(sh.qu + (size_t)r * H + st * 512 + l * 16);
+    }
+    const float sg = sh.sg[r], su = sh.su[r];
+    for (int m = 0; m < M; m++) {
+        float xs[NST][16];
+        load_x_slice_bf16<H>(x + (size_t)m * H, l, xs);
+        float xsum = 0.0f;
+#pragma unroll
+        for (int st = 0; st < NST; st++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) xsum += xs[st][i];
+        float ag = -128.0f * xsum, au = ag;
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            ag = dot16_u8(wg[st], xs[st], ag);
+            au = dot16_u8(wu[st], xs[st], au);
+        }
+        ag = group_sum<32>(ag);
+        au = group_sum<32>(au);
+        if (l == 0) hsh[(size_t)m * ldh + r] = silu(ag * sg) * (au * su);
     }
 }
 
 // Reference form: W bf16 [E][H], x fp32 [H] (qf_rtr_gemv signature).
 template <int NJ>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64)
 k_router_bf16w(const uint16_t *__restrict__ W, const float *__restrict__ x, int E, float *__restrict__ logits) {
     constexpr int H = NJ * 256;
-    const int lane = threadIdx.x & 63;
-    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x;
+    const int e = blockIdx.x;
     if (e >= E) return;
     float4 w[NJ];
     float xv[NJ][4];
@@ -88,70 +124,44 @@ k_router_bf16w(const uint16_t *__restrict__ W, const float *__restrict__ x, int 
     if (lane == 0) logits[e] = a;
 }
 
-// One wave per row: EPL = E/64 logits per lane (lane l holds e = i*64 + l).
+// One wave per row; see wave_topk.
 template <int EPL>
 __global__ void __launch_bounds__(256)
 k_topk(const float *__restrict__ logits, int ld, int M, int K, int renorm,
        int *__restrict__ sel, float *__restrict__ wts) {
+    __shared__ unsigned long long s_tk[4][272];
     const int lane = threadIdx.x & 63;
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (m >= M) return;
-    const float *lr = logits + (size_t)m * ld;
-    float v[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; i++) v[i] = lr[i * 64 + lane];
-    uint32_t taken = 0;
-    float my_v = 0.0f, mx = 0.0f;
-    int my_i = 0;
-    for (int k = 0; k < K; k++) {
-        float bv = -INFINITY;
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int i = 0; i < EPL; i++) {
-            const int e = i * 64 + lane;
-            if (!((taken >> i) & 1u) && (v[i] > bv || (v[i] == bv && e < bi))) { bv = v[i]; bi = e; }
-        }
-#pragma unroll
-        for (int msk = 32; msk >= 1; msk >>= 1) {
-            const float ov = __shfl_xor(bv, msk, WAVE);
-            const int oi = __shfl_xor(bi, msk, WAVE);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (k == 0) mx = bv;
-        if (lane == k) { my_v = bv; my_i = bi; }
-    }
-    const float ek = lane < K ? __expf(my_v - mx) : 0.0f;
-    float denom;
-    if (renorm) {
-        denom = group_sum<64>(ek);
-    } else {
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < EPL; i++) s += __expf(v[i] - mx);
-        denom = group_sum<64>(s);
-    }
+    int my_i;
+    float my_w;
+    wave_topk<EPL>(logits + (size_t)m * ld, K, renorm, lane, s_tk[threadIdx.x >> 6], my_i, my_w);
     if (lane < K) {
         sel[(size_t)m * K + lane] = my_i;
-        wts[(size_t)m * K + lane] = ek / denom;
+        wts[(size_t)m * K + lane] = my_w;
     }
 }
 
-int launch_router_f32w(const float *W, const float *bias, const float *g, const uint16_t *x, int M,
-                       float *logits, int ld, hipStream_t s) {
-    const int E = g_cfg.E, rows = E + (g ? 1 : 0);
-    const dim3 grid((rows + 3) / 4, (M + 7) / 8), block(256);
-    switch (g_cfg.H) {
-    case 2048: hipLaunchKernelGGL(k_router_f32w<8>, grid, block, 0, s, W, bias, g, x, M, E, logits, ld); break;
-    case 2560: hipLaunchKernelGGL(k_router_f32w<10>, grid, block, 0, s, W, bias, g, x, M, E, logits, ld); break;
-    default: set_error(-2, "router: unsupported hidden %d", g_cfg.H); return -2;
+int launch_router_shared(const float *W, const float *bias, const float *g, const ShPtrs *sh,
+                         const uint16_t *x, int M, float *logits, int ld, float *hsh, int ldh, hipStream_t s) {
+    const int E = g_cfg.E, I = g_cfg.I;
+    if (sh && !hsh) { set_error(-1, "router: shared rows need an output"); return -1; }
+    ShPtrs sp{};
+    if (sh) sp = *sh;
+    const int nblk = E + (g ? 1 : 0) + (sh ? I / 2 : 0);
+    if (shape_2048()) {
+        hipLaunchKernelGGL((k_router_shared<8, 512>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
+    } else if (shape_2560()) {
+        hipLaunchKernelGGL((k_router_shared<10, 640>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
+    } else {
+        set_error(-2, "router: unsupported shape"); return -2;
     }
-    return check_launch("router_f32w");
+    return check_launch("router_shared");
 }
 
 int launch_router_bf16w(const uint16_t *W, const float *x, float *logits, hipStream_t s) {
     const int E = g_cfg.E;
-    const dim3 grid((E + 3) / 4), block(256);
+    const dim3 grid(E), block(64);
     switch (g_cfg.H) {
     case 2048: hipLaunchKernelGGL(k_router_bf16w<8>, grid, block, 0, s, W, x, E, logits); break;
     case 2560: hipLaunchKernelGGL(k_router_bf16w<10>, grid, block, 0, s, W, x, E, logits); break;
