@@ -31,6 +31,14 @@ ACT_BYTES = 2 * H * 2                                  # x in, y out (bf16)
 GATE_VEC_BYTES = H * 4                                 # shared-expert sigmoid gate vector
 LAYER_BYTES_M1 = (K + 1) * EXPERT_BYTES + ROUTER_BYTES + ACT_BYTES + GATE_VEC_BYTES
 HBM_PEAK_GBS = 8000.0
+# algorithmic bytes of the three M=1 launches of one layer
+SEC_NAMES = ["k_router_shared (router + shared gate/up)", "k_i8_gateup_m1 (top-K + routed gate/up)",
+             "k_i8_down_m1 (routed + shared down, combine)"]
+SEC_BYTES = [
+    E * H * 4 + H * 4 + 2 * I * H + 2 * I * 4 + H * 2 + (E + 1) * 4 + I * 4,
+    K * (2 * I * H + 2 * I * 4) + H * 2 + E * 4 + K * I * 4 + 2 * K * 4,
+    (K + 1) * (H * I + H * 4) + (K + 1) * I * 4 + H * 2 + 2 * K * 4 + 4,
+]
 
 
 def log(*a):
@@ -80,6 +88,84 @@ def cpu_baseline(n_layers, seconds, threads):
                       f"fp32-accumulate oracle path, OpenMP {threads} threads"}
 
 
+def time_graph(lib, st, enqueue, steps, warmup):
+    """Capture enqueue() once, replay warmup + steps times; ms per replay."""
+    import qfm
+    qfm.check(lib.qfm_graph_capture_begin(st.h), "capture")
+    enqueue()
+    g = lib.qfm_graph_capture_end(st.h)
+    if not g:
+        raise qfm.QfmError(lib.qfm_last_error().decode())
+    for _ in range(warmup):
+        qfm.check(lib.qfm_graph_launch(g, st.h), "graph launch")
+    st.sync()
+    e0, e1 = qfm.Event(), qfm.Event()
+    e0.record(st)
+    for _ in range(steps):
+        qfm.check(lib.qfm_graph_launch(g, st.h), "graph launch")
+    e1.record(st)
+    st.sync()
+    lib.qfm_graph_destroy(g)
+    return e0.elapsed_ms(e1) / steps
+
+
+def m8_bytes(lib, layers_sel, nl, M, expert_bytes):
+    """Algorithmic bytes of an M-row step: distinct experts counted once per layer."""
+    tot = 0
+    for sel in layers_sel:
+        U = len(np.unique(sel))
+        tot += U * expert_bytes + EXPERT_BYTES + ROUTER_BYTES + GATE_VEC_BYTES + 2 * M * H * 2
+    return tot
+
+
+def run_rows(lib, st, layers, nl, M, args, label, fmt_bytes=EXPERT_BYTES):
+    import qfm
+    arr = (qfm.QfmLayer * nl)(*[L.s.layer for L in layers])
+    x = qfm.DevBuf(nl * M * H * 2)
+    y = qfm.DevBuf(nl * M * H * 2)
+    for l in range(nl):
+        qfm.check(lib.qfm_gen_input_rows(x.ptr + l * M * H * 2, M, 0, 2000 + l, 0, st.h), "x")
+    wsb = lib.qfm_workspace_bytes(M)
+    ws = qfm.DevBuf(wsb)
+    st.sync()
+    # distinct experts per layer (from one eager pass, reading the workspace's routing)
+    sels = []
+    view = qfm.QfmWsView()
+    for l in range(nl):
+        qfm.check(lib.qfm_moe_forward(C.byref(arr[l]), x.ptr + l * M * H * 2, M, y.ptr + l * M * H * 2,
+                                      ws.ptr, wsb, st.h), "forward")
+        st.sync()
+        lib.qfm_workspace_view(ws.ptr, M, C.byref(view))
+        sels.append(qfm.d2h(view.sel, np.int32, (M, K)))
+
+    def enq():
+        qfm.check(lib.qfm_moe_forward_layers(arr, nl, x.ptr, M * H, M, y.ptr, M * H, ws.ptr, wsb, st.h), "fwd")
+    ms = time_graph(lib, st, enq, args.steps, args.warmup)
+    us_layer = ms * 1000.0 / nl
+    nbytes = m8_bytes(lib, sels, nl, M, fmt_bytes)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    U = float(np.mean([len(np.unique(s)) for s in sels]))
+    log(f"{label}: {us_layer:.2f} us/layer ({us_layer / M:.2f} us/token/layer), {gbs:.0f} GB/s, mean distinct experts {U:.1f}")
+    return {"workload": label, "rows": M, "us_per_layer": round(us_layer, 3), "us_per_token_layer": round(us_layer / M, 3),
+            "achieved_GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "mean_distinct_experts": round(U, 2), "algorithmic_bytes_per_step": nbytes}
+
+
+NVFP4_EXPERT_BYTES = 3 * (H * I // 2 + H * I // 16) + 3 * 4     # codes + e4m3 block scales + 3 fp32 global scales
+
+
+def run_nvfp4(lib, st, nl, args):
+    import qfm
+    t0 = time.time()
+    layers = [qfm.SynthLayer(qfm.QFM_FMT_NVFP4, 0, l, stream=st) for l in range(nl)]
+    st.sync()
+    log(f"generated {nl} NVFP4 layers ({time.time() - t0:.1f}s)")
+    out = run_rows(lib, st, layers, nl, 8, args, "BASELINE config 3: M=8 NVFP4 routed experts", NVFP4_EXPERT_BYTES)
+    for L in layers:
+        L.destroy()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -90,6 +176,7 @@ def main():
     ap.add_argument("--cpu-layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the M=8 INT8 / NVFP4 lines")
     args = ap.parse_args()
     ws_env = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or ws_env != 1:
@@ -155,6 +242,27 @@ def main():
     gbs = LAYER_BYTES_M1 / (us_layer * 1e-6) / 1e9
     log(f"step {ms_step:.3f} ms ({us_layer:.2f} us/layer, {gbs:.0f} GB/s), host wall {t_host:.2f}s")
 
+    # per-launch durations: each section of the step captured alone (48
+    # launches of one kernel, reading the workspace a full pass left) and replayed
+    sec_us = []
+    for sec in range(3):
+        def enq_sec(sec=sec):
+            for l in range(nl):
+                qfm.check(lib.qfm_moe_forward_sections(C.byref(arr[l]), x.ptr + l * H * 2, 1, y.ptr + l * H * 2,
+                                                       ws.ptr, wsb, 1 << sec, st.h), "section")
+        sec_us.append(time_graph(lib, st, enq_sec, args.steps, args.warmup) * 1000.0 / nl)
+    dom = max(range(3), key=lambda i: sec_us[i])
+    dom_gbs = SEC_BYTES[dom] / (sec_us[dom] * 1e-6) / 1e9
+    log("sections (us/launch, one-kernel graphs): " + ", ".join(f"{SEC_NAMES[i].split()[0]}={sec_us[i]:.2f}" for i in range(3)))
+
+    extra = {}
+    if not args.no_extra:
+        extra["config2_int8_m8"] = run_rows(lib, st, layers, nl, 8, args, "BASELINE config 2: M=8 INT8 fork rows")
+        for L in layers:
+            L.destroy()
+        layers = []
+        extra["config3_nvfp4_m8"] = run_nvfp4(lib, st, nl, args)
+
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
@@ -178,11 +286,15 @@ def main():
         "config": {"workload": "BASELINE config 1: M=1 INT8 MoE decode step, 48 distinct layers",
                    "hidden": H, "inter": I, "experts": E, "top_k": K, "shared_experts": 1,
                    "layers": nl, "rows": 1, "graph": graph is not None},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "whole MoE layer (router, top-k, gate/up, down launches)",
-                     "algorithmic_bytes_per_layer": LAYER_BYTES_M1},
+        "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": SEC_NAMES[dom], "algorithmic_bytes_per_launch": SEC_BYTES[dom],
+                     "avg_launch_us": round(sec_us[dom], 3),
+                     "sections_us": {SEC_NAMES[i].split()[0]: round(sec_us[i], 3) for i in range(3)},
+                     "layer": {"algorithmic_bytes": LAYER_BYTES_M1, "achieved": round(gbs, 1),
+                               "frac": round(gbs / HBM_PEAK_GBS, 4)}},
         "cpu_baseline": cpu,
+        "extra": extra,
     }
     print(json.dumps(out), flush=True)
     if graph:

@@ -170,10 +170,26 @@ int qfm_workspace_view(void *ws, int M, qfm_ws_view *v);
 int qfm_moe_forward(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y,
                     void *ws, size_t ws_bytes, hipStream_t s);
 
+/* Profiling form of the M=1 forward: launches only the sections in mask
+ * (bit 0 router + shared gate/up, bit 1 top-K + routed gate/up, bit 2 down +
+ * combine), reading the workspace the earlier sections left behind. */
+int qfm_moe_forward_sections(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y,
+                             void *ws, size_t ws_bytes, int mask, hipStream_t s);
+
 /* nl layers back to back on one stream: layer l reads x + l*x_stride and
  * writes y + l*y_stride (elements); layer l+1 starts after layer l ends. */
 int qfm_moe_forward_layers(const qfm_layer *layers, int nl, const uint16_t *x, long x_stride, int M,
                            uint16_t *y, long y_stride, void *ws, size_t ws_bytes, hipStream_t s);
+
+/* Section profiler: while enabled, every M=1 qfm_moe_forward records
+ * hipEvents between its launches (also inside a stream capture, where they
+ * become event-record nodes that fire on every replay). read() waits for the
+ * last mark and returns the summed milliseconds of section 0 (router + shared
+ * gate/up), 1 (routed gate/up with the top-K selection) and 2 (down +
+ * combine) over the recorded forwards, and their number; enable() (on or
+ * off) clears the marks. */
+int qfm_profile_enable(int on);
+int qfm_profile_read(double *ms, int n_sections, int *calls);
 
 /* HIP graph capture of whatever is enqueued on a stream between begin and
  * end (used to replay a whole decode step without host launch cost). */

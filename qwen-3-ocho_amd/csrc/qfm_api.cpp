@@ -3,7 +3,9 @@
 // utilities. Host code only; every kernel lives in the .hip files.
 #include "qfm_internal.h"
 
+#include <array>
 #include <cstdarg>
+#include <vector>
 #include <cstdio>
 #include <cstddef>
 #include <cstring>
@@ -47,10 +49,32 @@ static_assert(sizeof(Qf4ExpCache) == 312, "Qf4ExpCache layout");
 static_assert(sizeof(Qf8I8Mat) == 24, "Qf8I8Mat layout");
 static_assert(sizeof(Qf5M8Route) == 56, "Qf5M8Route layout");
 
+// ---- section profiler: hipEvent marks between the launches of a forward
+// (eager launches only; the reference's QF8_PROFILE section marks play the
+// same role). Sections: 0 router + shared gate/up, 1 routed gate/up (with the
+// selection), 2 down + combine. Not thread-safe; one profiling stream.
+struct Prof {
+    bool on = false;
+    std::vector<hipEvent_t> pool;
+    size_t used = 0;
+    std::vector<std::array<size_t, 4>> marks;   // event indices per forward
+};
+static Prof g_prof;
+static size_t prof_event(hipStream_t s) {
+    if (g_prof.used == g_prof.pool.size()) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return (size_t)-1;
+        g_prof.pool.push_back(e);
+    }
+    const size_t i = g_prof.used++;
+    (void)hipEventRecord(g_prof.pool[i], s);
+    return i;
+}
+
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct WsLayout {
-    size_t logits, sel, wts, hidden, total;
+    size_t logits, sel, wts, hidden, csr, part, total;
 };
 static WsLayout ws_layout(int M) {
     const Cfg &c = g_cfg;
@@ -60,15 +84,21 @@ static WsLayout ws_layout(int M) {
     w.sel = off;    off += align256((size_t)M * c.K * sizeof(int));
     w.wts = off;    off += align256((size_t)M * c.K * sizeof(float));
     w.hidden = off; off += align256((size_t)M * (c.K + 1) * c.I * sizeof(float));
+    w.csr = off;    off += align256((size_t)(3 * M * c.K + 2) * sizeof(int));
+    w.part = off;   off += align256((size_t)M * c.K * c.H * sizeof(float));
     w.total = off;
     return w;
 }
 
 static bool layer_ok(const qfm_layer *L) {
     if (!L || !L->arena || !L->router) return false;
+    const Qf4ExpCache *a = L->arena;
     if (L->fmt == QFM_FMT_INT8) {
-        const Qf4ExpCache *a = L->arena;
         if (!a->i8_gate || !a->i8_up || !a->i8_down || !a->i8s_gate || !a->i8s_up || !a->i8s_down) return false;
+    } else if (L->fmt == QFM_FMT_NVFP4) {
+        if (!a->w_gate || !a->w_up || !a->w_down || !a->s_gate || !a->s_up || !a->s_down || !a->s2g_dev ||
+            !a->s2u_dev || !a->s2d_dev)
+            return false;
     } else {
         return false;
     }
@@ -185,8 +215,22 @@ int qfm_workspace_view(void *ws, int M, qfm_ws_view *v) {
     return 0;
 }
 
+static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
+                        int mask, hipStream_t s);
+
 int qfm_moe_forward(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
                     hipStream_t s) {
+    return forward_impl(L, x, M, y, ws, ws_bytes, 7, s);
+}
+
+int qfm_moe_forward_sections(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
+                             int mask, hipStream_t s) {
+    if (M != 1 || mask < 1 || mask > 7) { set_error(-1, "qfm_moe_forward_sections: M=1 and mask 1..7 only"); return -1; }
+    return forward_impl(L, x, M, y, ws, ws_bytes, mask, s);
+}
+
+static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
+                        int mask, hipStream_t s) {
     if (!layer_ok(L) || !x || !y || !ws || M < 1) { set_error(-1, "qfm_moe_forward: bad arguments"); return -1; }
     if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) { set_error(-1, "qfm_moe_forward: workspace not 256-byte aligned"); return -1; }
     const WsLayout w = ws_layout(M);
@@ -197,8 +241,8 @@ int qfm_moe_forward(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, v
     int *sel = reinterpret_cast<int *>(b + w.sel);
     float *wts = reinterpret_cast<float *>(b + w.wts);
     float *hidden = reinterpret_cast<float *>(b + w.hidden);
-    const size_t ldh = (size_t)(c.K + 1) * c.I;    // per row: K routed hidden vectors, then the shared one
-    float *hsh = hidden + (size_t)c.K * c.I;
+    int *csr = reinterpret_cast<int *>(b + w.csr);
+    float *part = reinterpret_cast<float *>(b + w.part);
     const bool has_sh = L->sh_gate.w != nullptr;
     const float *g = (has_sh && c.gated && L->sh_gate_inp) ? L->sh_gate_inp : nullptr;
     if (has_sh && c.gated && !g) { set_error(-1, "qfm_moe_forward: gated shared expert needs sh_gate_inp"); return -1; }
@@ -209,23 +253,32 @@ int qfm_moe_forward(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, v
     }
     const ShPtrs *sp = has_sh ? &shp : nullptr;
     const int ld = c.E + 1;
-    // 1. router logits (+ shared gate dot) and the shared expert's hidden: depend on x only
-    int rc = launch_router_shared(L->router, L->router_bias, g, sp, x, M, logits, ld, hsh, (int)ldh, s);
-    if (rc) return rc;
-    if (M == 1 && c.E == 512) {
+    std::array<size_t, 4> pm{};
+    if (g_prof.on) pm[0] = prof_event(s);
+    if (M == 1 && L->fmt == QFM_FMT_INT8 && c.E == 512) {
+        // per row: K routed hidden vectors, then the shared one (read as one block by the down kernel)
+        float *hsh = hidden + (size_t)c.K * c.I;
+        // 1. router logits (+ shared gate dot) and the shared expert's hidden: depend on x only
+        int rc = 0;
+        if (mask & 1) rc = launch_router_shared(L->router, L->router_bias, g, sp, x, 1, logits, ld, hsh, c.I, s);
+        if (g_prof.on) pm[1] = prof_event(s);
         // 2. top-K inside the gate/up kernel; 3. down + combine (+ shared) -> y bf16
-        rc = launch_i8_gateup_m1(L->arena, x, nullptr, logits, sel, wts, c.K, hidden, s);
-        if (!rc) rc = launch_i8_down_m1(L->arena, hidden, wts, sel, c.K, sp, g ? logits + c.E : nullptr, nullptr, y, s);
+        if (!rc && (mask & 2)) rc = launch_i8_gateup_m1(L->arena, x, nullptr, logits, sel, wts, c.K, hidden, s);
+        if (g_prof.on) pm[2] = prof_event(s);
+        if (!rc && (mask & 4))
+            rc = launch_i8_down_m1(L->arena, hidden, wts, sel, c.K, sp, g ? logits + c.E : nullptr, nullptr, y, s);
+        if (g_prof.on) { pm[3] = prof_event(s); g_prof.marks.push_back(pm); }
         return rc;
     }
-    rc = launch_topk(logits, ld, M, sel, wts, s);
-    for (int m = 0; m < M && !rc; m++) {
-        float *hm = hidden + (size_t)m * ldh;
-        rc = launch_i8_gateup_m1(L->arena, x + (size_t)m * c.H, nullptr, nullptr, sel + m * c.K, nullptr, c.K, hm, s);
-        if (!rc) rc = launch_i8_down_m1(L->arena, hm, wts + m * c.K, sel + m * c.K, c.K, sp,
-                                        g ? logits + (size_t)m * ld + c.E : nullptr, nullptr, y + (size_t)m * c.H, s);
+    if (M <= 8) {
+        float *hsh = hidden + (size_t)M * c.K * c.I;
+        int rc = launch_router_shared(L->router, L->router_bias, g, sp, x, M, logits, ld, hsh, c.I, s);
+        if (!rc) rc = launch_csr_forward(L->arena, L->fmt, sp, x, logits, ld, g ? 1 : 0, M, hidden, hsh, sel, wts, csr,
+                                         part, y, s);
+        return rc;
     }
-    return rc;
+    set_error(-2, "qfm_moe_forward: M=%d rows is not supported by this build", M);
+    return -2;
 }
 
 int qfm_moe_forward_layers(const qfm_layer *layers, int nl, const uint16_t *x, long x_stride, int M, uint16_t *y,
@@ -235,6 +288,28 @@ int qfm_moe_forward_layers(const qfm_layer *layers, int nl, const uint16_t *x, l
         const int rc = qfm_moe_forward(&layers[l], x + (size_t)l * x_stride, M, y + (size_t)l * y_stride, ws, ws_bytes, s);
         if (rc) return rc;
     }
+    return 0;
+}
+
+int qfm_profile_enable(int on) {
+    g_prof.on = on != 0;
+    g_prof.used = 0;
+    g_prof.marks.clear();
+    return 0;
+}
+
+int qfm_profile_read(double *ms, int n, int *calls) {
+    if (!ms || n < 1) return -1;
+    for (int i = 0; i < n; i++) ms[i] = 0.0;
+    if (calls) *calls = (int)g_prof.marks.size();
+    if (g_prof.marks.empty()) return 0;
+    if (hipEventSynchronize(g_prof.pool[g_prof.marks.back()[3]]) != hipSuccess) return -1;
+    for (const auto &m : g_prof.marks)
+        for (int i = 0; i < 3 && i < n; i++) {
+            float t = 0.0f;
+            if (hipEventElapsedTime(&t, g_prof.pool[m[i]], g_prof.pool[m[i + 1]]) != hipSuccess) return -1;
+            ms[i] += t;
+        }
     return 0;
 }
 

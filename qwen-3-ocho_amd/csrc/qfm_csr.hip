@@ -1,0 +1,402 @@
+// qfm_csr.hip -- multi-row decode (M <= 8 "Ocho" fork rows): routing
+// inversion + weight-once-per-distinct-expert gate/up and down, INT8 and
+// NVFP4 arenas.
+//
+// Reference behaviour: the M=8 CSR tier k_m8_build_csr / k_m8_gateup /
+// k_m8_downacc (ocho/amd_server/qf_moe_m8_wave64.hip:72-211, :261-299) and the
+// chunk path k_i8_csr_build / k_i8_gateup_csr / k_i8_downacc_csr /
+// k_i8_combine (ocho/amd_server/qf8_moe_i8.hip:196-358): distinct experts in
+// ascending id, the pairs of an expert in (token, k) order, every weight row
+// read once per distinct expert and dotted against all rows routed to it,
+// owned partials part[t][k][H] summed in k order (no atomics, deterministic).
+//
+// Launch sequence (all stream-ordered):
+//   k_topk_csr     one block, 512 threads: the top-K of all M rows (one wave
+//                  per row), then the routing inversion in LDS (O(P^2) rank
+//                  counting over P = M*K <= 128 pairs); publishes sel/wts/CSR.
+//   k_csr_gateup   grid (I/rows, min(M*K, E)), 256 threads: distinct expert
+//                  blockIdx.y. One lane group per gate/up row: the row is
+//                  loaded once, then dotted with the x slice of each routed
+//                  token (L2-resident). hidden is written per pair, in CSR
+//                  order.
+//   k_csr_down     grid (H/64, min(M*K, E)), 256 threads: expert u's down rows
+//                  [64b, 64b+64), pairs' hidden vectors staged in LDS; writes
+//                  part[t*K + k][c] = w * <Wd_e[c], h_pair> * scale.
+//   k_csr_combine  grid (H/rows), 256 threads: y[t][c] = sum_k part[t*K+k][c]
+//                  + gamma_t * <Wd_sh[c], hsh_t> * sd_sh[c], bf16 out.
+#include "qfm_dev.h"
+#include "qfm_internal.h"
+
+namespace qfm {
+
+constexpr int kMaxRows = 8;
+constexpr int kMaxPairs = kMaxRows * 16;
+
+// ---- weight-format policies ----------------------------------------------------
+// A row of K values is K/VPB bytes; lanes read 16-byte chunks (VPC values).
+struct FmtI8 {
+    static constexpr int VPB = 1, VPC = 16;
+};
+struct FmtF4 {
+    static constexpr int VPB = 2, VPC = 32;
+};
+
+// x slice for a chunk-strided lane layout: chunk q of a row covers values
+// [q*VPC, q*VPC + VPC); lane l of an LPR group owns chunks st*LPR + l.
+template <int K, int LPR, int VPC>
+__device__ __forceinline__ void load_slice_bf16(const uint16_t *x, int l, float (&xs)[K / (LPR * VPC)][VPC]) {
+    constexpr int NST = K / (LPR * VPC);
+#pragma unroll
+    for (int st = 0; st < NST; st++) {
+        const uint16_t *p = x + (st * LPR + l) * VPC;
+#pragma unroll
+        for (int q = 0; q < VPC / 8; q++) {
+            const uint4 a = *reinterpret_cast<const uint4 *>(p + q * 8);
+            const uint32_t d[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int b = 0; b < 4; b++) { xs[st][q * 8 + 2 * b] = bf16_lo(d[b]); xs[st][q * 8 + 2 * b + 1] = bf16_hi(d[b]); }
+        }
+    }
+}
+
+// NVFP4 chunk: 32 e2m1 values (adjacent pairs: byte i = value 2i low nibble,
+// 2i+1 high nibble) with two e4m3 block scales (values 0..15 and 16..31).
+// Codes are converted by the gfx950 v_cvt_scalef32_pk_f32_fp4 instruction
+// with a unit scale (exact e2m1 values); each 16-value group is scaled once.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float f4_group16(uint32_t lo, uint32_t hi, const float *x) {
+    float a = 0.0f;
+    const uint32_t w[2] = {lo, hi};
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+        f32x2_t v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 0);
+        f32x2_t v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 1);
+        f32x2_t v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 2);
+        f32x2_t v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 3);
+        a = fmaf(v0.x, x[d * 8 + 0], a); a = fmaf(v0.y, x[d * 8 + 1], a);
+        a = fmaf(v1.x, x[d * 8 + 2], a); a = fmaf(v1.y, x[d * 8 + 3], a);
+        a = fmaf(v2.x, x[d * 8 + 4], a); a = fmaf(v2.y, x[d * 8 + 5], a);
+        a = fmaf(v3.x, x[d * 8 + 6], a); a = fmaf(v3.y, x[d * 8 + 7], a);
+    }
+    return a;
+}
+__device__ __forceinline__ float e4m3_scale(uint32_t b) {
+    return __builtin_amdgcn_cvt_f32_fp8((int)b, 0);
+}
+__device__ __forceinline__ float f4_chunk(uint4 w, uint32_t s2b, const float *x) {
+    const float g0 = f4_group16(w.x, w.y, x);
+    const float g1 = f4_group16(w.z, w.w, x + 16);
+    return fmaf(e4m3_scale(s2b & 0xFFu), g0, e4m3_scale((s2b >> 8) & 0xFFu) * g1);
+}
+
+// ---- routing inversion in LDS ---------------------------------------------------
+struct CsrLds {
+    int sel[kMaxPairs];
+    float wts[kMaxPairs];
+    int pair[kMaxPairs];      // CSR position -> original pair index t*K + k
+    int exp_id[kMaxPairs];
+    int exp_ptr[kMaxPairs + 1];
+    int first[kMaxPairs];
+    int n_exp;
+    unsigned long long tk[8][272];
+};
+
+// Called by all threads of the block after sel of the P pairs is in LDS.
+// Position of pair p in (expert, token, k) order = #{q: e_q < e_p} +
+// #{q < p: e_q == e_p}; an expert's distinct index = #{distinct e' < e_p}.
+__device__ __forceinline__ void csr_build_lds(CsrLds &c, int P) {
+    const int p = threadIdx.x;
+    int less = 0, before = 0, e = 0;
+    if (p < P) {
+        e = c.sel[p];
+        for (int q = 0; q < P; q++) {
+            const int f = c.sel[q];
+            less += f < e;
+            before += (f == e) & (q < p);
+        }
+        c.first[p] = before == 0;
+    }
+    __syncthreads();
+    if (p < P) {
+        int first_less = 0;
+        for (int q = 0; q < P; q++) first_less += (c.first[q] && c.sel[q] < e) ? 1 : 0;
+        c.pair[less + before] = p;
+        if (before == 0) { c.exp_id[first_less] = e; c.exp_ptr[first_less] = less; }
+    }
+    if (threadIdx.x == 0) {
+        int n = 0;
+        for (int q = 0; q < P; q++) n += c.first[q];
+        c.n_exp = n;
+        c.exp_ptr[n] = P;
+    }
+    __syncthreads();
+}
+
+constexpr int lpr_of(int cpr) { return cpr % 32 == 0 ? 32 : cpr % 16 == 0 ? 16 : cpr % 8 == 0 ? 8 : 4; }
+
+// ---- top-K of all rows + routing inversion: one block, one wave per row ---------
+// Published: sel/wts [M][K]; csr = {n_exp, exp_id[P], exp_ptr[P+1], pair[P]}.
+template <int EPL>
+__global__ void __launch_bounds__(512)
+k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, int *__restrict__ g_sel,
+           float *__restrict__ g_wts, int *__restrict__ g_csr) {
+    __shared__ CsrLds c;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int P = M * K;
+    if (wave < M) {
+        int my_i;
+        float my_w;
+        wave_topk<EPL>(logits + (size_t)wave * ld, K, renorm, lane, c.tk[wave], my_i, my_w);
+        if (lane < K) { c.sel[wave * K + lane] = my_i; c.wts[wave * K + lane] = my_w; }
+    }
+    __syncthreads();
+    csr_build_lds(c, P);
+    for (int i = threadIdx.x; i < P; i += 512) {
+        g_sel[i] = c.sel[i]; g_wts[i] = c.wts[i];
+        g_csr[1 + i] = c.exp_id[i];
+        g_csr[1 + P + (P + 1) + i] = c.pair[i];
+    }
+    for (int i = threadIdx.x; i <= P; i += 512) g_csr[1 + P + i] = c.exp_ptr[i];
+    if (threadIdx.x == 0) g_csr[0] = c.n_exp;
+}
+
+// ---- gate/up: one distinct expert per blockIdx.y ---------------------------------
+// One LPR-lane group per gate/up row; the row pair is loaded once and dotted
+// with the x slice of every routed token (x rows are L2-resident; each
+// 16-byte chunk's activations are converted right before use).
+template <class F, int H, int I>
+__global__ void __launch_bounds__(256)
+k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
+             const float *__restrict__ Sg, const float *__restrict__ Su,          // INT8 row scales
+             const uint8_t *__restrict__ Bg, const uint8_t *__restrict__ Bu,      // NVFP4 block scales
+             const float *__restrict__ s2g, const float *__restrict__ s2u,        // NVFP4 per-expert scale
+             const uint16_t *__restrict__ x, int K, const int *__restrict__ g_csr, int P,
+             float *__restrict__ hpair) {
+    constexpr int ROWB = H / F::VPB;             // bytes per gate/up row
+    constexpr int LPR = lpr_of(ROWB / 16);       // lanes per row
+    constexpr int NST = ROWB / (LPR * 16);
+    constexpr int RPB = 256 / LPR;               // rows per block
+    const int u = blockIdx.y;
+    const int n_exp = g_csr[0];
+    if (u >= n_exp) return;
+    const int *exp_ptr = g_csr + 1 + P, *pair = g_csr + 1 + P + P + 1;
+    const int e = g_csr[1 + u], p0 = exp_ptr[u], np = exp_ptr[u + 1] - p0;
+    const int l = threadIdx.x % LPR;
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR;
+    const size_t roff = ((size_t)e * I + row) * ROWB;
+    uint4 wg[NST], wu[NST];
+#pragma unroll
+    for (int st = 0; st < NST; st++) {
+        wg[st] = ld_nt16(Wg + roff + (st * LPR + l) * 16);
+        wu[st] = ld_nt16(Wu + roff + (st * LPR + l) * 16);
+    }
+    uint32_t bg[NST], bu[NST];
+    float rsg, rsu;
+    if constexpr (F::VPB == 2) {
+        const size_t boff = ((size_t)e * I + row) * (H / 16);
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            bg[st] = *reinterpret_cast<const uint16_t *>(Bg + boff + (st * LPR + l) * 2);
+            bu[st] = *reinterpret_cast<const uint16_t *>(Bu + boff + (st * LPR + l) * 2);
+        }
+        rsg = s2g[e]; rsu = s2u[e];
+    } else {
+        rsg = Sg[(size_t)e * I + row]; rsu = Su[(size_t)e * I + row];
+    }
+    for (int j = 0; j < np; j++) {
+        const int t = pair[p0 + j] / K;
+        const uint16_t *xt = x + (size_t)t * H;
+        float ag = 0.0f, au = 0.0f, xsum = 0.0f;
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            float xs[F::VPC];
+            const uint16_t *p = xt + (st * LPR + l) * F::VPC;
+#pragma unroll
+            for (int q = 0; q < F::VPC / 8; q++) {
+                const uint4 a = *reinterpret_cast<const uint4 *>(p + q * 8);
+                const uint32_t d[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+                for (int b = 0; b < 4; b++) { xs[q * 8 + 2 * b] = bf16_lo(d[b]); xs[q * 8 + 2 * b + 1] = bf16_hi(d[b]); }
+            }
+            if constexpr (F::VPB == 1) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) xsum += xs[i];
+                ag = dot16_u8(wg[st], xs, ag);
+                au = dot16_u8(wu[st], xs, au);
+            } else {
+                ag += f4_chunk(wg[st], bg[st], xs);
+                au += f4_chunk(wu[st], bu[st], xs);
+            }
+        }
+        if constexpr (F::VPB == 1) { ag = fmaf(-128.0f, xsum, ag); au = fmaf(-128.0f, xsum, au); }
+        ag = group_sum<LPR>(ag);
+        au = group_sum<LPR>(au);
+        if (l == 0) hpair[(size_t)(p0 + j) * I + row] = silu(ag * rsg) * (au * rsu);
+    }
+}
+
+// ---- down: one distinct expert x 64 rows per block, owned partials ---------------
+template <class F, int H, int I>
+__global__ void __launch_bounds__(256)
+k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const uint8_t *__restrict__ Bd,
+           const float *__restrict__ s2d, const float *__restrict__ hpair, const float *__restrict__ g_wts,
+           const int *__restrict__ g_csr, int P, float *__restrict__ part) {
+    constexpr int ROWB = I / F::VPB;                   // bytes per down row
+    constexpr int CPR = ROWB / 16;                     // 16-byte chunks per row
+    constexpr int LPR = lpr_of(CPR);                   // lanes per row
+    constexpr int NST = CPR / LPR;
+    constexpr int GROUPS = 256 / LPR;                  // row groups per block
+    constexpr int ROWS = 64;
+    __shared__ __align__(16) float sh_h[kMaxRows * I];
+    __shared__ float sh_cs[kMaxRows * I / 16];
+    const int u = blockIdx.y;
+    const int n_exp = g_csr[0];
+    if (u >= n_exp) return;
+    const int *exp_id = g_csr + 1, *exp_ptr = g_csr + 1 + P, *pair = g_csr + 1 + P + P + 1;
+    const int e = exp_id[u], p0 = exp_ptr[u], np = exp_ptr[u + 1] - p0;
+    const int l = threadIdx.x % LPR, grp = threadIdx.x / LPR;
+    // weights for this thread's rows first (ROWS/GROUPS rows per group)
+    constexpr int RPG = ROWS / GROUPS;
+    uint4 w[RPG][NST];
+    uint32_t bs[RPG][NST];
+    float rs[RPG];
+#pragma unroll
+    for (int q = 0; q < RPG; q++) {
+        const int c = blockIdx.x * ROWS + q * GROUPS + grp;
+        const size_t roff = ((size_t)e * H + c) * ROWB;
+#pragma unroll
+        for (int st = 0; st < NST; st++) w[q][st] = ld_nt16(Wd + roff + (st * LPR + l) * 16);
+        if constexpr (F::VPB == 2) {
+            const size_t boff = ((size_t)e * H + c) * (I / 16);
+#pragma unroll
+            for (int st = 0; st < NST; st++) bs[q][st] = *reinterpret_cast<const uint16_t *>(Bd + boff + (st * LPR + l) * 2);
+            rs[q] = s2d[e];
+        } else {
+            rs[q] = Sd[(size_t)e * H + c];
+        }
+    }
+    for (int i = threadIdx.x; i < np * I / 4; i += 256)
+        reinterpret_cast<float4 *>(sh_h)[i] = reinterpret_cast<const float4 *>(hpair + (size_t)p0 * I)[i];
+    __syncthreads();
+    if constexpr (F::VPB == 1) {
+        for (int i = threadIdx.x; i < np * I / 16; i += 256) {
+            float t = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) t += sh_h[i * 16 + q];
+            sh_cs[i] = -128.0f * t;
+        }
+        __syncthreads();
+    }
+    for (int j = 0; j < np; j++) {
+        const int pr = pair[p0 + j];
+        const float wp = g_wts[pr];
+#pragma unroll
+        for (int q = 0; q < RPG; q++) {
+            const int c = blockIdx.x * ROWS + q * GROUPS + grp;
+            float d = 0.0f;
+#pragma unroll
+            for (int st = 0; st < NST; st++) {
+                const int ch = st * LPR + l;
+                if constexpr (F::VPB == 1) {
+                    d += sh_cs[j * (I / 16) + ch];
+                    d = dot16_u8(w[q][st], sh_h + j * I + ch * 16, d);
+                } else {
+                    d += f4_chunk(w[q][st], bs[q][st], sh_h + j * I + ch * 32);
+                }
+            }
+            d = group_sum<LPR>(d);
+            if (l == 0) part[(size_t)pr * H + c] = wp * (d * rs[q]);
+        }
+    }
+}
+
+// ---- combine + shared expert down (INT8) -------------------------------------------
+template <int H, int I>
+__global__ void __launch_bounds__(256)
+k_csr_combine(const float *__restrict__ part, int M, int K, ShPtrs sh, const float *__restrict__ hsh,
+              const float *__restrict__ logits, int ld, int gated, uint16_t *__restrict__ y) {
+    constexpr int LPR = lpr_of(I / 16), NST = I / (16 * LPR), RPB = 256 / LPR;
+    __shared__ __align__(16) float sh_h[kMaxRows * I];
+    __shared__ float sh_cs[kMaxRows * I / 16];
+    const int l = threadIdx.x % LPR;
+    const int c = blockIdx.x * RPB + threadIdx.x / LPR;
+    const bool has_sh = sh.qd != nullptr;
+    uint4 w[NST];
+    float sd = 0.0f;
+    if (has_sh) {
+#pragma unroll
+        for (int st = 0; st < NST; st++) w[st] = ld_nt16(sh.qd + (size_t)c * I + (st * LPR + l) * 16);
+        sd = sh.sd[c];
+        for (int i = threadIdx.x; i < M * I / 4; i += 256)
+            reinterpret_cast<float4 *>(sh_h)[i] = reinterpret_cast<const float4 *>(hsh)[i];
+        __syncthreads();
+        for (int i = threadIdx.x; i < M * I / 16; i += 256) {
+            float t = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) t += sh_h[i * 16 + q];
+            sh_cs[i] = -128.0f * t;
+        }
+        __syncthreads();
+    }
+    for (int t = 0; t < M; t++) {
+        float d = 0.0f;
+        if (has_sh) {
+#pragma unroll
+            for (int st = 0; st < NST; st++) {
+                d += sh_cs[t * (I / 16) + st * LPR + l];
+                d = dot16_u8(w[st], sh_h + t * I + (st * LPR + l) * 16, d);
+            }
+            d = group_sum<LPR>(d);
+        }
+        if (l == 0) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++) acc += part[((size_t)t * K + k) * H + c];
+            if (has_sh) {
+                const float gam = gated ? sigmoid(logits[(size_t)t * ld + (ld - 1)]) : 1.0f;
+                acc = fmaf(gam * sd, d, acc);
+            }
+            y[(size_t)t * H + c] = f32_to_bf16(acc);
+        }
+    }
+}
+
+// ---- launchers -------------------------------------------------------------------
+int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,
+                       int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
+                       float *part, uint16_t *y, hipStream_t s) {
+    const int K = g_cfg.K, E = g_cfg.E, P = M * K;
+    if (M < 1 || M > kMaxRows || P > kMaxPairs || E != 512) {
+        set_error(-2, "csr path: needs 1 <= M <= %d, M*top_k <= %d, 512 experts", kMaxRows, kMaxPairs); return -2;
+    }
+    const int umax = P < E ? P : E;
+    ShPtrs sp{};
+    if (sh) sp = *sh;
+    const dim3 b512(512), b256(256);
+    const uint8_t *wg, *wu, *wd, *bg = nullptr, *bu = nullptr, *bd = nullptr;
+    if (fmt == QFM_FMT_INT8) {
+        if (!a->i8_gate || !a->i8_up || !a->i8_down) { set_error(-1, "csr path: arena has no INT8 blobs"); return -1; }
+        wg = (const uint8_t *)a->i8_gate; wu = (const uint8_t *)a->i8_up; wd = (const uint8_t *)a->i8_down;
+    } else {
+        if (!a->w_gate || !a->s_gate || !a->s2g_dev) { set_error(-1, "csr path: arena has no NVFP4 blobs"); return -1; }
+        wg = a->w_gate; wu = a->w_up; wd = a->w_down; bg = a->s_gate; bu = a->s_up; bd = a->s_down;
+    }
+#define QFM_CSR_LAUNCH(F, HH, II)                                                                                   \
+    hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), b512, 0, s, logits, ld, M, K, g_cfg.renorm, sel, wts, csr);       \
+    hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(II / (256 / lpr_of(HH / F::VPB / 16)), umax), b256, 0, s,  \
+                       wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, K, csr, P, hpair);       \
+    hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / 64, umax), b256, 0, s, wd, a->i8s_down, bd, a->s2d_dev,  \
+                       hpair, wts, csr, P, part);                                                                  \
+    hipLaunchKernelGGL((k_csr_combine<HH, II>), dim3(HH / (256 / lpr_of(II / 16))), b256, 0, s, part, M, K, sp, hsh, \
+                       logits, ld, gated, y)
+    if (shape_2048()) {
+        if (fmt == QFM_FMT_INT8) { QFM_CSR_LAUNCH(FmtI8, 2048, 512); } else { QFM_CSR_LAUNCH(FmtF4, 2048, 512); }
+    } else if (shape_2560()) {
+        if (fmt == QFM_FMT_INT8) { QFM_CSR_LAUNCH(FmtI8, 2560, 640); } else { QFM_CSR_LAUNCH(FmtF4, 2560, 640); }
+    } else {
+        set_error(-2, "csr path: unsupported shape"); return -2;
+    }
+#undef QFM_CSR_LAUNCH
+    return check_launch("csr_forward");
+}
+
+}  // namespace qfm

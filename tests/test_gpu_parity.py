@@ -222,12 +222,15 @@ def _run_layer(lib, M, seed, layer, x_layer, fmt=qfm.QFM_FMT_INT8, bias=False):
     return out
 
 
-@pytest.mark.parametrize("M,seed,layer", [(1, 0, 0), (1, 1, 17), (8, 0, 3)])
-def test_moe_layer_int8(lib, M, seed, layer):
-    _say("layer int8", M, seed, layer)
+@pytest.mark.parametrize("M,seed,layer,fmt", [(1, 0, 0, 0), (1, 1, 17, 0), (8, 0, 3, 0), (2, 4, 9, 0), (5, 2, 2, 0),
+                                               (1, 0, 5, 1), (8, 1, 6, 1), (3, 3, 7, 1)])
+def test_moe_layer(lib, M, seed, layer, fmt):
+    """INT8 (fmt 0) and NVFP4 (fmt 1) routed experts; M=1 uses the single-row
+    kernels (INT8) or the CSR kernels (NVFP4); M>1 always the CSR kernels."""
+    _say("layer", "int8" if fmt == 0 else "nvfp4", M, seed, layer)
     _cfg(lib)
-    g = _run_layer(lib, M, seed, layer, x_layer=100 + layer)
-    r = orc.moe_layer(2048, 512, 512, 10, M, seed, layer, 100 + layer)
+    g = _run_layer(lib, M, seed, layer, x_layer=100 + layer, fmt=fmt)
+    r = orc.moe_layer(2048, 512, 512, 10, M, seed, layer, 100 + layer, fmt=fmt)
     assert np.array_equal(g["x"], r["x"])
     assert np.array_equal(g["logits"].view(np.uint32), r["logits"].view(np.uint32))
     assert np.array_equal(g["sel"], r["sel"])
@@ -238,11 +241,21 @@ def test_moe_layer_int8(lib, M, seed, layer):
         assert rel <= TOL
 
 
-def test_moe_layer_int8_reference_shape_ungated(lib):
-    _say("layer int8 2560/640 ungated")
+@pytest.mark.parametrize("M,fmt", [(1, 0), (4, 0), (4, 1)])
+def test_moe_layer_reference_shape_ungated(lib, M, fmt):
+    _say("layer 2560/640 ungated", M, fmt)
     _cfg(lib, H=2560, I=640, gated=0)
-    g = _run_layer(lib, 1, 2, 4, x_layer=7)
-    r = orc.moe_layer(2560, 640, 512, 10, 1, 2, 4, 7, gated=0)
+    g = _run_layer(lib, M, 2, 4, x_layer=7, fmt=fmt)
+    r = orc.moe_layer(2560, 640, 512, 10, M, 2, 4, 7, gated=0, fmt=fmt)
     assert np.array_equal(g["sel"], r["sel"])
-    assert _rel(g["y"][0], r["y"][0]) <= TOL
+    for m in range(M):
+        assert _rel(g["y"][m], r["y"][m]) <= TOL
     _cfg(lib)
+
+
+def test_moe_layer_deterministic(lib):
+    """Two runs of the same layer give identical bits (no atomics on outputs)."""
+    _cfg(lib)
+    a = _run_layer(lib, 8, 5, 1, x_layer=3)
+    b = _run_layer(lib, 8, 5, 1, x_layer=3)
+    assert np.array_equal(a["y"].view(np.uint32), b["y"].view(np.uint32))
