@@ -158,6 +158,9 @@ typedef struct {
 
 /* Workspace for M rows (device memory, caller-owned, >= 256-byte aligned). */
 size_t qfm_workspace_bytes(int M);
+/* For M > 8 (prefill) logits is [M][E] of the MFMA router GEMM (the exact
+ * canonical logits are computed only for the selection candidates) and
+ * hidden is NULL. */
 typedef struct {
     float *logits;   /* [M][E+1]: router logits; column E = <sh_gate_inp, x> */
     int   *sel;      /* [M][K] */

@@ -179,14 +179,14 @@ static float canon_dot(const float *w, const float *xf, int H) {
 }
 void orc_router_logits(const float *W, const uint16_t *x, const float *bias,
                        int M, int E, int H, float *logits) {
-    float *xf = (float *)malloc(sizeof(float) * (size_t)H);
-    for (int m = 0; m < M; m++) {
-        for (int k = 0; k < H; k++) xf[k] = orc_bf16_to_f32(x[(size_t)m * H + k]);
-        for (int e = 0; e < E; e++) {
-            float v = canon_dot(W + (size_t)e * H, xf, H);
-            if (bias) v = v + bias[e];
-            logits[(size_t)m * E + e] = v;
-        }
+    float *xf = (float *)malloc(sizeof(float) * (size_t)M * H);
+    for (size_t i = 0; i < (size_t)M * H; i++) xf[i] = orc_bf16_to_f32(x[i]);
+    #pragma omp parallel for schedule(static)
+    for (int64_t me = 0; me < (int64_t)M * E; me++) {
+        const int m = (int)(me / E), e = (int)(me % E);
+        float v = canon_dot(W + (size_t)e * H, xf + (size_t)m * H, H);
+        if (bias) v = v + bias[e];
+        logits[(size_t)m * E + e] = v;
     }
     free(xf);
 }
@@ -386,27 +386,39 @@ int orc_moe_layer(const orc_layer_cfg *c, int M, uint16_t *x_out, float *logits,
             orc_fill_e4m3scale(c->seed, c->layer, ORC_T_FSU, (uint64_t)e * IH / 16, IH / 16, fsu);
             orc_fill_e4m3scale(c->seed, c->layer, ORC_T_FSD, (uint64_t)e * IH / 16, IH / 16, fsd);
         }
-        for (int m = 0; m < M; m++)
-            for (int k = 0; k < K; k++) {
-                if (sel[m * K + k] != e) continue;
-                for (int i = 0; i < H; i++) xd[i] = (double)orc_bf16_to_f32(x[(size_t)m * H + i]);
-                if (c->fmt == 0) orc_i8_expert(xd, qg, sg, qu, su, qd, sd, H, I, h, ye);
-                else orc_nvfp4_expert(xd, fg, fsg, 0.01f, fu, fsu, 0.01f, fd, fsd, 0.01f, H, I, h, ye);
-                const double w = w64[m * K + k];
-                for (int i = 0; i < H; i++) y64[(size_t)m * H + i] += w * ye[i];
-            }
+        /* a row selects an expert at most once: the rows of one expert are
+           distinct, so the pairs of this expert run in parallel */
+        #pragma omp parallel for schedule(dynamic)
+        for (int mk = 0; mk < M * K; mk++) {
+            if (sel[mk] != e) continue;
+            const int m = mk / K;
+            double *xl = (double *)malloc(sizeof(double) * (size_t)H);
+            double *hl = (double *)malloc(sizeof(double) * (size_t)I);
+            double *yl = (double *)malloc(sizeof(double) * (size_t)H);
+            for (int i = 0; i < H; i++) xl[i] = (double)orc_bf16_to_f32(x[(size_t)m * H + i]);
+            if (c->fmt == 0) orc_i8_expert(xl, qg, sg, qu, su, qd, sd, H, I, hl, yl);
+            else orc_nvfp4_expert(xl, fg, fsg, 0.01f, fu, fsu, 0.01f, fd, fsd, 0.01f, H, I, hl, yl);
+            const double w = w64[mk];
+            for (int i = 0; i < H; i++) y64[(size_t)m * H + i] += w * yl[i];
+            free(xl); free(hl); free(yl);
+        }
     }
     /* shared expert (index E of the generator), always INT8 */
     gen_i8_expert(c, E, qg, sg, qu, su, qd, sd);
+    #pragma omp parallel for schedule(dynamic)
     for (int m = 0; m < M; m++) {
+        double *xl = (double *)malloc(sizeof(double) * (size_t)H);
+        double *hl = (double *)malloc(sizeof(double) * (size_t)I);
+        double *yl = (double *)malloc(sizeof(double) * (size_t)H);
         double gx = 0.0;
         for (int i = 0; i < H; i++) {
-            xd[i] = (double)orc_bf16_to_f32(x[(size_t)m * H + i]);
-            gx += (double)g[i] * xd[i];
+            xl[i] = (double)orc_bf16_to_f32(x[(size_t)m * H + i]);
+            gx += (double)g[i] * xl[i];
         }
-        orc_i8_expert(xd, qg, sg, qu, su, qd, sd, H, I, h, ye);
+        orc_i8_expert(xl, qg, sg, qu, su, qd, sd, H, I, hl, yl);
         const double gam = c->gated ? 1.0 / (1.0 + exp(-gx)) : 1.0;
-        for (int i = 0; i < H; i++) y64[(size_t)m * H + i] += gam * ye[i];
+        for (int i = 0; i < H; i++) y64[(size_t)m * H + i] += gam * yl[i];
+        free(xl); free(hl); free(yl);
     }
     if (ybf16)
         for (size_t i = 0; i < (size_t)M * H; i++) ybf16[i] = orc_bf16_rne((float)y64[i]);

@@ -202,10 +202,18 @@ void qf8_i8_down_m1(const Qf4ExpCache *c, const float *hidden, int8_t *h8q, floa
 }
 
 // ---- fused layer ---------------------------------------------------------------
-size_t qfm_workspace_bytes(int M) { return M < 1 ? 0 : ws_layout(M).total; }
+size_t qfm_workspace_bytes(int M) {
+    if (M < 1) return 0;
+    return M <= 8 ? ws_layout(M).total : prefill_ws_bytes(M);
+}
 
 int qfm_workspace_view(void *ws, int M, qfm_ws_view *v) {
     if (!ws || !v || M < 1) return -1;
+    if (M > 8) {
+        prefill_ws_view(ws, M, &v->logits, &v->sel, &v->wts);
+        v->hidden = nullptr;
+        return 0;
+    }
     const WsLayout w = ws_layout(M);
     char *b = static_cast<char *>(ws);
     v->logits = reinterpret_cast<float *>(b + w.logits);
@@ -233,8 +241,11 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
                         int mask, hipStream_t s) {
     if (!layer_ok(L) || !x || !y || !ws || M < 1) { set_error(-1, "qfm_moe_forward: bad arguments"); return -1; }
     if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) { set_error(-1, "qfm_moe_forward: workspace not 256-byte aligned"); return -1; }
+    if (ws_bytes < qfm_workspace_bytes(M)) {
+        set_error(-1, "qfm_moe_forward: workspace too small (%zu < %zu)", ws_bytes, qfm_workspace_bytes(M)); return -1;
+    }
+    if (M > 8) return launch_prefill(L, x, M, y, ws, g_cfg.gated, s);
     const WsLayout w = ws_layout(M);
-    if (ws_bytes < w.total) { set_error(-1, "qfm_moe_forward: workspace too small (%zu < %zu)", ws_bytes, w.total); return -1; }
     const Cfg &c = g_cfg;
     char *b = static_cast<char *>(ws);
     float *logits = reinterpret_cast<float *>(b + w.logits);
@@ -277,8 +288,7 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
                                          part, y, s);
         return rc;
     }
-    set_error(-2, "qfm_moe_forward: M=%d rows is not supported by this build", M);
-    return -2;
+    return launch_prefill(L, x, M, y, ws, c.gated, s);
 }
 
 int qfm_moe_forward_layers(const qfm_layer *layers, int nl, const uint16_t *x, long x_stride, int M, uint16_t *y,

@@ -58,4 +58,10 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
                        int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
                        float *part, uint16_t *y, hipStream_t s);
 
+// Prefill (T > 8 rows): MFMA router + exact candidate selection, grouped
+// MFMA gate/up and down over the routing inversion, owned-partial combine.
+size_t prefill_ws_bytes(int T);
+void prefill_ws_view(void *ws, int T, float **lg_approx, int **sel, float **wts);
+int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, void *ws, int gated, hipStream_t s);
+
 }  // namespace qfm

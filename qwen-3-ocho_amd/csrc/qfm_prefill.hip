@@ -1,0 +1,594 @@
+// qfm_prefill.hip -- prefill (T tokens, T large): MFMA grouped GEMMs.
+//
+// Reference behaviour: the chunk path qf8_i8_experts_chunk
+// (ocho/amd_server/qf8_moe_i8.hip:196-322, :372-395) and Spark's
+// qf_prefill_experts_csr / qf_prefill_experts_mma
+// (ocho/engine_spark/cuda/qf_prefill_moe.cu:129-265,
+// ocho/engine_spark/cuda/qf_prefill_mma.cu:513-563): tokens grouped by expert,
+// each expert's weights dotted against all of its tokens, owned partials per
+// (token, k) summed by a combine kernel. Here the shared expert is one more
+// group (every token, weight sigmoid(<g, x_t>)).
+//
+// Router (bit-exact selection at GEMM speed):
+//   k_pf_router_mfma   logits~ = x . bf16(W)^T (+ bias) on bf16 MFMA, plus
+//                      per-token ||x_t||_2; W rows' ||w_e||_2 come from
+//                      k_pf_router_prep. |logit~ - logit| <= B_te =
+//                      c * ||w_e|| ||x_t|| (Cauchy-Schwarz over the bf16
+//                      rounding of W, the MFMA accumulation and the canonical
+//                      fp32 order; constants below).
+//   k_pf_select        one wave per token: tau = K-th largest (logit~ - B),
+//                      candidates = {e : logit~ + B >= tau} (a superset of the
+//                      exact top-K, ties included), their logits recomputed in
+//                      the canonical order, then the exact top-K among them;
+//                      also the exact shared-gate dot. Tokens whose candidate
+//                      set overflows recompute every logit.
+// Experts:
+//   k_pf_count / k_pf_plan / k_pf_scatter   routing inversion with atomics
+//                      (row order inside a group is unspecified: every GEMM
+//                      row is independent and partials are owned by (t, k),
+//                      so y does not depend on it) and the GEMM work lists.
+//   k_pf_gemm<GATEUP>  hidden[p][n] = silu(sg (x_p . Wg_n)) * (su (x_p . Wu_n))
+//   k_pf_gemm<DOWN>    part[slot_p][c] = w_p * sd_c * (h_p . Wd_c)
+//                      Both: BM=128 rows x BN=128 weight rows x BK=32, four
+//                      waves, v_mfma_f32_16x16x32_bf16; int8 weights are
+//                      staged to LDS as bf16 in offset-binary form
+//                      (u = q + 128 is exact in bf16) and the row sum of A
+//                      times 128 is subtracted in the epilogue.
+//   k_pf_combine       y[t] = sum over the K+1 slots of t, in slot order.
+#include "qfm_dev.h"
+#include "qfm_internal.h"
+
+namespace qfm {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int LDS_STRIDE = BK + 8;           // bf16 elements per LDS row (80 bytes)
+constexpr int kCandMax = 64;
+
+// bf16 bits of an exactly representable value (integers |v| <= 256): truncation is exact
+__device__ __forceinline__ uint32_t pack_bf16_exact(float lo, float hi) {
+    return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+}
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// 16 int8 codes -> 16 bf16 in offset-binary form (q + 128, exact)
+__device__ __forceinline__ void i8_to_bf16_ob(uint4 w, uint4 &o0, uint4 &o1) {
+    const uint32_t d[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
+    uint32_t o[8];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        o[2 * q] = pack_bf16_exact((float)(d[q] & 0xFFu), (float)((d[q] >> 8) & 0xFFu));
+        o[2 * q + 1] = pack_bf16_exact((float)((d[q] >> 16) & 0xFFu), (float)(d[q] >> 24));
+    }
+    o0 = make_uint4(o[0], o[1], o[2], o[3]);
+    o1 = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+// ---- router prep: ||w_e||_2 (fp64 accumulate, rounded up) --------------------------
+__global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict__ W, int E, int H,
+                                                         float *__restrict__ wnorm) {
+    const int e = blockIdx.x;
+    double s = 0.0;
+    for (int k = threadIdx.x; k < H; k += 256) {
+        const double v = (double)W[(size_t)e * H + k];
+        s += v * v;
+    }
+    __shared__ double red[256];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int m = 128; m >= 1; m >>= 1) {
+        if ((int)threadIdx.x < m) red[threadIdx.x] += red[threadIdx.x + m];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) wnorm[e] = (float)(sqrt(red[0]) * (1.0 + 1e-6));
+}
+
+// ---- the MFMA tile engine ---------------------------------------------------------
+// A rows: bf16, row r of the tile at A + arow[r] * lda (arow < 0: row absent,
+// staged as zeros). B rows: int8 (offset-binary) or fp32 (rounded to bf16),
+// row n at (n < nsplit ? B0 : B1) + brow[n] * ldb. K % BK == 0. acc[mb][nb]
+// over the tile: wave w covers rows [32w, 32w + 32), all BN columns.
+template <bool B_I8>
+struct TileEngine {
+    __device__ static void run(const uint16_t *__restrict__ A, long lda, const int *arow, const void *B0,
+                               const void *B1, int nsplit, long ldb, const int *brow, int K,
+                               uint16_t (*lds)[2][BM * LDS_STRIDE], f32x4_t (&acc)[2][8], float *rowsum_out) {
+        const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+        const int sr = t >> 1, sh = (t & 1) * 16;           // staging: row, first k of this thread's half
+        const int ar = arow[sr];
+        const uint16_t *ap = A + (ar >= 0 ? (long)ar * lda : 0) + sh;
+        const int br = brow[sr];
+        const void *B = sr < nsplit ? B0 : B1;
+        float rsum = 0.0f;
+        uint4 a0, a1, b0, b1, b2, b3;
+        auto gload = [&](int k0) {
+            if (ar >= 0) {
+                a0 = *reinterpret_cast<const uint4 *>(ap + k0);
+                a1 = *reinterpret_cast<const uint4 *>(ap + k0 + 8);
+            } else {
+                a0 = a1 = make_uint4(0, 0, 0, 0);
+            }
+            if constexpr (B_I8) {
+                b0 = ld_nt16(reinterpret_cast<const int8_t *>(B) + (long)br * ldb + k0 + sh);
+            } else {
+                const float *bp = reinterpret_cast<const float *>(B) + (long)br * ldb + k0 + sh;
+                b0 = *reinterpret_cast<const uint4 *>(bp);
+                b1 = *reinterpret_cast<const uint4 *>(bp + 4);
+                b2 = *reinterpret_cast<const uint4 *>(bp + 8);
+                b3 = *reinterpret_cast<const uint4 *>(bp + 12);
+            }
+        };
+        auto sstore = [&](int buf) {
+            uint4 *la = reinterpret_cast<uint4 *>(&lds[0][buf][sr * LDS_STRIDE + sh]);
+            la[0] = a0; la[1] = a1;
+            if (rowsum_out) {
+                const uint32_t d[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+                for (int q = 0; q < 8; q++) rsum += bf16_lo(d[q]) + bf16_hi(d[q]);
+            }
+            uint4 o0, o1;
+            if constexpr (B_I8) {
+                i8_to_bf16_ob(b0, o0, o1);
+            } else {
+                const uint32_t f[16] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w,
+                                        b2.x, b2.y, b2.z, b2.w, b3.x, b3.y, b3.z, b3.w};
+                uint32_t o[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) o[q] = pack_bf16_rne(__uint_as_float(f[2 * q]), __uint_as_float(f[2 * q + 1]));
+                o0 = make_uint4(o[0], o[1], o[2], o[3]);
+                o1 = make_uint4(o[4], o[5], o[6], o[7]);
+            }
+            uint4 *lb = reinterpret_cast<uint4 *>(&lds[1][buf][sr * LDS_STRIDE + sh]);
+            lb[0] = o0; lb[1] = o1;
+        };
+#pragma unroll
+        for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+            for (int nb = 0; nb < 8; nb++) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        const int nk = K / BK;
+        gload(0);
+        sstore(0);
+        __syncthreads();
+        const int lr = lane & 15, lk = (lane >> 4) * 8;
+        for (int s = 0; s < nk; s++) {
+            const int buf = s & 1;
+            if (s + 1 < nk) gload((s + 1) * BK);
+            bf16x8_t av[2];
+#pragma unroll
+            for (int mb = 0; mb < 2; mb++)
+                av[mb] = *reinterpret_cast<const bf16x8_t *>(&lds[0][buf][(wave * 32 + mb * 16 + lr) * LDS_STRIDE + lk]);
+#pragma unroll
+            for (int nb = 0; nb < 8; nb++) {
+                const bf16x8_t bv = *reinterpret_cast<const bf16x8_t *>(&lds[1][buf][(nb * 16 + lr) * LDS_STRIDE + lk]);
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mb], bv, acc[mb][nb], 0, 0, 0);
+            }
+            if (s + 1 < nk) sstore(buf ^ 1);
+            __syncthreads();
+        }
+        if (rowsum_out) {
+            rsum += __shfl_xor(rsum, 1, WAVE);
+            if ((t & 1) == 0) rowsum_out[sr] = rsum;
+        }
+    }
+};
+
+// ---- router GEMM: logits~ [T][E] --------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const float *__restrict__ W, int E,
+                 const float *__restrict__ bias, float *__restrict__ lg_approx, float *__restrict__ xnorm) {
+    __shared__ __align__(16) uint16_t lds[2][2][BM * LDS_STRIDE];
+    __shared__ int arow[BM], brow[BN];
+    const int t0 = blockIdx.x * BM, e0 = blockIdx.y * BN;
+    if (threadIdx.x < BM) arow[threadIdx.x] = (t0 + (int)threadIdx.x < T) ? t0 + (int)threadIdx.x : -1;
+    if (threadIdx.x < BN) brow[threadIdx.x] = e0 + (int)threadIdx.x;
+    __syncthreads();
+    f32x4_t acc[2][8];
+    TileEngine<false>::run(x, H, arow, W, W, BN, H, brow, H, lds, acc, nullptr);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+        for (int nb = 0; nb < 8; nb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = wave * 32 + mb * 16 + (lane >> 4) * 4 + i, c = nb * 16 + (lane & 15);
+                if (t0 + r < T) {
+                    float v = acc[mb][nb][i];
+                    if (bias) v += bias[e0 + c];
+                    lg_approx[(size_t)(t0 + r) * E + e0 + c] = v;
+                }
+            }
+    // ||x_t||_2 of this block's tokens (first column block only)
+    if (blockIdx.y == 0 && threadIdx.x < BM && t0 + (int)threadIdx.x < T) {
+        const uint16_t *xr = x + (size_t)(t0 + threadIdx.x) * H;
+        double s = 0.0;
+        for (int k = 0; k < H; k += 8) {
+            const uint4 p = *reinterpret_cast<const uint4 *>(xr + k);
+            const uint32_t d[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const double a = bf16_lo(d[q]), b = bf16_hi(d[q]);
+                s += a * a + b * b;
+            }
+        }
+        xnorm[t0 + threadIdx.x] = (float)(sqrt(s) * (1.0 + 1e-6));
+    }
+}
+
+// canonical-order dot of one router row with one token, computed by a full wave
+template <int NJ>
+__device__ __forceinline__ float canon_dot_wave(const float *__restrict__ w, const uint16_t *__restrict__ x, int lane) {
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const float4 wv = *reinterpret_cast<const float4 *>(w + j * 256 + lane * 4);
+        const uint2 p = *reinterpret_cast<const uint2 *>(x + j * 256 + lane * 4);
+        a = __fmaf_rn(wv.x, bf16_lo(p.x), a);
+        a = __fmaf_rn(wv.y, bf16_hi(p.x), a);
+        a = __fmaf_rn(wv.z, bf16_lo(p.y), a);
+        a = __fmaf_rn(wv.w, bf16_hi(p.y), a);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) a = __fadd_rn(a, __shfl_xor(a, m, WAVE));
+    return a;
+}
+
+// Error-bound constant per unit of ||w_e|| ||x_t||: bf16 rounding of W
+// (2^-9), MFMA fp32 accumulation over H products (<= 2 H ulps, any order),
+// canonical order (H/64 + 6 roundings), with a factor-2 margin.
+__device__ __forceinline__ float bound_coeff(int H) {
+    return 2.0f * (0x1p-9f + (float)(2 * H) * 0x1p-24f + (float)(H / 64 + 8) * 0x1p-24f);
+}
+
+// one wave per token: candidates, exact logits, exact top-K, shared gate
+template <int NJ, int EPL>
+__global__ void __launch_bounds__(256)
+k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, const float *__restrict__ bias,
+            const float *__restrict__ g, const float *__restrict__ lg_approx, const float *__restrict__ xnorm,
+            const float *__restrict__ wnorm, int K, int renorm, int *__restrict__ sel, float *__restrict__ wts,
+            float *__restrict__ gam, int *__restrict__ n_fallback) {
+    constexpr int H = NJ * 256, E = EPL * 64;
+    __shared__ int s_cand[4][kCandMax];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + wave;
+    if (t >= T) return;
+    const uint16_t *xt = x + (size_t)t * H;
+    const float cB = bound_coeff(H) * xnorm[t];
+    float lo[EPL], hi[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int e = i * 64 + lane;
+        const float l = lg_approx[(size_t)t * E + e];
+        const float b = cB * wnorm[e] + 1e-6f * (fabsf(l) + (bias ? fabsf(bias[e]) : 0.0f) + 1.0f);
+        lo[i] = l - b;
+        hi[i] = l + b;
+    }
+    // tau = K-th largest lower bound: rank counting over the E values
+    float tau;
+    {
+        // K-th largest of lo[] by repeated wave max (K <= 16, values need not be distinct)
+        unsigned long long kk[EPL];
+#pragma unroll
+        for (int i = 0; i < EPL; i++) kk[i] = topk_key(lo[i], i * 64 + lane);
+        unsigned long long b = 0;
+        for (int k = 0; k < K; k++) {
+            b = 0;
+#pragma unroll
+            for (int i = 0; i < EPL; i++) b = kk[i] > b ? kk[i] : b;
+            b = __ockl_wfred_max_u64(b);
+#pragma unroll
+            for (int i = 0; i < EPL; i++) kk[i] = kk[i] == b ? 0ull : kk[i];
+        }
+        tau = topk_key_value(b);
+    }
+    // candidates: hi >= tau
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < EPL; i++) cnt += hi[i] >= tau ? 1 : 0;
+    const unsigned long long ltm = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int off = 0, total = 0;
+#pragma unroll
+    for (int bt = 0; bt < 5; bt++) {
+        const unsigned long long bb = __ballot((cnt >> bt) & 1);
+        off += __popcll(bb & ltm) << bt;
+        total += __popcll(bb) << bt;
+    }
+    const bool full = total > kCandMax;
+    if (!full) {
+#pragma unroll
+        for (int i = 0; i < EPL; i++)
+            if (hi[i] >= tau) s_cand[wave][off++] = i * 64 + lane;
+    } else if (lane == 0) {
+        atomicAdd(n_fallback, 1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const int nc = full ? E : total;
+    // exact logits of the candidates (all E on overflow) -> 64-bit keys; lane k < K
+    // keeps the k-th best key so far (descending), maintained by insertion
+    unsigned long long best = 0;
+    for (int c = 0; c < nc; c++) {
+        const int e = full ? c : s_cand[wave][c];
+        float l = canon_dot_wave<NJ>(W + (size_t)e * H, xt, lane);
+        if (bias) l = __fadd_rn(l, bias[e]);
+        const unsigned long long key = topk_key(l, e);
+        // insert into the sorted lane list: lanes with a smaller key shift down
+        const unsigned long long prev = __shfl_up(best, 1, WAVE);
+        const bool ge_prev = lane == 0 || prev > key;
+        if (lane < K && best < key) best = ge_prev ? key : prev;
+    }
+    const float mx = topk_key_value(__shfl(best, 0, WAVE));
+    const float ek = lane < K ? __expf(topk_key_value(best) - mx) : 0.0f;
+    float denom = __ockl_wfred_add_f32(ek);
+    if (!renorm) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < EPL; i++) s += __expf(lg_approx[(size_t)t * E + i * 64 + lane] - mx);
+        denom = __ockl_wfred_add_f32(s);
+    }
+    if (lane < K) {
+        sel[(size_t)t * K + lane] = topk_key_index(best);
+        wts[(size_t)t * K + lane] = ek / denom;
+    }
+    if (g) {
+        const float gd = canon_dot_wave<NJ>(g, xt, lane);
+        if (lane == 0) gam[t] = sigmoid(gd);
+    }
+}
+
+// ---- routing inversion --------------------------------------------------------------
+__global__ void k_pf_count(const int *__restrict__ sel, int TK, int *__restrict__ cnt) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < TK) atomicAdd(&cnt[sel[i]], 1);
+}
+
+// One block: group offsets (groups 0..E-1 routed, E = shared with T rows when
+// has_sh), fill counters reset, GEMM work lists: item = (group, row0, rows,
+// n-tile) for every 128-row m-tile of every group, n-tiles fastest.
+__global__ void __launch_bounds__(1024)
+k_pf_plan(int *__restrict__ cnt, int E, int has_sh, int T, int nt_gu, int nt_dn, int *__restrict__ off,
+          int *__restrict__ fill, int4 *__restrict__ items_gu, int4 *__restrict__ items_dn, int *__restrict__ n_items,
+          int max_gu, int max_dn) {
+    __shared__ int s_mt[1024 + 1], s_cnt[1024];
+    const int G = E + (has_sh ? 1 : 0);
+    const int g = threadIdx.x;
+    int c = 0;
+    if (g < E) c = cnt[g];
+    else if (g == E && has_sh) c = T;
+    s_cnt[g] = c;
+    s_mt[g] = (c + BM - 1) / BM;
+    __syncthreads();
+    if (g == 0) {
+        int o = 0, m = 0;
+        for (int q = 0; q < G; q++) {
+            off[q] = o; o += s_cnt[q];
+            const int mt = s_mt[q];
+            s_mt[q] = m; m += mt;
+        }
+        off[G] = o;
+        s_mt[G] = m;
+        n_items[0] = m * nt_gu;
+        n_items[1] = m * nt_dn;
+    }
+    __syncthreads();
+    if (g < G) {
+        fill[g] = 0;
+        const int m0 = s_mt[g], nmt = (s_cnt[g] + BM - 1) / BM;
+        for (int mt = 0; mt < nmt; mt++) {
+            const int rows = min(BM, s_cnt[g] - mt * BM);
+            for (int n = 0; n < nt_gu; n++) {
+                const int it = (m0 + mt) * nt_gu + n;
+                if (it < max_gu) items_gu[it] = make_int4(g, mt * BM, rows, n);
+            }
+            for (int n = 0; n < nt_dn; n++) {
+                const int it = (m0 + mt) * nt_dn + n;
+                if (it < max_dn) items_dn[it] = make_int4(g, mt * BM, rows, n);
+            }
+        }
+    }
+}
+
+// pair -> group position; routed pairs by atomic fill, shared pairs in token order
+__global__ void k_pf_scatter(const int *__restrict__ sel, const float *__restrict__ wts, const float *__restrict__ gam,
+                             int T, int K, int E, int has_sh, const int *__restrict__ off, int *__restrict__ fill,
+                             int *__restrict__ p_tok, int *__restrict__ p_slot, float *__restrict__ p_wt) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int S = K + has_sh;
+    if (i < T * K) {
+        const int e = sel[i], t = i / K, k = i - t * K;
+        const int pos = off[e] + atomicAdd(&fill[e], 1);
+        p_tok[pos] = t; p_slot[pos] = t * S + k; p_wt[pos] = wts[i];
+    } else if (has_sh && i < T * K + T) {
+        const int t = i - T * K, pos = off[E] + t;
+        p_tok[pos] = t; p_slot[pos] = t * S + K; p_wt[pos] = gam ? gam[t] : 1.0f;
+    }
+}
+
+// ---- grouped expert GEMMs -------------------------------------------------------------
+struct GroupW {
+    const int8_t *w;      // routed arena blob, [E][rows][K]
+    const float *s;       // routed row scales [E][rows]
+    const int8_t *w_sh;   // shared expert [rows][K]
+    const float *s_sh;    // shared row scales [rows]
+};
+
+template <bool GATEUP>
+__global__ void __launch_bounds__(256)
+k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int which, const int *__restrict__ off,
+          const int *__restrict__ p_tok, const int *__restrict__ p_slot, const float *__restrict__ p_wt,
+          const uint16_t *__restrict__ A, int Kdim, int Nrows, GroupW g0, GroupW g1, int E,
+          uint16_t *__restrict__ hid, float *__restrict__ part, int Hout) {
+    __shared__ __align__(16) uint16_t lds[2][2][BM * LDS_STRIDE];
+    __shared__ int arow[BM], brow[BN];
+    __shared__ float rsum[BM];
+    if ((int)blockIdx.x >= n_items[which]) return;
+    const int4 it = items[blockIdx.x];
+    const int grp = it.x, r0 = it.y, rows = it.z, nt = it.w;
+    const int pbase = off[grp] + r0;
+    const int8_t *Wb;
+    const float *Sb;
+    long ldb = Kdim;
+    if (grp < E) { Wb = g0.w + (size_t)grp * Nrows * Kdim; Sb = g0.s + (size_t)grp * Nrows; }
+    else { Wb = g0.w_sh; Sb = g0.s_sh; }
+    const int8_t *Wb2 = nullptr;
+    const float *Sb2 = nullptr;
+    if (GATEUP) {
+        if (grp < E) { Wb2 = g1.w + (size_t)grp * Nrows * Kdim; Sb2 = g1.s + (size_t)grp * Nrows; }
+        else { Wb2 = g1.w_sh; Sb2 = g1.s_sh; }
+    }
+    if (threadIdx.x < BM) {
+        const int r = threadIdx.x;
+        if (GATEUP) arow[r] = r < rows ? p_tok[pbase + r] : -1;
+        else arow[r] = r < rows ? pbase + r : -1;
+    }
+    if (threadIdx.x < BN) {
+        const int n = threadIdx.x;
+        // gate/up: rows 0..63 = gate rows [64 nt, +64), rows 64..127 = the same up rows
+        brow[n] = GATEUP ? (nt * 64 + (n & 63)) : (nt * BN + n);
+    }
+    __syncthreads();
+    f32x4_t acc[2][8];
+    TileEngine<true>::run(A, Kdim, arow, Wb, GATEUP ? (const void *)Wb2 : (const void *)Wb, GATEUP ? 64 : BN, ldb,
+                          brow, Kdim, lds, acc, rsum);
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (GATEUP) {
+#pragma unroll
+        for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = wave * 32 + mb * 16 + (lane >> 4) * 4 + i, n = nt * 64 + nb * 16 + (lane & 15);
+                    if (r < rows) {
+                        const float cr = 128.0f * rsum[r];
+                        const float gv = (acc[mb][nb][i] - cr) * Sb[n];
+                        const float uv = (acc[mb][nb + 4][i] - cr) * Sb2[n];
+                        hid[(size_t)(pbase + r) * Nrows + n] = f32_to_bf16(silu(gv) * uv);
+                    }
+                }
+    } else {
+#pragma unroll
+        for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+            for (int nb = 0; nb < 8; nb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = wave * 32 + mb * 16 + (lane >> 4) * 4 + i, c = nt * BN + nb * 16 + (lane & 15);
+                    if (r < rows) {
+                        const int p = pbase + r;
+                        const float v = (acc[mb][nb][i] - 128.0f * rsum[r]) * Sb[c];
+                        part[(size_t)p_slot[p] * Hout + c] = p_wt[p] * v;
+                    }
+                }
+    }
+}
+
+__global__ void __launch_bounds__(256)
+k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__restrict__ y) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)T * H) return;
+    const size_t t = i / H, c = i - t * H;
+    float a = 0.0f;
+    for (int k = 0; k < S; k++) a += part[(t * S + k) * H + c];
+    y[i] = f32_to_bf16(a);
+}
+
+// ---- launcher -------------------------------------------------------------------------
+size_t prefill_ws_bytes(int T) {
+    const Cfg &c = g_cfg;
+    const size_t P = (size_t)T * (c.K + 1);
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    size_t b = 0;
+    b += al((size_t)T * c.E * 4);          // lg_approx
+    b += al((size_t)T * 4) + al((size_t)c.E * 4);   // xnorm, wnorm
+    b += al((size_t)T * c.K * 4) * 2;      // sel, wts
+    b += al((size_t)T * 4);                // gam
+    b += al(4 * 8);                        // counters
+    b += al((size_t)(c.E + 2) * 4) * 3;    // cnt, off, fill
+    const size_t max_mt = P / BM + c.E + 2;
+    b += al(max_mt * (c.I / 64) * 16) + al(max_mt * (c.H / BN) * 16);   // item lists
+    b += al(P * 4) * 3;                    // p_tok, p_slot, p_wt
+    b += al(P * c.I * 2);                  // hidden bf16
+    b += al(P * c.H * 4);                  // partials
+    return b;
+}
+
+void prefill_ws_view(void *ws, int T, float **lg, int **sel, float **wts) {
+    const Cfg &c = g_cfg;
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    char *b = static_cast<char *>(ws);
+    *lg = reinterpret_cast<float *>(b); b += al((size_t)T * c.E * 4);
+    b += al((size_t)T * 4);
+    b += al((size_t)c.E * 4);
+    *sel = reinterpret_cast<int *>(b); b += al((size_t)T * c.K * 4);
+    *wts = reinterpret_cast<float *>(b);
+}
+
+int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, void *ws, int gated, hipStream_t s) {
+    const Cfg &c = g_cfg;
+    if (L->fmt != QFM_FMT_INT8) { set_error(-2, "prefill: INT8 routed experts only"); return -2; }
+    if (c.E != 512 || !(shape_2048() || shape_2560())) { set_error(-2, "prefill: unsupported shape"); return -2; }
+    const int E = c.E, K = c.K, H = c.H, I = c.I;
+    const bool has_sh = L->sh_gate.w != nullptr;
+    const int S = K + (has_sh ? 1 : 0);      // partial slots per token: K routed (+ shared)
+    const size_t P = (size_t)T * S;
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    char *b = static_cast<char *>(ws);
+    float *lg = reinterpret_cast<float *>(b); b += al((size_t)T * E * 4);
+    float *xnorm = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
+    float *wnorm = reinterpret_cast<float *>(b); b += al((size_t)E * 4);
+    int *sel = reinterpret_cast<int *>(b); b += al((size_t)T * K * 4);
+    float *wts = reinterpret_cast<float *>(b); b += al((size_t)T * K * 4);
+    float *gam = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
+    int *ctr = reinterpret_cast<int *>(b); b += al(4 * 8);
+    int *cnt = reinterpret_cast<int *>(b); b += al((size_t)(E + 2) * 4);
+    int *off = reinterpret_cast<int *>(b); b += al((size_t)(E + 2) * 4);
+    int *fill = reinterpret_cast<int *>(b); b += al((size_t)(E + 2) * 4);
+    const size_t max_mt = P / BM + E + 2;
+    const int nt_gu = I / 64, nt_dn = H / BN;
+    int4 *items_gu = reinterpret_cast<int4 *>(b); b += al(max_mt * nt_gu * 16);
+    int4 *items_dn = reinterpret_cast<int4 *>(b); b += al(max_mt * nt_dn * 16);
+    int *p_tok = reinterpret_cast<int *>(b); b += al(P * 4);
+    int *p_slot = reinterpret_cast<int *>(b); b += al(P * 4);
+    float *p_wt = reinterpret_cast<float *>(b); b += al(P * 4);
+    uint16_t *hid = reinterpret_cast<uint16_t *>(b); b += al(P * I * 2);
+    float *part = reinterpret_cast<float *>(b);
+
+    const float *g = (has_sh && gated) ? L->sh_gate_inp : nullptr;
+    // zero the small counters with a fill kernel (no memset node in captured graphs)
+    launch_fill_f32(reinterpret_cast<float *>(ctr), 8, 0.0f, s);
+    launch_fill_f32(reinterpret_cast<float *>(cnt), (uint64_t)(E + 2), 0.0f, s);
+    hipLaunchKernelGGL(k_pf_router_prep, dim3(E), dim3(256), 0, s, L->router, E, H, wnorm);
+    hipLaunchKernelGGL(k_pf_router_mfma, dim3((T + BM - 1) / BM, E / BN), dim3(256), 0, s, x, T, H, L->router, E,
+                       L->router_bias, lg, xnorm);
+    if (H == 2048)
+        hipLaunchKernelGGL((k_pf_select<8, 8>), dim3((T + 3) / 4), dim3(256), 0, s, x, T, L->router, L->router_bias,
+                           g, lg, xnorm, wnorm, K, c.renorm, sel, wts, gam, ctr);
+    else
+        hipLaunchKernelGGL((k_pf_select<10, 8>), dim3((T + 3) / 4), dim3(256), 0, s, x, T, L->router, L->router_bias,
+                           g, lg, xnorm, wnorm, K, c.renorm, sel, wts, gam, ctr);
+    hipLaunchKernelGGL(k_pf_count, dim3((T * K + 255) / 256), dim3(256), 0, s, sel, T * K, cnt);
+    hipLaunchKernelGGL(k_pf_plan, dim3(1), dim3(1024), 0, s, cnt, E, has_sh ? 1 : 0, T, nt_gu, nt_dn, off, fill,
+                       items_gu, items_dn, ctr + 1, (int)(max_mt * nt_gu), (int)(max_mt * nt_dn));
+    hipLaunchKernelGGL(k_pf_scatter, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, s, sel, wts, g ? gam : nullptr,
+                       T, K, E, has_sh ? 1 : 0, off, fill, p_tok, p_slot, p_wt);
+    const Qf4ExpCache *a = L->arena;
+    if (!a->i8_gate || !a->i8_up || !a->i8_down) { set_error(-1, "prefill: arena has no INT8 blobs"); return -1; }
+    GroupW gg{a->i8_gate, a->i8s_gate, L->sh_gate.w, L->sh_gate.s};
+    GroupW gu{a->i8_up, a->i8s_up, L->sh_up.w, L->sh_up.s};
+    GroupW gd{a->i8_down, a->i8s_down, L->sh_down.w, L->sh_down.s};
+    hipLaunchKernelGGL((k_pf_gemm<true>), dim3((unsigned)(max_mt * nt_gu)), dim3(256), 0, s, items_gu, ctr + 1, 0, off,
+                       p_tok, p_slot, p_wt, x, H, I, gg, gu, E, hid, part, H);
+    hipLaunchKernelGGL((k_pf_gemm<false>), dim3((unsigned)(max_mt * nt_dn)), dim3(256), 0, s, items_dn, ctr + 1, 1, off,
+                       p_tok, p_slot, p_wt, hid, I, H, gd, gd, E, hid, part, H);
+    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)(((size_t)T * H + 255) / 256)), dim3(256), 0, s, part, T, S, H, y);
+    return check_launch("prefill");
+}
+
+}  // namespace qfm

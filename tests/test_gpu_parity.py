@@ -259,3 +259,58 @@ def test_moe_layer_deterministic(lib):
     a = _run_layer(lib, 8, 5, 1, x_layer=3)
     b = _run_layer(lib, 8, 5, 1, x_layer=3)
     assert np.array_equal(a["y"].view(np.uint32), b["y"].view(np.uint32))
+
+
+# ------------------------------------------------------------------ prefill
+def _run_prefill(lib, T, seed, layer, x_layer, bias=True):
+    st = qfm.Stream()
+    L = qfm.SynthLayer(qfm.QFM_FMT_INT8, seed, layer, with_bias=bias, stream=st)
+    H = 2048
+    dx, dy = qfm.DevBuf(T * H * 2), qfm.DevBuf(T * H * 2)
+    qfm.check(lib.qfm_gen_input_rows(dx.ptr, T, seed, x_layer, 0, st.h), "x")
+    wsb = lib.qfm_workspace_bytes(T)
+    ws = qfm.DevBuf(wsb)
+    qfm.check(lib.qfm_moe_forward(C.byref(L.s.layer), dx.ptr, T, dy.ptr, ws.ptr, wsb, st.h), "forward")
+    st.sync()
+    view = qfm.QfmWsView()
+    lib.qfm_workspace_view(ws.ptr, T, C.byref(view))
+    out = dict(y=orc.bf16_to_f32(dy.download(np.uint16, (T, H))), sel=qfm.d2h(view.sel, np.int32, (T, 10)),
+               wts=qfm.d2h(view.wts, np.float32, (T, 10)), x=dx.download(np.uint16, (T, H)))
+    L.destroy()
+    st.destroy()
+    return out
+
+
+@pytest.mark.parametrize("T,bias", [(37, True), (300, True), (129, False)])
+def test_prefill_small(lib, T, bias):
+    """Prefill path (T > 8): MFMA router + exact candidate selection, grouped GEMMs."""
+    _say("prefill", T, bias)
+    _cfg(lib)
+    g = _run_prefill(lib, T, 1, 2, 600 + T, bias)
+    r = orc.moe_layer(2048, 512, 512, 10, T, 1, 2, 600 + T, use_bias=int(bias))
+    assert np.array_equal(g["x"], r["x"])
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    rel = max(_rel(g["y"][m], r["y"][m]) for m in range(T))
+    _say("  max rel err", rel)
+    assert rel <= TOL
+
+
+def test_prefill_config4_routing_and_sample(lib):
+    """BASELINE config 4 shape: T=8038, skewed router bias. Routing is checked for
+    every token (bit-exact); outputs on two 32-token windows (oracle cost)."""
+    T, seed, layer, xl = 8038, 0, 3, 700
+    _say("prefill config4", T)
+    _cfg(lib)
+    g = _run_prefill(lib, T, seed, layer, xl, True)
+    E, H = 512, 2048
+    W = orc.fill("gauss", seed, layer, orc.T_ROUTER, 0, E * H, 0.02).reshape(E, H)
+    b = orc.fill("gauss", seed, layer, orc.T_BIAS, 0, E, 1.5)
+    sel, w64, _ = orc.topk(orc.router_logits(W, g["x"], b), 10)
+    assert np.array_equal(g["sel"], sel)
+    assert np.allclose(g["wts"], w64, rtol=2e-6, atol=1e-7)
+    for row0 in (0, 5000):
+        r = orc.moe_layer(2048, 512, 512, 10, 32, seed, layer, xl, x_row0=row0, use_bias=1)
+        rel = max(_rel(g["y"][row0 + m], r["y"][m]) for m in range(32))
+        _say("  rows", row0, "max rel err", rel)
+        assert rel <= TOL
