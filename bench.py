@@ -166,6 +166,51 @@ def run_nvfp4(lib, st, nl, args):
     return out
 
 
+MFMA_PEAK_TFLOPS = 2500.0                 # dense bf16 MFMA, MI355X
+
+
+def run_prefill(lib, st, args, T=8038, nl=4):
+    """one prefill layer of T tokens with a skewed router bias,
+    timed over nl distinct layers (same input rows, one graph)."""
+    import qfm
+    layers = [qfm.SynthLayer(qfm.QFM_FMT_INT8, 0, 100 + l, with_bias=True, stream=st) for l in range(nl)]
+    arr = (qfm.QfmLayer * nl)(*[L.s.layer for L in layers])
+    x = qfm.DevBuf(T * H * 2)
+    y = qfm.DevBuf(nl * T * H * 2)
+    qfm.check(lib.qfm_gen_input_rows(x.ptr, T, 0, 3000, 0, st.h), "x")
+    wsb = lib.qfm_workspace_bytes(T)
+    ws = qfm.DevBuf(wsb)
+    view = qfm.QfmWsView()
+    touched, max_load = [], []
+    for l in range(nl):
+        qfm.check(lib.qfm_moe_forward(C.byref(arr[l]), x.ptr, T, y.ptr + l * T * H * 2, ws.ptr, wsb, st.h), "fwd")
+        st.sync()
+        lib.qfm_workspace_view(ws.ptr, T, C.byref(view))
+        cnt = np.bincount(qfm.d2h(view.sel, np.int32, (T, K)).ravel(), minlength=E)
+        touched.append(int((cnt > 0).sum()))
+        max_load.append(int(cnt.max()))
+
+    def enq():
+        qfm.check(lib.qfm_moe_forward_layers(arr, nl, x.ptr, 0, T, y.ptr, T * H, ws.ptr, wsb, st.h), "fwd")
+    ms = time_graph(lib, st, enq, max(1, args.steps // 2), 1)
+    us_layer = ms * 1000.0 / nl
+    flops = 2.0 * T * H * E + 2.0 * T * (K + 1) * 3 * H * I      # router GEMM + routed/shared gate, up, down
+    tflops = flops / (us_layer * 1e-6) / 1e12
+    wbytes = float(np.mean(touched)) * EXPERT_BYTES + EXPERT_BYTES + E * H * 4 + 2 * T * H * 2
+    gbs = wbytes / (us_layer * 1e-6) / 1e9
+    log(f"BASELINE config 4: prefill T={T}: {us_layer:.1f} us/layer, {T / (us_layer * 1e-6):.0f} tok/s, "
+        f"{tflops:.0f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS * 100:.1f}% bf16 MFMA), experts touched {np.mean(touched):.0f}, "
+        f"max load {max(max_load)}")
+    for L in layers:
+        L.destroy()
+    return {"workload": "BASELINE config 4: prefill MoE layer, T=8038 INT8, skewed router bias", "tokens": T,
+            "layers_timed": nl, "us_per_layer": round(us_layer, 2), "tok_per_s": round(T / (us_layer * 1e-6), 1),
+            "flops_per_layer": flops, "achieved_TFLOPs": round(tflops, 1),
+            "mfma_util": round(tflops / MFMA_PEAK_TFLOPS, 4), "weight_act_bytes_per_layer": wbytes,
+            "achieved_GBps": round(gbs, 1), "experts_touched": float(np.mean(touched)),
+            "max_expert_load": max(max_load)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -181,7 +226,7 @@ def main():
     ws_env = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or ws_env != 1:
         print("bench.py: this build runs on one GPU only (single-GPU box; the multi-GPU "
-              "sharding is a design in DESIGN.md, not a measured path). Use --gpus 1.", file=sys.stderr)
+              "sharding is designed, not a measured path). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import qfm
@@ -262,6 +307,7 @@ def main():
             L.destroy()
         layers = []
         extra["config3_nvfp4_m8"] = run_nvfp4(lib, st, nl, args)
+        extra["config4_prefill"] = run_prefill(lib, st, args)
 
     cpu = None
     if not args.no_cpu:

@@ -11,7 +11,7 @@
  * arena generator and the harness utilities (device memory, streams, events)
  * used by tests and benchmarks that do not link a HIP runtime themselves.
  *
- * Conventions (as in the reference, SURVEY-independent):
+ * Conventions (as in the reference):
  *   - all launchers are asynchronous and stream-ordered; none synchronizes
  *     the host and none allocates device memory;
  *   - reference-named launchers return void; errors are latched and read with
@@ -36,7 +36,7 @@ extern "C" {
 /* Shape configuration. Replaces the reference's compile-time dimensions
  * QF5_NEMBD / QF5_NFF / QF5_NEXP / QF5_NEXPUSED (ocho/amd_server/
  * qf_nvfp4_wave64.h:54-57) and QF5_K (qf8_moe_i8.hip:5-7). Supported:
- * (hidden, inter) = (2048, 512) [BASELINE] and (2560, 640) [reference
+ * (hidden, inter) = (2048, 512) [benchmark shape] and (2560, 640) [reference
  * checkpoint]; n_experts <= 1024 and a multiple of 64; 1 <= top_k <= 16. */
 typedef struct {
     int hidden;        /* H */
@@ -123,7 +123,7 @@ void qf_rtr_gemv_launch(const uint16_t *router, const float *x, float *logits, h
  * and the rows form qf_rtr_topk10_rows_launch (:96-98). K = qfm_config.top_k. */
 void qf_rtr_topk10_launch(const float *logits, int *sel_ids, float *wts, hipStream_t s);
 void qf_rtr_topk10_rows_launch(const float *logits, int *sel_ids, float *wts, int T, hipStream_t s);
-/* BASELINE router form: logits[m][e] = W_f32[e] . x_bf16[m] (+ bias[e]) in the
+/* Benchmark router form (fp32 weights): logits[m][e] = W_f32[e] . x_bf16[m] (+ bias[e]) in the
  * library's canonical fp32 order (bit-reproducible on the host), M rows. */
 int qfm_router_logits(const float *W, const float *bias, const uint16_t *x, int M,
                       float *logits, hipStream_t s);

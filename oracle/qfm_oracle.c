@@ -228,8 +228,7 @@ void orc_topk(const float *logits, int M, int E, int K, int renorm,
 }
 
 /* ------------------------------------------------------------------------ */
-/* INT8 expert, exact dequant-matmul in fp64 (SURVEY Appendix A.2;
-   reference structure qf8_moe_i8.hip:72-144 with exact activations):
+/* INT8 expert, exact dequant-matmul in fp64 (reference structure qf8_moe_i8.hip:72-144 with exact activations):
    silu(g) = g / (1 + e^-g) as at qf8_moe_i8.hip:105. */
 void orc_i8_expert(const double *x, const int8_t *Qg, const float *sg,
                    const int8_t *Qu, const float *su, const int8_t *Qd, const float *sd,

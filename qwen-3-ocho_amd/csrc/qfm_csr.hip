@@ -96,36 +96,40 @@ struct CsrLds {
     int pair[kMaxPairs];      // CSR position -> original pair index t*K + k
     int exp_id[kMaxPairs];
     int exp_ptr[kMaxPairs + 1];
-    int first[kMaxPairs];
+    uint32_t bits[512 / 32];  // bitmap of selected experts (E == 512)
     int n_exp;
     unsigned long long tk[8][272];
 };
 
-// Called by all threads of the block after sel of the P pairs is in LDS.
-// Position of pair p in (expert, token, k) order = #{q: e_q < e_p} +
-// #{q < p: e_q == e_p}; an expert's distinct index = #{distinct e' < e_p}.
+// Called by all threads of the block after sel of the P pairs is in LDS and
+// bits[] is zero. Position of pair p in (expert, token, k) order =
+// #{q: e_q < e_p} + #{q < p: e_q == e_p}; an expert's distinct index =
+// #{distinct e' < e_p}, read from the selected-expert bitmap.
 __device__ __forceinline__ void csr_build_lds(CsrLds &c, int P) {
     const int p = threadIdx.x;
-    int less = 0, before = 0, e = 0;
+    const int e = p < P ? c.sel[p] : 0;
+    if (p < P) atomicOr(&c.bits[e >> 5], 1u << (e & 31));
+    int less = 0, before = 0;
     if (p < P) {
-        e = c.sel[p];
+#pragma unroll 8
         for (int q = 0; q < P; q++) {
             const int f = c.sel[q];
             less += f < e;
             before += (f == e) & (q < p);
         }
-        c.first[p] = before == 0;
     }
     __syncthreads();
     if (p < P) {
-        int first_less = 0;
-        for (int q = 0; q < P; q++) first_less += (c.first[q] && c.sel[q] < e) ? 1 : 0;
+        int first_less = __popc(c.bits[e >> 5] & ((1u << (e & 31)) - 1u));
+#pragma unroll
+        for (int w = 0; w < 16; w++) first_less += w < (e >> 5) ? __popc(c.bits[w]) : 0;
         c.pair[less + before] = p;
         if (before == 0) { c.exp_id[first_less] = e; c.exp_ptr[first_less] = less; }
     }
     if (threadIdx.x == 0) {
         int n = 0;
-        for (int q = 0; q < P; q++) n += c.first[q];
+#pragma unroll
+        for (int w = 0; w < 16; w++) n += __popc(c.bits[w]);
         c.n_exp = n;
         c.exp_ptr[n] = P;
     }
@@ -143,6 +147,7 @@ k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, i
     __shared__ CsrLds c;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int P = M * K;
+    if (threadIdx.x < 16) c.bits[threadIdx.x] = 0u;
     if (wave < M) {
         int my_i;
         float my_w;
@@ -338,25 +343,41 @@ k_csr_combine(const float *__restrict__ part, int M, int K, ShPtrs sh, const flo
         }
         __syncthreads();
     }
-    for (int t = 0; t < M; t++) {
-        float d = 0.0f;
+    // Routed partials: lane l of a row group owns slots k = l, l + LPR, ... of
+    // every row. All loads are issued before any is consumed (clamped indices,
+    // masked afterwards) so their latencies overlap.
+    constexpr int NKL = (16 + LPR - 1) / LPR;
+    float pv[kMaxRows][NKL];
+#pragma unroll
+    for (int t = 0; t < kMaxRows; t++)
+#pragma unroll
+        for (int j = 0; j < NKL; j++) {
+            const int k = l + j * LPR, tt = t < M ? t : 0, kk = k < K ? k : 0;
+            pv[t][j] = part[((size_t)tt * K + kk) * H + c];
+        }
+    float gs[kMaxRows];
+#pragma unroll
+    for (int t = 0; t < kMaxRows; t++) {
+        const int tt = t < M ? t : 0;
+        gs[t] = (has_sh && gated) ? sigmoid(logits[(size_t)tt * ld + (ld - 1)]) * sd : sd;
+    }
+#pragma unroll
+    for (int t = 0; t < kMaxRows; t++) {
+        if (t >= M) break;
+        float r = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NKL; j++) r += (l + j * LPR < K) ? pv[t][j] : 0.0f;
         if (has_sh) {
+            float d = 0.0f;
 #pragma unroll
             for (int st = 0; st < NST; st++) {
                 d += sh_cs[t * (I / 16) + st * LPR + l];
                 d = dot16_u8(w[st], sh_h + t * I + (st * LPR + l) * 16, d);
             }
-            d = group_sum<LPR>(d);
+            r = fmaf(gs[t], d, r);
         }
-        if (l == 0) {
-            float acc = 0.0f;
-            for (int k = 0; k < K; k++) acc += part[((size_t)t * K + k) * H + c];
-            if (has_sh) {
-                const float gam = gated ? sigmoid(logits[(size_t)t * ld + (ld - 1)]) : 1.0f;
-                acc = fmaf(gam * sd, d, acc);
-            }
-            y[(size_t)t * H + c] = f32_to_bf16(acc);
-        }
+        r = group_sum<LPR>(r);
+        if (l == 0) y[(size_t)t * H + c] = f32_to_bf16(r);
     }
 }
 

@@ -5,7 +5,7 @@
 
 namespace qfm {
 
-// Active shape configuration (set by qfm_init; defaults to the BASELINE shape).
+// Active shape configuration (set by qfm_init; defaults to H=2048, I=512, E=512, K=10).
 struct Cfg {
     int H = 2048, I = 512, E = 512, K = 10, renorm = 1, gated = 1;
 };
