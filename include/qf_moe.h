@@ -144,6 +144,99 @@ void qf8_i8_gateup_m1(const Qf4ExpCache *c, const float *x, int8_t *x8q, float *
 void qf8_i8_down_m1(const Qf4ExpCache *c, const float *hidden, int8_t *h8q, float *h8s,
                     const float *wts, const int *sel_ids, float *y, int nexp, hipStream_t s);
 
+/* X8 activation quantizer: per 32-value block s = absmax/127 (1 for an
+ * all-zero block), q = rint(v/s) clamped to +-127; n a multiple of 32.
+ * Replaces qf8_i8_x8 (ocho/amd_server/qf8_dense_i8.h:30); same rule as
+ * k_i8_x8quant (qf8_moe_i8.hip:58-70). */
+void qf8_i8_x8(const float *x, int8_t *q, float *sc, int n, hipStream_t s);
+
+/* ------------------------------------------------------------------------ */
+/* INT8 chunk (CSR) tier: T token rows with their own routing. */
+/* Routing inversion of sel/wt [T][K]: exp_slot[n] ascending expert ids,
+ * exp_ptr[n+1], pair_tok/pair_wt [T*K] in (expert, token) order,
+ * counts = {n_exp, n_pairs}. Any T; deterministic.
+ * Replaces qf8_i8_csr_build (ocho/amd_server/qf8_moe_i8.h:53-54). */
+void qf8_i8_csr_build(const int *sel, const float *wt, int T, int *exp_slot, int *exp_ptr,
+                      int *pair_tok, float *pair_wt, int *counts, hipStream_t s);
+/* Every distinct expert's rows read once and dotted with its tokens' X8 rows
+ * xq/xs [T][H]; hidden [pairs][I] fp32; owned partials part [T*K][H]
+ * (the k of a pair is the position of exp_slot in the token's sel row); y
+ * [T][H] fp32 OVERWRITTEN with the sum of the K partials in k order.
+ * h8q/h8s and n_pairs_max are accepted and unused (hidden stays fp32).
+ * Replaces qf8_i8_experts_chunk (qf8_moe_i8.h:55-59). */
+void qf8_i8_experts_chunk(const Qf4ExpCache *c, const int8_t *xq, const float *xs,
+                          float *hidden, int8_t *h8q, float *h8s,
+                          const int *exp_slot, const int *exp_ptr, const int *pair_tok,
+                          const float *pair_wt, const int *n_exp_dev, int n_exp_max,
+                          int n_pairs_max, const int *sel, float *part, int T, float *y, hipStream_t s);
+
+/* INT8 arena from the NVFP4 slots: value = e2m1 * ue4m3 * s2 (s2 per slot),
+ * row scale = absmax/127, code = rint(value/scale) clamped to +-127. c->i8_*
+ * must be allocated. Returns 0, or -1 on a missing buffer / launch error.
+ * Replaces qf8_i8_build and qf8_i8_build_slot (qf8_moe_i8.h:34-37; the slot
+ * form uses the s2 of `expert`). */
+int qf8_i8_build(Qf4ExpCache *c, hipStream_t s);
+int qf8_i8_build_slot(Qf4ExpCache *c, int src_slot, int dst_slot, int expert, hipStream_t s);
+
+/* ------------------------------------------------------------------------ */
+/* NVFP4 routed experts, one row (M=1). Weights by slot_ids[k] (slot < 0:
+ * hidden row zero, no contribution), s2 tables by expert sel_ids[k]; x fp32
+ * [H]; hidden [nexp][I]; y [H] SEEDED (one writer per row, fixed k order).
+ * Replace qf5_nvfp4_moe_all, qf5_nvfp4_gateup_all_launch and
+ * qf5_nvfp4_downacc_all_launch (ocho/amd_server/qf_nvfp4_wave64.h:218-237). */
+void qf5_nvfp4_moe_all(const uint8_t *Wg, const uint8_t *Sg,
+                       const uint8_t *Wu, const uint8_t *Su,
+                       const uint8_t *Wd, const uint8_t *Sd,
+                       const float *x, float *hidden, float *y,
+                       const float *s2g_dev, const float *s2u_dev,
+                       const float *s2d_dev, const float *wts,
+                       const int *sel_ids, const int *slot_ids,
+                       int nexp, hipStream_t stream);
+void qf5_nvfp4_gateup_all_launch(const uint8_t *Wg, const uint8_t *Sg,
+                                 const uint8_t *Wu, const uint8_t *Su,
+                                 const float *x, float *hidden,
+                                 const float *s2g_dev, const float *s2u_dev,
+                                 const int *sel_ids, const int *slot_ids,
+                                 int nexp, hipStream_t stream);
+void qf5_nvfp4_downacc_all_launch(const uint8_t *Wd, const uint8_t *Sd,
+                                  const float *hidden, const float *wts, float *y,
+                                  const float *s2d_dev, const int *sel_ids,
+                                  const int *slot_ids, int nexp, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* NVFP4 M=8 tier (ocho/amd_server/qf_moe_m8_wave64.h:51-70). x fp32 [M][H];
+ * hidden [pairs][I]; s2*_res indexed by the resident slot; y_partial
+ * [M][H] PRE-ZEROED by the caller, pairs accumulate with atomics. */
+void qf5_m8_gateup(const uint8_t *Wg, const uint8_t *Sg,
+                   const uint8_t *Wu, const uint8_t *Su,
+                   const float *s2g_res, const float *s2u_res,
+                   const float *x, float *hidden,
+                   const Qf5M8Route *rt, hipStream_t stream);
+void qf5_m8_downacc(const uint8_t *Wd, const uint8_t *Sd, const float *s2d_res,
+                    const float *hidden, float *y_partial,
+                    const Qf5M8Route *rt, hipStream_t stream);
+/* Device routing inversion over the experts [card*epc, card*epc + epc):
+ * exp_slot = il*epc + (e - card*epc), ascending; counts = {n_exp, n_pairs}.
+ * M*K <= 1024. */
+void qf5_m8_build_csr(const int *sel_dev, const float *wt_dev, int M, int K,
+                      int card, int epc, int il, int *exp_slot, int *exp_ptr,
+                      int *pair_tok, float *pair_wt, int *counts, hipStream_t s);
+
+/* ------------------------------------------------------------------------ */
+/* INT8 shared expert on X8 rows: eg = silu(gate.x) * up.x, eu = up.x,
+ * g1 = gate_inp.x (row 0), ed = down.eg, y2560 += sigmoid(g1) * ed.
+ * e8q/e8s are accepted and unused (eg stays fp32).
+ * Replace qf8_i8_shexp_m1 (ocho/amd_server/qf8_dense_i8.h:88-91) and the rows
+ * form qf8_i8_shexp_rows (:41-43; returns 0 or a negative code). */
+void qf8_i8_shexp_m1(const Qf8I8Mat *gate, const Qf8I8Mat *up, const Qf8I8Mat *gate_inp,
+                     const Qf8I8Mat *down, const int8_t *xq, const float *xs,
+                     float *eg, float *eu, float *g1, float *ed, int8_t *e8q, float *e8s,
+                     float *y2560, hipStream_t s);
+int qf8_i8_shexp_rows(const Qf8I8Mat *gate, const Qf8I8Mat *up, const Qf8I8Mat *gate_inp,
+                      const Qf8I8Mat *down, const int8_t *xq, const float *xs, float *eg,
+                      float *eu, float *g1, float *ed, int8_t *e8q, float *e8s, float *y2560,
+                      int T, hipStream_t s);
+
 /* ------------------------------------------------------------------------ */
 /* Fused MoE layer (this library's entry point for the whole path). */
 enum { QFM_FMT_INT8 = 0, QFM_FMT_NVFP4 = 1 };

@@ -297,6 +297,40 @@ void orc_x8_quant(const float *v, int n, int8_t *q, float *s) {
     }
 }
 
+/* NVFP4 -> INT8 arena conversion (qf8_moe_i8.hip:146-195): for each row,
+   v_k = e2m1(nibble k) * ue4m3(scale byte k/16) * s2 in fp32, multiplied in
+   that order; scale = absmax * (1/127) (1 when every v is zero); code =
+   rint(v * (1/scale)) clamped to +-127. The scale decode reads the exponent
+   as byte >> 3 (all five high bits, qf8_moe_i8.hip:154-159), 0x7F -> +Inf. */
+static float ue4m3_5bit(uint32_t b) {
+    const uint32_t e = b >> 3, m = b & 7u;
+    if (e == 0) return ldexpf((float)m, -9);
+    if (e == 15 && m == 7) return INFINITY;
+    return ldexpf(1.0f + (float)m / 8.0f, (int)e - 7);
+}
+void orc_nvfp4_to_i8(const uint8_t *W, const uint8_t *S, float s2, int rows, int K, int8_t *Wo, float *So) {
+    float *v = (float *)malloc((size_t)K * sizeof(float));
+    for (int r = 0; r < rows; r++) {
+        float mx = 0.0f;
+        for (int k = 0; k < K; k++) {
+            const uint32_t byte = W[(size_t)r * (K / 2) + k / 2];
+            const uint32_t nib = (k & 1) ? (byte >> 4) : (byte & 15u);
+            const float a = orc_e2m1(nib) * ue4m3_5bit(S[(size_t)r * (K / 16) + k / 16]);
+            v[k] = a * s2;
+            mx = fmaxf(mx, fabsf(v[k]));
+        }
+        const float scale = mx > 0.0f ? mx * (1.0f / 127.0f) : 1.0f;
+        const float inv = 1.0f / scale;
+        for (int k = 0; k < K; k++) {
+            int q = (int)rintf(v[k] * inv);
+            q = q > 127 ? 127 : (q < -127 ? -127 : q);
+            Wo[(size_t)r * K + k] = (int8_t)q;
+        }
+        So[r] = scale;
+    }
+    free(v);
+}
+
 /* Routing inversion: experts ascending; within an expert, pairs in (token, k)
    order (qf8_moe_i8.hip:323-358; qf_moe_m8_wave64.hip:261-299). */
 int orc_csr_build(const int *sel, const float *wt, int T, int K, int E,

@@ -10,6 +10,7 @@
  *   router softmax / top-k / renorm  ocho/amd_server/qf_router_wave64.hip:69-155,
  *                                    ocho/engine_spark/cuda/qf.cu:1184-1271
  *   INT8 expert (exact + X8 modes)   ocho/amd_server/qf8_moe_i8.hip:58-144
+ *   NVFP4 -> INT8 arena build        ocho/amd_server/qf8_moe_i8.hip:146-195
  *   NVFP4 decode / expert            ocho/amd_server/qf_nvfp4_wave64.hip:10-21, 62-101,
  *                                    :175-216, :406-454
  *   routing inversion (CSR)          ocho/amd_server/qf8_moe_i8.hip:323-358,
@@ -34,6 +35,10 @@
  *   orc_nvfp4_expert       numpy fp64 matmul after an independent numpy dequant
  *   orc_csr_build          invariants (permutation, ascending ids, token order)
  *   orc_x8_quant           numpy restatement + invariants (|q| <= 127, q*s ~ v)
+ *   orc_nvfp4_to_i8        closed forms: the row maximum maps to +-127, an
+ *                          all-zero row keeps scale 1, constant rows, codes
+ *                          reconstruct within scale/2, 5-bit exponent field
+ *   orc_moe_layer          recomposition from the pieces with numpy fp64 experts
  */
 #ifndef QFM_ORACLE_H
 #define QFM_ORACLE_H
@@ -95,6 +100,9 @@ void orc_nvfp4_expert(const double *x, const uint8_t *Fg, const uint8_t *Sg, flo
                       int H, int I, double *h, double *y);
 /* dequantize one NVFP4 matrix [rows][K] into fp64 */
 void orc_nvfp4_dequant(const uint8_t *F, const uint8_t *S, float s2, int rows, int K, double *out);
+
+/* ---- NVFP4 -> INT8 arena conversion (bit-exact restatement) ---- */
+void orc_nvfp4_to_i8(const uint8_t *W, const uint8_t *S, float s2, int rows, int K, int8_t *Wo, float *So);
 
 /* ---- X8 activation quantizer (reference's lossy activation mode) ---- */
 void orc_x8_quant(const float *v, int n, int8_t *q, float *s);

@@ -59,36 +59,6 @@ __device__ __forceinline__ void load_slice_bf16(const uint16_t *x, int l, float 
     }
 }
 
-// NVFP4 chunk: 32 e2m1 values (adjacent pairs: byte i = value 2i low nibble,
-// 2i+1 high nibble) with two e4m3 block scales (values 0..15 and 16..31).
-// Codes are converted by the gfx950 v_cvt_scalef32_pk_f32_fp4 instruction
-// with a unit scale (exact e2m1 values); each 16-value group is scaled once.
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ float f4_group16(uint32_t lo, uint32_t hi, const float *x) {
-    float a = 0.0f;
-    const uint32_t w[2] = {lo, hi};
-#pragma unroll
-    for (int d = 0; d < 2; d++) {
-        f32x2_t v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 0);
-        f32x2_t v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 1);
-        f32x2_t v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 2);
-        f32x2_t v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 3);
-        a = fmaf(v0.x, x[d * 8 + 0], a); a = fmaf(v0.y, x[d * 8 + 1], a);
-        a = fmaf(v1.x, x[d * 8 + 2], a); a = fmaf(v1.y, x[d * 8 + 3], a);
-        a = fmaf(v2.x, x[d * 8 + 4], a); a = fmaf(v2.y, x[d * 8 + 5], a);
-        a = fmaf(v3.x, x[d * 8 + 6], a); a = fmaf(v3.y, x[d * 8 + 7], a);
-    }
-    return a;
-}
-__device__ __forceinline__ float e4m3_scale(uint32_t b) {
-    return __builtin_amdgcn_cvt_f32_fp8((int)b, 0);
-}
-__device__ __forceinline__ float f4_chunk(uint4 w, uint32_t s2b, const float *x) {
-    const float g0 = f4_group16(w.x, w.y, x);
-    const float g1 = f4_group16(w.z, w.w, x + 16);
-    return fmaf(e4m3_scale(s2b & 0xFFu), g0, e4m3_scale((s2b >> 8) & 0xFFu) * g1);
-}
-
 // ---- routing inversion in LDS ---------------------------------------------------
 struct CsrLds {
     int sel[kMaxPairs];
@@ -136,7 +106,6 @@ __device__ __forceinline__ void csr_build_lds(CsrLds &c, int P) {
     __syncthreads();
 }
 
-constexpr int lpr_of(int cpr) { return cpr % 32 == 0 ? 32 : cpr % 16 == 0 ? 16 : cpr % 8 == 0 ? 8 : 4; }
 
 // ---- top-K of all rows + routing inversion: one block, one wave per row ---------
 // Published: sel/wts [M][K]; csr = {n_exp, exp_id[P], exp_ptr[P+1], pair[P]}.

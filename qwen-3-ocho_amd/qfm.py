@@ -83,6 +83,20 @@ _SIGS = {
     "qfm_topk": (C.c_int, [vp, C.c_int, vp, vp, vp]),
     "qf8_i8_gateup_m1": (None, [C.POINTER(Qf4ExpCache), vp, vp, vp, vp, vp, C.c_int, C.c_int, vp]),
     "qf8_i8_down_m1": (None, [C.POINTER(Qf4ExpCache), vp, vp, vp, vp, vp, vp, C.c_int, vp]),
+    "qf8_i8_x8": (None, [vp, vp, vp, C.c_int, vp]),
+    "qf8_i8_csr_build": (None, [vp, vp, C.c_int, vp, vp, vp, vp, vp, vp]),
+    "qf8_i8_experts_chunk": (None, [C.POINTER(Qf4ExpCache), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int,
+                                    C.c_int, vp, vp, C.c_int, vp, vp]),
+    "qf8_i8_build": (C.c_int, [C.POINTER(Qf4ExpCache), vp]),
+    "qf8_i8_build_slot": (C.c_int, [C.POINTER(Qf4ExpCache), C.c_int, C.c_int, C.c_int, vp]),
+    "qf5_nvfp4_moe_all": (None, [vp] * 15 + [C.c_int, vp]),
+    "qf5_nvfp4_gateup_all_launch": (None, [vp] * 10 + [C.c_int, vp]),
+    "qf5_nvfp4_downacc_all_launch": (None, [vp] * 8 + [C.c_int, vp]),
+    "qf5_m8_gateup": (None, [vp] * 8 + [C.POINTER(Qf5M8Route), vp]),
+    "qf5_m8_downacc": (None, [vp] * 5 + [C.POINTER(Qf5M8Route), vp]),
+    "qf5_m8_build_csr": (None, [vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp, vp]),
+    "qf8_i8_shexp_m1": (None, [C.POINTER(Qf8I8Mat)] * 4 + [vp] * 9 + [vp]),
+    "qf8_i8_shexp_rows": (C.c_int, [C.POINTER(Qf8I8Mat)] * 4 + [vp] * 9 + [C.c_int, vp]),
     "qfm_workspace_bytes": (C.c_size_t, [C.c_int]),
     "qfm_workspace_view": (C.c_int, [vp, C.c_int, C.POINTER(QfmWsView)]),
     "qfm_moe_forward": (C.c_int, [C.POINTER(QfmLayer), vp, C.c_int, vp, vp, C.c_size_t, vp]),

@@ -58,6 +58,7 @@ _SIGS = {
                                 C.c_int, C.c_int, vp, vp]),
     "orc_nvfp4_dequant": (None, [vp, vp, C.c_float, C.c_int, C.c_int, vp]),
     "orc_x8_quant": (None, [vp, C.c_int, vp, vp]),
+    "orc_nvfp4_to_i8": (None, [vp, vp, C.c_float, C.c_int, C.c_int, vp, vp]),
     "orc_csr_build": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp, vp]),
     "orc_moe_layer": (C.c_int, [C.POINTER(LayerCfg), C.c_int, vp, vp, vp, vp, vp, vp]),
     "orc_cpu_moe_layer_fast": (None, [C.POINTER(HostLayer), C.c_int, C.c_int, C.c_int, C.c_int,
@@ -169,6 +170,15 @@ def nvfp4_expert(x, Fg, Sg, s2g, Fu, Su, s2u, Fd, Sd, s2d, H, I):
     lib.orc_nvfp4_expert(ptr(xd), ptr(c(Fg)), ptr(c(Sg)), s2g, ptr(c(Fu)), ptr(c(Su)), s2u,
                          ptr(c(Fd)), ptr(c(Sd)), s2d, H, I, ptr(h), ptr(y))
     return h, y
+
+
+def nvfp4_to_i8(F, S, s2, rows, K):
+    lib = load()
+    q = np.empty((rows, K), np.int8)
+    sc = np.empty(rows, np.float32)
+    lib.orc_nvfp4_to_i8(ptr(np.ascontiguousarray(F, np.uint8)), ptr(np.ascontiguousarray(S, np.uint8)), s2, rows, K,
+                        ptr(q), ptr(sc))
+    return q, sc
 
 
 def x8_quant(v):

@@ -272,3 +272,40 @@ def test_layer_composes_the_pieces():
         y += (1 / (1 + np.exp(-(g @ xf[m])))) * ((Qd * sd[:, None].astype(np.float64)) @ hh)
         assert np.allclose(out["y"][m], y, rtol=1e-9, atol=1e-12 * np.abs(y).max())
     assert np.array_equal(out["ybf"], _bf16(out["y"].astype(np.float32)))
+
+
+# ---------------------------------------------------------------- NVFP4 -> INT8 build
+def test_nvfp4_to_i8_closed_forms():
+    K = 2048
+    rows = 6
+    F = RNG.integers(0, 256, (rows, K // 2), dtype=np.uint8)
+    S = RNG.integers(40, 65, (rows, K // 16), dtype=np.uint8)
+    F[1] = 0                                   # all-zero row: scale 1, codes 0
+    F[2] = 0x22                                # every code 1.0 with a unit scale: constant row
+    S[2] = 56
+    F[3, 0] = 0x07                             # a +6 code (the row maximum at element 0)
+    S[3, 0] = 63                               # largest scale in the row
+    S[3, 1:] = np.minimum(S[3, 1:], 62)
+    q, sc = orc.nvfp4_to_i8(F, S, 0.01, rows, K)
+    v = orc.nvfp4_dequant(F, S, 0.01, rows, K)
+    assert sc[1] == 1.0 and not q[1].any()
+    assert np.all(q[2] == 127) and sc[2] == np.float32(np.float32(0.01) * np.float32(1 / 127))
+    assert q[3, 0] == 127
+    for r in range(rows):
+        if r == 1:
+            continue
+        amax = np.abs(v[r]).max()
+        assert abs(sc[r] - amax / 127) <= 2e-7 * sc[r]
+        assert np.abs(q[r]).max() == 127
+        # rint of the fp32 product v * (1/scale): within half a code plus the rounding of that product
+        assert np.all(np.abs(q[r] * np.float64(sc[r]) - v[r]) <= (0.5 + 1e-5) * sc[r])
+    # sign symmetry: flipping every code's sign bit negates every output code
+    q2, sc2 = orc.nvfp4_to_i8(F ^ 0x88, S, 0.01, rows, K)
+    assert np.array_equal(sc2, sc)
+    assert np.array_equal(q2.astype(int), -q.astype(int))
+    # the scale byte's exponent field is five bits wide: 0x80 | b reads as exponent >= 16
+    F1 = np.full((1, 32), 0x22, np.uint8)
+    S1 = np.array([[0x80 | 56, 56, 56, 56]], np.uint8)   # byte 0xB8: exponent 23 -> 2^16; the rest 1.0
+    q1, s1 = orc.nvfp4_to_i8(F1, S1, 1.0, 1, 64)
+    assert s1[0] == np.float32(np.float32((1 + 0 / 8) * 2.0 ** 16) * np.float32(1 / 127))
+    assert np.all(q1[0, :16] == 127) and np.all(q1[0, 16:] == 0)
