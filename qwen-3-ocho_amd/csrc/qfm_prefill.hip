@@ -23,7 +23,8 @@
 //                      also the exact shared-gate dot. Tokens whose candidate
 //                      set overflows recompute every logit.
 // Experts:
-//   k_pf_count / k_pf_plan / k_pf_scatter   routing inversion with atomics
+//   k_pf_count / k_pf_plan / k_pf_scatter   routing inversion: per-block LDS
+//                      histograms, one planning block, LDS-counter scatter
 //                      (row order inside a group is unspecified: every GEMM
 //                      row is independent and partials are owned by (t, k),
 //                      so y does not depend on it) and the GEMM work lists.
@@ -342,70 +343,108 @@ k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, 
 }
 
 // ---- routing inversion --------------------------------------------------------------
-__global__ void k_pf_count(const int *__restrict__ sel, int TK, int *__restrict__ cnt) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < TK) atomicAdd(&cnt[sel[i]], 1);
+constexpr int kPairsPerBlk = 4096;            // routed pairs per counting / scatter block
+
+// Per-block expert histograms of the routed pairs, in LDS (no global atomics:
+// a skewed router puts most pairs on a few experts).
+__global__ void __launch_bounds__(256)
+k_pf_count(const int *__restrict__ sel, int TK, int E, int *__restrict__ blk) {
+    __shared__ int h[1024];
+    for (int i = threadIdx.x; i < E; i += 256) h[i] = 0;
+    __syncthreads();
+    const int p0 = blockIdx.x * kPairsPerBlk, p1 = min(TK, p0 + kPairsPerBlk);
+    for (int p = p0 + threadIdx.x; p < p1; p += 256) atomicAdd(&h[sel[p]], 1);
+    __syncthreads();
+    for (int i = threadIdx.x; i < E; i += 256) blk[(size_t)blockIdx.x * E + i] = h[i];
 }
 
-// One block: group offsets (groups 0..E-1 routed, E = shared with T rows when
-// has_sh), fill counters reset, GEMM work lists: item = (group, row0, rows,
-// n-tile) for every 128-row m-tile of every group, n-tiles fastest.
+// One block of 1024 threads (G = E + has_sh <= 1024 groups): per-expert totals,
+// blk turned in place into each block's exclusive prefix over the earlier
+// blocks, group offsets off[0..G], and the GEMM work lists: item = (group,
+// row0, rows, n-tile) for every 128-row m-tile of every group, n-tiles fastest,
+// written by all threads (a hot expert owns most of the m-tiles).
 __global__ void __launch_bounds__(1024)
-k_pf_plan(int *__restrict__ cnt, int E, int has_sh, int T, int nt_gu, int nt_dn, int *__restrict__ off,
-          int *__restrict__ fill, int4 *__restrict__ items_gu, int4 *__restrict__ items_dn, int *__restrict__ n_items,
-          int max_gu, int max_dn) {
-    __shared__ int s_mt[1024 + 1], s_cnt[1024];
+k_pf_plan(int *__restrict__ blk, int nblk, int E, int has_sh, int T, int nt_gu, int nt_dn, int *__restrict__ off,
+          int4 *__restrict__ items_gu, int4 *__restrict__ items_dn, int *__restrict__ n_items, int max_gu,
+          int max_dn) {
+    __shared__ int s_cnt[1024], s_mt[1024], sa[1024], sb[1024];
     const int G = E + (has_sh ? 1 : 0);
     const int g = threadIdx.x;
     int c = 0;
-    if (g < E) c = cnt[g];
-    else if (g == E && has_sh) c = T;
-    s_cnt[g] = c;
-    s_mt[g] = (c + BM - 1) / BM;
-    __syncthreads();
-    if (g == 0) {
-        int o = 0, m = 0;
-        for (int q = 0; q < G; q++) {
-            off[q] = o; o += s_cnt[q];
-            const int mt = s_mt[q];
-            s_mt[q] = m; m += mt;
+    if (g < E) {
+        int run = 0;
+        for (int b0 = 0; b0 < nblk; b0 += 16) {      // 16 loads in flight, then the stores
+            int v[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = b0 + j < nblk ? blk[(size_t)(b0 + j) * E + g] : 0;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                if (b0 + j < nblk) blk[(size_t)(b0 + j) * E + g] = run;
+                run += v[j];
+            }
         }
-        off[G] = o;
-        s_mt[G] = m;
-        n_items[0] = m * nt_gu;
-        n_items[1] = m * nt_dn;
+        c = run;
+    } else if (g == E && has_sh) {
+        c = T;
     }
+    const int mt = (c + BM - 1) / BM;
+    sa[g] = c;
+    sb[g] = mt;
     __syncthreads();
-    if (g < G) {
-        fill[g] = 0;
-        const int m0 = s_mt[g], nmt = (s_cnt[g] + BM - 1) / BM;
-        for (int mt = 0; mt < nmt; mt++) {
-            const int rows = min(BM, s_cnt[g] - mt * BM);
-            for (int n = 0; n < nt_gu; n++) {
-                const int it = (m0 + mt) * nt_gu + n;
-                if (it < max_gu) items_gu[it] = make_int4(g, mt * BM, rows, n);
+    for (int st = 1; st < 1024; st <<= 1) {      // inclusive scans of counts and m-tiles
+        const int a = g >= st ? sa[g - st] : 0, b = g >= st ? sb[g - st] : 0;
+        __syncthreads();
+        sa[g] += a;
+        sb[g] += b;
+        __syncthreads();
+    }
+    s_cnt[g] = c;
+    s_mt[g] = sb[g] - mt;                        // exclusive: first m-tile of group g
+    if (g <= G) off[g] = sa[g] - c;              // groups >= G are empty: off[G] = all pairs
+    __syncthreads();
+    const int mtot = s_mt[G];
+    if (g == 0) { n_items[0] = mtot * nt_gu; n_items[1] = mtot * nt_dn; }
+    for (int pass = 0; pass < 2; pass++) {
+        const int nt = pass ? nt_dn : nt_gu, mx = pass ? max_dn : max_gu;
+        int4 *items = pass ? items_dn : items_gu;
+        for (int it = g; it < mtot * nt && it < mx; it += 1024) {
+            const int m = it / nt, n = it - m * nt;
+            int lo = 0, hi = G - 1;                  // last group whose first m-tile is <= m
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (s_mt[mid] <= m) lo = mid; else hi = mid - 1;
             }
-            for (int n = 0; n < nt_dn; n++) {
-                const int it = (m0 + mt) * nt_dn + n;
-                if (it < max_dn) items_dn[it] = make_int4(g, mt * BM, rows, n);
-            }
+            const int row0 = (m - s_mt[lo]) * BM;
+            items[it] = make_int4(lo, row0, min(BM, s_cnt[lo] - row0), n);
         }
     }
 }
 
-// pair -> group position; routed pairs by atomic fill, shared pairs in token order
-__global__ void k_pf_scatter(const int *__restrict__ sel, const float *__restrict__ wts, const float *__restrict__ gam,
-                             int T, int K, int E, int has_sh, const int *__restrict__ off, int *__restrict__ fill,
-                             int *__restrict__ p_tok, int *__restrict__ p_slot, float *__restrict__ p_wt) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    const int S = K + has_sh;
-    if (i < T * K) {
-        const int e = sel[i], t = i / K, k = i - t * K;
-        const int pos = off[e] + atomicAdd(&fill[e], 1);
-        p_tok[pos] = t; p_slot[pos] = t * S + k; p_wt[pos] = wts[i];
-    } else if (has_sh && i < T * K + T) {
-        const int t = i - T * K, pos = off[E] + t;
-        p_tok[pos] = t; p_slot[pos] = t * S + K; p_wt[pos] = gam ? gam[t] : 1.0f;
+// pair -> group position. Routed pairs: block b starts expert e at off[e] +
+// blk[b][e] and places its pairs with LDS counters; shared-expert pairs
+// (blocks past the routed ones) in token order.
+__global__ void __launch_bounds__(256)
+k_pf_scatter(const int *__restrict__ sel, const float *__restrict__ wts, const float *__restrict__ gam, int T, int K,
+             int E, int has_sh, const int *__restrict__ off, const int *__restrict__ blk, int *__restrict__ p_tok,
+             int *__restrict__ p_slot, float *__restrict__ p_wt) {
+    __shared__ int ctr[1024];
+    const int S = K + has_sh, TK = T * K;
+    const int nblk = (TK + kPairsPerBlk - 1) / kPairsPerBlk;
+    if ((int)blockIdx.x < nblk) {
+        for (int i = threadIdx.x; i < E; i += 256) ctr[i] = off[i] + blk[(size_t)blockIdx.x * E + i];
+        __syncthreads();
+        const int p0 = blockIdx.x * kPairsPerBlk, p1 = min(TK, p0 + kPairsPerBlk);
+        for (int p = p0 + threadIdx.x; p < p1; p += 256) {
+            const int e = sel[p], t = p / K, k = p - t * K;
+            const int pos = atomicAdd(&ctr[e], 1);
+            p_tok[pos] = t; p_slot[pos] = t * S + k; p_wt[pos] = wts[p];
+        }
+    } else if (has_sh) {
+        const int t = ((int)blockIdx.x - nblk) * 256 + threadIdx.x;
+        if (t < T) {
+            const int pos = off[E] + t;
+            p_tok[pos] = t; p_slot[pos] = t * S + K; p_wt[pos] = gam ? gam[t] : 1.0f;
+        }
     }
 }
 
@@ -510,7 +549,8 @@ size_t prefill_ws_bytes(int T) {
     b += al((size_t)T * c.K * 4) * 2;      // sel, wts
     b += al((size_t)T * 4);                // gam
     b += al(4 * 8);                        // counters
-    b += al((size_t)(c.E + 2) * 4) * 3;    // cnt, off, fill
+    b += al((size_t)(c.E + 2) * 4);        // off
+    b += al((size_t)((size_t)T * c.K + kPairsPerBlk - 1) / kPairsPerBlk * c.E * 4);   // per-block counts
     const size_t max_mt = P / BM + c.E + 2;
     b += al(max_mt * (c.I / 64) * 16) + al(max_mt * (c.H / BN) * 16);   // item lists
     b += al(P * 4) * 3;                    // p_tok, p_slot, p_wt
@@ -535,6 +575,8 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     if (L->fmt != QFM_FMT_INT8) { set_error(-2, "prefill: INT8 routed experts only"); return -2; }
     if (c.E != 512 || !(shape_2048() || shape_2560())) { set_error(-2, "prefill: unsupported shape"); return -2; }
     const int E = c.E, K = c.K, H = c.H, I = c.I;
+    const Qf4ExpCache *a = L->arena;
+    if (!a || !a->i8_gate || !a->i8_up || !a->i8_down) { set_error(-1, "prefill: arena has no INT8 blobs"); return -1; }
     const bool has_sh = L->sh_gate.w != nullptr;
     const int S = K + (has_sh ? 1 : 0);      // partial slots per token: K routed (+ shared)
     const size_t P = (size_t)T * S;
@@ -547,9 +589,9 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     float *wts = reinterpret_cast<float *>(b); b += al((size_t)T * K * 4);
     float *gam = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
     int *ctr = reinterpret_cast<int *>(b); b += al(4 * 8);
-    int *cnt = reinterpret_cast<int *>(b); b += al((size_t)(E + 2) * 4);
     int *off = reinterpret_cast<int *>(b); b += al((size_t)(E + 2) * 4);
-    int *fill = reinterpret_cast<int *>(b); b += al((size_t)(E + 2) * 4);
+    const int nblk = (int)(((size_t)T * K + kPairsPerBlk - 1) / kPairsPerBlk);
+    int *blk = reinterpret_cast<int *>(b); b += al((size_t)nblk * E * 4);
     const size_t max_mt = P / BM + E + 2;
     const int nt_gu = I / 64, nt_dn = H / BN;
     int4 *items_gu = reinterpret_cast<int4 *>(b); b += al(max_mt * nt_gu * 16);
@@ -563,7 +605,6 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     const float *g = (has_sh && gated) ? L->sh_gate_inp : nullptr;
     // zero the small counters with a fill kernel (no memset node in captured graphs)
     launch_fill_f32(reinterpret_cast<float *>(ctr), 8, 0.0f, s);
-    launch_fill_f32(reinterpret_cast<float *>(cnt), (uint64_t)(E + 2), 0.0f, s);
     hipLaunchKernelGGL(k_pf_router_prep, dim3(E), dim3(256), 0, s, L->router, E, H, wnorm);
     hipLaunchKernelGGL(k_pf_router_mfma, dim3((T + BM - 1) / BM, E / BN), dim3(256), 0, s, x, T, H, L->router, E,
                        L->router_bias, lg, xnorm);
@@ -573,13 +614,11 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     else
         hipLaunchKernelGGL((k_pf_select<10, 8>), dim3((T + 3) / 4), dim3(256), 0, s, x, T, L->router, L->router_bias,
                            g, lg, xnorm, wnorm, K, c.renorm, sel, wts, gam, ctr);
-    hipLaunchKernelGGL(k_pf_count, dim3((T * K + 255) / 256), dim3(256), 0, s, sel, T * K, cnt);
-    hipLaunchKernelGGL(k_pf_plan, dim3(1), dim3(1024), 0, s, cnt, E, has_sh ? 1 : 0, T, nt_gu, nt_dn, off, fill,
+    hipLaunchKernelGGL(k_pf_count, dim3(nblk), dim3(256), 0, s, sel, T * K, E, blk);
+    hipLaunchKernelGGL(k_pf_plan, dim3(1), dim3(1024), 0, s, blk, nblk, E, has_sh ? 1 : 0, T, nt_gu, nt_dn, off,
                        items_gu, items_dn, ctr + 1, (int)(max_mt * nt_gu), (int)(max_mt * nt_dn));
-    hipLaunchKernelGGL(k_pf_scatter, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, s, sel, wts, g ? gam : nullptr,
-                       T, K, E, has_sh ? 1 : 0, off, fill, p_tok, p_slot, p_wt);
-    const Qf4ExpCache *a = L->arena;
-    if (!a->i8_gate || !a->i8_up || !a->i8_down) { set_error(-1, "prefill: arena has no INT8 blobs"); return -1; }
+    hipLaunchKernelGGL(k_pf_scatter, dim3((unsigned)(nblk + (has_sh ? (T + 255) / 256 : 0))), dim3(256), 0, s, sel,
+                       wts, g ? gam : nullptr, T, K, E, has_sh ? 1 : 0, off, blk, p_tok, p_slot, p_wt);
     GroupW gg{a->i8_gate, a->i8s_gate, L->sh_gate.w, L->sh_gate.s};
     GroupW gu{a->i8_up, a->i8s_up, L->sh_up.w, L->sh_up.s};
     GroupW gd{a->i8_down, a->i8s_down, L->sh_down.w, L->sh_down.s};
