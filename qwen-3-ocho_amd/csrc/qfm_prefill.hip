@@ -30,8 +30,8 @@
 //                      so y does not depend on it) and the GEMM work lists.
 //   k_pf_gemm<GATEUP>  hidden[p][n] = silu(sg (x_p . Wg_n)) * (su (x_p . Wu_n))
 //   k_pf_gemm<DOWN>    part[slot_p][c] = w_p * sd_c * (h_p . Wd_c)
-//                      Both: BM=128 rows x BN=128 weight rows x BK=32, four
-//                      waves, v_mfma_f32_16x16x32_bf16; int8 weights are
+//                      Both: BM=128 rows x BN=128 weight rows x BK=64, 2 x 2
+//                      waves of 64 x 64, v_mfma_f32_16x16x32_bf16; int8 weights are
 //                      staged to LDS as bf16 in offset-binary form
 //                      (u = q + 128 is exact in bf16) and the row sum of A
 //                      times 128 is subtracted in the epilogue.
@@ -44,8 +44,8 @@ namespace qfm {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128, BN = 128, BK = 32;
-constexpr int LDS_STRIDE = BK + 8;           // bf16 elements per LDS row (80 bytes)
+constexpr int BM = 128, BN = 128;
+constexpr int kStagesI8 = 2, kStagesF32 = 2;   // register stages of global loads in flight
 constexpr int kCandMax = 64;
 
 // bf16 bits of an exactly representable value (integers |v| <= 256): truncation is exact
@@ -89,88 +89,121 @@ __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict_
 }
 
 // ---- the MFMA tile engine ---------------------------------------------------------
-// A rows: bf16, row r of the tile at A + arow[r] * lda (arow < 0: row absent,
-// staged as zeros). B rows: int8 (offset-binary) or fp32 (rounded to bf16),
-// row n at (n < nsplit ? B0 : B1) + brow[n] * ldb. K % BK == 0. acc[mb][nb]
-// over the tile: wave w covers rows [32w, 32w + 32), all BN columns.
-template <bool B_I8>
-struct TileEngine {
-    __device__ static void run(const uint16_t *__restrict__ A, long lda, const int *arow, const void *B0,
-                               const void *B1, int nsplit, long ldb, const int *brow, int K,
-                               uint16_t (*lds)[2][BM * LDS_STRIDE], f32x4_t (&acc)[2][8], float *rowsum_out) {
+// Block tile BM x BN = 128 x 128, k-step BK2 = 64 (two 32-deep MFMA steps),
+// 256 threads = 2 x 2 waves, each wave a 64 x 64 sub-tile = 4 x 4
+// v_mfma_f32_16x16x32_bf16 accumulators. Two LDS buffers (the k-step being
+// multiplied and the next one) and D register stages of global loads in
+// flight, one barrier per k-step.
+// A rows: bf16, row r at A + arow[r] * lda (arow < 0: absent row, staged as
+// zeros). B rows: int8 (staged as bf16 in offset-binary form u = q + 128,
+// exact) or fp32 (rounded to bf16), row n at bptr[n] (bytes). K % BK2 == 0.
+// acc[mb][nb][i] = C[64 wm + 16 mb + 4 (lane >> 4) + i][64 wn + 16 nb + (lane & 15)],
+// wave = 2 wm + wn. rowsum_out[r] = sum_k A[r][k] when requested.
+constexpr int BK2 = 64;
+constexpr int LDS2 = BK2 + 8;                  // bf16 elements per LDS row (144 bytes)
+struct TileLds {
+    uint16_t a[2][BM * LDS2];
+    uint16_t b[2][BN * LDS2];
+};
+template <bool B_I8, int D>
+struct TileEngine2 {
+    __device__ static void run(const uint16_t *__restrict__ A, long lda, const int *arow,
+                               const char *const *bptr, int K, TileLds &L, f32x4_t (&acc)[4][4],
+                               float *rowsum_out) {
+        constexpr int NB = B_I8 ? 2 : 8;
         const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-        const int sr = t >> 1, sh = (t & 1) * 16;           // staging: row, first k of this thread's half
+        const int wm = wave >> 1, wn = wave & 1;
+        const int sr = t >> 1, sh = (t & 1) * 32;           // staging: row, first k of this thread's half
         const int ar = arow[sr];
         const uint16_t *ap = A + (ar >= 0 ? (long)ar * lda : 0) + sh;
-        const int br = brow[sr];
-        const void *B = sr < nsplit ? B0 : B1;
+        const char *bp = bptr[sr];
         float rsum = 0.0f;
-        uint4 a0, a1, b0, b1, b2, b3;
-        auto gload = [&](int k0) {
-            if (ar >= 0) {
-                a0 = *reinterpret_cast<const uint4 *>(ap + k0);
-                a1 = *reinterpret_cast<const uint4 *>(ap + k0 + 8);
-            } else {
-                a0 = a1 = make_uint4(0, 0, 0, 0);
-            }
+        uint4 ra[D][4], rb[D][NB];
+        auto gload = [&](int k0, uint4 (&a)[4], uint4 (&bb)[NB]) {
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                a[q] = ar >= 0 ? *reinterpret_cast<const uint4 *>(ap + k0 + 8 * q) : make_uint4(0, 0, 0, 0);
             if constexpr (B_I8) {
-                b0 = ld_nt16(reinterpret_cast<const int8_t *>(B) + (long)br * ldb + k0 + sh);
+#pragma unroll
+                for (int q = 0; q < NB; q++) bb[q] = ld_nt16(bp + k0 + sh + 16 * q);
             } else {
-                const float *bp = reinterpret_cast<const float *>(B) + (long)br * ldb + k0 + sh;
-                b0 = *reinterpret_cast<const uint4 *>(bp);
-                b1 = *reinterpret_cast<const uint4 *>(bp + 4);
-                b2 = *reinterpret_cast<const uint4 *>(bp + 8);
-                b3 = *reinterpret_cast<const uint4 *>(bp + 12);
+#pragma unroll
+                for (int q = 0; q < NB; q++)
+                    bb[q] = *reinterpret_cast<const uint4 *>(bp + (size_t)(k0 + sh) * 4 + 16 * q);
             }
         };
-        auto sstore = [&](int buf) {
-            uint4 *la = reinterpret_cast<uint4 *>(&lds[0][buf][sr * LDS_STRIDE + sh]);
-            la[0] = a0; la[1] = a1;
+        auto sstore = [&](int buf, const uint4 (&a)[4], const uint4 (&bb)[NB]) {
+            uint4 *la = reinterpret_cast<uint4 *>(&L.a[buf][sr * LDS2 + sh]);
+#pragma unroll
+            for (int q = 0; q < 4; q++) la[q] = a[q];
             if (rowsum_out) {
-                const uint32_t d[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
 #pragma unroll
-                for (int q = 0; q < 8; q++) rsum += bf16_lo(d[q]) + bf16_hi(d[q]);
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t d[4] = {a[q].x, a[q].y, a[q].z, a[q].w};
+#pragma unroll
+                    for (int u = 0; u < 4; u++) rsum += bf16_lo(d[u]) + bf16_hi(d[u]);
+                }
             }
-            uint4 o0, o1;
+            uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][sr * LDS2 + sh]);
             if constexpr (B_I8) {
-                i8_to_bf16_ob(b0, o0, o1);
-            } else {
-                const uint32_t f[16] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w,
-                                        b2.x, b2.y, b2.z, b2.w, b3.x, b3.y, b3.z, b3.w};
-                uint32_t o[8];
 #pragma unroll
-                for (int q = 0; q < 8; q++) o[q] = pack_bf16_rne(__uint_as_float(f[2 * q]), __uint_as_float(f[2 * q + 1]));
-                o0 = make_uint4(o[0], o[1], o[2], o[3]);
-                o1 = make_uint4(o[4], o[5], o[6], o[7]);
+                for (int q = 0; q < 2; q++) {
+                    uint4 o0, o1;
+                    i8_to_bf16_ob(bb[q], o0, o1);
+                    lb[2 * q] = o0;
+                    lb[2 * q + 1] = o1;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint4 f0 = bb[2 * q], f1 = bb[2 * q + 1];
+                    lb[q] = make_uint4(pack_bf16_rne(__uint_as_float(f0.x), __uint_as_float(f0.y)),
+                                       pack_bf16_rne(__uint_as_float(f0.z), __uint_as_float(f0.w)),
+                                       pack_bf16_rne(__uint_as_float(f1.x), __uint_as_float(f1.y)),
+                                       pack_bf16_rne(__uint_as_float(f1.z), __uint_as_float(f1.w)));
+                }
             }
-            uint4 *lb = reinterpret_cast<uint4 *>(&lds[1][buf][sr * LDS_STRIDE + sh]);
-            lb[0] = o0; lb[1] = o1;
         };
 #pragma unroll
-        for (int mb = 0; mb < 2; mb++)
+        for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-            for (int nb = 0; nb < 8; nb++) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        const int nk = K / BK;
-        gload(0);
-        sstore(0);
+            for (int nb = 0; nb < 4; nb++) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        const int nk = K / BK2;
+#pragma unroll
+        for (int j = 0; j < D; j++)
+            if (j < nk) gload(j * BK2, ra[j], rb[j]);
+        sstore(0, ra[0], rb[0]);
+        if (D < nk) gload(D * BK2, ra[0], rb[0]);
         __syncthreads();
         const int lr = lane & 15, lk = (lane >> 4) * 8;
-        for (int s = 0; s < nk; s++) {
-            const int buf = s & 1;
-            if (s + 1 < nk) gload((s + 1) * BK);
-            bf16x8_t av[2];
+        for (int s0 = 0; s0 < nk; s0 += D) {
 #pragma unroll
-            for (int mb = 0; mb < 2; mb++)
-                av[mb] = *reinterpret_cast<const bf16x8_t *>(&lds[0][buf][(wave * 32 + mb * 16 + lr) * LDS_STRIDE + lk]);
+            for (int j = 0; j < D; j++) {
+                const int s = s0 + j;
+                if (s >= nk) break;
+                const int buf = s & 1;
 #pragma unroll
-            for (int nb = 0; nb < 8; nb++) {
-                const bf16x8_t bv = *reinterpret_cast<const bf16x8_t *>(&lds[1][buf][(nb * 16 + lr) * LDS_STRIDE + lk]);
+                for (int kk = 0; kk < BK2; kk += 32) {
+                    bf16x8_t av[4], bv[4];
 #pragma unroll
-                for (int mb = 0; mb < 2; mb++)
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mb], bv, acc[mb][nb], 0, 0, 0);
+                    for (int mb = 0; mb < 4; mb++)
+                        av[mb] = *reinterpret_cast<const bf16x8_t *>(&L.a[buf][(wm * 64 + mb * 16 + lr) * LDS2 + kk + lk]);
+#pragma unroll
+                    for (int nb = 0; nb < 4; nb++)
+                        bv[nb] = *reinterpret_cast<const bf16x8_t *>(&L.b[buf][(wn * 64 + nb * 16 + lr) * LDS2 + kk + lk]);
+#pragma unroll
+                    for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+                        for (int nb = 0; nb < 4; nb++)
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mb], bv[nb], acc[mb][nb], 0, 0, 0);
+                }
+                const int jn = (j + 1) % D;                  // register stage holding k-step s + 1 (unrolled: constant)
+                if (s + 1 < nk) {
+                    sstore(buf ^ 1, ra[jn], rb[jn]);
+                    if (s + 1 + D < nk) gload((s + 1 + D) * BK2, ra[jn], rb[jn]);
+                }
+                __syncthreads();
             }
-            if (s + 1 < nk) sstore(buf ^ 1);
-            __syncthreads();
         }
         if (rowsum_out) {
             rsum += __shfl_xor(rsum, 1, WAVE);
@@ -179,26 +212,40 @@ struct TileEngine {
     }
 };
 
+// Workgroups are dispatched to the 8 XCDs round-robin (block b on XCD b % 8).
+// Map block b to tile (m, n) so that the nt n-tiles of one m-tile run back to
+// back on the same XCD, whose L2 then serves the m-tile's A rows nt times.
+// Bijective on [0, 8 * ceil(mt / 8) * nt).
+__device__ __forceinline__ void xcd_tile(int b, int nt, int &m, int &n) {
+    const int x = b & 7, slot = b >> 3;
+    m = (slot / nt) * 8 + x;
+    n = slot - (slot / nt) * nt;
+}
+
 // ---- router GEMM: logits~ [T][E] --------------------------------------------------
 __global__ void __launch_bounds__(256)
 k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const float *__restrict__ W, int E,
                  const float *__restrict__ bias, float *__restrict__ lg_approx, float *__restrict__ xnorm) {
-    __shared__ __align__(16) uint16_t lds[2][2][BM * LDS_STRIDE];
-    __shared__ int arow[BM], brow[BN];
-    const int t0 = blockIdx.x * BM, e0 = blockIdx.y * BN;
+    __shared__ __align__(16) TileLds lds;
+    __shared__ int arow[BM];
+    __shared__ const char *bptr[BN];
+    int mt, et;
+    xcd_tile(blockIdx.x, E / BN, mt, et);
+    if (mt * BM >= T) return;
+    const int t0 = mt * BM, e0 = et * BN;
     if (threadIdx.x < BM) arow[threadIdx.x] = (t0 + (int)threadIdx.x < T) ? t0 + (int)threadIdx.x : -1;
-    if (threadIdx.x < BN) brow[threadIdx.x] = e0 + (int)threadIdx.x;
+    if (threadIdx.x < BN) bptr[threadIdx.x] = reinterpret_cast<const char *>(W + (size_t)(e0 + threadIdx.x) * H);
     __syncthreads();
-    f32x4_t acc[2][8];
-    TileEngine<false>::run(x, H, arow, W, W, BN, H, brow, H, lds, acc, nullptr);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    f32x4_t acc[4][4];
+    TileEngine2<false, kStagesF32>::run(x, H, arow, bptr, H, lds, acc, nullptr);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave >> 1, wn = wave & 1;
 #pragma unroll
-    for (int mb = 0; mb < 2; mb++)
+    for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-        for (int nb = 0; nb < 8; nb++)
+        for (int nb = 0; nb < 4; nb++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int r = wave * 32 + mb * 16 + (lane >> 4) * 4 + i, c = nb * 16 + (lane & 15);
+                const int r = wm * 64 + mb * 16 + (lane >> 4) * 4 + i, c = wn * 64 + nb * 16 + (lane & 15);
                 if (t0 + r < T) {
                     float v = acc[mb][nb][i];
                     if (bias) v += bias[e0 + c];
@@ -206,7 +253,7 @@ k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const float *__re
                 }
             }
     // ||x_t||_2 of this block's tokens (first column block only)
-    if (blockIdx.y == 0 && threadIdx.x < BM && t0 + (int)threadIdx.x < T) {
+    if (et == 0 && threadIdx.x < BM && t0 + (int)threadIdx.x < T) {
         const uint16_t *xr = x + (size_t)(t0 + threadIdx.x) * H;
         double s = 0.0;
         for (int k = 0; k < H; k += 8) {
@@ -461,17 +508,19 @@ __global__ void __launch_bounds__(256)
 k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int which, const int *__restrict__ off,
           const int *__restrict__ p_tok, const int *__restrict__ p_slot, const float *__restrict__ p_wt,
           const uint16_t *__restrict__ A, int Kdim, int Nrows, GroupW g0, GroupW g1, int E,
-          uint16_t *__restrict__ hid, float *__restrict__ part, int Hout) {
-    __shared__ __align__(16) uint16_t lds[2][2][BM * LDS_STRIDE];
-    __shared__ int arow[BM], brow[BN];
+          uint16_t *__restrict__ hid, float *__restrict__ part, int Hout, int ntiles) {
+    __shared__ __align__(16) TileLds lds;
+    __shared__ int arow[BM];
+    __shared__ const char *bptr[BN];
     __shared__ float rsum[BM];
-    if ((int)blockIdx.x >= n_items[which]) return;
-    const int4 it = items[blockIdx.x];
+    int mi, ni;
+    xcd_tile(blockIdx.x, ntiles, mi, ni);
+    if (mi * ntiles >= n_items[which]) return;
+    const int4 it = items[mi * ntiles + ni];
     const int grp = it.x, r0 = it.y, rows = it.z, nt = it.w;
     const int pbase = off[grp] + r0;
     const int8_t *Wb;
     const float *Sb;
-    long ldb = Kdim;
     if (grp < E) { Wb = g0.w + (size_t)grp * Nrows * Kdim; Sb = g0.s + (size_t)grp * Nrows; }
     else { Wb = g0.w_sh; Sb = g0.s_sh; }
     const int8_t *Wb2 = nullptr;
@@ -487,38 +536,45 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     }
     if (threadIdx.x < BN) {
         const int n = threadIdx.x;
-        // gate/up: rows 0..63 = gate rows [64 nt, +64), rows 64..127 = the same up rows
-        brow[n] = GATEUP ? (nt * 64 + (n & 63)) : (nt * BN + n);
+        if (GATEUP) {
+            // wave column half wn = n / 64 holds intermediate rows [64 nt + 32 wn, +32):
+            // its n-blocks 0, 1 are their gate rows and n-blocks 2, 3 the same up rows
+            const int wn = n >> 6, q = (n >> 4) & 3, o = nt * 64 + wn * 32 + (q & 1) * 16 + (n & 15);
+            bptr[n] = reinterpret_cast<const char *>((q < 2 ? Wb : Wb2) + (size_t)o * Kdim);
+        } else {
+            bptr[n] = reinterpret_cast<const char *>(Wb + (size_t)(nt * BN + n) * Kdim);
+        }
     }
     __syncthreads();
-    f32x4_t acc[2][8];
-    TileEngine<true>::run(A, Kdim, arow, Wb, GATEUP ? (const void *)Wb2 : (const void *)Wb, GATEUP ? 64 : BN, ldb,
-                          brow, Kdim, lds, acc, rsum);
+    f32x4_t acc[4][4];
+    TileEngine2<true, kStagesI8>::run(A, Kdim, arow, bptr, Kdim, lds, acc, rsum);
     __syncthreads();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave >> 1, wn = wave & 1;
     if (GATEUP) {
 #pragma unroll
-        for (int mb = 0; mb < 2; mb++)
+        for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-            for (int nb = 0; nb < 4; nb++)
+            for (int nb = 0; nb < 2; nb++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int r = wave * 32 + mb * 16 + (lane >> 4) * 4 + i, n = nt * 64 + nb * 16 + (lane & 15);
+                    const int r = wm * 64 + mb * 16 + (lane >> 4) * 4 + i;
+                    const int o = nt * 64 + wn * 32 + nb * 16 + (lane & 15);
                     if (r < rows) {
                         const float cr = 128.0f * rsum[r];
-                        const float gv = (acc[mb][nb][i] - cr) * Sb[n];
-                        const float uv = (acc[mb][nb + 4][i] - cr) * Sb2[n];
-                        hid[(size_t)(pbase + r) * Nrows + n] = f32_to_bf16(silu(gv) * uv);
+                        const float gv = (acc[mb][nb][i] - cr) * Sb[o];
+                        const float uv = (acc[mb][nb + 2][i] - cr) * Sb2[o];
+                        hid[(size_t)(pbase + r) * Nrows + o] = f32_to_bf16(silu(gv) * uv);
                     }
                 }
     } else {
 #pragma unroll
-        for (int mb = 0; mb < 2; mb++)
+        for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-            for (int nb = 0; nb < 8; nb++)
+            for (int nb = 0; nb < 4; nb++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int r = wave * 32 + mb * 16 + (lane >> 4) * 4 + i, c = nt * BN + nb * 16 + (lane & 15);
+                    const int r = wm * 64 + mb * 16 + (lane >> 4) * 4 + i;
+                    const int c = nt * BN + wn * 64 + nb * 16 + (lane & 15);
                     if (r < rows) {
                         const int p = pbase + r;
                         const float v = (acc[mb][nb][i] - 128.0f * rsum[r]) * Sb[c];
@@ -551,7 +607,7 @@ size_t prefill_ws_bytes(int T) {
     b += al(4 * 8);                        // counters
     b += al((size_t)(c.E + 2) * 4);        // off
     b += al((size_t)((size_t)T * c.K + kPairsPerBlk - 1) / kPairsPerBlk * c.E * 4);   // per-block counts
-    const size_t max_mt = P / BM + c.E + 2;
+    const size_t max_mt = (P / BM + c.E + 2 + 7) / 8 * 8;
     b += al(max_mt * (c.I / 64) * 16) + al(max_mt * (c.H / BN) * 16);   // item lists
     b += al(P * 4) * 3;                    // p_tok, p_slot, p_wt
     b += al(P * c.I * 2);                  // hidden bf16
@@ -592,7 +648,7 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     int *off = reinterpret_cast<int *>(b); b += al((size_t)(E + 2) * 4);
     const int nblk = (int)(((size_t)T * K + kPairsPerBlk - 1) / kPairsPerBlk);
     int *blk = reinterpret_cast<int *>(b); b += al((size_t)nblk * E * 4);
-    const size_t max_mt = P / BM + E + 2;
+    const size_t max_mt = (P / BM + E + 2 + 7) / 8 * 8;   // bound on m-tiles, a multiple of 8
     const int nt_gu = I / 64, nt_dn = H / BN;
     int4 *items_gu = reinterpret_cast<int4 *>(b); b += al(max_mt * nt_gu * 16);
     int4 *items_dn = reinterpret_cast<int4 *>(b); b += al(max_mt * nt_dn * 16);
@@ -606,7 +662,8 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     // zero the small counters with a fill kernel (no memset node in captured graphs)
     launch_fill_f32(reinterpret_cast<float *>(ctr), 8, 0.0f, s);
     hipLaunchKernelGGL(k_pf_router_prep, dim3(E), dim3(256), 0, s, L->router, E, H, wnorm);
-    hipLaunchKernelGGL(k_pf_router_mfma, dim3((T + BM - 1) / BM, E / BN), dim3(256), 0, s, x, T, H, L->router, E,
+    const int mt_router = ((T + BM - 1) / BM + 7) / 8 * 8;
+    hipLaunchKernelGGL(k_pf_router_mfma, dim3(mt_router * (E / BN)), dim3(256), 0, s, x, T, H, L->router, E,
                        L->router_bias, lg, xnorm);
     if (H == 2048)
         hipLaunchKernelGGL((k_pf_select<8, 8>), dim3((T + 3) / 4), dim3(256), 0, s, x, T, L->router, L->router_bias,
@@ -623,9 +680,9 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     GroupW gu{a->i8_up, a->i8s_up, L->sh_up.w, L->sh_up.s};
     GroupW gd{a->i8_down, a->i8s_down, L->sh_down.w, L->sh_down.s};
     hipLaunchKernelGGL((k_pf_gemm<true>), dim3((unsigned)(max_mt * nt_gu)), dim3(256), 0, s, items_gu, ctr + 1, 0, off,
-                       p_tok, p_slot, p_wt, x, H, I, gg, gu, E, hid, part, H);
+                       p_tok, p_slot, p_wt, x, H, I, gg, gu, E, hid, part, H, nt_gu);
     hipLaunchKernelGGL((k_pf_gemm<false>), dim3((unsigned)(max_mt * nt_dn)), dim3(256), 0, s, items_dn, ctr + 1, 1, off,
-                       p_tok, p_slot, p_wt, hid, I, H, gd, gd, E, hid, part, H);
+                       p_tok, p_slot, p_wt, hid, I, H, gd, gd, E, hid, part, H, nt_dn);
     hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)(((size_t)T * H + 255) / 256)), dim3(256), 0, s, part, T, S, H, y);
     return check_launch("prefill");
 }
