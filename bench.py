@@ -221,7 +221,10 @@ def main():
     ap.add_argument("--cpu-layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the M=8 INT8 / NVFP4 lines")
+    ap.add_argument("--no-extra", action="store_true", help="skip the M=8 INT8 / NVFP4 / prefill lines")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="before the timed region, one device-to-device copy of this many MiB (the "
+                         "known-size copy that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     ws_env = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or ws_env != 1:
@@ -251,6 +254,13 @@ def main():
     wsb = lib.qfm_workspace_bytes(1)
     ws = qfm.DevBuf(wsb)
     st.sync()
+    if args.calib_copy_mib > 0:
+        nb = args.calib_copy_mib << 20
+        src, dst = qfm.DevBuf(nb), qfm.DevBuf(nb)
+        qfm.check(lib.qfm_memcpy_d2d(dst.ptr, src.ptr, nb), "calibration copy")
+        qfm.check(lib.qfm_device_sync(), "sync")
+        src.free()
+        dst.free()
 
     def enqueue_step():
         qfm.check(lib.qfm_moe_forward_layers(arr, nl, x.ptr, H, 1, y.ptr, H, ws.ptr, wsb, st.h), "forward")
@@ -316,6 +326,17 @@ def main():
         cpu = cpu_baseline(args.cpu_layers, args.cpu_seconds, threads)
         log("cpu baseline", cpu)
 
+    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    # FETCH_SIZE / WRITE_SIZE runs (scaled by a known-size copy); see profiles/
+    traffic, traffic_src = None, None
+    tpath = os.path.join(ROOT, "profiles", "m1_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tj = json.load(f)
+        kname = SEC_NAMES[dom].split()[0]
+        if kname in tj.get("kernels", {}):
+            traffic = tj["kernels"][kname]["traffic_bytes"]
+            traffic_src = "profiles/m1_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
     out = {
         "metric": "MoE-layer us/token at M=1 & M=8 (HBM GB/s, % peak); prefill MoE tok/s",
         "value": round(us_layer, 3),
@@ -333,7 +354,8 @@ def main():
                    "hidden": H, "inter": I, "experts": E, "top_k": K, "shared_experts": 1,
                    "layers": nl, "rows": 1, "graph": graph is not None},
         "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": SEC_NAMES[dom], "algorithmic_bytes_per_launch": SEC_BYTES[dom],
                      "avg_launch_us": round(sec_us[dom], 3),
                      "sections_us": {SEC_NAMES[i].split()[0]: round(sec_us[i], 3) for i in range(3)},

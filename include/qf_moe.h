@@ -334,6 +334,7 @@ void  *qfm_dev_malloc(size_t bytes);
 int    qfm_dev_free(void *p);
 int    qfm_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int    qfm_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int    qfm_memcpy_d2d(void *dst, const void *src, size_t bytes);   /* device copy (runtime blit kernel) */
 int    qfm_memset(void *dst, int value, size_t bytes);
 void  *qfm_stream_create(void);
 int    qfm_stream_destroy(void *s);

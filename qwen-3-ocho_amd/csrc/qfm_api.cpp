@@ -365,6 +365,7 @@ void *qfm_dev_malloc(size_t bytes) {
 int qfm_dev_free(void *p) { return hipFree(p) == hipSuccess ? 0 : -1; }
 int qfm_memcpy_h2d(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1; }
 int qfm_memcpy_d2h(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1; }
+int qfm_memcpy_d2d(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyDeviceToDevice) == hipSuccess ? 0 : -1; }
 int qfm_memset(void *dst, int v, size_t n) { return hipMemset(dst, v, n) == hipSuccess ? 0 : -1; }
 void *qfm_stream_create(void) {
     hipStream_t s = nullptr;

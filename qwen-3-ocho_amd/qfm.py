@@ -122,6 +122,7 @@ _SIGS = {
     "qfm_dev_free": (C.c_int, [vp]),
     "qfm_memcpy_h2d": (C.c_int, [vp, vp, C.c_size_t]),
     "qfm_memcpy_d2h": (C.c_int, [vp, vp, C.c_size_t]),
+    "qfm_memcpy_d2d": (C.c_int, [vp, vp, C.c_size_t]),
     "qfm_memset": (C.c_int, [vp, C.c_int, C.c_size_t]),
     "qfm_stream_create": (vp, []),
     "qfm_stream_destroy": (C.c_int, [vp]),
