@@ -183,23 +183,29 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
         float ag = 0.0f, au = 0.0f, xsum = 0.0f;
 #pragma unroll
         for (int st = 0; st < NST; st++) {
-            float xs[F::VPC];
             const uint16_t *p = xt + (st * LPR + l) * F::VPC;
-#pragma unroll
-            for (int q = 0; q < F::VPC / 8; q++) {
-                const uint4 a = *reinterpret_cast<const uint4 *>(p + q * 8);
-                const uint32_t d[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-                for (int b = 0; b < 4; b++) { xs[q * 8 + 2 * b] = bf16_lo(d[b]); xs[q * 8 + 2 * b + 1] = bf16_hi(d[b]); }
-            }
             if constexpr (F::VPB == 1) {
+                float xs[F::VPC];
+#pragma unroll
+                for (int q = 0; q < F::VPC / 8; q++) {
+                    const uint4 a = *reinterpret_cast<const uint4 *>(p + q * 8);
+                    const uint32_t d[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+                    for (int b = 0; b < 4; b++) { xs[q * 8 + 2 * b] = bf16_lo(d[b]); xs[q * 8 + 2 * b + 1] = bf16_hi(d[b]); }
+                }
 #pragma unroll
                 for (int i = 0; i < 16; i++) xsum += xs[i];
                 ag = dot16_u8(wg[st], xs, ag);
                 au = dot16_u8(wu[st], xs, au);
             } else {
-                ag += f4_chunk(wg[st], bg[st], xs);
-                au += f4_chunk(wu[st], bu[st], xs);
+                uint32_t xw[16];                     // the 32 bf16 activations as packed pairs
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint4 a = *reinterpret_cast<const uint4 *>(p + q * 8);
+                    xw[4 * q] = a.x; xw[4 * q + 1] = a.y; xw[4 * q + 2] = a.z; xw[4 * q + 3] = a.w;
+                }
+                ag += f4_chunk_bx(wg[st], bg[st], xw);
+                au += f4_chunk_bx(wu[st], bu[st], xw);
             }
         }
         if constexpr (F::VPB == 1) { ag = fmaf(-128.0f, xsum, ag); au = fmaf(-128.0f, xsum, au); }

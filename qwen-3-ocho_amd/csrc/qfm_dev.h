@@ -229,6 +229,35 @@ __device__ __forceinline__ float f4_chunk(uint4 w, uint32_t s2b, const float *x)
     return fmaf(e4m3_scale(s2b & 0xFFu), g0, e4m3_scale((s2b >> 8) & 0xFFu) * g1);
 }
 
+// NVFP4 chunk against bf16 activations: 32 e2m1 codes (w) with two e4m3 block
+// scales (s2b) dotted with 32 bf16 values held as 16 packed pairs (xw[i] =
+// x[2i] | x[2i+1] << 16, the memory order). gfx950 converts each code pair to
+// a bf16 pair (v_cvt_scalef32_pk_bf16_fp4, unit scale: exact) and
+// v_dot2_f32_bf16 multiplies a pair with fp32 accumulation (bf16 products
+// are exact in fp32), so one conversion and one dot per two weights.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float f4_group16_bx(uint32_t lo, uint32_t hi, const uint32_t *xw) {
+    float a = 0.0f;
+    const uint32_t w[2] = {lo, hi};
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+        a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 0),
+                                            __builtin_bit_cast(bf16x2_t, xw[d * 4 + 0]), a, false);
+        a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 1),
+                                            __builtin_bit_cast(bf16x2_t, xw[d * 4 + 1]), a, false);
+        a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 2),
+                                            __builtin_bit_cast(bf16x2_t, xw[d * 4 + 2]), a, false);
+        a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 3),
+                                            __builtin_bit_cast(bf16x2_t, xw[d * 4 + 3]), a, false);
+    }
+    return a;
+}
+__device__ __forceinline__ float f4_chunk_bx(uint4 w, uint32_t s2b, const uint32_t *xw) {
+    const float g0 = f4_group16_bx(w.x, w.y, xw);
+    const float g1 = f4_group16_bx(w.z, w.w, xw + 8);
+    return fmaf(e4m3_scale(s2b & 0xFFu), g0, e4m3_scale((s2b >> 8) & 0xFFu) * g1);
+}
+
 // ---- Philox-4x32-10 (Salmon et al. 2011) ------------------------------------
 struct u4 { uint32_t v[4]; };
 __device__ __forceinline__ u4 philox(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,

@@ -50,7 +50,7 @@ constexpr int kCandMax = 64;
 
 // bf16 bits of an exactly representable value (integers |v| <= 256): truncation is exact
 __device__ __forceinline__ uint32_t pack_bf16_exact(float lo, float hi) {
-    return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);   // high halves
 }
 __device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
     return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
@@ -98,7 +98,7 @@ __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict_
 // zeros). B rows: int8 (staged as bf16 in offset-binary form u = q + 128,
 // exact) or fp32 (rounded to bf16), row n at bptr[n] (bytes). K % BK2 == 0.
 // acc[mb][nb][i] = C[64 wm + 16 mb + 4 (lane >> 4) + i][64 wn + 16 nb + (lane & 15)],
-// wave = 2 wm + wn. rowsum_out[r] = sum_k A[r][k] when requested.
+// wave = 2 wm + wn.
 constexpr int BK2 = 64;
 constexpr int LDS2 = BK2 + 8;                  // bf16 elements per LDS row (144 bytes)
 struct TileLds {
@@ -108,8 +108,7 @@ struct TileLds {
 template <bool B_I8, int D>
 struct TileEngine2 {
     __device__ static void run(const uint16_t *__restrict__ A, long lda, const int *arow,
-                               const char *const *bptr, int K, TileLds &L, f32x4_t (&acc)[4][4],
-                               float *rowsum_out) {
+                               const char *const *bptr, int K, TileLds &L, f32x4_t (&acc)[4][4]) {
         constexpr int NB = B_I8 ? 2 : 8;
         const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
         const int wm = wave >> 1, wn = wave & 1;
@@ -117,7 +116,6 @@ struct TileEngine2 {
         const int ar = arow[sr];
         const uint16_t *ap = A + (ar >= 0 ? (long)ar * lda : 0) + sh;
         const char *bp = bptr[sr];
-        float rsum = 0.0f;
         uint4 ra[D][4], rb[D][NB];
         auto gload = [&](int k0, uint4 (&a)[4], uint4 (&bb)[NB]) {
 #pragma unroll
@@ -136,14 +134,6 @@ struct TileEngine2 {
             uint4 *la = reinterpret_cast<uint4 *>(&L.a[buf][sr * LDS2 + sh]);
 #pragma unroll
             for (int q = 0; q < 4; q++) la[q] = a[q];
-            if (rowsum_out) {
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint32_t d[4] = {a[q].x, a[q].y, a[q].z, a[q].w};
-#pragma unroll
-                    for (int u = 0; u < 4; u++) rsum += bf16_lo(d[u]) + bf16_hi(d[u]);
-                }
-            }
             uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][sr * LDS2 + sh]);
             if constexpr (B_I8) {
 #pragma unroll
@@ -205,10 +195,6 @@ struct TileEngine2 {
                 __syncthreads();
             }
         }
-        if (rowsum_out) {
-            rsum += __shfl_xor(rsum, 1, WAVE);
-            if ((t & 1) == 0) rowsum_out[sr] = rsum;
-        }
     }
 };
 
@@ -225,7 +211,8 @@ __device__ __forceinline__ void xcd_tile(int b, int nt, int &m, int &n) {
 // ---- router GEMM: logits~ [T][E] --------------------------------------------------
 __global__ void __launch_bounds__(256)
 k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const float *__restrict__ W, int E,
-                 const float *__restrict__ bias, float *__restrict__ lg_approx, float *__restrict__ xnorm) {
+                 const float *__restrict__ bias, float *__restrict__ lg_approx, float *__restrict__ xnorm,
+                 float *__restrict__ xsum) {
     __shared__ __align__(16) TileLds lds;
     __shared__ int arow[BM];
     __shared__ const char *bptr[BN];
@@ -237,7 +224,7 @@ k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const float *__re
     if (threadIdx.x < BN) bptr[threadIdx.x] = reinterpret_cast<const char *>(W + (size_t)(e0 + threadIdx.x) * H);
     __syncthreads();
     f32x4_t acc[4][4];
-    TileEngine2<false, kStagesF32>::run(x, H, arow, bptr, H, lds, acc, nullptr);
+    TileEngine2<false, kStagesF32>::run(x, H, arow, bptr, H, lds, acc);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave >> 1, wn = wave & 1;
 #pragma unroll
     for (int mb = 0; mb < 4; mb++)
@@ -256,6 +243,7 @@ k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const float *__re
     if (et == 0 && threadIdx.x < BM && t0 + (int)threadIdx.x < T) {
         const uint16_t *xr = x + (size_t)(t0 + threadIdx.x) * H;
         double s = 0.0;
+        float sx = 0.0f;
         for (int k = 0; k < H; k += 8) {
             const uint4 p = *reinterpret_cast<const uint4 *>(xr + k);
             const uint32_t d[4] = {p.x, p.y, p.z, p.w};
@@ -263,9 +251,11 @@ k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const float *__re
             for (int q = 0; q < 4; q++) {
                 const double a = bf16_lo(d[q]), b = bf16_hi(d[q]);
                 s += a * a + b * b;
+                sx += bf16_lo(d[q]) + bf16_hi(d[q]);
             }
         }
         xnorm[t0 + threadIdx.x] = (float)(sqrt(s) * (1.0 + 1e-6));
+        xsum[t0 + threadIdx.x] = sx;
     }
 }
 
@@ -508,11 +498,12 @@ __global__ void __launch_bounds__(256)
 k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int which, const int *__restrict__ off,
           const int *__restrict__ p_tok, const int *__restrict__ p_slot, const float *__restrict__ p_wt,
           const uint16_t *__restrict__ A, int Kdim, int Nrows, GroupW g0, GroupW g1, int E,
-          uint16_t *__restrict__ hid, float *__restrict__ part, int Hout, int ntiles) {
+          uint16_t *__restrict__ hid, float *__restrict__ part, int Hout, int ntiles,
+          const float *__restrict__ xsum, float *__restrict__ hsum, int nt_gu) {
     __shared__ __align__(16) TileLds lds;
     __shared__ int arow[BM];
     __shared__ const char *bptr[BN];
-    __shared__ float rsum[BM];
+    __shared__ float rsum[BM], hrow[BM];
     int mi, ni;
     xcd_tile(blockIdx.x, ntiles, mi, ni);
     if (mi * ntiles >= n_items[which]) return;
@@ -529,10 +520,22 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
         if (grp < E) { Wb2 = g1.w + (size_t)grp * Nrows * Kdim; Sb2 = g1.s + (size_t)grp * Nrows; }
         else { Wb2 = g1.w_sh; Sb2 = g1.s_sh; }
     }
+    // A row sums (the offset-binary correction): x rows' sums for gate/up; for
+    // down, the sum of the nt_gu per-tile partial sums the gate/up epilogue
+    // wrote for the pair's bf16 hidden row (fixed order: deterministic)
     if (threadIdx.x < BM) {
         const int r = threadIdx.x;
-        if (GATEUP) arow[r] = r < rows ? p_tok[pbase + r] : -1;
-        else arow[r] = r < rows ? pbase + r : -1;
+        float rs = 0.0f;
+        if (GATEUP) {
+            arow[r] = r < rows ? p_tok[pbase + r] : -1;
+            if (r < rows) rs = xsum[arow[r]];
+        } else {
+            arow[r] = r < rows ? pbase + r : -1;
+            if (r < rows)
+                for (int q = 0; q < nt_gu; q++) rs += hsum[(size_t)(pbase + r) * nt_gu + q];
+        }
+        rsum[r] = rs;
+        if (GATEUP) hrow[r] = 0.0f;
     }
     if (threadIdx.x < BN) {
         const int n = threadIdx.x;
@@ -547,10 +550,11 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     }
     __syncthreads();
     f32x4_t acc[4][4];
-    TileEngine2<true, kStagesI8>::run(A, Kdim, arow, bptr, Kdim, lds, acc, rsum);
+    TileEngine2<true, kStagesI8>::run(A, Kdim, arow, bptr, Kdim, lds, acc);
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave >> 1, wn = wave & 1;
     if (GATEUP) {
+        float hsacc[4][4] = {};
 #pragma unroll
         for (int mb = 0; mb < 4; mb++)
 #pragma unroll
@@ -559,13 +563,30 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
                 for (int i = 0; i < 4; i++) {
                     const int r = wm * 64 + mb * 16 + (lane >> 4) * 4 + i;
                     const int o = nt * 64 + wn * 32 + nb * 16 + (lane & 15);
+                    float hs = 0.0f;
                     if (r < rows) {
                         const float cr = 128.0f * rsum[r];
                         const float gv = (acc[mb][nb][i] - cr) * Sb[o];
                         const float uv = (acc[mb][nb + 2][i] - cr) * Sb2[o];
-                        hid[(size_t)(pbase + r) * Nrows + o] = f32_to_bf16(silu(gv) * uv);
+                        const uint16_t hb = f32_to_bf16(silu(gv) * uv);
+                        hid[(size_t)(pbase + r) * Nrows + o] = hb;
+                        hs = bf16_to_f32(hb);
                     }
+                    hsacc[mb][i] += hs;
                 }
+        // per-row sum of this tile's 64 bf16 hidden values: 16 columns in the
+        // lanes of a row group, two n-blocks here, the other 32 in wave wn ^ 1
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float v = hsacc[mb][i];
+#pragma unroll
+                for (int m = 1; m < 16; m <<= 1) v += __shfl_xor(v, m, WAVE);
+                if ((lane & 15) == 0) atomicAdd(&hrow[wm * 64 + mb * 16 + (lane >> 4) * 4 + i], v);
+            }
+        __syncthreads();
+        if (threadIdx.x < rows) hsum[(size_t)(pbase + threadIdx.x) * nt_gu + nt] = hrow[threadIdx.x];
     } else {
 #pragma unroll
         for (int mb = 0; mb < 4; mb++)
@@ -612,6 +633,8 @@ size_t prefill_ws_bytes(int T) {
     b += al(P * 4) * 3;                    // p_tok, p_slot, p_wt
     b += al(P * c.I * 2);                  // hidden bf16
     b += al(P * c.H * 4);                  // partials
+    b += al((size_t)T * 4);                // x row sums
+    b += al(P * (c.I / 64) * 4);           // hidden row sums per gate/up n-tile
     return b;
 }
 
@@ -656,7 +679,9 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     int *p_slot = reinterpret_cast<int *>(b); b += al(P * 4);
     float *p_wt = reinterpret_cast<float *>(b); b += al(P * 4);
     uint16_t *hid = reinterpret_cast<uint16_t *>(b); b += al(P * I * 2);
-    float *part = reinterpret_cast<float *>(b);
+    float *part = reinterpret_cast<float *>(b); b += al(P * H * 4);
+    float *xsum = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
+    float *hsum = reinterpret_cast<float *>(b);
 
     const float *g = (has_sh && gated) ? L->sh_gate_inp : nullptr;
     // zero the small counters with a fill kernel (no memset node in captured graphs)
@@ -664,7 +689,7 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     hipLaunchKernelGGL(k_pf_router_prep, dim3(E), dim3(256), 0, s, L->router, E, H, wnorm);
     const int mt_router = ((T + BM - 1) / BM + 7) / 8 * 8;
     hipLaunchKernelGGL(k_pf_router_mfma, dim3(mt_router * (E / BN)), dim3(256), 0, s, x, T, H, L->router, E,
-                       L->router_bias, lg, xnorm);
+                       L->router_bias, lg, xnorm, xsum);
     if (H == 2048)
         hipLaunchKernelGGL((k_pf_select<8, 8>), dim3((T + 3) / 4), dim3(256), 0, s, x, T, L->router, L->router_bias,
                            g, lg, xnorm, wnorm, K, c.renorm, sel, wts, gam, ctr);
@@ -680,9 +705,9 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     GroupW gu{a->i8_up, a->i8s_up, L->sh_up.w, L->sh_up.s};
     GroupW gd{a->i8_down, a->i8s_down, L->sh_down.w, L->sh_down.s};
     hipLaunchKernelGGL((k_pf_gemm<true>), dim3((unsigned)(max_mt * nt_gu)), dim3(256), 0, s, items_gu, ctr + 1, 0, off,
-                       p_tok, p_slot, p_wt, x, H, I, gg, gu, E, hid, part, H, nt_gu);
+                       p_tok, p_slot, p_wt, x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu);
     hipLaunchKernelGGL((k_pf_gemm<false>), dim3((unsigned)(max_mt * nt_dn)), dim3(256), 0, s, items_dn, ctr + 1, 1, off,
-                       p_tok, p_slot, p_wt, hid, I, H, gd, gd, E, hid, part, H, nt_dn);
+                       p_tok, p_slot, p_wt, hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu);
     hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)(((size_t)T * H + 255) / 256)), dim3(256), 0, s, part, T, S, H, y);
     return check_launch("prefill");
 }
