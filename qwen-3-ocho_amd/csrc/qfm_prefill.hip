@@ -30,11 +30,12 @@
 //                      so y does not depend on it) and the GEMM work lists.
 //   k_pf_gemm<GATEUP>  hidden[p][n] = silu(sg (x_p . Wg_n)) * (su (x_p . Wu_n))
 //   k_pf_gemm<DOWN>    part[slot_p][c] = w_p * sd_c * (h_p . Wd_c)
-//                      Both: BM=128 rows x BN=128 weight rows x BK=64, 2 x 2
+//                      Both: BM=128 rows x BN=256 weight rows x BK=64, 2 x 4
 //                      waves of 64 x 64, v_mfma_f32_16x16x32_bf16; int8 weights are
 //                      staged to LDS as bf16 in offset-binary form
 //                      (u = q + 128 is exact in bf16) and the row sum of A
-//                      times 128 is subtracted in the epilogue.
+//                      (precomputed: x sums in the router, hidden sums in the
+//                      gate/up epilogue) times 128 is subtracted in the epilogue.
 //   k_pf_combine       y[t] = sum over the K+1 slots of t, in slot order.
 #include "qfm_dev.h"
 #include "qfm_internal.h"
@@ -45,7 +46,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128;
-constexpr int kStagesI8 = 2, kStagesF32 = 2;   // register stages of global loads in flight
+constexpr int kStagesI8 = 3, kStagesF32 = 2;   // register stages of global loads in flight
 constexpr int kCandMax = 64;
 
 // bf16 bits of an exactly representable value (integers |v| <= 256): truncation is exact
@@ -89,68 +90,79 @@ __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict_
 }
 
 // ---- the MFMA tile engine ---------------------------------------------------------
-// Block tile BM x BN = 128 x 128, k-step BK2 = 64 (two 32-deep MFMA steps),
-// 256 threads = 2 x 2 waves, each wave a 64 x 64 sub-tile = 4 x 4
-// v_mfma_f32_16x16x32_bf16 accumulators. Two LDS buffers (the k-step being
-// multiplied and the next one) and D register stages of global loads in
-// flight, one barrier per k-step.
+// Block tile (64 WM) x (64 WN), WM x WN waves of 64 x 64 (4 x 4
+// v_mfma_f32_16x16x32_bf16 accumulators each), k-step BK2 = 64 (two 32-deep
+// MFMA steps). Two LDS buffers (the k-step being multiplied and the next one)
+// and D register stages of global loads in flight, one barrier per k-step.
 // A rows: bf16, row r at A + arow[r] * lda (arow < 0: absent row, staged as
 // zeros). B rows: int8 (staged as bf16 in offset-binary form u = q + 128,
 // exact) or fp32 (rounded to bf16), row n at bptr[n] (bytes). K % BK2 == 0.
 // acc[mb][nb][i] = C[64 wm + 16 mb + 4 (lane >> 4) + i][64 wn + 16 nb + (lane & 15)],
-// wave = 2 wm + wn.
+// wave = WN wm + wn. Staging: 16-byte chunks, consecutive threads on
+// consecutive chunks of a row (A: 8 chunks per row, B: 4 int8 / 16 fp32).
 constexpr int BK2 = 64;
 constexpr int LDS2 = BK2 + 8;                  // bf16 elements per LDS row (144 bytes)
+template <int BMt, int BNt>
 struct TileLds {
-    uint16_t a[2][BM * LDS2];
-    uint16_t b[2][BN * LDS2];
+    uint16_t a[2][BMt * LDS2];
+    uint16_t b[2][BNt * LDS2];
 };
-template <bool B_I8, int D>
+template <bool B_I8, int WM, int WN, int D>
 struct TileEngine2 {
+    static constexpr int BMt = 64 * WM, BNt = 64 * WN, NT = 64 * WM * WN;
+    static constexpr int BCPR = B_I8 ? 4 : 16;                   // B chunks per row per k-step
+    static constexpr int NA = BMt * 8 / NT, NB = BNt * BCPR / NT;  // chunks per thread
+    static_assert(NA * NT == BMt * 8 && NB * NT == BNt * BCPR, "staging must divide evenly");
     __device__ static void run(const uint16_t *__restrict__ A, long lda, const int *arow,
-                               const char *const *bptr, int K, TileLds &L, f32x4_t (&acc)[4][4]) {
-        constexpr int NB = B_I8 ? 2 : 8;
+                               const char *const *bptr, int K, TileLds<BMt, BNt> &L, f32x4_t (&acc)[4][4]) {
         const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-        const int wm = wave >> 1, wn = wave & 1;
-        const int sr = t >> 1, sh = (t & 1) * 32;           // staging: row, first k of this thread's half
-        const int ar = arow[sr];
-        const uint16_t *ap = A + (ar >= 0 ? (long)ar * lda : 0) + sh;
-        const char *bp = bptr[sr];
-        uint4 ra[D][4], rb[D][NB];
-        auto gload = [&](int k0, uint4 (&a)[4], uint4 (&bb)[NB]) {
+        const int wm = wave / WN, wn = wave % WN;
+        const uint16_t *ap[NA];
+        int a_lds[NA];
+        bool a_ok[NA];
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-                a[q] = ar >= 0 ? *reinterpret_cast<const uint4 *>(ap + k0 + 8 * q) : make_uint4(0, 0, 0, 0);
-            if constexpr (B_I8) {
+        for (int j = 0; j < NA; j++) {
+            const int c = t + j * NT, r = c >> 3, kc = c & 7;
+            const int ar = arow[r];
+            a_ok[j] = ar >= 0;
+            ap[j] = A + (ar >= 0 ? (long)ar * lda : 0) + kc * 8;
+            a_lds[j] = r * LDS2 + kc * 8;
+        }
+        const char *bp[NB];
+        int b_lds[NB];
 #pragma unroll
-                for (int q = 0; q < NB; q++) bb[q] = ld_nt16(bp + k0 + sh + 16 * q);
-            } else {
+        for (int j = 0; j < NB; j++) {
+            const int c = t + j * NT, r = c / BCPR, kc = c % BCPR;
+            bp[j] = bptr[r] + (B_I8 ? kc * 16 : kc * 16);
+            b_lds[j] = r * LDS2 + (B_I8 ? kc * 16 : kc * 4);
+        }
+        uint4 ra[D][NA], rb[D][NB];
+        auto gload = [&](int k0, uint4 (&a)[NA], uint4 (&bb)[NB]) {
 #pragma unroll
-                for (int q = 0; q < NB; q++)
-                    bb[q] = *reinterpret_cast<const uint4 *>(bp + (size_t)(k0 + sh) * 4 + 16 * q);
+            for (int j = 0; j < NA; j++)
+                a[j] = a_ok[j] ? *reinterpret_cast<const uint4 *>(ap[j] + k0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                if constexpr (B_I8) bb[j] = ld_nt16(bp[j] + k0);
+                else bb[j] = *reinterpret_cast<const uint4 *>(bp[j] + (size_t)k0 * 4);
             }
         };
-        auto sstore = [&](int buf, const uint4 (&a)[4], const uint4 (&bb)[NB]) {
-            uint4 *la = reinterpret_cast<uint4 *>(&L.a[buf][sr * LDS2 + sh]);
+        auto sstore = [&](int buf, const uint4 (&a)[NA], const uint4 (&bb)[NB]) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) la[q] = a[q];
-            uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][sr * LDS2 + sh]);
-            if constexpr (B_I8) {
+            for (int j = 0; j < NA; j++) *reinterpret_cast<uint4 *>(&L.a[buf][a_lds[j]]) = a[j];
 #pragma unroll
-                for (int q = 0; q < 2; q++) {
+            for (int j = 0; j < NB; j++) {
+                if constexpr (B_I8) {
                     uint4 o0, o1;
-                    i8_to_bf16_ob(bb[q], o0, o1);
-                    lb[2 * q] = o0;
-                    lb[2 * q + 1] = o1;
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint4 f0 = bb[2 * q], f1 = bb[2 * q + 1];
-                    lb[q] = make_uint4(pack_bf16_rne(__uint_as_float(f0.x), __uint_as_float(f0.y)),
-                                       pack_bf16_rne(__uint_as_float(f0.z), __uint_as_float(f0.w)),
-                                       pack_bf16_rne(__uint_as_float(f1.x), __uint_as_float(f1.y)),
-                                       pack_bf16_rne(__uint_as_float(f1.z), __uint_as_float(f1.w)));
+                    i8_to_bf16_ob(bb[j], o0, o1);
+                    uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]);
+                    lb[0] = o0;
+                    lb[1] = o1;
+                } else {
+                    const uint4 f = bb[j];
+                    *reinterpret_cast<uint2 *>(&L.b[buf][b_lds[j]]) =
+                        make_uint2(pack_bf16_rne(__uint_as_float(f.x), __uint_as_float(f.y)),
+                                   pack_bf16_rne(__uint_as_float(f.z), __uint_as_float(f.w)));
                 }
             }
         };
@@ -197,6 +209,10 @@ struct TileEngine2 {
         }
     }
 };
+// router GEMM: 128 x 128 tiles, 2 x 2 waves; grouped expert GEMMs: 128 x 256, 2 x 4 waves
+using RouterEngine = TileEngine2<false, 2, 2, kStagesF32>;
+using ExpertEngine = TileEngine2<true, 2, 4, kStagesI8>;
+constexpr int GBN = ExpertEngine::BNt;          // weight rows per grouped-GEMM tile
 
 // Workgroups are dispatched to the 8 XCDs round-robin (block b on XCD b % 8).
 // Map block b to tile (m, n) so that the nt n-tiles of one m-tile run back to
@@ -213,7 +229,7 @@ __global__ void __launch_bounds__(256)
 k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const float *__restrict__ W, int E,
                  const float *__restrict__ bias, float *__restrict__ lg_approx, float *__restrict__ xnorm,
                  float *__restrict__ xsum) {
-    __shared__ __align__(16) TileLds lds;
+    __shared__ __align__(16) TileLds<RouterEngine::BMt, RouterEngine::BNt> lds;
     __shared__ int arow[BM];
     __shared__ const char *bptr[BN];
     int mt, et;
@@ -224,7 +240,7 @@ k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const float *__re
     if (threadIdx.x < BN) bptr[threadIdx.x] = reinterpret_cast<const char *>(W + (size_t)(e0 + threadIdx.x) * H);
     __syncthreads();
     f32x4_t acc[4][4];
-    TileEngine2<false, kStagesF32>::run(x, H, arow, bptr, H, lds, acc);
+    RouterEngine::run(x, H, arow, bptr, H, lds, acc);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave >> 1, wn = wave & 1;
 #pragma unroll
     for (int mb = 0; mb < 4; mb++)
@@ -494,16 +510,17 @@ struct GroupW {
 };
 
 template <bool GATEUP>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(ExpertEngine::NT)
 k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int which, const int *__restrict__ off,
           const int *__restrict__ p_tok, const int *__restrict__ p_slot, const float *__restrict__ p_wt,
           const uint16_t *__restrict__ A, int Kdim, int Nrows, GroupW g0, GroupW g1, int E,
           uint16_t *__restrict__ hid, float *__restrict__ part, int Hout, int ntiles,
           const float *__restrict__ xsum, float *__restrict__ hsum, int nt_gu) {
-    __shared__ __align__(16) TileLds lds;
+    constexpr int WN = 4;
+    __shared__ __align__(16) TileLds<BM, GBN> lds;
     __shared__ int arow[BM];
-    __shared__ const char *bptr[BN];
-    __shared__ float rsum[BM], hrow[BM];
+    __shared__ const char *bptr[GBN];
+    __shared__ float rsum[BM], hpart[WN][BM];
     int mi, ni;
     xcd_tile(blockIdx.x, ntiles, mi, ni);
     if (mi * ntiles >= n_items[which]) return;
@@ -535,24 +552,22 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
                 for (int q = 0; q < nt_gu; q++) rs += hsum[(size_t)(pbase + r) * nt_gu + q];
         }
         rsum[r] = rs;
-        if (GATEUP) hrow[r] = 0.0f;
     }
-    if (threadIdx.x < BN) {
+    if (threadIdx.x < GBN) {
         const int n = threadIdx.x;
         if (GATEUP) {
-            // wave column half wn = n / 64 holds intermediate rows [64 nt + 32 wn, +32):
+            // wave column wn = n / 64 holds intermediate rows [128 nt + 32 wn, +32):
             // its n-blocks 0, 1 are their gate rows and n-blocks 2, 3 the same up rows
-            const int wn = n >> 6, q = (n >> 4) & 3, o = nt * 64 + wn * 32 + (q & 1) * 16 + (n & 15);
+            const int wn = n >> 6, q = (n >> 4) & 3, o = nt * 128 + wn * 32 + (q & 1) * 16 + (n & 15);
             bptr[n] = reinterpret_cast<const char *>((q < 2 ? Wb : Wb2) + (size_t)o * Kdim);
         } else {
-            bptr[n] = reinterpret_cast<const char *>(Wb + (size_t)(nt * BN + n) * Kdim);
+            bptr[n] = reinterpret_cast<const char *>(Wb + (size_t)(nt * GBN + n) * Kdim);
         }
     }
     __syncthreads();
     f32x4_t acc[4][4];
-    TileEngine2<true, kStagesI8>::run(A, Kdim, arow, bptr, Kdim, lds, acc);
-    __syncthreads();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave >> 1, wn = wave & 1;
+    ExpertEngine::run(A, Kdim, arow, bptr, Kdim, lds, acc);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave / WN, wn = wave % WN;
     if (GATEUP) {
         float hsacc[4][4] = {};
 #pragma unroll
@@ -562,7 +577,7 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int r = wm * 64 + mb * 16 + (lane >> 4) * 4 + i;
-                    const int o = nt * 64 + wn * 32 + nb * 16 + (lane & 15);
+                    const int o = nt * 128 + wn * 32 + nb * 16 + (lane & 15);
                     float hs = 0.0f;
                     if (r < rows) {
                         const float cr = 128.0f * rsum[r];
@@ -574,8 +589,9 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
                     }
                     hsacc[mb][i] += hs;
                 }
-        // per-row sum of this tile's 64 bf16 hidden values: 16 columns in the
-        // lanes of a row group, two n-blocks here, the other 32 in wave wn ^ 1
+        // per-row sum of this tile's 128 bf16 hidden values: 16 columns in the
+        // lanes of a row group, two n-blocks here, the rest in the other WN - 1
+        // waves of the row; summed in wave order (deterministic)
 #pragma unroll
         for (int mb = 0; mb < 4; mb++)
 #pragma unroll
@@ -583,10 +599,15 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
                 float v = hsacc[mb][i];
 #pragma unroll
                 for (int m = 1; m < 16; m <<= 1) v += __shfl_xor(v, m, WAVE);
-                if ((lane & 15) == 0) atomicAdd(&hrow[wm * 64 + mb * 16 + (lane >> 4) * 4 + i], v);
+                if ((lane & 15) == 0) hpart[wn][wm * 64 + mb * 16 + (lane >> 4) * 4 + i] = v;
             }
         __syncthreads();
-        if (threadIdx.x < rows) hsum[(size_t)(pbase + threadIdx.x) * nt_gu + nt] = hrow[threadIdx.x];
+        if (threadIdx.x < rows) {
+            float v = 0.0f;
+#pragma unroll
+            for (int q = 0; q < WN; q++) v += hpart[q][threadIdx.x];
+            hsum[(size_t)(pbase + threadIdx.x) * nt_gu + nt] = v;
+        }
     } else {
 #pragma unroll
         for (int mb = 0; mb < 4; mb++)
@@ -595,7 +616,7 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int r = wm * 64 + mb * 16 + (lane >> 4) * 4 + i;
-                    const int c = nt * BN + wn * 64 + nb * 16 + (lane & 15);
+                    const int c = nt * GBN + wn * 64 + nb * 16 + (lane & 15);
                     if (r < rows) {
                         const int p = pbase + r;
                         const float v = (acc[mb][nb][i] - 128.0f * rsum[r]) * Sb[c];
@@ -605,6 +626,7 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     }
 }
 
+// y[t] = sum over the K (+ shared) owned partial slots of token t, in slot order
 __global__ void __launch_bounds__(256)
 k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__restrict__ y) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -629,12 +651,12 @@ size_t prefill_ws_bytes(int T) {
     b += al((size_t)(c.E + 2) * 4);        // off
     b += al((size_t)((size_t)T * c.K + kPairsPerBlk - 1) / kPairsPerBlk * c.E * 4);   // per-block counts
     const size_t max_mt = (P / BM + c.E + 2 + 7) / 8 * 8;
-    b += al(max_mt * (c.I / 64) * 16) + al(max_mt * (c.H / BN) * 16);   // item lists
+    b += al(max_mt * (c.I / (GBN / 2)) * 16) + al(max_mt * (c.H / GBN) * 16);   // item lists
     b += al(P * 4) * 3;                    // p_tok, p_slot, p_wt
     b += al(P * c.I * 2);                  // hidden bf16
     b += al(P * c.H * 4);                  // partials
     b += al((size_t)T * 4);                // x row sums
-    b += al(P * (c.I / 64) * 4);           // hidden row sums per gate/up n-tile
+    b += al(P * (c.I / (GBN / 2)) * 4);    // hidden row sums per gate/up n-tile
     return b;
 }
 
@@ -672,7 +694,7 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     const int nblk = (int)(((size_t)T * K + kPairsPerBlk - 1) / kPairsPerBlk);
     int *blk = reinterpret_cast<int *>(b); b += al((size_t)nblk * E * 4);
     const size_t max_mt = (P / BM + E + 2 + 7) / 8 * 8;   // bound on m-tiles, a multiple of 8
-    const int nt_gu = I / 64, nt_dn = H / BN;
+    const int nt_gu = I / (GBN / 2), nt_dn = H / GBN;
     int4 *items_gu = reinterpret_cast<int4 *>(b); b += al(max_mt * nt_gu * 16);
     int4 *items_dn = reinterpret_cast<int4 *>(b); b += al(max_mt * nt_dn * 16);
     int *p_tok = reinterpret_cast<int *>(b); b += al(P * 4);
@@ -704,9 +726,9 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     GroupW gg{a->i8_gate, a->i8s_gate, L->sh_gate.w, L->sh_gate.s};
     GroupW gu{a->i8_up, a->i8s_up, L->sh_up.w, L->sh_up.s};
     GroupW gd{a->i8_down, a->i8s_down, L->sh_down.w, L->sh_down.s};
-    hipLaunchKernelGGL((k_pf_gemm<true>), dim3((unsigned)(max_mt * nt_gu)), dim3(256), 0, s, items_gu, ctr + 1, 0, off,
+    hipLaunchKernelGGL((k_pf_gemm<true>), dim3((unsigned)(max_mt * nt_gu)), dim3(ExpertEngine::NT), 0, s, items_gu, ctr + 1, 0, off,
                        p_tok, p_slot, p_wt, x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu);
-    hipLaunchKernelGGL((k_pf_gemm<false>), dim3((unsigned)(max_mt * nt_dn)), dim3(256), 0, s, items_dn, ctr + 1, 1, off,
+    hipLaunchKernelGGL((k_pf_gemm<false>), dim3((unsigned)(max_mt * nt_dn)), dim3(ExpertEngine::NT), 0, s, items_dn, ctr + 1, 1, off,
                        p_tok, p_slot, p_wt, hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu);
     hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)(((size_t)T * H + 255) / 256)), dim3(256), 0, s, part, T, S, H, y);
     return check_launch("prefill");
