@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict_
 // and D register stages of global loads in flight, one barrier per k-step.
 // A rows: bf16, row r at A + arow[r] * lda (arow < 0: absent row, staged as
 // zeros). B rows: int8 (staged as bf16 in offset-binary form u = q + 128,
-// exact) or fp32 (rounded to bf16), row n at bptr[n] (bytes). K % BK2 == 0.
+// exact), fp32 (rounded to bf16) or bf16, row n at bptr[n] (bytes). K % BK2 == 0.
 // acc[mb][nb][i] = C[64 wm + 16 mb + 4 (lane >> 4) + i][64 wn + 16 nb + (lane & 15)],
 // wave = WN wm + wn. Staging: 16-byte chunks, consecutive threads on
 // consecutive chunks of a row (A: 8 chunks per row, B: 4 int8 / 16 fp32).
@@ -107,10 +107,12 @@ struct TileLds {
     uint16_t a[2][BMt * LDS2];
     uint16_t b[2][BNt * LDS2];
 };
-template <bool B_I8, int WM, int WN, int D>
+enum { kB_I8 = 0, kB_F32 = 1, kB_BF16 = 2 };
+template <int BMODE, int WM, int WN, int D>
 struct TileEngine2 {
+    static constexpr bool B_I8 = BMODE == kB_I8;
     static constexpr int BMt = 64 * WM, BNt = 64 * WN, NT = 64 * WM * WN;
-    static constexpr int BCPR = B_I8 ? 4 : 16;                   // B chunks per row per k-step
+    static constexpr int BCPR = BMODE == kB_I8 ? 4 : BMODE == kB_F32 ? 16 : 8;   // B chunks per row per k-step
     static constexpr int NA = BMt * 8 / NT, NB = BNt * BCPR / NT;  // chunks per thread
     static_assert(NA * NT == BMt * 8 && NB * NT == BNt * BCPR, "staging must divide evenly");
     __device__ static void run(const uint16_t *__restrict__ A, long lda, const int *arow,
@@ -133,8 +135,8 @@ struct TileEngine2 {
 #pragma unroll
         for (int j = 0; j < NB; j++) {
             const int c = t + j * NT, r = c / BCPR, kc = c % BCPR;
-            bp[j] = bptr[r] + (B_I8 ? kc * 16 : kc * 16);
-            b_lds[j] = r * LDS2 + (B_I8 ? kc * 16 : kc * 4);
+            bp[j] = bptr[r] + kc * 16;
+            b_lds[j] = r * LDS2 + (BMODE == kB_I8 ? kc * 16 : BMODE == kB_F32 ? kc * 4 : kc * 8);
         }
         uint4 ra[D][NA], rb[D][NB];
         auto gload = [&](int k0, uint4 (&a)[NA], uint4 (&bb)[NB]) {
@@ -143,8 +145,9 @@ struct TileEngine2 {
                 a[j] = a_ok[j] ? *reinterpret_cast<const uint4 *>(ap[j] + k0) : make_uint4(0, 0, 0, 0);
 #pragma unroll
             for (int j = 0; j < NB; j++) {
-                if constexpr (B_I8) bb[j] = ld_nt16(bp[j] + k0);
-                else bb[j] = *reinterpret_cast<const uint4 *>(bp[j] + (size_t)k0 * 4);
+                if constexpr (BMODE == kB_I8) bb[j] = ld_nt16(bp[j] + k0);
+                else if constexpr (BMODE == kB_F32) bb[j] = *reinterpret_cast<const uint4 *>(bp[j] + (size_t)k0 * 4);
+                else bb[j] = *reinterpret_cast<const uint4 *>(bp[j] + (size_t)k0 * 2);
             }
         };
         auto sstore = [&](int buf, const uint4 (&a)[NA], const uint4 (&bb)[NB]) {
@@ -152,12 +155,14 @@ struct TileEngine2 {
             for (int j = 0; j < NA; j++) *reinterpret_cast<uint4 *>(&L.a[buf][a_lds[j]]) = a[j];
 #pragma unroll
             for (int j = 0; j < NB; j++) {
-                if constexpr (B_I8) {
+                if constexpr (BMODE == kB_I8) {
                     uint4 o0, o1;
                     i8_to_bf16_ob(bb[j], o0, o1);
                     uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]);
                     lb[0] = o0;
                     lb[1] = o1;
+                } else if constexpr (BMODE == kB_BF16) {
+                    *reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]) = bb[j];
                 } else {
                     const uint4 f = bb[j];
                     *reinterpret_cast<uint2 *>(&L.b[buf][b_lds[j]]) =
@@ -210,8 +215,8 @@ struct TileEngine2 {
     }
 };
 // router GEMM: 128 x 128 tiles, 2 x 2 waves; grouped expert GEMMs: 128 x 256, 2 x 4 waves
-using RouterEngine = TileEngine2<false, 2, 2, kStagesF32>;
-using ExpertEngine = TileEngine2<true, 2, 4, kStagesI8>;
+using RouterEngine = TileEngine2<kB_F32, 2, 2, kStagesF32>;
+using ExpertEngine = TileEngine2<kB_I8, 2, 4, kStagesI8>;
 constexpr int GBN = ExpertEngine::BNt;          // weight rows per grouped-GEMM tile
 
 // Workgroups are dispatched to the 8 XCDs round-robin (block b on XCD b % 8).
@@ -626,15 +631,25 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     }
 }
 
-// y[t] = sum over the K (+ shared) owned partial slots of token t, in slot order
+// y[t] = sum over the K (+ shared) owned partial slots of token t, in slot
+// order; four columns per thread (16-byte loads, all S in flight together).
 __global__ void __launch_bounds__(256)
 k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__restrict__ y) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (size_t)T * H) return;
-    const size_t t = i / H, c = i - t * H;
-    float a = 0.0f;
-    for (int k = 0; k < S; k++) a += part[(t * S + k) * H + c];
-    y[i] = f32_to_bf16(a);
+    constexpr int kMaxS = 17;
+    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;       // index of 4 outputs
+    if (i4 * 4 >= (size_t)T * H) return;
+    const size_t t = i4 * 4 / H, c = i4 * 4 - t * H;
+    float4 v[kMaxS];
+#pragma unroll
+    for (int k = 0; k < kMaxS; k++)
+        if (k < S) v[k] = *reinterpret_cast<const float4 *>(part + (t * S + k) * H + c);
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < kMaxS; k++)
+        if (k < S) { a.x += v[k].x; a.y += v[k].y; a.z += v[k].z; a.w += v[k].w; }
+    *reinterpret_cast<uint2 *>(y + t * H + c) =
+        make_uint2((uint32_t)f32_to_bf16(a.x) | ((uint32_t)f32_to_bf16(a.y) << 16),
+                   (uint32_t)f32_to_bf16(a.z) | ((uint32_t)f32_to_bf16(a.w) << 16));
 }
 
 // ---- launcher -------------------------------------------------------------------------
@@ -730,7 +745,8 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
                        p_tok, p_slot, p_wt, x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu);
     hipLaunchKernelGGL((k_pf_gemm<false>), dim3((unsigned)(max_mt * nt_dn)), dim3(ExpertEngine::NT), 0, s, items_dn, ctr + 1, 1, off,
                        p_tok, p_slot, p_wt, hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu);
-    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)(((size_t)T * H + 255) / 256)), dim3(256), 0, s, part, T, S, H, y);
+    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)(((size_t)T * H / 4 + 255) / 256)), dim3(256), 0, s, part, T, S,
+                       H, y);
     return check_launch("prefill");
 }
 
