@@ -169,11 +169,12 @@ def run_nvfp4(lib, st, nl, args):
 MFMA_PEAK_TFLOPS = 2500.0                 # dense bf16 MFMA, MI355X
 
 
-def run_prefill(lib, st, args, T=8038, nl=4):
+def run_prefill(lib, st, args, T=8038, nl=4, fmt=0):
     """one prefill layer of T tokens with a skewed router bias,
-    timed over nl distinct layers (same input rows, one graph)."""
+    timed over nl distinct layers (same input rows, one graph). fmt=1 runs the
+    same workload on NVFP4 routed experts (config 3's arena format)."""
     import qfm
-    layers = [qfm.SynthLayer(qfm.QFM_FMT_INT8, 0, 100 + l, with_bias=True, stream=st) for l in range(nl)]
+    layers = [qfm.SynthLayer(fmt, 0, 100 + l, with_bias=True, stream=st) for l in range(nl)]
     arr = (qfm.QfmLayer * nl)(*[L.s.layer for L in layers])
     x = qfm.DevBuf(T * H * 2)
     y = qfm.DevBuf(nl * T * H * 2)
@@ -196,14 +197,18 @@ def run_prefill(lib, st, args, T=8038, nl=4):
     us_layer = ms * 1000.0 / nl
     flops = 2.0 * T * H * E + 2.0 * T * (K + 1) * 3 * H * I      # router GEMM + routed/shared gate, up, down
     tflops = flops / (us_layer * 1e-6) / 1e12
-    wbytes = float(np.mean(touched)) * EXPERT_BYTES + EXPERT_BYTES + E * H * 4 + 2 * T * H * 2
+    routed_bytes = NVFP4_EXPERT_BYTES if fmt else EXPERT_BYTES
+    wbytes = float(np.mean(touched)) * routed_bytes + EXPERT_BYTES + E * H * 4 + 2 * T * H * 2
     gbs = wbytes / (us_layer * 1e-6) / 1e9
-    log(f"BASELINE config 4: prefill T={T}: {us_layer:.1f} us/layer, {T / (us_layer * 1e-6):.0f} tok/s, "
+    name = "BASELINE config 4" if fmt == 0 else "config 4 on an NVFP4 arena"
+    log(f"{name}: prefill T={T}: {us_layer:.1f} us/layer, {T / (us_layer * 1e-6):.0f} tok/s, "
         f"{tflops:.0f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS * 100:.1f}% bf16 MFMA), experts touched {np.mean(touched):.0f}, "
         f"max load {max(max_load)}")
     for L in layers:
         L.destroy()
-    return {"workload": "BASELINE config 4: prefill MoE layer, T=8038 INT8, skewed router bias", "tokens": T,
+    wl = ("BASELINE config 4: prefill MoE layer, T=8038 INT8, skewed router bias" if fmt == 0 else
+          "config 4 shape (T=8038, skewed router bias) on NVFP4 routed experts, INT8 shared expert")
+    return {"workload": wl, "tokens": T,
             "layers_timed": nl, "us_per_layer": round(us_layer, 2), "tok_per_s": round(T / (us_layer * 1e-6), 1),
             "flops_per_layer": flops, "achieved_TFLOPs": round(tflops, 1),
             "mfma_util": round(tflops / MFMA_PEAK_TFLOPS, 4), "weight_act_bytes_per_layer": wbytes,
@@ -318,6 +323,7 @@ def main():
         layers = []
         extra["config3_nvfp4_m8"] = run_nvfp4(lib, st, nl, args)
         extra["config4_prefill"] = run_prefill(lib, st, args)
+        extra["config4_prefill_nvfp4"] = run_prefill(lib, st, args, fmt=1)
 
     cpu = None
     if not args.no_cpu:

@@ -117,16 +117,18 @@ void orc_fill_e4m3scale(uint32_t seed, uint32_t layer, uint32_t tensor, uint64_t
 
 /* ------------------------------------------------------------------------ */
 /* Number formats. E2M1: +-{0, .5, 1, 1.5, 2, 3, 4, 6}[n & 7], sign bit 3
-   (qf_nvfp4_wave64.hip:62-67). E4M3: e = b >> 3, m = b & 7; e == 0 ->
-   m * 2^-9, else (1 + m/8) * 2^(e-7); 0x7F -> +inf as in the reference
-   (qf_nvfp4_wave64.hip:68-73). Written from the closed forms with ldexp. */
+   (qf_nvfp4_wave64.hip:62-67). UE4M3 as the reference decodes the scale
+   byte (qf_nvfp4_wave64.hip:68-73): e = b >> 3 (the five high bits: codes
+   >= 0x80 are larger unsigned scales, not negative ones), m = b & 7; e == 0
+   -> m * 2^-9, else (1 + m/8) * 2^(e-7); 0x7F -> +inf. Written from the
+   closed forms with ldexp. */
 float orc_e2m1(uint32_t nib) {
     const uint32_t mag = nib & 7u, e = mag >> 1, m = mag & 1u;
     const float v = e ? ldexpf(1.0f + 0.5f * (float)m, (int)e - 1) : 0.5f * (float)m;
     return (nib & 8u) ? -v : v;
 }
 float orc_e4m3(uint32_t b) {
-    const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+    const uint32_t e = (b & 0xFFu) >> 3, m = b & 7u;
     if (e == 0) return ldexpf((float)m, -9);
     if (e == 15 && m == 7) return INFINITY;
     return ldexpf(1.0f + (float)m / 8.0f, (int)e - 7);
@@ -300,14 +302,8 @@ void orc_x8_quant(const float *v, int n, int8_t *q, float *s) {
 /* NVFP4 -> INT8 arena conversion (qf8_moe_i8.hip:146-195): for each row,
    v_k = e2m1(nibble k) * ue4m3(scale byte k/16) * s2 in fp32, multiplied in
    that order; scale = absmax * (1/127) (1 when every v is zero); code =
-   rint(v * (1/scale)) clamped to +-127. The scale decode reads the exponent
-   as byte >> 3 (all five high bits, qf8_moe_i8.hip:154-159), 0x7F -> +Inf. */
-static float ue4m3_5bit(uint32_t b) {
-    const uint32_t e = b >> 3, m = b & 7u;
-    if (e == 0) return ldexpf((float)m, -9);
-    if (e == 15 && m == 7) return INFINITY;
-    return ldexpf(1.0f + (float)m / 8.0f, (int)e - 7);
-}
+   rint(v * (1/scale)) clamped to +-127. The scale decode is orc_e4m3 (the
+   exponent read as byte >> 3, qf8_moe_i8.hip:154-159). */
 void orc_nvfp4_to_i8(const uint8_t *W, const uint8_t *S, float s2, int rows, int K, int8_t *Wo, float *So) {
     float *v = (float *)malloc((size_t)K * sizeof(float));
     for (int r = 0; r < rows; r++) {
@@ -315,7 +311,7 @@ void orc_nvfp4_to_i8(const uint8_t *W, const uint8_t *S, float s2, int rows, int
         for (int k = 0; k < K; k++) {
             const uint32_t byte = W[(size_t)r * (K / 2) + k / 2];
             const uint32_t nib = (k & 1) ? (byte >> 4) : (byte & 15u);
-            const float a = orc_e2m1(nib) * ue4m3_5bit(S[(size_t)r * (K / 16) + k / 16]);
+            const float a = orc_e2m1(nib) * orc_e4m3(S[(size_t)r * (K / 16) + k / 16]);
             v[k] = a * s2;
             mx = fmaxf(mx, fabsf(v[k]));
         }

@@ -475,12 +475,6 @@ k_cx_shexp_down(Qf8I8Mat down, const float *__restrict__ eg, const float *__rest
 // = e2m1(nibble k) * ue4m3(scale byte k/16) * s2 (in that order), per-row scale
 // absmax * (1/127) (1 for an all-zero row), code rint(v * (1/scale)) clamped to
 // +-127. grid (rows, slots), K <= 2560.
-__device__ __forceinline__ float ue4m3_ref(uint32_t b) {
-    const uint32_t e = b >> 3, m = b & 7u;            // 5-bit exponent field, as the reference reads it
-    if (e == 0) return (float)m * 0x1p-9f;
-    if (e == 15 && m == 7) return __uint_as_float(0x7F800000u);
-    return __uint_as_float(((e + 120u) << 23) | (m << 20));
-}
 __global__ void __launch_bounds__(256)
 k_cx_nvfp4_to_i8(const uint8_t *__restrict__ W, const uint8_t *__restrict__ S, const float *__restrict__ s2,
                  int rows, int K, int8_t *__restrict__ Wo, float *__restrict__ So) {
@@ -499,7 +493,7 @@ k_cx_nvfp4_to_i8(const uint8_t *__restrict__ W, const uint8_t *__restrict__ S, c
         if (k < K) {
             const uint32_t byte = wr[k >> 1];
             const uint32_t nib = (k & 1) ? (byte >> 4) : (byte & 15u);
-            v[i] = e2m1(nib) * ue4m3_ref(sr[k >> 4]) * sc2;
+            v[i] = e2m1(nib) * e4m3_scale(sr[k >> 4]) * sc2;
             mx = fmaxf(mx, fabsf(v[i]));
         }
     }

@@ -220,8 +220,16 @@ __device__ __forceinline__ float f4_group16(uint32_t lo, uint32_t hi, const floa
     }
     return a;
 }
+// ue4m3 block scale byte exactly as the reference decodes it
+// (ocho/amd_server/qf_nvfp4_wave64.hip:68-73): e = b >> 3 (five bits: bytes
+// >= 0x80 are large unsigned scales), m = b & 7; e == 0 -> m * 2^-9, else
+// (1 + m/8) * 2^(e-7); 0x7F -> +inf. Not the OCP E4M3 hardware convert, which
+// reads bit 7 as a sign and 0x7F as NaN.
 __device__ __forceinline__ float e4m3_scale(uint32_t b) {
-    return __builtin_amdgcn_cvt_f32_fp8((int)b, 0);
+    b &= 0xFFu;
+    const uint32_t e = b >> 3, m = b & 7u;
+    const uint32_t bits = b == 0x7Fu ? 0x7F800000u : ((e + 120u) << 23) | (m << 20);
+    return e ? __uint_as_float(bits) : (float)m * 0x1p-9f;
 }
 __device__ __forceinline__ float f4_chunk(uint4 w, uint32_t s2b, const float *x) {
     const float g0 = f4_group16(w.x, w.y, x);

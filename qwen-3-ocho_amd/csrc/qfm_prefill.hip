@@ -70,6 +70,25 @@ __device__ __forceinline__ void i8_to_bf16_ob(uint4 w, uint4 &o0, uint4 &o1) {
     o1 = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
+// Two e2m1 codes of byte `sel` of w -> exact fp32 pair (unit scale), times the
+// block scale s (products of a 2-bit and a 4-bit significand: exact in fp32 and
+// in bf16), packed to bf16 by truncation (exact).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <int SEL>
+__device__ __forceinline__ uint32_t f4_pair_bf16(uint32_t w, float s) {
+    const f32x2_t v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, SEL);
+    return pack_bf16_exact(v.x * s, v.y * s);
+}
+// 32 e2m1 codes (16 bytes, element 2i in the low nibble of byte i) with the
+// two e4m3 block scales of their 16-element halves -> 32 bf16 (4 x 16 bytes)
+__device__ __forceinline__ void f4_to_bf16(uint4 w, uint32_t sc2, uint4 (&o)[4]) {
+    const float s0 = e4m3_scale(sc2 & 0xFFu), s1 = e4m3_scale((sc2 >> 8) & 0xFFu);
+    o[0] = make_uint4(f4_pair_bf16<0>(w.x, s0), f4_pair_bf16<1>(w.x, s0), f4_pair_bf16<2>(w.x, s0), f4_pair_bf16<3>(w.x, s0));
+    o[1] = make_uint4(f4_pair_bf16<0>(w.y, s0), f4_pair_bf16<1>(w.y, s0), f4_pair_bf16<2>(w.y, s0), f4_pair_bf16<3>(w.y, s0));
+    o[2] = make_uint4(f4_pair_bf16<0>(w.z, s1), f4_pair_bf16<1>(w.z, s1), f4_pair_bf16<2>(w.z, s1), f4_pair_bf16<3>(w.z, s1));
+    o[3] = make_uint4(f4_pair_bf16<0>(w.w, s1), f4_pair_bf16<1>(w.w, s1), f4_pair_bf16<2>(w.w, s1), f4_pair_bf16<3>(w.w, s1));
+}
+
 // ---- router prep: ||w_e||_2 (fp64 accumulate, rounded up) --------------------------
 __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict__ W, int E, int H,
                                                          float *__restrict__ wnorm) {
@@ -96,7 +115,9 @@ __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict_
 // and D register stages of global loads in flight, one barrier per k-step.
 // A rows: bf16, row r at A + arow[r] * lda (arow < 0: absent row, staged as
 // zeros). B rows: int8 (staged as bf16 in offset-binary form u = q + 128,
-// exact), fp32 (rounded to bf16) or bf16, row n at bptr[n] (bytes). K % BK2 == 0.
+// exact), fp32 (rounded to bf16), bf16, or NVFP4 (packed e2m1 at bptr[n],
+// e4m3 block scales per 16 at sptr[n]; staged as bf16 of e2m1 * scale,
+// exact), row n at bptr[n] (bytes). K % BK2 == 0.
 // acc[mb][nb][i] = C[64 wm + 16 mb + 4 (lane >> 4) + i][64 wn + 16 nb + (lane & 15)],
 // wave = WN wm + wn. Staging: 16-byte chunks, consecutive threads on
 // consecutive chunks of a row (A: 8 chunks per row, B: 4 int8 / 16 fp32).
@@ -107,16 +128,17 @@ struct TileLds {
     uint16_t a[2][BMt * LDS2];
     uint16_t b[2][BNt * LDS2];
 };
-enum { kB_I8 = 0, kB_F32 = 1, kB_BF16 = 2 };
+enum { kB_I8 = 0, kB_F32 = 1, kB_BF16 = 2, kB_F4 = 3 };
 template <int BMODE, int WM, int WN, int D>
 struct TileEngine2 {
     static constexpr bool B_I8 = BMODE == kB_I8;
     static constexpr int BMt = 64 * WM, BNt = 64 * WN, NT = 64 * WM * WN;
-    static constexpr int BCPR = BMODE == kB_I8 ? 4 : BMODE == kB_F32 ? 16 : 8;   // B chunks per row per k-step
+    static constexpr int BCPR = BMODE == kB_I8 ? 4 : BMODE == kB_F32 ? 16 : BMODE == kB_F4 ? 2 : 8;   // B chunks per row per k-step
     static constexpr int NA = BMt * 8 / NT, NB = BNt * BCPR / NT;  // chunks per thread
     static_assert(NA * NT == BMt * 8 && NB * NT == BNt * BCPR, "staging must divide evenly");
     __device__ static void run(const uint16_t *__restrict__ A, long lda, const int *arow,
-                               const char *const *bptr, int K, TileLds<BMt, BNt> &L, f32x4_t (&acc)[4][4]) {
+                               const char *const *bptr, int K, TileLds<BMt, BNt> &L, f32x4_t (&acc)[4][4],
+                               const char *const *sptr = nullptr) {
         const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
         const int wm = wave / WN, wn = wave % WN;
         const uint16_t *ap[NA];
@@ -130,27 +152,32 @@ struct TileEngine2 {
             ap[j] = A + (ar >= 0 ? (long)ar * lda : 0) + kc * 8;
             a_lds[j] = r * LDS2 + kc * 8;
         }
-        const char *bp[NB];
+        const char *bp[NB], *sp[NB];
         int b_lds[NB];
 #pragma unroll
         for (int j = 0; j < NB; j++) {
             const int c = t + j * NT, r = c / BCPR, kc = c % BCPR;
             bp[j] = bptr[r] + kc * 16;
-            b_lds[j] = r * LDS2 + (BMODE == kB_I8 ? kc * 16 : BMODE == kB_F32 ? kc * 4 : kc * 8);
+            if constexpr (BMODE == kB_F4) sp[j] = sptr[r] + kc * 2;   // the chunk's two block scales
+            b_lds[j] = r * LDS2 + (BMODE == kB_I8 ? kc * 16 : BMODE == kB_F32 ? kc * 4 : BMODE == kB_F4 ? kc * 32 : kc * 8);
         }
         uint4 ra[D][NA], rb[D][NB];
-        auto gload = [&](int k0, uint4 (&a)[NA], uint4 (&bb)[NB]) {
+        uint32_t rsc[D][NB];                       // NVFP4 scale pairs (unused otherwise)
+        auto gload = [&](int k0, uint4 (&a)[NA], uint4 (&bb)[NB], uint32_t (&sc)[NB]) {
 #pragma unroll
             for (int j = 0; j < NA; j++)
                 a[j] = a_ok[j] ? *reinterpret_cast<const uint4 *>(ap[j] + k0) : make_uint4(0, 0, 0, 0);
 #pragma unroll
             for (int j = 0; j < NB; j++) {
                 if constexpr (BMODE == kB_I8) bb[j] = ld_nt16(bp[j] + k0);
-                else if constexpr (BMODE == kB_F32) bb[j] = *reinterpret_cast<const uint4 *>(bp[j] + (size_t)k0 * 4);
+                else if constexpr (BMODE == kB_F4) {
+                    bb[j] = ld_nt16(bp[j] + k0 / 2);
+                    sc[j] = *reinterpret_cast<const uint16_t *>(sp[j] + k0 / 16);
+                } else if constexpr (BMODE == kB_F32) bb[j] = *reinterpret_cast<const uint4 *>(bp[j] + (size_t)k0 * 4);
                 else bb[j] = *reinterpret_cast<const uint4 *>(bp[j] + (size_t)k0 * 2);
             }
         };
-        auto sstore = [&](int buf, const uint4 (&a)[NA], const uint4 (&bb)[NB]) {
+        auto sstore = [&](int buf, const uint4 (&a)[NA], const uint4 (&bb)[NB], const uint32_t (&sc)[NB]) {
 #pragma unroll
             for (int j = 0; j < NA; j++) *reinterpret_cast<uint4 *>(&L.a[buf][a_lds[j]]) = a[j];
 #pragma unroll
@@ -161,6 +188,12 @@ struct TileEngine2 {
                     uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]);
                     lb[0] = o0;
                     lb[1] = o1;
+                } else if constexpr (BMODE == kB_F4) {
+                    uint4 o[4];
+                    f4_to_bf16(bb[j], sc[j], o);
+                    uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) lb[q] = o[q];
                 } else if constexpr (BMODE == kB_BF16) {
                     *reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]) = bb[j];
                 } else {
@@ -178,9 +211,9 @@ struct TileEngine2 {
         const int nk = K / BK2;
 #pragma unroll
         for (int j = 0; j < D; j++)
-            if (j < nk) gload(j * BK2, ra[j], rb[j]);
-        sstore(0, ra[0], rb[0]);
-        if (D < nk) gload(D * BK2, ra[0], rb[0]);
+            if (j < nk) gload(j * BK2, ra[j], rb[j], rsc[j]);
+        sstore(0, ra[0], rb[0], rsc[0]);
+        if (D < nk) gload(D * BK2, ra[0], rb[0], rsc[0]);
         __syncthreads();
         const int lr = lane & 15, lk = (lane >> 4) * 8;
         for (int s0 = 0; s0 < nk; s0 += D) {
@@ -206,8 +239,8 @@ struct TileEngine2 {
                 }
                 const int jn = (j + 1) % D;                  // register stage holding k-step s + 1 (unrolled: constant)
                 if (s + 1 < nk) {
-                    sstore(buf ^ 1, ra[jn], rb[jn]);
-                    if (s + 1 + D < nk) gload((s + 1 + D) * BK2, ra[jn], rb[jn]);
+                    sstore(buf ^ 1, ra[jn], rb[jn], rsc[jn]);
+                    if (s + 1 + D < nk) gload((s + 1 + D) * BK2, ra[jn], rb[jn], rsc[jn]);
                 }
                 __syncthreads();
             }
@@ -217,6 +250,7 @@ struct TileEngine2 {
 // router GEMM: 128 x 128 tiles, 2 x 2 waves; grouped expert GEMMs: 128 x 256, 2 x 4 waves
 using RouterEngine = TileEngine2<kB_F32, 2, 2, kStagesF32>;
 using ExpertEngine = TileEngine2<kB_I8, 2, 4, kStagesI8>;
+using ExpertEngineF4 = TileEngine2<kB_F4, 2, 4, kStagesI8>;
 constexpr int GBN = ExpertEngine::BNt;          // weight rows per grouped-GEMM tile
 
 // Workgroups are dispatched to the 8 XCDs round-robin (block b on XCD b % 8).
@@ -508,13 +542,18 @@ k_pf_scatter(const int *__restrict__ sel, const float *__restrict__ wts, const f
 
 // ---- grouped expert GEMMs -------------------------------------------------------------
 struct GroupW {
-    const int8_t *w;      // routed arena blob, [E][rows][K]
-    const float *s;       // routed row scales [E][rows]
-    const int8_t *w_sh;   // shared expert [rows][K]
+    const int8_t *w;      // routed arena blob: INT8 [E][rows][K], or NVFP4 packed e2m1 [E][rows][K/2]
+    const float *s;       // INT8 routed row scales [E][rows]
+    const int8_t *w_sh;   // shared expert [rows][K] (INT8 in both formats)
     const float *s_sh;    // shared row scales [rows]
+    const uint8_t *sc4;   // NVFP4 e4m3 block scales [E][rows][K/16]
+    const float *s2;      // NVFP4 per-expert global scales [E]
 };
 
-template <bool GATEUP>
+// F4: routed groups (grp < E) read an NVFP4 arena (block scales staged into
+// the bf16 B tile, the global scale s2 applied in the epilogue); the shared
+// expert (grp == E) is INT8 in both formats.
+template <bool GATEUP, bool F4>
 __global__ void __launch_bounds__(ExpertEngine::NT)
 k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int which, const int *__restrict__ off,
           const int *__restrict__ p_tok, const int *__restrict__ p_slot, const float *__restrict__ p_wt,
@@ -525,6 +564,7 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     __shared__ __align__(16) TileLds<BM, GBN> lds;
     __shared__ int arow[BM];
     __shared__ const char *bptr[GBN];
+    __shared__ const char *sptr[F4 ? GBN : 1];
     __shared__ float rsum[BM], hpart[WN][BM];
     int mi, ni;
     xcd_tile(blockIdx.x, ntiles, mi, ni);
@@ -532,15 +572,24 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     const int4 it = items[mi * ntiles + ni];
     const int grp = it.x, r0 = it.y, rows = it.z, nt = it.w;
     const int pbase = off[grp] + r0;
-    const int8_t *Wb;
-    const float *Sb;
-    if (grp < E) { Wb = g0.w + (size_t)grp * Nrows * Kdim; Sb = g0.s + (size_t)grp * Nrows; }
-    else { Wb = g0.w_sh; Sb = g0.s_sh; }
-    const int8_t *Wb2 = nullptr;
-    const float *Sb2 = nullptr;
-    if (GATEUP) {
-        if (grp < E) { Wb2 = g1.w + (size_t)grp * Nrows * Kdim; Sb2 = g1.s + (size_t)grp * Nrows; }
-        else { Wb2 = g1.w_sh; Sb2 = g1.s_sh; }
+    const bool f4 = F4 && grp < E;
+    const size_t rowb = f4 ? (size_t)Kdim / 2 : (size_t)Kdim;       // weight row bytes
+    const int8_t *Wb, *Wb2 = nullptr;
+    const float *Sb = nullptr, *Sb2 = nullptr;
+    const uint8_t *Cb = nullptr, *Cb2 = nullptr;
+    float s2a = 1.0f, s2b = 1.0f;
+    if (grp < E) {
+        Wb = g0.w + (size_t)grp * Nrows * rowb;
+        if (f4) { Cb = g0.sc4 + (size_t)grp * Nrows * (Kdim / 16); s2a = g0.s2[grp]; }
+        else Sb = g0.s + (size_t)grp * Nrows;
+        if (GATEUP) {
+            Wb2 = g1.w + (size_t)grp * Nrows * rowb;
+            if (f4) { Cb2 = g1.sc4 + (size_t)grp * Nrows * (Kdim / 16); s2b = g1.s2[grp]; }
+            else Sb2 = g1.s + (size_t)grp * Nrows;
+        }
+    } else {
+        Wb = g0.w_sh; Sb = g0.s_sh;
+        if (GATEUP) { Wb2 = g1.w_sh; Sb2 = g1.s_sh; }
     }
     // A row sums (the offset-binary correction): x rows' sums for gate/up; for
     // down, the sum of the nt_gu per-tile partial sums the gate/up epilogue
@@ -564,14 +613,21 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
             // wave column wn = n / 64 holds intermediate rows [128 nt + 32 wn, +32):
             // its n-blocks 0, 1 are their gate rows and n-blocks 2, 3 the same up rows
             const int wn = n >> 6, q = (n >> 4) & 3, o = nt * 128 + wn * 32 + (q & 1) * 16 + (n & 15);
-            bptr[n] = reinterpret_cast<const char *>((q < 2 ? Wb : Wb2) + (size_t)o * Kdim);
+            bptr[n] = reinterpret_cast<const char *>((q < 2 ? Wb : Wb2) + (size_t)o * rowb);
+            if (F4 && f4) sptr[n] = reinterpret_cast<const char *>((q < 2 ? Cb : Cb2) + (size_t)o * (Kdim / 16));
         } else {
-            bptr[n] = reinterpret_cast<const char *>(Wb + (size_t)(nt * GBN + n) * Kdim);
+            bptr[n] = reinterpret_cast<const char *>(Wb + (size_t)(nt * GBN + n) * rowb);
+            if (F4 && f4) sptr[n] = reinterpret_cast<const char *>(Cb + (size_t)(nt * GBN + n) * (Kdim / 16));
         }
     }
     __syncthreads();
     f32x4_t acc[4][4];
-    ExpertEngine::run(A, Kdim, arow, bptr, Kdim, lds, acc);
+    if constexpr (F4) {
+        if (f4) ExpertEngineF4::run(A, Kdim, arow, bptr, Kdim, lds, acc, sptr);
+        else ExpertEngine::run(A, Kdim, arow, bptr, Kdim, lds, acc);
+    } else {
+        ExpertEngine::run(A, Kdim, arow, bptr, Kdim, lds, acc);
+    }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave / WN, wn = wave % WN;
     if (GATEUP) {
         float hsacc[4][4] = {};
@@ -585,9 +641,9 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
                     const int o = nt * 128 + wn * 32 + nb * 16 + (lane & 15);
                     float hs = 0.0f;
                     if (r < rows) {
-                        const float cr = 128.0f * rsum[r];
-                        const float gv = (acc[mb][nb][i] - cr) * Sb[o];
-                        const float uv = (acc[mb][nb + 2][i] - cr) * Sb2[o];
+                        const float cr = f4 ? 0.0f : 128.0f * rsum[r];
+                        const float gv = (acc[mb][nb][i] - cr) * (f4 ? s2a : Sb[o]);
+                        const float uv = (acc[mb][nb + 2][i] - cr) * (f4 ? s2b : Sb2[o]);
                         const uint16_t hb = f32_to_bf16(silu(gv) * uv);
                         hid[(size_t)(pbase + r) * Nrows + o] = hb;
                         hs = bf16_to_f32(hb);
@@ -624,7 +680,7 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
                     const int c = nt * GBN + wn * 64 + nb * 16 + (lane & 15);
                     if (r < rows) {
                         const int p = pbase + r;
-                        const float v = (acc[mb][nb][i] - 128.0f * rsum[r]) * Sb[c];
+                        const float v = f4 ? acc[mb][nb][i] * s2a : (acc[mb][nb][i] - 128.0f * rsum[r]) * Sb[c];
                         part[(size_t)p_slot[p] * Hout + c] = p_wt[p] * v;
                     }
                 }
@@ -688,11 +744,18 @@ void prefill_ws_view(void *ws, int T, float **lg, int **sel, float **wts) {
 
 int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, void *ws, int gated, hipStream_t s) {
     const Cfg &c = g_cfg;
-    if (L->fmt != QFM_FMT_INT8) { set_error(-2, "prefill: INT8 routed experts only"); return -2; }
     if (c.E != 512 || !(shape_2048() || shape_2560())) { set_error(-2, "prefill: unsupported shape"); return -2; }
     const int E = c.E, K = c.K, H = c.H, I = c.I;
     const Qf4ExpCache *a = L->arena;
-    if (!a || !a->i8_gate || !a->i8_up || !a->i8_down) { set_error(-1, "prefill: arena has no INT8 blobs"); return -1; }
+    const bool f4 = L->fmt == QFM_FMT_NVFP4;
+    if (!a) { set_error(-1, "prefill: no arena"); return -1; }
+    if (!f4 && (!a->i8_gate || !a->i8_up || !a->i8_down || !a->i8s_gate || !a->i8s_up || !a->i8s_down)) {
+        set_error(-1, "prefill: arena has no INT8 blobs"); return -1;
+    }
+    if (f4 && (!a->w_gate || !a->w_up || !a->w_down || !a->s_gate || !a->s_up || !a->s_down || !a->s2g_dev ||
+               !a->s2u_dev || !a->s2d_dev)) {
+        set_error(-1, "prefill: arena has no NVFP4 blobs"); return -1;
+    }
     const bool has_sh = L->sh_gate.w != nullptr;
     const int S = K + (has_sh ? 1 : 0);      // partial slots per token: K routed (+ shared)
     const size_t P = (size_t)T * S;
@@ -738,13 +801,28 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
                        items_gu, items_dn, ctr + 1, (int)(max_mt * nt_gu), (int)(max_mt * nt_dn));
     hipLaunchKernelGGL(k_pf_scatter, dim3((unsigned)(nblk + (has_sh ? (T + 255) / 256 : 0))), dim3(256), 0, s, sel,
                        wts, g ? gam : nullptr, T, K, E, has_sh ? 1 : 0, off, blk, p_tok, p_slot, p_wt);
-    GroupW gg{a->i8_gate, a->i8s_gate, L->sh_gate.w, L->sh_gate.s};
-    GroupW gu{a->i8_up, a->i8s_up, L->sh_up.w, L->sh_up.s};
-    GroupW gd{a->i8_down, a->i8s_down, L->sh_down.w, L->sh_down.s};
-    hipLaunchKernelGGL((k_pf_gemm<true>), dim3((unsigned)(max_mt * nt_gu)), dim3(ExpertEngine::NT), 0, s, items_gu, ctr + 1, 0, off,
-                       p_tok, p_slot, p_wt, x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu);
-    hipLaunchKernelGGL((k_pf_gemm<false>), dim3((unsigned)(max_mt * nt_dn)), dim3(ExpertEngine::NT), 0, s, items_dn, ctr + 1, 1, off,
-                       p_tok, p_slot, p_wt, hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu);
+    GroupW gg, gu, gd;
+    if (f4) {
+        gg = GroupW{reinterpret_cast<const int8_t *>(a->w_gate), nullptr, L->sh_gate.w, L->sh_gate.s, a->s_gate, a->s2g_dev};
+        gu = GroupW{reinterpret_cast<const int8_t *>(a->w_up), nullptr, L->sh_up.w, L->sh_up.s, a->s_up, a->s2u_dev};
+        gd = GroupW{reinterpret_cast<const int8_t *>(a->w_down), nullptr, L->sh_down.w, L->sh_down.s, a->s_down, a->s2d_dev};
+    } else {
+        gg = GroupW{a->i8_gate, a->i8s_gate, L->sh_gate.w, L->sh_gate.s, nullptr, nullptr};
+        gu = GroupW{a->i8_up, a->i8s_up, L->sh_up.w, L->sh_up.s, nullptr, nullptr};
+        gd = GroupW{a->i8_down, a->i8s_down, L->sh_down.w, L->sh_down.s, nullptr, nullptr};
+    }
+    const dim3 g_gu((unsigned)(max_mt * nt_gu)), g_dn((unsigned)(max_mt * nt_dn)), nth(ExpertEngine::NT);
+    if (f4) {
+        hipLaunchKernelGGL((k_pf_gemm<true, true>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, off, p_tok, p_slot, p_wt,
+                           x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu);
+        hipLaunchKernelGGL((k_pf_gemm<false, true>), g_dn, nth, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot, p_wt,
+                           hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu);
+    } else {
+        hipLaunchKernelGGL((k_pf_gemm<true, false>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, off, p_tok, p_slot, p_wt,
+                           x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu);
+        hipLaunchKernelGGL((k_pf_gemm<false, false>), g_dn, nth, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot, p_wt,
+                           hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu);
+    }
     hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)(((size_t)T * H / 4 + 255) / 256)), dim3(256), 0, s, part, T, S,
                        H, y);
     return check_launch("prefill");

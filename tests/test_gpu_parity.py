@@ -262,9 +262,9 @@ def test_moe_layer_deterministic(lib):
 
 
 # ------------------------------------------------------------------ prefill
-def _run_prefill(lib, T, seed, layer, x_layer, bias=True):
+def _run_prefill(lib, T, seed, layer, x_layer, bias=True, fmt=qfm.QFM_FMT_INT8):
     st = qfm.Stream()
-    L = qfm.SynthLayer(qfm.QFM_FMT_INT8, seed, layer, with_bias=bias, stream=st)
+    L = qfm.SynthLayer(fmt, seed, layer, with_bias=bias, stream=st)
     H = 2048
     dx, dy = qfm.DevBuf(T * H * 2), qfm.DevBuf(T * H * 2)
     qfm.check(lib.qfm_gen_input_rows(dx.ptr, T, seed, x_layer, 0, st.h), "x")
@@ -281,13 +281,15 @@ def _run_prefill(lib, T, seed, layer, x_layer, bias=True):
     return out
 
 
-@pytest.mark.parametrize("T,bias", [(37, True), (300, True), (129, False)])
-def test_prefill_small(lib, T, bias):
-    """Prefill path (T > 8): MFMA router + exact candidate selection, grouped GEMMs."""
-    _say("prefill", T, bias)
+@pytest.mark.parametrize("T,bias,fmt", [(37, True, 0), (300, True, 0), (129, False, 0), (37, True, 1), (300, True, 1),
+                                        (9, False, 1)])
+def test_prefill_small(lib, T, bias, fmt):
+    """Prefill path (T > 8): MFMA router + exact candidate selection, grouped GEMMs
+    on INT8 (fmt 0) or NVFP4 (fmt 1) routed experts (the shared expert is INT8)."""
+    _say("prefill", T, bias, "int8" if fmt == 0 else "nvfp4")
     _cfg(lib)
-    g = _run_prefill(lib, T, 1, 2, 600 + T, bias)
-    r = orc.moe_layer(2048, 512, 512, 10, T, 1, 2, 600 + T, use_bias=int(bias))
+    g = _run_prefill(lib, T, 1, 2, 600 + T, bias, fmt)
+    r = orc.moe_layer(2048, 512, 512, 10, T, 1, 2, 600 + T, use_bias=int(bias), fmt=fmt)
     assert np.array_equal(g["x"], r["x"])
     assert np.array_equal(g["sel"], r["sel"])
     assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
@@ -314,3 +316,21 @@ def test_prefill_config4_routing_and_sample(lib):
         rel = max(_rel(g["y"][row0 + m], r["y"][m]) for m in range(32))
         _say("  rows", row0, "max rel err", rel)
         assert rel <= TOL
+
+
+def test_prefill_config4_nvfp4_sample(lib):
+    """Config 4's prefill (T=8038, skewed router bias) on an NVFP4 arena: routing
+    for every token, outputs on a 32-token window (includes the hottest expert)."""
+    T, seed, layer, xl = 8038, 0, 3, 700
+    _say("prefill config4 nvfp4", T)
+    _cfg(lib)
+    g = _run_prefill(lib, T, seed, layer, xl, True, qfm.QFM_FMT_NVFP4)
+    E, H = 512, 2048
+    W = orc.fill("gauss", seed, layer, orc.T_ROUTER, 0, E * H, 0.02).reshape(E, H)
+    b = orc.fill("gauss", seed, layer, orc.T_BIAS, 0, E, 1.5)
+    sel, w64, _ = orc.topk(orc.router_logits(W, g["x"], b), 10)
+    assert np.array_equal(g["sel"], sel)
+    r = orc.moe_layer(2048, 512, 512, 10, 32, seed, layer, xl, x_row0=3000, use_bias=1, fmt=1)
+    rel = max(_rel(g["y"][3000 + m], r["y"][m]) for m in range(32))
+    _say("  rows 3000 max rel err", rel)
+    assert rel <= TOL

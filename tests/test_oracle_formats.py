@@ -112,6 +112,12 @@ def test_e4m3_all_codes_vs_torch_and_reference_formula():
         e, m = c >> 3, c & 7
         f = m * 2.0 ** -9 if e == 0 else (8 + m) * 2.0 ** (e - 10)
         assert got[c] == f
+    # bytes >= 0x80: the reference reads e = byte >> 3 (five bits), so these are
+    # unsigned scales 2^9 .. 2^24 * 1.875, not the negative OCP codes
+    for c in range(128, 256):
+        e, m = c >> 3, c & 7
+        assert lib.orc_e4m3(c) == np.float32((8 + m) * 2.0 ** (e - 10))
+    assert lib.orc_e4m3(0x80) == 512.0 and lib.orc_e4m3(0xFF) == np.float32(1.875 * 2.0 ** 24)
 
 
 def test_e4m3_encode_roundtrip_and_nearest():
