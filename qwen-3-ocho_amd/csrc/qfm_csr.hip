@@ -68,7 +68,7 @@ struct CsrLds {
     int exp_ptr[kMaxPairs + 1];
     uint32_t bits[512 / 32];  // bitmap of selected experts (E == 512)
     int n_exp;
-    unsigned long long tk[8][272];
+    alignas(16) unsigned long long tk[8][kTopkLds];
 };
 
 // Called by all threads of the block after sel of the P pairs is in LDS and

@@ -77,62 +77,128 @@ __device__ __forceinline__ float topk_key_value(unsigned long long key) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-// One wave selects the top-K (K <= 16) of E = 64*EPL logits lr[0..E):
+// ---- wave top-K --------------------------------------------------------------
+// One wave selects the top-K (K <= 16) of E = 64*EPL logits lr[0..E) (EPL <= 16):
 // descending value, ties to the lower index (64-bit keys, all distinct).
-// Lane k < K receives the k-th expert id and its weight exp(l_k - l_max) /
-// denom, denom = sum over the K selected (renorm) or over all E (plain
-// softmax). Wave-uniform control flow; lds: 16 + 16*EPL u64 of wave-private LDS.
-// Method: T = the K-th largest of the 64 lane maxima (rank counting over
-// broadcast lane values) bounds the K-th largest key from below, so the
-// elements >= T (at most 8K of them, typically ~K) contain the top-K; those
-// candidates are compacted to LDS and ranked against each other.
+// Wave-uniform control flow; lds: kTopkLds u64 of wave-private LDS, 16-byte aligned.
+//
+// Method (latency-bound: one wave, so few dependent steps and independent
+// accumulators). 31-bit keys k31 = (value prefix << IB) | (E - 1 - e), IB =
+// index bits (9 for E = 512, 22-bit prefix of the sortable value bits), are distinct; T31 = the K-th largest of the 64 lane maxima of k31 (rank by
+// broadcast compares, sign of the 31-bit difference), P = its value prefix.
+// Every element of the true top-K has a prefix >= P (K distinct lane maxima
+// have prefix >= P and the K-th largest element is >= the least of them), so
+// C = {prefix >= P} contains the top-K; typically |C| ~ K. If |C| > 64 (ties
+// in the prefix) the exact 64-bit form of the same bound is used instead:
+// T = K-th largest 64-bit lane maximum, C = {key >= T}, |C| <= K*EPL. C is
+// compacted to LDS with ballots and mbcnt and each candidate's exact rank
+// within C is its rank among all E.
+constexpr int kTopkLds = 16 + 256 + 64 + 64;   // results, candidates, junk slots, lane maxima
 template <int EPL>
-__device__ __forceinline__ void wave_topk(const float *lr, int K, int renorm, int lane,
-                                          unsigned long long *lds, int &my_i, float &my_w) {
+__device__ __forceinline__ int topk_candidates(const float *lr, int K, int lane, unsigned long long *lds,
+                                               float (&v)[EPL]) {
+    static_assert(EPL >= 1 && EPL <= 16, "E = 64 * EPL, EPL <= 16");
+    constexpr int E = 64 * EPL;
+    constexpr int IB = E <= 64 ? 6 : E <= 128 ? 7 : E <= 256 ? 8 : E <= 512 ? 9 : 10;   // index bits
+    constexpr int PB = 31 - IB;                                                        // value-prefix bits
     unsigned long long key[EPL];
-    float v[EPL];
+    uint32_t k31[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
         v[i] = lr[i * 64 + lane];
         key[i] = topk_key(v[i], i * 64 + lane);
+        k31[i] = ((uint32_t)(key[i] >> (64 - PB)) << IB) | (uint32_t)(E - 1 - (i * 64 + lane));
     }
-    unsigned long long mx = key[0];
+    unsigned long long *cand = lds + 16, *lm = lds + 16 + 256 + 64;
+    uint32_t *lm32 = reinterpret_cast<uint32_t *>(lm);
+    uint32_t mx = k31[0];
 #pragma unroll
-    for (int i = 1; i < EPL; i++) mx = key[i] > mx ? key[i] : mx;
-    // rank of this lane's maximum among the 64 lane maxima
-    int rank = 0;
-    for (int j = 0; j < 64; j++) {
-        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mx, j);
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(mx >> 32), j);
-        rank += ((((unsigned long long)hi << 32) | lo) > mx) ? 1 : 0;
-    }
-    const unsigned long long bal = __ballot(rank == K - 1);
-    const int tl = __builtin_ctzll(bal);
-    // (readlane returns a signed int: widen through uint32_t, never directly)
-    const uint32_t t_hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(mx >> 32), tl);
-    const uint32_t t_lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mx, tl);
-    const unsigned long long T = ((unsigned long long)t_hi << 32) | t_lo;
-    // compact the candidates (keys >= T) into lds[64 ..]
-    int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < EPL; i++) cnt += key[i] >= T ? 1 : 0;
-    const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int off = 0;
-#pragma unroll
-    for (int b = 0; b < 4; b++) off += __popcll(__ballot((cnt >> b) & 1) & lt) << b;
-    int total = 0;
-#pragma unroll
-    for (int b = 0; b < 4; b++) total += __popcll(__ballot((cnt >> b) & 1)) << b;
-    unsigned long long *cand = lds + 16;
-#pragma unroll
-    for (int i = 0; i < EPL; i++)
-        if (key[i] >= T) cand[off++] = key[i];
+    for (int i = 1; i < EPL; i++) mx = max(mx, k31[i]);
+    lm32[lane] = mx;
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    // rank the candidates against each other; the K best land in lds[0..K)
-    for (int j = lane; j < total; j += 64) {
+    uint32_t r4[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        uint4 p[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) p[q] = reinterpret_cast<const uint4 *>(lm32)[h * 8 + q];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {      // keys < 2^31: the difference's sign bit is (other > mine)
+            r4[0] += (mx - p[q].x) >> 31; r4[1] += (mx - p[q].y) >> 31;
+            r4[2] += (mx - p[q].z) >> 31; r4[3] += (mx - p[q].w) >> 31;
+        }
+    }
+    const uint32_t rank = r4[0] + r4[1] + r4[2] + r4[3];
+    const uint32_t T31 = (uint32_t)__builtin_amdgcn_readlane((int)mx, __builtin_ctzll(__ballot(rank == (uint32_t)(K - 1))));
+    const uint32_t P = T31 & ~((1u << IB) - 1u);
+    unsigned long long b[EPL];
+    int base[EPL], tot = 0;
+#pragma unroll
+    for (int i = 0; i < EPL; i++) b[i] = __ballot(k31[i] >= P);
+#pragma unroll
+    for (int i = 0; i < EPL; i++) { base[i] = tot; tot += __popcll(b[i]); }
+    if (tot > 64) {
+        // exact bound: 64-bit lane maxima (wave-uniform branch)
+        unsigned long long m64 = key[0];
+#pragma unroll
+        for (int i = 1; i < EPL; i++) m64 = key[i] > m64 ? key[i] : m64;
+        lm[lane] = m64;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        int ra[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 64; j += 8) {
+            ulonglong2 p[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) p[q] = *reinterpret_cast<const ulonglong2 *>(lm + j + 2 * q);
+#pragma unroll
+            for (int q = 0; q < 4; q++) ra[q] += (p[q].x > m64 ? 1 : 0) + (p[q].y > m64 ? 1 : 0);
+        }
+        const int r64 = ra[0] + ra[1] + ra[2] + ra[3];
+        const int tl = __builtin_ctzll(__ballot(r64 == K - 1));
+        const uint32_t t_hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(m64 >> 32), tl);
+        const uint32_t t_lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)m64, tl);
+        const unsigned long long T = ((unsigned long long)t_hi << 32) | t_lo;
+        tot = 0;
+#pragma unroll
+        for (int i = 0; i < EPL; i++) b[i] = __ballot(key[i] >= T);
+#pragma unroll
+        for (int i = 0; i < EPL; i++) { base[i] = tot; tot += __popcll(b[i]); }
+    }
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const bool in = (b[i] >> lane) & 1ull;
+        const int pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(b[i] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b[i], base[i]));
+        cand[in ? pos : 256 + lane] = key[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    return tot;
+}
+// rank of candidate key c among the first n candidates (16 per pass, 4 accumulators)
+__device__ __forceinline__ int topk_cand_rank(const unsigned long long *cand, int n, unsigned long long c) {
+    int ra[4] = {0, 0, 0, 0};
+    for (int i0 = 0; i0 < n; i0 += 16) {
+        ulonglong2 p[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) p[q] = *reinterpret_cast<const ulonglong2 *>(cand + i0 + 2 * q);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            ra[q & 3] += (i0 + 2 * q < n && p[q].x > c) ? 1 : 0;
+            ra[(q + 2) & 3] += (i0 + 2 * q + 1 < n && p[q].y > c) ? 1 : 0;
+        }
+    }
+    return ra[0] + ra[1] + ra[2] + ra[3];
+}
+// Lane k < K receives the k-th expert id and its weight exp(l_k - l_max) /
+// denom, denom = sum over the K selected (renorm) or over all E (plain softmax).
+template <int EPL>
+__device__ __forceinline__ void wave_topk(const float *lr, int K, int renorm, int lane,
+                                          unsigned long long *lds, int &my_i, float &my_w) {
+    float v[EPL];
+    const int n = topk_candidates<EPL>(lr, K, lane, lds, v);
+    const unsigned long long *cand = lds + 16;
+    for (int j = lane; j < n; j += 64) {
         const unsigned long long cj = cand[j];
-        int r = 0;
-        for (int i = 0; i < total; i++) r += cand[i] > cj ? 1 : 0;
+        const int r = topk_cand_rank(cand, n, cj);
         if (r < K) lds[r] = cj;
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -151,6 +217,20 @@ __device__ __forceinline__ void wave_topk(const float *lr, int K, int renorm, in
     }
     my_i = lane < K ? topk_key_index(mine) : -1;
     my_w = ek / denom;
+}
+// The expert id of rank `job` (< K) only (wave-uniform result): same candidate
+// set and ranks as wave_topk, no permutation through LDS and no softmax.
+template <int EPL>
+__device__ __forceinline__ int wave_topk_one(const float *lr, int K, int job, int lane, unsigned long long *lds) {
+    float v[EPL];
+    const int n = topk_candidates<EPL>(lr, K, lane, lds, v);
+    const unsigned long long *cand = lds + 16;
+    int found = -1;
+    for (int j = lane; j < n; j += 64) {
+        const unsigned long long cj = cand[j];
+        if (topk_cand_rank(cand, n, cj) == job) found = topk_key_index(cj);
+    }
+    return __builtin_amdgcn_readlane(found, __builtin_ctzll(__ballot(found >= 0)));
 }
 
 // x slice of one 32-lane group: lane l holds x[st*512 + 16l + i], i < 16.

@@ -38,8 +38,7 @@ k_i8_gateup_m1(const int8_t *__restrict__ Qg, const int8_t *__restrict__ Qu,
                const float *__restrict__ logits, int *__restrict__ sel, float *__restrict__ wts,
                int K, int renorm, float *__restrict__ hidden) {
     constexpr int NST = H / 512;
-    __shared__ int s_e;
-    __shared__ unsigned long long s_tk[272];
+    __shared__ __align__(16) unsigned long long s_tk[4][kTopkLds];
     const int job = blockIdx.y;
     const int l = threadIdx.x & 31;
     const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
@@ -48,18 +47,21 @@ k_i8_gateup_m1(const int8_t *__restrict__ Qg, const int8_t *__restrict__ Qu,
     else load_x_slice_f32<H>(xf, l, xs);
     int e;
     if (logits) {
-        if (threadIdx.x < 64) {
+        // every wave selects its block's expert itself (no barrier): the rank-`job`
+        // id only; wave 0 of block (0, 0) also writes the routing (ids + weights)
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        if (blockIdx.x == 0 && job == 0 && wave == 0) {
             int my_i;
             float my_w;
-            wave_topk<EPL>(logits, K, renorm, threadIdx.x, s_tk, my_i, my_w);
-            if (threadIdx.x == job) s_e = my_i;
-            if (blockIdx.x == 0 && job == 0 && threadIdx.x < K) {
-                sel[threadIdx.x] = my_i;
-                wts[threadIdx.x] = my_w;
+            wave_topk<EPL>(logits, K, renorm, lane, s_tk[0], my_i, my_w);
+            if (lane < K) {
+                sel[lane] = my_i;
+                wts[lane] = my_w;
             }
+            e = __builtin_amdgcn_readfirstlane(my_i);
+        } else {
+            e = wave_topk_one<EPL>(logits, K, job, lane, s_tk[wave]);
         }
-        __syncthreads();
-        e = s_e;
     } else {
         e = sel[job];
     }

@@ -129,7 +129,7 @@ template <int EPL>
 __global__ void __launch_bounds__(256)
 k_topk(const float *__restrict__ logits, int ld, int M, int K, int renorm,
        int *__restrict__ sel, float *__restrict__ wts) {
-    __shared__ unsigned long long s_tk[4][272];
+    __shared__ __align__(16) unsigned long long s_tk[4][kTopkLds];
     const int lane = threadIdx.x & 63;
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (m >= M) return;
