@@ -30,6 +30,10 @@
 namespace qfm {
 
 constexpr int kMaxRows = 8;
+#ifndef QFM_DOWN_ROWS
+#define QFM_DOWN_ROWS 32
+#endif
+constexpr int kDownRows = QFM_DOWN_ROWS;   // down rows per block
 constexpr int kMaxPairs = kMaxRows * 16;
 
 // ---- weight-format policies ----------------------------------------------------
@@ -215,7 +219,11 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
     }
 }
 
-// ---- down: one distinct expert x 64 rows per block, owned partials ---------------
+// ---- down: one distinct expert x ROWS rows per block, owned partials ---------------
+template <class F, int I>
+constexpr int down_rows() {
+    return kDownRows > 256 / lpr_of(I / F::VPB / 16) ? kDownRows : 256 / lpr_of(I / F::VPB / 16);
+}
 template <class F, int H, int I>
 __global__ void __launch_bounds__(256)
 k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const uint8_t *__restrict__ Bd,
@@ -226,7 +234,7 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
     constexpr int LPR = lpr_of(CPR);                   // lanes per row
     constexpr int NST = CPR / LPR;
     constexpr int GROUPS = 256 / LPR;                  // row groups per block
-    constexpr int ROWS = 64;
+    constexpr int ROWS = down_rows<F, I>();
     __shared__ __align__(16) float sh_h[kMaxRows * I];
     __shared__ float sh_cs[kMaxRows * I / 16];
     const int u = blockIdx.y;
@@ -301,6 +309,22 @@ k_csr_combine(const float *__restrict__ part, int M, int K, ShPtrs sh, const flo
     const int l = threadIdx.x % LPR;
     const int c = blockIdx.x * RPB + threadIdx.x / LPR;
     const bool has_sh = sh.qd != nullptr;
+    // Routed partials: lane l of a row group owns slots k = l, l + LPR, ... of
+    // every row. All loads (partials, gates, shared weights, shared hidden)
+    // are issued before any is consumed (clamped indices, masked afterwards)
+    // so their latencies overlap.
+    constexpr int NKL = (16 + LPR - 1) / LPR;
+    float pv[kMaxRows][NKL];
+#pragma unroll
+    for (int t = 0; t < kMaxRows; t++)
+#pragma unroll
+        for (int j = 0; j < NKL; j++) {
+            const int k = l + j * LPR, tt = t < M ? t : 0, kk = k < K ? k : 0;
+            pv[t][j] = part[((size_t)tt * K + kk) * H + c];
+        }
+    float glg[kMaxRows];
+#pragma unroll
+    for (int t = 0; t < kMaxRows; t++) glg[t] = (has_sh && gated) ? logits[(size_t)(t < M ? t : 0) * ld + (ld - 1)] : 0.0f;
     uint4 w[NST];
     float sd = 0.0f;
     if (has_sh) {
@@ -318,42 +342,29 @@ k_csr_combine(const float *__restrict__ part, int M, int K, ShPtrs sh, const flo
         }
         __syncthreads();
     }
-    // Routed partials: lane l of a row group owns slots k = l, l + LPR, ... of
-    // every row. All loads are issued before any is consumed (clamped indices,
-    // masked afterwards) so their latencies overlap.
-    constexpr int NKL = (16 + LPR - 1) / LPR;
-    float pv[kMaxRows][NKL];
-#pragma unroll
-    for (int t = 0; t < kMaxRows; t++)
-#pragma unroll
-        for (int j = 0; j < NKL; j++) {
-            const int k = l + j * LPR, tt = t < M ? t : 0, kk = k < K ? k : 0;
-            pv[t][j] = part[((size_t)tt * K + kk) * H + c];
-        }
-    float gs[kMaxRows];
+    float rr[kMaxRows];
 #pragma unroll
     for (int t = 0; t < kMaxRows; t++) {
-        const int tt = t < M ? t : 0;
-        gs[t] = (has_sh && gated) ? sigmoid(logits[(size_t)tt * ld + (ld - 1)]) * sd : sd;
-    }
-#pragma unroll
-    for (int t = 0; t < kMaxRows; t++) {
-        if (t >= M) break;
         float r = 0.0f;
 #pragma unroll
         for (int j = 0; j < NKL; j++) r += (l + j * LPR < K) ? pv[t][j] : 0.0f;
-        if (has_sh) {
+        if (has_sh && t < M) {
+            const float gs = gated ? sigmoid(glg[t]) * sd : sd;
             float d = 0.0f;
 #pragma unroll
             for (int st = 0; st < NST; st++) {
                 d += sh_cs[t * (I / 16) + st * LPR + l];
                 d = dot16_u8(w[st], sh_h + t * I + (st * LPR + l) * 16, d);
             }
-            r = fmaf(gs[t], d, r);
+            r = fmaf(gs, d, r);
         }
-        r = group_sum<LPR>(r);
-        if (l == 0) y[(size_t)t * H + c] = f32_to_bf16(r);
+        rr[t] = r;
     }
+#pragma unroll
+    for (int t = 0; t < kMaxRows; t++) rr[t] = group_sum<LPR>(rr[t]);      // independent: interleaved
+#pragma unroll
+    for (int t = 0; t < kMaxRows; t++)
+        if (l == 0 && t < M) y[(size_t)t * H + c] = f32_to_bf16(rr[t]);
 }
 
 // ---- launchers -------------------------------------------------------------------
@@ -380,7 +391,7 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
     hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), b512, 0, s, logits, ld, M, K, g_cfg.renorm, sel, wts, csr);       \
     hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(II / (256 / lpr_of(HH / F::VPB / 16)), umax), b256, 0, s,  \
                        wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, K, csr, P, hpair);       \
-    hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / 64, umax), b256, 0, s, wd, a->i8s_down, bd, a->s2d_dev,  \
+    hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / down_rows<F, II>(), umax), b256, 0, s, wd, a->i8s_down, bd, a->s2d_dev,  \
                        hpair, wts, csr, P, part);                                                                  \
     hipLaunchKernelGGL((k_csr_combine<HH, II>), dim3(HH / (256 / lpr_of(II / 16))), b256, 0, s, part, M, K, sp, hsh, \
                        logits, ld, gated, y)

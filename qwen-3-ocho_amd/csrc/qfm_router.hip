@@ -42,7 +42,12 @@ __device__ __forceinline__ float canon_reduce_row(const float4 (&w)[NJ], const f
 // two shared-expert gate/up rows each, one per half-wave, giving
 // hsh[m][r] = silu(sg_r <Qg_r, x_m>) * (su_r <Qu_r, x_m>). x is bf16 [M][H],
 // logits [M][ld]. Every output depends on x only, so one launch covers all.
-template <int NJ, int I>
+// MR rows of x are processed together: their fma chains and butterflies are
+// independent, so they overlap (each row keeps the canonical order). With
+// MR > 1 the shared-expert rows are also split over x rows: block (pair, mg)
+// computes rows [2 mg, 2 mg + 2) of x for its row pair, MG = ceil(M / 2) blocks
+// per pair, laid out so that one pair's blocks share an XCD (and its L2).
+template <int NJ, int I, int MR>
 __global__ void __launch_bounds__(64)
 k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, const float *__restrict__ g,
                 ShPtrs sh, const uint16_t *__restrict__ x, int M, int E, float *__restrict__ logits, int ld,
@@ -58,24 +63,51 @@ k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, con
 #pragma unroll
         for (int j = 0; j < NJ; j++) w[j] = *reinterpret_cast<const float4 *>(wr + j * 256 + lane * 4);
         const float bb = (!is_g && bias) ? bias[b] : 0.0f;
-        for (int m = 0; m < M; m++) {
-            float xv[NJ][4];
+        for (int m0 = 0; m0 < M; m0 += MR) {
+            uint2 xp[MR][NJ];
 #pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const uint2 p = *reinterpret_cast<const uint2 *>(x + (size_t)m * H + j * 256 + lane * 4);
-                xv[j][0] = bf16_lo(p.x); xv[j][1] = bf16_hi(p.x);
-                xv[j][2] = bf16_lo(p.y); xv[j][3] = bf16_hi(p.y);
+            for (int r = 0; r < MR; r++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    xp[r][j] = m0 + r < M ? *reinterpret_cast<const uint2 *>(x + (size_t)(m0 + r) * H + j * 256 + lane * 4)
+                                          : make_uint2(0u, 0u);
+            float a[MR];
+#pragma unroll
+            for (int r = 0; r < MR; r++) {
+                a[r] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    a[r] = __fmaf_rn(w[j].x, bf16_lo(xp[r][j].x), a[r]);
+                    a[r] = __fmaf_rn(w[j].y, bf16_hi(xp[r][j].x), a[r]);
+                    a[r] = __fmaf_rn(w[j].z, bf16_lo(xp[r][j].y), a[r]);
+                    a[r] = __fmaf_rn(w[j].w, bf16_hi(xp[r][j].y), a[r]);
+                }
             }
-            float a = canon_reduce_row<NJ>(w, xv);
-            if (bias && !is_g) a = __fadd_rn(a, bb);
-            if (lane == 0) logits[(size_t)m * ld + b] = a;
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1)
+#pragma unroll
+                for (int r = 0; r < MR; r++) a[r] = __fadd_rn(a[r], __shfl_xor(a[r], m, WAVE));
+#pragma unroll
+            for (int r = 0; r < MR; r++) {
+                float v = a[r];
+                if (bias && !is_g) v = __fadd_rn(v, bb);
+                if (lane == 0 && m0 + r < M) logits[(size_t)(m0 + r) * ld + b] = v;
+            }
         }
         return;
     }
     // shared-expert gate/up rows
     constexpr int NST = H / 512;
     const int l = lane & 31;
-    const int r = (b - E - ng) * 2 + (lane >> 5);
+    const int sb = b - E - ng;
+    int pair = sb, mlo = 0, mhi = M;
+    if (MR > 1) {
+        const int MG = (M + 1) / 2, t = sb >> 3, mg = t % MG;
+        pair = (t / MG) * 8 + (sb & 7);
+        mlo = mg * 2;
+        mhi = min(M, mlo + 2);
+    }
+    const int r = pair * 2 + (lane >> 5);
     uint4 wg[NST], wu[NST];
 #pragma unroll
     for (int st = 0; st < NST; st++) {
@@ -83,23 +115,33 @@ k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, con
         wu[st] = ld_nt16(sh.qu + (size_t)r * H + st * 512 + l * 16);
     }
     const float sg = sh.sg[r], su = sh.su[r];
-    for (int m = 0; m < M; m++) {
-        float xs[NST][16];
-        load_x_slice_bf16<H>(x + (size_t)m * H, l, xs);
-        float xsum = 0.0f;
+    constexpr int SR = MR > 1 ? 2 : 1;          // x rows per pass of the shared rows
+    for (int m0 = mlo; m0 < mhi; m0 += SR) {
+        float ag[SR], au[SR];
 #pragma unroll
-        for (int st = 0; st < NST; st++)
+        for (int q = 0; q < SR; q++) {
+            ag[q] = 0.0f; au[q] = 0.0f;
+            if (m0 + q < mhi) {
+                float xs[NST][16];
+                load_x_slice_bf16<H>(x + (size_t)(m0 + q) * H, l, xs);
+                float xsum = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 16; i++) xsum += xs[st][i];
-        float ag = -128.0f * xsum, au = ag;
+                for (int st = 0; st < NST; st++)
 #pragma unroll
-        for (int st = 0; st < NST; st++) {
-            ag = dot16_u8(wg[st], xs[st], ag);
-            au = dot16_u8(wu[st], xs[st], au);
+                    for (int i = 0; i < 16; i++) xsum += xs[st][i];
+                ag[q] = -128.0f * xsum; au[q] = ag[q];
+#pragma unroll
+                for (int st = 0; st < NST; st++) {
+                    ag[q] = dot16_u8(wg[st], xs[st], ag[q]);
+                    au[q] = dot16_u8(wu[st], xs[st], au[q]);
+                }
+            }
         }
-        ag = group_sum<32>(ag);
-        au = group_sum<32>(au);
-        if (l == 0) hsh[(size_t)m * ldh + r] = silu(ag * sg) * (au * su);
+#pragma unroll
+        for (int q = 0; q < SR; q++) { ag[q] = group_sum<32>(ag[q]); au[q] = group_sum<32>(au[q]); }
+#pragma unroll
+        for (int q = 0; q < SR; q++)
+            if (l == 0 && m0 + q < mhi) hsh[(size_t)(m0 + q) * ldh + r] = silu(ag[q] * sg) * (au[q] * su);
     }
 }
 
@@ -148,11 +190,17 @@ int launch_router_shared(const float *W, const float *bias, const float *g, cons
     if (sh && !hsh) { set_error(-1, "router: shared rows need an output"); return -1; }
     ShPtrs sp{};
     if (sh) sp = *sh;
-    const int nblk = E + (g ? 1 : 0) + (sh ? I / 2 : 0);
+    const int nblk = E + (g ? 1 : 0) + (sh ? (I / 2) * (M == 1 ? 1 : (M + 1) / 2) : 0);
     if (shape_2048()) {
-        hipLaunchKernelGGL((k_router_shared<8, 512>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
+        if (M == 1)
+            hipLaunchKernelGGL((k_router_shared<8, 512, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
+        else
+            hipLaunchKernelGGL((k_router_shared<8, 512, 4>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
     } else if (shape_2560()) {
-        hipLaunchKernelGGL((k_router_shared<10, 640>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
+        if (M == 1)
+            hipLaunchKernelGGL((k_router_shared<10, 640, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
+        else
+            hipLaunchKernelGGL((k_router_shared<10, 640, 4>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
     } else {
         set_error(-2, "router: unsupported shape"); return -2;
     }
