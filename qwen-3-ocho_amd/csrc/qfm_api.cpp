@@ -85,7 +85,7 @@ static WsLayout ws_layout(int M) {
     w.wts = off;    off += align256((size_t)M * c.K * sizeof(float));
     w.hidden = off; off += align256((size_t)M * (c.K + 1) * c.I * sizeof(float));
     w.csr = off;    off += align256((size_t)(3 * M * c.K + 2) * sizeof(int));
-    w.part = off;   off += align256((size_t)M * c.K * c.H * sizeof(float));
+    w.part = off;   off += align256((size_t)M * (c.K + 1) * c.H * sizeof(float));   // K routed + shared slots
     w.total = off;
     return w;
 }

@@ -19,11 +19,13 @@
 //                  loaded once, then dotted with the x slice of each routed
 //                  token (L2-resident). hidden is written per pair, in CSR
 //                  order.
-//   k_csr_down     grid (H/64, min(M*K, E)), 256 threads: expert u's down rows
-//                  [64b, 64b+64), pairs' hidden vectors staged in LDS; writes
-//                  part[t*K + k][c] = w * <Wd_e[c], h_pair> * scale.
-//   k_csr_combine  grid (H/rows), 256 threads: y[t][c] = sum_k part[t*K+k][c]
-//                  + gamma_t * <Wd_sh[c], hsh_t> * sd_sh[c], bf16 out.
+//   k_csr_down     grid (H/ROWS, min(M*K, E) + shared), 256 threads: expert
+//                  u's down rows [ROWS b, ROWS b + ROWS), pairs' hidden vectors
+//                  staged in LDS; writes part[t*S + k][c] = w * <Wd_e[c], h_pair>
+//                  * scale, S = K + 1 with a shared expert. Grid rows
+//                  [0, ceil(M/2)) are then the shared expert (INT8), two tokens
+//                  each: part[t*S + K][c] = gamma_t * <Wd_sh[c], hsh_t> * sd_sh[c].
+//   k_pf_combine   y[t][c] = sum over the S slots of t in slot order, bf16 out.
 #include "qfm_dev.h"
 #include "qfm_internal.h"
 
@@ -219,6 +221,59 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
     }
 }
 
+// ---- shared expert's down rows (INT8) for tokens [t0, t1): one k_csr_down block ----
+// rows [c0, c0 + ROWS); hsh rows staged in LDS (sh_h, sh_cs as in k_csr_down)
+template <int H, int I, int ROWS>
+__device__ __forceinline__ void csr_down_shared(const ShPtrs &sh, const float *__restrict__ hsh,
+                                                const float *__restrict__ logits, int ld, int gated, int t0,
+                                                int t1, int S, int K, int c0, float *sh_h, float *sh_cs,
+                                                float *__restrict__ part) {
+    constexpr int CPR = I / 16, LPR = lpr_of(CPR), NST = CPR / LPR, GROUPS = 256 / LPR, RPG = ROWS / GROUPS;
+    static_assert(RPG >= 1 && RPG * GROUPS == ROWS, "shared rows must tile the block");
+    const int l = threadIdx.x % LPR, grp = threadIdx.x / LPR;
+    uint4 w[RPG][NST];
+    float rs[RPG];
+#pragma unroll
+    for (int q = 0; q < RPG; q++) {
+        const int c = c0 + q * GROUPS + grp;
+#pragma unroll
+        for (int st = 0; st < NST; st++) w[q][st] = ld_nt16(sh.qd + (size_t)c * I + (st * LPR + l) * 16);
+        rs[q] = sh.sd[c];
+    }
+    constexpr int TS = 2;                         // tokens per shared block
+    const int nt = t1 - t0;
+    float gam[TS];
+#pragma unroll
+    for (int t = 0; t < TS; t++) gam[t] = gated ? logits[(size_t)(t0 + (t < nt ? t : 0)) * ld + (ld - 1)] : 0.0f;
+    for (int i = threadIdx.x; i < nt * I / 4; i += 256)
+        reinterpret_cast<float4 *>(sh_h)[i] = reinterpret_cast<const float4 *>(hsh + (size_t)t0 * I)[i];
+    __syncthreads();
+    for (int i = threadIdx.x; i < nt * I / 16; i += 256) {
+        float t = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; q++) t += sh_h[i * 16 + q];
+        sh_cs[i] = -128.0f * t;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TS; t++) {
+        if (t >= nt) break;
+        const float g = gated ? sigmoid(gam[t]) : 1.0f;
+#pragma unroll
+        for (int q = 0; q < RPG; q++) {
+            const int c = c0 + q * GROUPS + grp;
+            float d = 0.0f;
+#pragma unroll
+            for (int st = 0; st < NST; st++) {
+                d += sh_cs[t * (I / 16) + st * LPR + l];
+                d = dot16_u8(w[q][st], sh_h + t * I + (st * LPR + l) * 16, d);
+            }
+            d = group_sum<LPR>(d);
+            if (l == 0) part[((size_t)(t0 + t) * S + K) * H + c] = g * (d * rs[q]);
+        }
+    }
+}
+
 // ---- down: one distinct expert x ROWS rows per block, owned partials ---------------
 template <class F, int I>
 constexpr int down_rows() {
@@ -228,7 +283,8 @@ template <class F, int H, int I>
 __global__ void __launch_bounds__(256)
 k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const uint8_t *__restrict__ Bd,
            const float *__restrict__ s2d, const float *__restrict__ hpair, const float *__restrict__ g_wts,
-           const int *__restrict__ g_csr, int P, float *__restrict__ part) {
+           const int *__restrict__ g_csr, int P, float *__restrict__ part, int K, ShPtrs sh,
+           const float *__restrict__ hsh, const float *__restrict__ logits, int ld, int gated, int M) {
     constexpr int ROWB = I / F::VPB;                   // bytes per down row
     constexpr int CPR = ROWB / 16;                     // 16-byte chunks per row
     constexpr int LPR = lpr_of(CPR);                   // lanes per row
@@ -237,7 +293,16 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
     constexpr int ROWS = down_rows<F, I>();
     __shared__ __align__(16) float sh_h[kMaxRows * I];
     __shared__ float sh_cs[kMaxRows * I / 16];
-    const int u = blockIdx.y;
+    const bool has_sh = sh.qd != nullptr;
+    const int S = K + (has_sh ? 1 : 0);
+    const int nsh = has_sh ? (M + 1) / 2 : 0;      // grid rows of shared blocks, two tokens each
+    if ((int)blockIdx.y < nsh) {                  // dispatched first
+        const int t0 = blockIdx.y * 2;
+        csr_down_shared<H, I, ROWS>(sh, hsh, logits, ld, gated, t0, min(M, t0 + 2), S, K, blockIdx.x * ROWS, sh_h,
+                                    sh_cs, part);
+        return;
+    }
+    const int u = blockIdx.y - nsh;
     const int n_exp = g_csr[0];
     if (u >= n_exp) return;
     const int *exp_id = g_csr + 1, *exp_ptr = g_csr + 1 + P, *pair = g_csr + 1 + P + P + 1;
@@ -293,78 +358,9 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
                 }
             }
             d = group_sum<LPR>(d);
-            if (l == 0) part[(size_t)pr * H + c] = wp * (d * rs[q]);
+            if (l == 0) part[((size_t)(pr / K) * S + pr % K) * H + c] = wp * (d * rs[q]);
         }
     }
-}
-
-// ---- combine + shared expert down (INT8) -------------------------------------------
-template <int H, int I>
-__global__ void __launch_bounds__(256)
-k_csr_combine(const float *__restrict__ part, int M, int K, ShPtrs sh, const float *__restrict__ hsh,
-              const float *__restrict__ logits, int ld, int gated, uint16_t *__restrict__ y) {
-    constexpr int LPR = lpr_of(I / 16), NST = I / (16 * LPR), RPB = 256 / LPR;
-    __shared__ __align__(16) float sh_h[kMaxRows * I];
-    __shared__ float sh_cs[kMaxRows * I / 16];
-    const int l = threadIdx.x % LPR;
-    const int c = blockIdx.x * RPB + threadIdx.x / LPR;
-    const bool has_sh = sh.qd != nullptr;
-    // Routed partials: lane l of a row group owns slots k = l, l + LPR, ... of
-    // every row. All loads (partials, gates, shared weights, shared hidden)
-    // are issued before any is consumed (clamped indices, masked afterwards)
-    // so their latencies overlap.
-    constexpr int NKL = (16 + LPR - 1) / LPR;
-    float pv[kMaxRows][NKL];
-#pragma unroll
-    for (int t = 0; t < kMaxRows; t++)
-#pragma unroll
-        for (int j = 0; j < NKL; j++) {
-            const int k = l + j * LPR, tt = t < M ? t : 0, kk = k < K ? k : 0;
-            pv[t][j] = part[((size_t)tt * K + kk) * H + c];
-        }
-    float glg[kMaxRows];
-#pragma unroll
-    for (int t = 0; t < kMaxRows; t++) glg[t] = (has_sh && gated) ? logits[(size_t)(t < M ? t : 0) * ld + (ld - 1)] : 0.0f;
-    uint4 w[NST];
-    float sd = 0.0f;
-    if (has_sh) {
-#pragma unroll
-        for (int st = 0; st < NST; st++) w[st] = ld_nt16(sh.qd + (size_t)c * I + (st * LPR + l) * 16);
-        sd = sh.sd[c];
-        for (int i = threadIdx.x; i < M * I / 4; i += 256)
-            reinterpret_cast<float4 *>(sh_h)[i] = reinterpret_cast<const float4 *>(hsh)[i];
-        __syncthreads();
-        for (int i = threadIdx.x; i < M * I / 16; i += 256) {
-            float t = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 16; q++) t += sh_h[i * 16 + q];
-            sh_cs[i] = -128.0f * t;
-        }
-        __syncthreads();
-    }
-    float rr[kMaxRows];
-#pragma unroll
-    for (int t = 0; t < kMaxRows; t++) {
-        float r = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NKL; j++) r += (l + j * LPR < K) ? pv[t][j] : 0.0f;
-        if (has_sh && t < M) {
-            const float gs = gated ? sigmoid(glg[t]) * sd : sd;
-            float d = 0.0f;
-#pragma unroll
-            for (int st = 0; st < NST; st++) {
-                d += sh_cs[t * (I / 16) + st * LPR + l];
-                d = dot16_u8(w[st], sh_h + t * I + (st * LPR + l) * 16, d);
-            }
-            r = fmaf(gs, d, r);
-        }
-        rr[t] = r;
-    }
-#pragma unroll
-    for (int t = 0; t < kMaxRows; t++) rr[t] = group_sum<LPR>(rr[t]);      // independent: interleaved
-#pragma unroll
-    for (int t = 0; t < kMaxRows; t++)
-        if (l == 0 && t < M) y[(size_t)t * H + c] = f32_to_bf16(rr[t]);
 }
 
 // ---- launchers -------------------------------------------------------------------
@@ -391,10 +387,9 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
     hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), b512, 0, s, logits, ld, M, K, g_cfg.renorm, sel, wts, csr);       \
     hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(II / (256 / lpr_of(HH / F::VPB / 16)), umax), b256, 0, s,  \
                        wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, K, csr, P, hpair);       \
-    hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / down_rows<F, II>(), umax), b256, 0, s, wd, a->i8s_down, bd, a->s2d_dev,  \
-                       hpair, wts, csr, P, part);                                                                  \
-    hipLaunchKernelGGL((k_csr_combine<HH, II>), dim3(HH / (256 / lpr_of(II / 16))), b256, 0, s, part, M, K, sp, hsh, \
-                       logits, ld, gated, y)
+    hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / down_rows<F, II>(), umax + (sh ? (M + 1) / 2 : 0)), b256, 0, s, wd,   \
+                       a->i8s_down, bd, a->s2d_dev, hpair, wts, csr, P, part, K, sp, hsh, logits, ld, gated, M);   \
+    launch_pf_combine(part, M, K + (sh ? 1 : 0), HH, y, s)
     if (shape_2048()) {
         if (fmt == QFM_FMT_INT8) { QFM_CSR_LAUNCH(FmtI8, 2048, 512); } else { QFM_CSR_LAUNCH(FmtF4, 2048, 512); }
     } else if (shape_2560()) {

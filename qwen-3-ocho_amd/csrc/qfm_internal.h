@@ -61,6 +61,8 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
 // Prefill (T > 8 rows): MFMA router + exact candidate selection, grouped
 // MFMA gate/up and down over the routing inversion, owned-partial combine.
 size_t prefill_ws_bytes(int T);
+// y[t] = sum of the S owned partial slots part[t*S + k][H] in slot order (bf16 out)
+void launch_pf_combine(const float *part, int T, int S, int H, uint16_t *y, hipStream_t s);
 void prefill_ws_view(void *ws, int T, float **lg_approx, int **sel, float **wts);
 int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, void *ws, int gated, hipStream_t s);
 

@@ -708,6 +708,11 @@ k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__re
                    (uint32_t)f32_to_bf16(a.z) | ((uint32_t)f32_to_bf16(a.w) << 16));
 }
 
+void launch_pf_combine(const float *part, int T, int S, int H, uint16_t *y, hipStream_t s) {
+    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)(((size_t)T * H / 4 + 255) / 256)), dim3(256), 0, s, part, T, S,
+                       H, y);
+}
+
 // ---- launcher -------------------------------------------------------------------------
 size_t prefill_ws_bytes(int T) {
     const Cfg &c = g_cfg;
@@ -823,8 +828,7 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
         hipLaunchKernelGGL((k_pf_gemm<false, false>), g_dn, nth, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot, p_wt,
                            hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu);
     }
-    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)(((size_t)T * H / 4 + 255) / 256)), dim3(256), 0, s, part, T, S,
-                       H, y);
+    launch_pf_combine(part, T, S, H, y, s);
     return check_launch("prefill");
 }
 
