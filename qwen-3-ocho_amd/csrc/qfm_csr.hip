@@ -141,6 +141,10 @@ k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, i
 }
 
 // ---- gate/up: one distinct expert per blockIdx.y ---------------------------------
+// lanes per gate/up row (32 measured best for both formats at M = 8; 16 and 8
+// were slower)
+template <class F, int H>
+constexpr int gateup_lpr() { return lpr_of(H / F::VPB / 16); }
 // One LPR-lane group per gate/up row; the row pair is loaded once and dotted
 // with the x slice of every routed token (x rows are L2-resident; each
 // 16-byte chunk's activations are converted right before use).
@@ -153,7 +157,7 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
              const uint16_t *__restrict__ x, int K, const int *__restrict__ g_csr, int P,
              float *__restrict__ hpair) {
     constexpr int ROWB = H / F::VPB;             // bytes per gate/up row
-    constexpr int LPR = lpr_of(ROWB / 16);       // lanes per row
+    constexpr int LPR = gateup_lpr<F, H>();      // lanes per row
     constexpr int NST = ROWB / (LPR * 16);
     constexpr int RPB = 256 / LPR;               // rows per block
     const int u = blockIdx.y;
@@ -385,7 +389,7 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
     }
 #define QFM_CSR_LAUNCH(F, HH, II)                                                                                   \
     hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), b512, 0, s, logits, ld, M, K, g_cfg.renorm, sel, wts, csr);       \
-    hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(II / (256 / lpr_of(HH / F::VPB / 16)), umax), b256, 0, s,  \
+    hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(II / (256 / gateup_lpr<F, HH>()), umax), b256, 0, s,  \
                        wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, K, csr, P, hpair);       \
     hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / down_rows<F, II>(), umax + (sh ? (M + 1) / 2 : 0)), b256, 0, s, wd,   \
                        a->i8s_down, bd, a->s2d_dev, hpair, wts, csr, P, part, K, sp, hsh, logits, ld, gated, M);   \
