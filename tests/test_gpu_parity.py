@@ -262,10 +262,9 @@ def test_moe_layer_deterministic(lib):
 
 
 # ------------------------------------------------------------------ prefill
-def _run_prefill(lib, T, seed, layer, x_layer, bias=True, fmt=qfm.QFM_FMT_INT8):
+def _run_prefill(lib, T, seed, layer, x_layer, bias=True, fmt=qfm.QFM_FMT_INT8, H=2048):
     st = qfm.Stream()
     L = qfm.SynthLayer(fmt, seed, layer, with_bias=bias, stream=st)
-    H = 2048
     dx, dy = qfm.DevBuf(T * H * 2), qfm.DevBuf(T * H * 2)
     qfm.check(lib.qfm_gen_input_rows(dx.ptr, T, seed, x_layer, 0, st.h), "x")
     wsb = lib.qfm_workspace_bytes(T)
@@ -316,6 +315,23 @@ def test_prefill_config4_routing_and_sample(lib):
         rel = max(_rel(g["y"][row0 + m], r["y"][m]) for m in range(32))
         _say("  rows", row0, "max rel err", rel)
         assert rel <= TOL
+
+
+@pytest.mark.parametrize("T,fmt,gated", [(37, 0, 1), (20, 1, 0)])
+def test_prefill_reference_shape(lib, T, fmt, gated):
+    """Prefill at the reference's own shape (H=2560, I=640): router tiles of
+    K=2560, five gate/up n-tiles, ten down n-tiles."""
+    _say("prefill 2560/640", T, fmt, gated)
+    _cfg(lib, H=2560, I=640, gated=gated)
+    g = _run_prefill(lib, T, 2, 5, 900 + T, True, fmt, H=2560)
+    r = orc.moe_layer(2560, 640, 512, 10, T, 2, 5, 900 + T, use_bias=1, fmt=fmt, gated=gated)
+    _cfg(lib)
+    assert np.array_equal(g["x"], r["x"])
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    rel = max(_rel(g["y"][m], r["y"][m]) for m in range(T))
+    _say("  max rel err", rel)
+    assert rel <= TOL
 
 
 def test_prefill_config4_nvfp4_sample(lib):
