@@ -32,11 +32,12 @@ GATE_VEC_BYTES = H * 4                                 # shared-expert sigmoid g
 LAYER_BYTES_M1 = (K + 1) * EXPERT_BYTES + ROUTER_BYTES + ACT_BYTES + GATE_VEC_BYTES
 HBM_PEAK_GBS = 8000.0
 # algorithmic bytes of the three M=1 launches of one layer
-SEC_NAMES = ["k_router_shared (router + shared gate/up)", "k_i8_gateup_m1 (top-K + routed gate/up)",
+SEC_NAMES = ["k_router_shared (router logits + shared gate logit)",
+             "k_i8_gateup_m1 (top-K + routed and shared gate/up)",
              "k_i8_down_m1 (routed + shared down, combine)"]
 SEC_BYTES = [
-    E * H * 4 + H * 4 + 2 * I * H + 2 * I * 4 + H * 2 + (E + 1) * 4 + I * 4,
-    K * (2 * I * H + 2 * I * 4) + H * 2 + E * 4 + K * I * 4 + 2 * K * 4,
+    E * H * 4 + H * 4 + H * 2 + (E + 1) * 4,
+    (K + 1) * (2 * I * H + 2 * I * 4) + H * 2 + E * 4 + (K + 1) * I * 4 + 2 * K * 4,
     (K + 1) * (H * I + H * 4) + (K + 1) * I * 4 + H * 2 + 2 * K * 4 + 4,
 ]
 
@@ -340,8 +341,9 @@ def main():
         with open(tpath) as f:
             tj = json.load(f)
         kname = SEC_NAMES[dom].split()[0]
-        if kname in tj.get("kernels", {}):
-            traffic = tj["kernels"][kname]["traffic_bytes"]
+        kj = tj.get("kernels", {}).get(kname)
+        if kj and kj.get("algorithmic_bytes") == SEC_BYTES[dom]:     # measured on this kernel's byte layout
+            traffic = kj["traffic_bytes"]
             traffic_src = "profiles/m1_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
     out = {
         "metric": "MoE-layer us/token at M=1 & M=8 (HBM GB/s, % peak); prefill MoE tok/s",

@@ -269,12 +269,13 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
     if (M == 1 && L->fmt == QFM_FMT_INT8 && c.E == 512) {
         // per row: K routed hidden vectors, then the shared one (read as one block by the down kernel)
         float *hsh = hidden + (size_t)c.K * c.I;
-        // 1. router logits (+ shared gate dot) and the shared expert's hidden: depend on x only
+        // 1. router logits (+ shared gate dot): depend on x only
         int rc = 0;
-        if (mask & 1) rc = launch_router_shared(L->router, L->router_bias, g, sp, x, 1, logits, ld, hsh, c.I, s);
+        if (mask & 1) rc = launch_router_shared(L->router, L->router_bias, g, nullptr, x, 1, logits, ld, hsh, c.I, s);
         if (g_prof.on) pm[1] = prof_event(s);
-        // 2. top-K inside the gate/up kernel; 3. down + combine (+ shared) -> y bf16
-        if (!rc && (mask & 2)) rc = launch_i8_gateup_m1(L->arena, x, nullptr, logits, sel, wts, c.K, hidden, s);
+        // 2. top-K inside the gate/up kernel, whose last grid row computes the shared
+        // expert's hidden (no selection needed there); 3. down + combine (+ shared) -> y bf16
+        if (!rc && (mask & 2)) rc = launch_i8_gateup_m1(L->arena, x, nullptr, logits, sel, wts, c.K, hidden, s, sp);
         if (g_prof.on) pm[2] = prof_event(s);
         if (!rc && (mask & 4))
             rc = launch_i8_down_m1(L->arena, hidden, wts, sel, c.K, sp, g ? logits + c.E : nullptr, nullptr, y, s);

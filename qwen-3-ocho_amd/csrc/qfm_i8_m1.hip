@@ -14,9 +14,12 @@
 // row, so it is held in registers as fp32 (no LDS). Each code q is used in
 // offset-binary form q + 128 (one v_cvt_f32_ubyte per code) and the
 // accumulator starts at -128 * sum(x_slice). When the launch carries the
-// router logits, wave 0 of every block runs the top-K selection itself (the
-// 2 KiB row of logits is L2-resident), which removes a dependent launch from
-// the decode chain; block (0, 0) publishes sel/wts for the down kernel.
+// router logits, every wave runs the top-K selection itself (the 2 KiB row of
+// logits is L2-resident), which removes a dependent launch from the decode
+// chain; block (0, 0) publishes sel/wts for the down kernel. With a shared
+// expert the last grid row computes its gate/up rows (job K, hidden row K):
+// those blocks need no selection, so their weight stream runs while the
+// routed blocks are still selecting.
 //
 // down: one LPR-lane group per output row (LPR = 32 for I = 512, 8 for
 // I = 640). Every weight load of the row is issued first (the 16-byte chunks
@@ -36,17 +39,20 @@ k_i8_gateup_m1(const int8_t *__restrict__ Qg, const int8_t *__restrict__ Qu,
                const float *__restrict__ Sg, const float *__restrict__ Su,
                const uint16_t *__restrict__ xb, const float *__restrict__ xf,
                const float *__restrict__ logits, int *__restrict__ sel, float *__restrict__ wts,
-               int K, int renorm, float *__restrict__ hidden) {
+               int K, int renorm, float *__restrict__ hidden, ShPtrs sh) {
     constexpr int NST = H / 512;
     __shared__ __align__(16) unsigned long long s_tk[4][kTopkLds];
     const int job = blockIdx.y;
+    const bool shared_job = sh.qg != nullptr && job == (int)gridDim.y - 1;
     const int l = threadIdx.x & 31;
     const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
     float xs[NST][16];
     if (xb) load_x_slice_bf16<H>(xb, l, xs);
     else load_x_slice_f32<H>(xf, l, xs);
-    int e;
-    if (logits) {
+    int e = 0;
+    if (shared_job) {
+        Qg = sh.qg; Qu = sh.qu; Sg = sh.sg; Su = sh.su;     // expert 0 of a one-expert arena
+    } else if (logits) {
         // every wave selects its block's expert itself (no barrier): the rank-`job`
         // id only; wave 0 of block (0, 0) also writes the routing (ids + weights)
         const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -209,7 +215,7 @@ static bool down_dispatch_nj(int nj, bool has_sh, const Qf4ExpCache *c, const fl
 }
 
 int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *xf, const float *logits, int *sel,
-                        float *wts, int nexp, float *hidden, hipStream_t s) {
+                        float *wts, int nexp, float *hidden, hipStream_t s, const ShPtrs *sh) {
     if (!c || !c->i8_gate || !c->i8_up || !c->i8s_gate || !c->i8s_up) {
         set_error(-1, "i8_gateup_m1: arena has no INT8 gate/up"); return -1;
     }
@@ -221,12 +227,15 @@ int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *x
     }
     const dim3 block(256);
     const int K = g_cfg.K, rn = g_cfg.renorm;
+    ShPtrs sp{};
+    if (sh) sp = *sh;
+    const unsigned jobs = (unsigned)nexp + (sh ? 1u : 0u);   // shared expert: last grid row, hidden row nexp
     if (shape_2048()) {
-        hipLaunchKernelGGL((k_i8_gateup_m1<2048, 512, 8>), dim3(512 / 8, nexp), block, 0, s, c->i8_gate, c->i8_up,
-                           c->i8s_gate, c->i8s_up, xb, xf, logits, sel, wts, K, rn, hidden);
+        hipLaunchKernelGGL((k_i8_gateup_m1<2048, 512, 8>), dim3(512 / 8, jobs), block, 0, s, c->i8_gate, c->i8_up,
+                           c->i8s_gate, c->i8s_up, xb, xf, logits, sel, wts, K, rn, hidden, sp);
     } else if (shape_2560()) {
-        hipLaunchKernelGGL((k_i8_gateup_m1<2560, 640, 8>), dim3(640 / 8, nexp), block, 0, s, c->i8_gate, c->i8_up,
-                           c->i8s_gate, c->i8s_up, xb, xf, logits, sel, wts, K, rn, hidden);
+        hipLaunchKernelGGL((k_i8_gateup_m1<2560, 640, 8>), dim3(640 / 8, jobs), block, 0, s, c->i8_gate, c->i8_up,
+                           c->i8s_gate, c->i8s_up, xb, xf, logits, sel, wts, K, rn, hidden, sp);
     } else {
         set_error(-2, "i8_gateup_m1: unsupported shape"); return -2;
     }

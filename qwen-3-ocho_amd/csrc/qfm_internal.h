@@ -39,9 +39,10 @@ int launch_topk(const float *logits, int ld_logits, int M, int *sel, float *wts,
 // INT8 M=1 routed gate/up: hidden[k][I] for the nexp experts sel[0..nexp).
 // With logits != nullptr the selection is made inside the kernel (every block
 // runs the top-K of its row of logits) and block 0 writes sel/wts; otherwise
-// sel is an input. x is bf16 (xb) or fp32 (xf).
+// sel is an input. x is bf16 (xb) or fp32 (xf). With sh != nullptr the shared
+// expert's hidden vector is computed too, into hidden row nexp.
 int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *xf, const float *logits,
-                        int *sel, float *wts, int nexp, float *hidden, hipStream_t s);
+                        int *sel, float *wts, int nexp, float *hidden, hipStream_t s, const ShPtrs *sh = nullptr);
 // y = sum_k wts[k] * down_k(hidden[k]) (+ gamma * shared_down(hidden[nexp]) when
 // sh != nullptr: the shared expert's hidden vector follows the routed ones),
 // gamma = sigmoid(*gdot) when gdot != nullptr, 1 otherwise. Writes y32 and/or ybf.
