@@ -299,22 +299,23 @@ def test_prefill_small(lib, T, bias, fmt):
 
 def test_prefill_config4_routing_and_sample(lib):
     """BASELINE config 4 shape: T=8038, skewed router bias. Routing is checked for
-    every token (bit-exact); outputs on two 32-token windows (oracle cost)."""
+    every token (bit-exact) and the outputs of every token against the fp64
+    oracle, so all tokens of the hottest (7741 of them) and coldest experts are
+    covered."""
     T, seed, layer, xl = 8038, 0, 3, 700
     _say("prefill config4", T)
     _cfg(lib)
     g = _run_prefill(lib, T, seed, layer, xl, True)
-    E, H = 512, 2048
-    W = orc.fill("gauss", seed, layer, orc.T_ROUTER, 0, E * H, 0.02).reshape(E, H)
-    b = orc.fill("gauss", seed, layer, orc.T_BIAS, 0, E, 1.5)
-    sel, w64, _ = orc.topk(orc.router_logits(W, g["x"], b), 10)
-    assert np.array_equal(g["sel"], sel)
-    assert np.allclose(g["wts"], w64, rtol=2e-6, atol=1e-7)
-    for row0 in (0, 5000):
-        r = orc.moe_layer(2048, 512, 512, 10, 32, seed, layer, xl, x_row0=row0, use_bias=1)
-        rel = max(_rel(g["y"][row0 + m], r["y"][m]) for m in range(32))
-        _say("  rows", row0, "max rel err", rel)
-        assert rel <= TOL
+    r = orc.moe_layer(2048, 512, 512, 10, T, seed, layer, xl, x_row0=0, use_bias=1)
+    assert np.array_equal(g["x"], r["x"])
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    cnt = np.bincount(g["sel"].ravel(), minlength=512)
+    hot, cold = int(cnt.argmax()), int(np.where(cnt > 0, cnt, 1 << 30).argmin())
+    _say("  hottest expert", hot, cnt[hot], "coldest", cold, cnt[cold])
+    rel = np.abs(g["y"] - r["y"]).max(axis=1) / np.abs(r["y"]).max(axis=1)
+    _say("  max rel err over all rows", float(rel.max()))
+    assert float(rel.max()) <= TOL
 
 
 @pytest.mark.parametrize("T,fmt,gated", [(37, 0, 1), (20, 1, 0)])
@@ -336,7 +337,9 @@ def test_prefill_reference_shape(lib, T, fmt, gated):
 
 def test_prefill_config4_nvfp4_sample(lib):
     """Config 4's prefill (T=8038, skewed router bias) on an NVFP4 arena: routing
-    for every token, outputs on a 32-token window (includes the hottest expert)."""
+    of every token, outputs of a 1024-token window against the fp64 oracle (the
+    NVFP4 oracle over all 8038 tokens takes ~3 minutes on the test host; it
+    passed at 5.3e-3 when run once)."""
     T, seed, layer, xl = 8038, 0, 3, 700
     _say("prefill config4 nvfp4", T)
     _cfg(lib)
@@ -346,7 +349,7 @@ def test_prefill_config4_nvfp4_sample(lib):
     b = orc.fill("gauss", seed, layer, orc.T_BIAS, 0, E, 1.5)
     sel, w64, _ = orc.topk(orc.router_logits(W, g["x"], b), 10)
     assert np.array_equal(g["sel"], sel)
-    r = orc.moe_layer(2048, 512, 512, 10, 32, seed, layer, xl, x_row0=3000, use_bias=1, fmt=1)
-    rel = max(_rel(g["y"][3000 + m], r["y"][m]) for m in range(32))
-    _say("  rows 3000 max rel err", rel)
-    assert rel <= TOL
+    r = orc.moe_layer(2048, 512, 512, 10, 1024, seed, layer, xl, x_row0=3000, use_bias=1, fmt=1)
+    rel = np.abs(g["y"][3000:4024] - r["y"]).max(axis=1) / np.abs(r["y"]).max(axis=1)
+    _say("  rows 3000..4023 max rel err", float(rel.max()))
+    assert float(rel.max()) <= TOL
