@@ -90,13 +90,55 @@ __device__ __forceinline__ void f4_to_bf16(uint4 w, uint32_t sc2, uint4 (&o)[4])
 }
 
 // ---- router prep: ||w_e||_2 (fp64 accumulate, rounded up) --------------------------
+// Blocks [0, E): ||w_e||_2 (fp64 accumulate, rounded up) and bf16(W) for the
+// router GEMM. Blocks [E, E + ceil(T/4)): one wave per token row, ||x_t||_2
+// (fp64, rounded up) and sum(x_t) (fp32; the offset-binary correction of the
+// gate/up GEMM), every load of the row in flight at once, lane partials
+// combined by a butterfly (fixed order).
 __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict__ W, int E, int H,
-                                                         float *__restrict__ wnorm) {
+                                                         float *__restrict__ wnorm, uint16_t *__restrict__ wb,
+                                                         const uint16_t *__restrict__ x, int T,
+                                                         float *__restrict__ xnorm, float *__restrict__ xsum) {
+    if ((int)blockIdx.x >= E) {
+        constexpr int kMaxCh = 5;                    // 16-byte chunks per lane: H / 512 <= 5
+        const int lane = threadIdx.x & 63;
+        const int t = ((int)blockIdx.x - E) * 4 + (threadIdx.x >> 6);
+        if (t >= T) return;
+        const uint4 *xr = reinterpret_cast<const uint4 *>(x + (size_t)t * H);
+        const int nch = H / 512;
+        uint4 v[kMaxCh];
+#pragma unroll
+        for (int q = 0; q < kMaxCh; q++) v[q] = q < nch ? xr[q * 64 + lane] : make_uint4(0u, 0u, 0u, 0u);
+        double sq = 0.0;
+        float sx = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kMaxCh; q++) {
+            const uint32_t d[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float a = bf16_lo(d[u]), b = bf16_hi(d[u]);
+                sq += (double)a * a + (double)b * b;
+                sx += a + b;
+            }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            sq += __shfl_xor(sq, m, WAVE);
+            sx += __shfl_xor(sx, m, WAVE);
+        }
+        if (lane == 0) {
+            xnorm[t] = (float)(sqrt(sq) * (1.0 + 1e-6));
+            xsum[t] = sx;
+        }
+        return;
+    }
     const int e = blockIdx.x;
     double s = 0.0;
     for (int k = threadIdx.x; k < H; k += 256) {
-        const double v = (double)W[(size_t)e * H + k];
+        const float w = W[(size_t)e * H + k];
+        const double v = (double)w;
         s += v * v;
+        wb[(size_t)e * H + k] = f32_to_bf16(w);     // the router GEMM's B operand (round to nearest even)
     }
     __shared__ double red[256];
     red[threadIdx.x] = s;
@@ -373,7 +415,10 @@ struct TileEngine3 {
 };
 
 // router GEMM: 128 x 128 tiles, 2 x 2 waves; grouped expert GEMMs: 128 x 256, 2 x 4 waves
-using RouterEngine = TileEngine2<kB_F32, 2, 2, kStagesF32>;
+using RouterEngine = TileEngine2<kB_BF16, 2, 2, kStagesF32>;
+// router GEMM slices along H, summed in slice order by k_pf_select (2 measured
+// 5% slower than 1 at T = 8038: the 63 m-tiles x 4 n-tiles already fill the chip)
+constexpr int kRouterKS = 1;
 // INT8 tiles: 128 x 256 in 8 waves of 64 x 64 (two waves per SIMD). Four
 // waves of 128 x 64 (MW = 8: one wave per SIMD, accumulators in AGPRs, 25%
 // fewer LDS reads per MFMA) measured 1343 / 1149 us against 797 / 719 us.
@@ -396,21 +441,22 @@ __device__ __forceinline__ void xcd_tile(int b, int nt, int &m, int &n) {
 
 // ---- router GEMM: logits~ [T][E] --------------------------------------------------
 __global__ void __launch_bounds__(256)
-k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const float *__restrict__ W, int E,
-                 const float *__restrict__ bias, float *__restrict__ lg_approx, float *__restrict__ xnorm,
-                 float *__restrict__ xsum) {
+k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const uint16_t *__restrict__ Wb, int E,
+                 float *__restrict__ lg_part) {
     __shared__ __align__(16) TileLds<RouterEngine::BMt, RouterEngine::BNt> lds;
     __shared__ int arow[BM];
     __shared__ const char *bptr[BN];
     int mt, et;
+    const int ks = blockIdx.y, Hk = H / kRouterKS, k0 = ks * Hk;     // this block's slice of H
     xcd_tile(blockIdx.x, E / BN, mt, et);
     if (mt * BM >= T) return;
     const int t0 = mt * BM, e0 = et * BN;
     if (threadIdx.x < BM) arow[threadIdx.x] = (t0 + (int)threadIdx.x < T) ? t0 + (int)threadIdx.x : -1;
-    if (threadIdx.x < BN) bptr[threadIdx.x] = reinterpret_cast<const char *>(W + (size_t)(e0 + threadIdx.x) * H);
+    if (threadIdx.x < BN) bptr[threadIdx.x] = reinterpret_cast<const char *>(Wb + (size_t)(e0 + threadIdx.x) * H + k0);
     __syncthreads();
     f32x4_t acc[4][4];
-    RouterEngine::run(x, H, arow, bptr, H, lds, acc);
+    RouterEngine::run(x + k0, H, arow, bptr, Hk, lds, acc);
+    float *lg_approx = lg_part + (size_t)ks * T * E;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave >> 1, wn = wave & 1;
 #pragma unroll
     for (int mb = 0; mb < 4; mb++)
@@ -419,30 +465,8 @@ k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const float *__re
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int r = wm * 64 + mb * 16 + (lane >> 4) * 4 + i, c = wn * 64 + nb * 16 + (lane & 15);
-                if (t0 + r < T) {
-                    float v = acc[mb][nb][i];
-                    if (bias) v += bias[e0 + c];
-                    lg_approx[(size_t)(t0 + r) * E + e0 + c] = v;
-                }
+                if (t0 + r < T) lg_approx[(size_t)(t0 + r) * E + e0 + c] = acc[mb][nb][i];
             }
-    // ||x_t||_2 of this block's tokens (first column block only)
-    if (et == 0 && threadIdx.x < BM && t0 + (int)threadIdx.x < T) {
-        const uint16_t *xr = x + (size_t)(t0 + threadIdx.x) * H;
-        double s = 0.0;
-        float sx = 0.0f;
-        for (int k = 0; k < H; k += 8) {
-            const uint4 p = *reinterpret_cast<const uint4 *>(xr + k);
-            const uint32_t d[4] = {p.x, p.y, p.z, p.w};
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const double a = bf16_lo(d[q]), b = bf16_hi(d[q]);
-                s += a * a + b * b;
-                sx += bf16_lo(d[q]) + bf16_hi(d[q]);
-            }
-        }
-        xnorm[t0 + threadIdx.x] = (float)(sqrt(s) * (1.0 + 1e-6));
-        xsum[t0 + threadIdx.x] = sx;
-    }
 }
 
 // canonical-order dot of one router row with one token, computed by a full wave
@@ -474,7 +498,7 @@ __device__ __forceinline__ float bound_coeff(int H) {
 template <int NJ, int EPL>
 __global__ void __launch_bounds__(256)
 k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, const float *__restrict__ bias,
-            const float *__restrict__ g, const float *__restrict__ lg_approx, const float *__restrict__ xnorm,
+            const float *__restrict__ g, float *__restrict__ lg_approx, const float *__restrict__ xnorm,
             const float *__restrict__ wnorm, int K, int renorm, int *__restrict__ sel, float *__restrict__ wts,
             float *__restrict__ gam, int *__restrict__ n_fallback) {
     constexpr int H = NJ * 256, E = EPL * 64;
@@ -488,7 +512,11 @@ k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, 
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
         const int e = i * 64 + lane;
-        const float l = lg_approx[(size_t)t * E + e];
+        float l = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kRouterKS; q++) l += lg_approx[((size_t)q * T + t) * E + e];   // slice order
+        if (bias) l += bias[e];
+        lg_approx[(size_t)t * E + e] = l;          // the view's approximate logits
         const float b = cB * wnorm[e] + 1e-6f * (fabsf(l) + (bias ? fabsf(bias[e]) : 0.0f) + 1.0f);
         lo[i] = l - b;
         hi[i] = l + b;
@@ -856,8 +884,9 @@ size_t prefill_ws_bytes(int T) {
     const size_t P = (size_t)T * (c.K + 1);
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     size_t b = 0;
-    b += al((size_t)T * c.E * 4);          // lg_approx
+    b += al((size_t)kRouterKS * T * c.E * 4);   // router GEMM slices (slice 0 ends as lg_approx)
     b += al((size_t)T * 4) + al((size_t)c.E * 4);   // xnorm, wnorm
+    b += al((size_t)c.E * c.H * 2);        // bf16 router weights
     b += al((size_t)T * c.K * 4) * 2;      // sel, wts
     b += al((size_t)T * 4);                // gam
     b += al(4 * 8);                        // counters
@@ -877,9 +906,10 @@ void prefill_ws_view(void *ws, int T, float **lg, int **sel, float **wts) {
     const Cfg &c = g_cfg;
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     char *b = static_cast<char *>(ws);
-    *lg = reinterpret_cast<float *>(b); b += al((size_t)T * c.E * 4);
+    *lg = reinterpret_cast<float *>(b); b += al((size_t)kRouterKS * T * c.E * 4);
     b += al((size_t)T * 4);
     b += al((size_t)c.E * 4);
+    b += al((size_t)c.E * c.H * 2);
     *sel = reinterpret_cast<int *>(b); b += al((size_t)T * c.K * 4);
     *wts = reinterpret_cast<float *>(b);
 }
@@ -903,9 +933,10 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     const size_t P = (size_t)T * S;
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     char *b = static_cast<char *>(ws);
-    float *lg = reinterpret_cast<float *>(b); b += al((size_t)T * E * 4);
+    float *lg = reinterpret_cast<float *>(b); b += al((size_t)kRouterKS * T * E * 4);
     float *xnorm = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
     float *wnorm = reinterpret_cast<float *>(b); b += al((size_t)E * 4);
+    uint16_t *wb16 = reinterpret_cast<uint16_t *>(b); b += al((size_t)E * H * 2);
     int *sel = reinterpret_cast<int *>(b); b += al((size_t)T * K * 4);
     float *wts = reinterpret_cast<float *>(b); b += al((size_t)T * K * 4);
     float *gam = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
@@ -928,10 +959,10 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     const float *g = (has_sh && gated) ? L->sh_gate_inp : nullptr;
     // zero the small counters with a fill kernel (no memset node in captured graphs)
     launch_fill_f32(reinterpret_cast<float *>(ctr), 8, 0.0f, s);
-    hipLaunchKernelGGL(k_pf_router_prep, dim3(E), dim3(256), 0, s, L->router, E, H, wnorm);
+    hipLaunchKernelGGL(k_pf_router_prep, dim3((unsigned)(E + (T + 3) / 4)), dim3(256), 0, s, L->router, E, H, wnorm,
+                       wb16, x, T, xnorm, xsum);
     const int mt_router = ((T + BM - 1) / BM + 7) / 8 * 8;
-    hipLaunchKernelGGL(k_pf_router_mfma, dim3(mt_router * (E / BN)), dim3(256), 0, s, x, T, H, L->router, E,
-                       L->router_bias, lg, xnorm, xsum);
+    hipLaunchKernelGGL(k_pf_router_mfma, dim3(mt_router * (E / BN), kRouterKS), dim3(256), 0, s, x, T, H, wb16, E, lg);
     if (H == 2048)
         hipLaunchKernelGGL((k_pf_select<8, 8>), dim3((T + 3) / 4), dim3(256), 0, s, x, T, L->router, L->router_bias,
                            g, lg, xnorm, wnorm, K, c.renorm, sel, wts, gam, ctr);
