@@ -487,6 +487,36 @@ __device__ __forceinline__ float canon_dot_wave(const float *__restrict__ w, con
     return a;
 }
 
+// The same canonical dot for CB router rows at once (x held in registers):
+// the CB rows' loads are all in flight before the first multiply and the CB
+// fma chains and butterflies are independent. Each dot keeps the order above.
+template <int NJ, int CB>
+__device__ __forceinline__ void canon_dot_wave_batch(const float *__restrict__ W, int H, const int (&e)[CB],
+                                                     const float (&xv)[NJ][4], int lane, float (&out)[CB]) {
+    float4 wv[CB][NJ];
+#pragma unroll
+    for (int c = 0; c < CB; c++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            wv[c][j] = *reinterpret_cast<const float4 *>(W + (size_t)e[c] * H + j * 256 + lane * 4);
+#pragma unroll
+    for (int c = 0; c < CB; c++) {
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            a = __fmaf_rn(wv[c][j].x, xv[j][0], a);
+            a = __fmaf_rn(wv[c][j].y, xv[j][1], a);
+            a = __fmaf_rn(wv[c][j].z, xv[j][2], a);
+            a = __fmaf_rn(wv[c][j].w, xv[j][3], a);
+        }
+        out[c] = a;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1)
+#pragma unroll
+        for (int c = 0; c < CB; c++) out[c] = __fadd_rn(out[c], __shfl_xor(out[c], m, WAVE));
+}
+
 // Error-bound constant per unit of ||w_e|| ||x_t||: bf16 rounding of W
 // (2^-9), MFMA fp32 accumulation over H products (<= 2 H ulps, any order),
 // canonical order (H/64 + 6 roundings), with a factor-2 margin.
@@ -564,15 +594,33 @@ k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, 
     // exact logits of the candidates (all E on overflow) -> 64-bit keys; lane k < K
     // keeps the k-th best key so far (descending), maintained by insertion
     unsigned long long best = 0;
-    for (int c = 0; c < nc; c++) {
-        const int e = full ? c : s_cand[wave][c];
-        float l = canon_dot_wave<NJ>(W + (size_t)e * H, xt, lane);
-        if (bias) l = __fadd_rn(l, bias[e]);
-        const unsigned long long key = topk_key(l, e);
-        // insert into the sorted lane list: lanes with a smaller key shift down
-        const unsigned long long prev = __shfl_up(best, 1, WAVE);
-        const bool ge_prev = lane == 0 || prev > key;
-        if (lane < K && best < key) best = ge_prev ? key : prev;
+    float xv[NJ][4];                                // this token's x slice, canonical lane layout
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const uint2 p = *reinterpret_cast<const uint2 *>(xt + j * 256 + lane * 4);
+        xv[j][0] = bf16_lo(p.x); xv[j][1] = bf16_hi(p.x); xv[j][2] = bf16_lo(p.y); xv[j][3] = bf16_hi(p.y);
+    }
+    constexpr int CB = 4;                           // candidates per batch of loads
+    for (int c0 = 0; c0 < nc; c0 += CB) {
+        int eb[CB];
+#pragma unroll
+        for (int q = 0; q < CB; q++) {
+            const int c = c0 + q < nc ? c0 + q : c0;  // past the end: repeat a candidate, result dropped
+            eb[q] = full ? c : s_cand[wave][c];
+        }
+        float lb[CB];
+        canon_dot_wave_batch<NJ, CB>(W, H, eb, xv, lane, lb);
+#pragma unroll
+        for (int q = 0; q < CB; q++) {
+            if (c0 + q >= nc) break;
+            float l = lb[q];
+            if (bias) l = __fadd_rn(l, bias[eb[q]]);
+            const unsigned long long key = topk_key(l, eb[q]);
+            // insert into the sorted lane list: lanes with a smaller key shift down
+            const unsigned long long prev = __shfl_up(best, 1, WAVE);
+            const bool ge_prev = lane == 0 || prev > key;
+            if (lane < K && best < key) best = ge_prev ? key : prev;
+        }
     }
     const float mx = topk_key_value(__shfl(best, 0, WAVE));
     const float ek = lane < K ? __expf(topk_key_value(best) - mx) : 0.0f;
