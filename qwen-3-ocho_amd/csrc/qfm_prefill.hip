@@ -308,8 +308,8 @@ struct TileEngine3 {
     static constexpr int BCPR = BMODE == kB_I8 ? 4 : 2;                 // 16-byte B chunks per row per k-step
     static constexpr int NA = BMt * 8 / NT, NB = BNt * BCPR / NT;      // chunks per thread
     static_assert(NA * NT == BMt * 8 && NB * NT == BNt * BCPR, "staging must divide evenly");
-    struct Stage {
-        uint4 a[NA], b[NB];
+    struct Stage {                                // native vector types: SROA keeps them in registers
+        u32x4_t a[NA], b[NB];                     // (with uint4 the stages were promoted to LDS or scratch)
         uint32_t sc[NB];
     };
     __device__ static void run(const uint16_t *__restrict__ A, long lda, const int *arow,
@@ -338,31 +338,32 @@ struct TileEngine3 {
         }
         auto gload = [&](int k0, Stage &g) __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < NA; j++) g.a[j] = *reinterpret_cast<const uint4 *>(ap[j] + k0);
+            for (int j = 0; j < NA; j++) g.a[j] = *reinterpret_cast<const u32x4_t *>(ap[j] + k0);
 #pragma unroll
             for (int j = 0; j < NB; j++) {
                 if constexpr (BMODE == kB_I8) {
-                    g.b[j] = *reinterpret_cast<const uint4 *>(bp[j] + k0);
+                    g.b[j] = *reinterpret_cast<const u32x4_t *>(bp[j] + k0);
                 } else {
-                    g.b[j] = *reinterpret_cast<const uint4 *>(bp[j] + k0 / 2);
+                    g.b[j] = *reinterpret_cast<const u32x4_t *>(bp[j] + k0 / 2);
                     g.sc[j] = *reinterpret_cast<const uint16_t *>(sp[j] + k0 / 16);
                 }
             }
         };
         auto sstore = [&](int buf, const Stage &g) __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < NA; j++) *reinterpret_cast<uint4 *>(&L.a[buf][a_lds[j]]) = g.a[j];
+            for (int j = 0; j < NA; j++) *reinterpret_cast<u32x4_t *>(&L.a[buf][a_lds[j]]) = g.a[j];
 #pragma unroll
             for (int j = 0; j < NB; j++) {
                 uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]);
+                const uint4 bw = make_uint4(g.b[j].x, g.b[j].y, g.b[j].z, g.b[j].w);
                 if constexpr (BMODE == kB_I8) {
                     uint4 o0, o1;
-                    i8_to_bf16_ob(g.b[j], o0, o1);
+                    i8_to_bf16_ob(bw, o0, o1);
                     lb[0] = o0;
                     lb[1] = o1;
                 } else {
                     uint4 o[4];
-                    f4_to_bf16(g.b[j], g.sc[j], o);
+                    f4_to_bf16(bw, g.sc[j], o);
 #pragma unroll
                     for (int q = 0; q < 4; q++) lb[q] = o[q];
                 }
@@ -423,6 +424,9 @@ constexpr int kRouterKS = 1;
 // waves of 128 x 64 (MW = 8: one wave per SIMD, accumulators in AGPRs, 25%
 // fewer LDS reads per MFMA) measured 1343 / 1149 us against 797 / 719 us.
 using ExpertEngine = TileEngine3<kB_I8, 2, 4, 4>;
+// INT8 down tiles: 128 x 128 in 4 waves, two blocks per CU (K = I is short, so
+// one block's prologue and epilogue overlap the other block's k-steps)
+using DownEngineI8 = TileEngine3<kB_I8, 2, 2, 4>;
 // NVFP4 launches keep the first engine for both tile kinds (measured faster
 // there: 923 / 778 us vs 959 / 840 us with the pipelined engine for e2m1 tiles)
 using ExpertEngineF4 = TileEngine2<kB_F4, 2, 4, kStagesI8>;
@@ -761,20 +765,24 @@ struct GroupW {
 // NVFP4 arena (block scales staged into the bf16 B tile, the global scale s2
 // applied in the epilogue) and the shared expert's tiles, INT8 in both formats,
 // through the first engine type.
-enum { kAllI8 = 0, kRoutedF4 = 1 };
+// kDownI8: INT8 down on 128 x 128 tiles (DownEngineI8).
+enum { kAllI8 = 0, kRoutedF4 = 1, kDownI8 = 2 };
 template <bool GATEUP, int MODE>
-__global__ void __launch_bounds__(MODE == kAllI8 ? ExpertEngine::NT : ExpertEngineF4::NT)
+__global__ void __launch_bounds__(MODE == kAllI8 ? ExpertEngine::NT : MODE == kDownI8 ? DownEngineI8::NT
+                                                                                      : ExpertEngineF4::NT)
+__attribute__((amdgpu_waves_per_eu(2, 2)))
 k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int which, const int *__restrict__ off,
           const int *__restrict__ p_tok, const int *__restrict__ p_slot, const float *__restrict__ p_wt,
           const uint16_t *__restrict__ A, int Kdim, int Nrows, GroupW g0, GroupW g1, int E,
           uint16_t *__restrict__ hid, float *__restrict__ part, int Hout, int ntiles,
           const float *__restrict__ xsum, float *__restrict__ hsum, int nt_gu) {
-    constexpr int WN = 4;
-    __shared__ __align__(16) TileLds<BM, GBN> lds;
+    static_assert(MODE != kDownI8 || !GATEUP, "the narrow tiles are for the down GEMM");
+    constexpr int WN = MODE == kDownI8 ? 2 : 4, TBN = 64 * WN;
+    __shared__ __align__(16) TileLds<BM, TBN> lds;
     __shared__ int arow[BM];
-    __shared__ const char *bptr[GBN];
+    __shared__ const char *bptr[TBN];
     constexpr bool F4 = MODE == kRoutedF4;
-    __shared__ const char *sptr[F4 ? GBN : 1];
+    __shared__ const char *sptr[F4 ? TBN : 1];
     __shared__ float rsum[BM], hpart[WN][BM];
     int mi, ni;
     xcd_tile(blockIdx.x, ntiles, mi, ni);
@@ -817,7 +825,7 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
         }
         rsum[r] = rs;
     }
-    if (threadIdx.x < GBN) {
+    if (threadIdx.x < TBN) {
         const int n = threadIdx.x;
         if (GATEUP) {
             // wave column wn = n / 64 holds intermediate rows [128 nt + 32 wn, +32):
@@ -826,18 +834,21 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
             bptr[n] = reinterpret_cast<const char *>((q < 2 ? Wb : Wb2) + (size_t)o * rowb);
             if (F4 && f4) sptr[n] = reinterpret_cast<const char *>((q < 2 ? Cb : Cb2) + (size_t)o * (Kdim / 16));
         } else {
-            bptr[n] = reinterpret_cast<const char *>(Wb + (size_t)(nt * GBN + n) * rowb);
-            if (F4 && f4) sptr[n] = reinterpret_cast<const char *>(Cb + (size_t)(nt * GBN + n) * (Kdim / 16));
+            bptr[n] = reinterpret_cast<const char *>(Wb + (size_t)(nt * TBN + n) * rowb);
+            if (F4 && f4) sptr[n] = reinterpret_cast<const char *>(Cb + (size_t)(nt * TBN + n) * (Kdim / 16));
         }
     }
     __syncthreads();
     // engine geometry: MWv m-blocks of 16 rows per wave, WMv waves along the rows
-    constexpr int MWv = F4 ? 4 : ExpertEngine::BMt / (16 * (ExpertEngine::NT / 64 / WN));
+    constexpr int MWv = 4;
+    static_assert(ExpertEngine::BMt == 16 * MWv * 2 && DownEngineI8::BMt == 16 * MWv * 2, "2 waves x 64 rows");
     constexpr int RPW = 16 * MWv;                   // rows per wave
     f32x4_t acc[MWv][4];
     if constexpr (F4) {
         if (grp < E) ExpertEngineF4::run(A, Kdim, arow, bptr, Kdim, lds, acc, sptr);
         else SharedEngineI8::run(A, Kdim, arow, bptr, Kdim, lds, acc);
+    } else if constexpr (MODE == kDownI8) {
+        DownEngineI8::run(A, Kdim, arow, bptr, Kdim, lds, acc);
     } else {
         ExpertEngine::run(A, Kdim, arow, bptr, Kdim, lds, acc);
     }
@@ -890,7 +901,7 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int r = wm * RPW + mb * 16 + (lane >> 4) * 4 + i;
-                    const int c = nt * GBN + wn * 64 + nb * 16 + (lane & 15);
+                    const int c = nt * TBN + wn * 64 + nb * 16 + (lane & 15);
                     if (r < rows) {
                         const int p = pbase + r;
                         const float v = f4 ? acc[mb][nb][i] * s2a : (acc[mb][nb][i] - 128.0f * rsum[r]) * Sb[c];
@@ -941,7 +952,7 @@ size_t prefill_ws_bytes(int T) {
     b += al((size_t)(c.E + 2) * 4);        // off
     b += al((size_t)((size_t)T * c.K + kPairsPerBlk - 1) / kPairsPerBlk * c.E * 4);   // per-block counts
     const size_t max_mt = (P / BM + c.E + 2 + 7) / 8 * 8;
-    b += al(max_mt * (c.I / (GBN / 2)) * 16) + al(max_mt * (c.H / GBN) * 16);   // item lists
+    b += al(max_mt * (c.I / (GBN / 2)) * 16) + al(max_mt * (c.H / DownEngineI8::BNt) * 16);   // item lists
     b += al(P * 4) * 3;                    // p_tok, p_slot, p_wt
     b += al(P * c.I * 2);                  // hidden bf16
     b += al(P * c.H * 4);                  // partials
@@ -993,9 +1004,9 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     const int nblk = (int)(((size_t)T * K + kPairsPerBlk - 1) / kPairsPerBlk);
     int *blk = reinterpret_cast<int *>(b); b += al((size_t)nblk * E * 4);
     const size_t max_mt = (P / BM + E + 2 + 7) / 8 * 8;   // bound on m-tiles, a multiple of 8
-    const int nt_gu = I / (GBN / 2), nt_dn = H / GBN;
+    const int nt_gu = I / (GBN / 2), nt_dn = H / (f4 ? GBN : DownEngineI8::BNt);
     int4 *items_gu = reinterpret_cast<int4 *>(b); b += al(max_mt * nt_gu * 16);
-    int4 *items_dn = reinterpret_cast<int4 *>(b); b += al(max_mt * nt_dn * 16);
+    int4 *items_dn = reinterpret_cast<int4 *>(b); b += al(max_mt * (H / DownEngineI8::BNt) * 16);
     int *p_tok = reinterpret_cast<int *>(b); b += al(P * 4);
     int *p_slot = reinterpret_cast<int *>(b); b += al(P * 4);
     float *p_wt = reinterpret_cast<float *>(b); b += al(P * 4);
@@ -1033,7 +1044,7 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
         gd = GroupW{a->i8_down, a->i8s_down, L->sh_down.w, L->sh_down.s, nullptr, nullptr};
     }
     const dim3 g_gu((unsigned)(max_mt * nt_gu)), g_dn((unsigned)(max_mt * nt_dn)),
-        nth(f4 ? ExpertEngineF4::NT : ExpertEngine::NT);
+        nth(f4 ? ExpertEngineF4::NT : ExpertEngine::NT), nth_dn(f4 ? ExpertEngineF4::NT : DownEngineI8::NT);
     if (f4) {
         hipLaunchKernelGGL((k_pf_gemm<true, kRoutedF4>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, off, p_tok, p_slot,
                            p_wt, x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu);
@@ -1042,7 +1053,7 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     } else {
         hipLaunchKernelGGL((k_pf_gemm<true, kAllI8>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, off, p_tok, p_slot, p_wt,
                            x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu);
-        hipLaunchKernelGGL((k_pf_gemm<false, kAllI8>), g_dn, nth, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot, p_wt,
+        hipLaunchKernelGGL((k_pf_gemm<false, kDownI8>), g_dn, nth_dn, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot, p_wt,
                            hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu);
     }
     launch_pf_combine(part, T, S, H, y, s);
