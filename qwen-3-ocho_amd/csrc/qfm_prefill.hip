@@ -427,10 +427,9 @@ using ExpertEngine = TileEngine3<kB_I8, 2, 4, 4>;
 // INT8 down tiles: 128 x 128 in 4 waves, two blocks per CU (K = I is short, so
 // one block's prologue and epilogue overlap the other block's k-steps)
 using DownEngineI8 = TileEngine3<kB_I8, 2, 2, 4>;
-// NVFP4 launches keep the first engine for both tile kinds (measured faster
-// there: 923 / 778 us vs 959 / 840 us with the pipelined engine for e2m1 tiles)
-using ExpertEngineF4 = TileEngine2<kB_F4, 2, 4, kStagesI8>;
-using SharedEngineI8 = TileEngine2<kB_I8, 2, 4, kStagesI8>;     // shared tiles inside the NVFP4 launch
+// NVFP4 launches: e2m1 tiles and the shared expert's INT8 tiles in one kernel
+using ExpertEngineF4 = TileEngine3<kB_F4, 2, 4, 4>;
+using SharedEngineI8 = TileEngine3<kB_I8, 2, 4, 4>;     // shared tiles inside the NVFP4 launch
 constexpr int GBN = ExpertEngine::BNt;          // weight rows per grouped-GEMM tile
 
 // Workgroups are dispatched to the 8 XCDs round-robin (block b on XCD b % 8).
@@ -763,8 +762,7 @@ struct GroupW {
 
 // MODE kAllI8: every tile INT8. kRoutedF4: routed tiles (grp < E) of an
 // NVFP4 arena (block scales staged into the bf16 B tile, the global scale s2
-// applied in the epilogue) and the shared expert's tiles, INT8 in both formats,
-// through the first engine type.
+// applied in the epilogue) and the shared expert's tiles, INT8 in both formats.
 // kDownI8: INT8 down on 128 x 128 tiles (DownEngineI8).
 enum { kAllI8 = 0, kRoutedF4 = 1, kDownI8 = 2 };
 template <bool GATEUP, int MODE>
