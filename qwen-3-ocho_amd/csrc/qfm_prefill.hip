@@ -46,15 +46,11 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128;
-constexpr int kStagesI8 = 3, kStagesF32 = 2;   // register stages of global loads in flight
 constexpr int kCandMax = 64;
 
 // bf16 bits of an exactly representable value (integers |v| <= 256): truncation is exact
 __device__ __forceinline__ uint32_t pack_bf16_exact(float lo, float hi) {
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);   // high halves
-}
-__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
-    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
 }
 
 // 16 int8 codes -> 16 bf16 in offset-binary form (q + 128, exact)
@@ -151,18 +147,27 @@ __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict_
 }
 
 // ---- the MFMA tile engine ---------------------------------------------------------
-// Block tile (64 WM) x (64 WN), WM x WN waves of 64 x 64 (4 x 4
+// Block tile (16 MW WM) x (64 WN), WM x WN waves of (16 MW) x 64 (MW x 4
 // v_mfma_f32_16x16x32_bf16 accumulators each), k-step BK2 = 64 (two 32-deep
 // MFMA steps). Two LDS buffers (the k-step being multiplied and the next one)
-// and D register stages of global loads in flight, one barrier per k-step.
-// A rows: bf16, row r at A + arow[r] * lda (arow < 0: absent row, staged as
-// zeros). B rows: int8 (staged as bf16 in offset-binary form u = q + 128,
-// exact), fp32 (rounded to bf16), bf16, or NVFP4 (packed e2m1 at bptr[n],
-// e4m3 block scales per 16 at sptr[n]; staged as bf16 of e2m1 * scale,
-// exact), row n at bptr[n] (bytes). K % BK2 == 0.
-// acc[mb][nb][i] = C[64 wm + 16 mb + 4 (lane >> 4) + i][64 wn + 16 nb + (lane & 15)],
+// and two register stages of global loads, one barrier per k-step.
+// A rows: bf16, row r at A + arow[r] * lda (arow < 0: absent row). B rows:
+// int8 (staged as bf16 in offset-binary form u = q + 128, exact), bf16, or
+// NVFP4 (packed e2m1 at bptr[n], e4m3 block scales per 16 at sptr[n]; staged
+// as bf16 of e2m1 * scale, exact), row n at bptr[n] (bytes). K % BK2 == 0.
+// acc[mb][nb][i] = C[16 MW wm + 16 mb + 4 (lane >> 4) + i][64 wn + 16 nb + (lane & 15)],
 // wave = WN wm + wn. Staging: 16-byte chunks, consecutive threads on
-// consecutive chunks of a row (A: 8 chunks per row, B: 4 int8 / 16 fp32).
+// consecutive chunks of a row (A: 8 chunks per row, B: 4 int8 / 2 NVFP4 / 8 bf16).
+//
+// The two register stages are two named stage sets of native vector type (a
+// dynamically indexed stage array went to scratch; uint4 stage members were
+// promoted to LDS), and every k-step is one basic block: the global loads of
+// step s + 3 are clamped to the last k-step (a repeat of an address already
+// loaded: L2 hits) and absent A rows read a present row (their results are
+// never stored), so no branch splits the step and the compiler schedules the
+// fragment reads, MFMAs, the next step's conversion, LDS writes and global
+// loads of a step together (explicit scheduling-group patterns measured
+// slower than the compiler's own order).
 constexpr int BK2 = 64;
 constexpr int LDS2 = BK2 + 8;                  // bf16 elements per LDS row (144 bytes)
 template <int BMt, int BNt>
@@ -170,142 +175,13 @@ struct TileLds {
     uint16_t a[2][BMt * LDS2];
     uint16_t b[2][BNt * LDS2];
 };
-enum { kB_I8 = 0, kB_F32 = 1, kB_BF16 = 2, kB_F4 = 3 };
-template <int BMODE, int WM, int WN, int D>
-struct TileEngine2 {
-    static constexpr bool B_I8 = BMODE == kB_I8;
-    static constexpr int BMt = 64 * WM, BNt = 64 * WN, NT = 64 * WM * WN;
-    static constexpr int BCPR = BMODE == kB_I8 ? 4 : BMODE == kB_F32 ? 16 : BMODE == kB_F4 ? 2 : 8;   // B chunks per row per k-step
-    static constexpr int NA = BMt * 8 / NT, NB = BNt * BCPR / NT;  // chunks per thread
-    static_assert(NA * NT == BMt * 8 && NB * NT == BNt * BCPR, "staging must divide evenly");
-    __device__ static void run(const uint16_t *__restrict__ A, long lda, const int *arow,
-                               const char *const *bptr, int K, TileLds<BMt, BNt> &L, f32x4_t (&acc)[4][4],
-                               const char *const *sptr = nullptr) {
-        const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-        const int wm = wave / WN, wn = wave % WN;
-        const uint16_t *ap[NA];
-        int a_lds[NA];
-        bool a_ok[NA];
-#pragma unroll
-        for (int j = 0; j < NA; j++) {
-            const int c = t + j * NT, r = c >> 3, kc = c & 7;
-            const int ar = arow[r];
-            a_ok[j] = ar >= 0;
-            ap[j] = A + (ar >= 0 ? (long)ar * lda : 0) + kc * 8;
-            a_lds[j] = r * LDS2 + kc * 8;
-        }
-        const char *bp[NB], *sp[NB];
-        int b_lds[NB];
-#pragma unroll
-        for (int j = 0; j < NB; j++) {
-            const int c = t + j * NT, r = c / BCPR, kc = c % BCPR;
-            bp[j] = bptr[r] + kc * 16;
-            if constexpr (BMODE == kB_F4) sp[j] = sptr[r] + kc * 2;   // the chunk's two block scales
-            b_lds[j] = r * LDS2 + (BMODE == kB_I8 ? kc * 16 : BMODE == kB_F32 ? kc * 4 : BMODE == kB_F4 ? kc * 32 : kc * 8);
-        }
-        uint4 ra[D][NA], rb[D][NB];
-        uint32_t rsc[D][NB];                       // NVFP4 scale pairs (unused otherwise)
-        auto gload = [&](int k0, uint4 (&a)[NA], uint4 (&bb)[NB], uint32_t (&sc)[NB]) {
-#pragma unroll
-            for (int j = 0; j < NA; j++)
-                a[j] = a_ok[j] ? *reinterpret_cast<const uint4 *>(ap[j] + k0) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-            for (int j = 0; j < NB; j++) {
-                if constexpr (BMODE == kB_I8) bb[j] = ld_nt16(bp[j] + k0);
-                else if constexpr (BMODE == kB_F4) {
-                    bb[j] = ld_nt16(bp[j] + k0 / 2);
-                    sc[j] = *reinterpret_cast<const uint16_t *>(sp[j] + k0 / 16);
-                } else if constexpr (BMODE == kB_F32) bb[j] = *reinterpret_cast<const uint4 *>(bp[j] + (size_t)k0 * 4);
-                else bb[j] = *reinterpret_cast<const uint4 *>(bp[j] + (size_t)k0 * 2);
-            }
-        };
-        auto sstore = [&](int buf, const uint4 (&a)[NA], const uint4 (&bb)[NB], const uint32_t (&sc)[NB]) {
-#pragma unroll
-            for (int j = 0; j < NA; j++) *reinterpret_cast<uint4 *>(&L.a[buf][a_lds[j]]) = a[j];
-#pragma unroll
-            for (int j = 0; j < NB; j++) {
-                if constexpr (BMODE == kB_I8) {
-                    uint4 o0, o1;
-                    i8_to_bf16_ob(bb[j], o0, o1);
-                    uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]);
-                    lb[0] = o0;
-                    lb[1] = o1;
-                } else if constexpr (BMODE == kB_F4) {
-                    uint4 o[4];
-                    f4_to_bf16(bb[j], sc[j], o);
-                    uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]);
-#pragma unroll
-                    for (int q = 0; q < 4; q++) lb[q] = o[q];
-                } else if constexpr (BMODE == kB_BF16) {
-                    *reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]) = bb[j];
-                } else {
-                    const uint4 f = bb[j];
-                    *reinterpret_cast<uint2 *>(&L.b[buf][b_lds[j]]) =
-                        make_uint2(pack_bf16_rne(__uint_as_float(f.x), __uint_as_float(f.y)),
-                                   pack_bf16_rne(__uint_as_float(f.z), __uint_as_float(f.w)));
-                }
-            }
-        };
-#pragma unroll
-        for (int mb = 0; mb < 4; mb++)
-#pragma unroll
-            for (int nb = 0; nb < 4; nb++) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        const int nk = K / BK2;
-#pragma unroll
-        for (int j = 0; j < D; j++)
-            if (j < nk) gload(j * BK2, ra[j], rb[j], rsc[j]);
-        sstore(0, ra[0], rb[0], rsc[0]);
-        if (D < nk) gload(D * BK2, ra[0], rb[0], rsc[0]);
-        __syncthreads();
-        const int lr = lane & 15, lk = (lane >> 4) * 8;
-        for (int s0 = 0; s0 < nk; s0 += D) {
-#pragma unroll
-            for (int j = 0; j < D; j++) {
-                const int s = s0 + j;
-                if (s >= nk) break;
-                const int buf = s & 1;
-#pragma unroll
-                for (int kk = 0; kk < BK2; kk += 32) {
-                    bf16x8_t av[4], bv[4];
-#pragma unroll
-                    for (int mb = 0; mb < 4; mb++)
-                        av[mb] = *reinterpret_cast<const bf16x8_t *>(&L.a[buf][(wm * 64 + mb * 16 + lr) * LDS2 + kk + lk]);
-#pragma unroll
-                    for (int nb = 0; nb < 4; nb++)
-                        bv[nb] = *reinterpret_cast<const bf16x8_t *>(&L.b[buf][(wn * 64 + nb * 16 + lr) * LDS2 + kk + lk]);
-#pragma unroll
-                    for (int mb = 0; mb < 4; mb++)
-#pragma unroll
-                        for (int nb = 0; nb < 4; nb++)
-                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mb], bv[nb], acc[mb][nb], 0, 0, 0);
-                }
-                const int jn = (j + 1) % D;                  // register stage holding k-step s + 1 (unrolled: constant)
-                if (s + 1 < nk) {
-                    sstore(buf ^ 1, ra[jn], rb[jn], rsc[jn]);
-                    if (s + 1 + D < nk) gload((s + 1 + D) * BK2, ra[jn], rb[jn], rsc[jn]);
-                }
-                __syncthreads();
-            }
-        }
-    }
-};
-// ---- grouped-GEMM tile engine (software-pipelined k-step) -------------------------
-// Same tile, operand and accumulator layout as TileEngine2 (WM x WN waves of
-// 64 x 64, BK2 = 64, two LDS buffers), with two register stages of global
-// loads held in two named stage sets (no dynamically indexed stage array)
-// and every k-step one basic block: the global loads of step s + 3 are
-// clamped to the last k-step (a repeat of an address already loaded: L2
-// hits) and absent A rows read a present row (their results are never
-// stored), so no branch splits the step and the compiler schedules the
-// fragment reads, MFMAs, the next step's int8/e2m1 -> bf16 conversion, LDS
-// writes and global loads of a step together (explicit scheduling-group
-// patterns measured slower than the compiler's own order).
+enum { kB_I8 = 0, kB_BF16 = 2, kB_F4 = 3 };
 template <int BMODE, int WM, int WN, int MW = 4>
-struct TileEngine3 {
-    static_assert(BMODE == kB_I8 || BMODE == kB_F4, "expert weights: int8 or NVFP4");
+struct TileEngine {
+    static_assert(BMODE == kB_I8 || BMODE == kB_F4 || BMODE == kB_BF16, "int8, NVFP4 or bf16 B rows");
     // MW m-blocks of 16 rows per wave: a wave computes (16 MW) x 64
     static constexpr int BMt = 16 * MW * WM, BNt = 64 * WN, NT = 64 * WM * WN;
-    static constexpr int BCPR = BMODE == kB_I8 ? 4 : 2;                 // 16-byte B chunks per row per k-step
+    static constexpr int BCPR = BMODE == kB_I8 ? 4 : BMODE == kB_F4 ? 2 : 8;   // 16-byte B chunks per row per k-step
     static constexpr int NA = BMt * 8 / NT, NB = BNt * BCPR / NT;      // chunks per thread
     static_assert(NA * NT == BMt * 8 && NB * NT == BNt * BCPR, "staging must divide evenly");
     struct Stage {                                // native vector types: SROA keeps them in registers
@@ -334,7 +210,7 @@ struct TileEngine3 {
             const int c = t + j * NT, r = c / BCPR, kc = c % BCPR;
             bp[j] = bptr[r] + kc * 16;
             sp[j] = BMODE == kB_F4 ? sptr[r] + kc * 2 : nullptr;
-            b_lds[j] = r * LDS2 + (BMODE == kB_I8 ? kc * 16 : kc * 32);
+            b_lds[j] = r * LDS2 + (BMODE == kB_I8 ? kc * 16 : BMODE == kB_F4 ? kc * 32 : kc * 8);
         }
         auto gload = [&](int k0, Stage &g) __attribute__((always_inline)) {
 #pragma unroll
@@ -343,6 +219,8 @@ struct TileEngine3 {
             for (int j = 0; j < NB; j++) {
                 if constexpr (BMODE == kB_I8) {
                     g.b[j] = *reinterpret_cast<const u32x4_t *>(bp[j] + k0);
+                } else if constexpr (BMODE == kB_BF16) {
+                    g.b[j] = *reinterpret_cast<const u32x4_t *>(bp[j] + (size_t)k0 * 2);
                 } else {
                     g.b[j] = *reinterpret_cast<const u32x4_t *>(bp[j] + k0 / 2);
                     g.sc[j] = *reinterpret_cast<const uint16_t *>(sp[j] + k0 / 16);
@@ -356,7 +234,9 @@ struct TileEngine3 {
             for (int j = 0; j < NB; j++) {
                 uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]);
                 const uint4 bw = make_uint4(g.b[j].x, g.b[j].y, g.b[j].z, g.b[j].w);
-                if constexpr (BMODE == kB_I8) {
+                if constexpr (BMODE == kB_BF16) {
+                    lb[0] = bw;
+                } else if constexpr (BMODE == kB_I8) {
                     uint4 o0, o1;
                     i8_to_bf16_ob(bw, o0, o1);
                     lb[0] = o0;
@@ -416,20 +296,20 @@ struct TileEngine3 {
 };
 
 // router GEMM: 128 x 128 tiles, 2 x 2 waves; grouped expert GEMMs: 128 x 256, 2 x 4 waves
-using RouterEngine = TileEngine2<kB_BF16, 2, 2, kStagesF32>;
+using RouterEngine = TileEngine<kB_BF16, 2, 2, 4>;
 // router GEMM slices along H, summed in slice order by k_pf_select (2 measured
 // 5% slower than 1 at T = 8038: the 63 m-tiles x 4 n-tiles already fill the chip)
 constexpr int kRouterKS = 1;
 // INT8 tiles: 128 x 256 in 8 waves of 64 x 64 (two waves per SIMD). Four
 // waves of 128 x 64 (MW = 8: one wave per SIMD, accumulators in AGPRs, 25%
 // fewer LDS reads per MFMA) measured 1343 / 1149 us against 797 / 719 us.
-using ExpertEngine = TileEngine3<kB_I8, 2, 4, 4>;
+using ExpertEngine = TileEngine<kB_I8, 2, 4, 4>;
 // INT8 down tiles: 128 x 128 in 4 waves, two blocks per CU (K = I is short, so
 // one block's prologue and epilogue overlap the other block's k-steps)
-using DownEngineI8 = TileEngine3<kB_I8, 2, 2, 4>;
+using DownEngineI8 = TileEngine<kB_I8, 2, 2, 4>;
 // NVFP4 launches: e2m1 tiles and the shared expert's INT8 tiles in one kernel
-using ExpertEngineF4 = TileEngine3<kB_F4, 2, 4, 4>;
-using SharedEngineI8 = TileEngine3<kB_I8, 2, 4, 4>;     // shared tiles inside the NVFP4 launch
+using ExpertEngineF4 = TileEngine<kB_F4, 2, 4, 4>;
+using SharedEngineI8 = TileEngine<kB_I8, 2, 4, 4>;     // shared tiles inside the NVFP4 launch
 constexpr int GBN = ExpertEngine::BNt;          // weight rows per grouped-GEMM tile
 
 // Workgroups are dispatched to the 8 XCDs round-robin (block b on XCD b % 8).
