@@ -37,7 +37,10 @@ extern "C" {
  * QF5_NEMBD / QF5_NFF / QF5_NEXP / QF5_NEXPUSED (ocho/amd_server/
  * qf_nvfp4_wave64.h:54-57) and QF5_K (qf8_moe_i8.hip:5-7). Supported:
  * (hidden, inter) = (2048, 512) [benchmark shape] and (2560, 640) [reference
- * checkpoint]; n_experts <= 1024 and a multiple of 64; 1 <= top_k <= 16. */
+ * checkpoint]; n_experts in {64, 128, 256, 512, 1024}; 1 <= top_k <= 16.
+ * The router and top-K entry points run at every accepted expert count; the
+ * fused layer forward (qfm_moe_forward*, every M) needs n_experts == 512, the
+ * reference's value, and returns -2 with a message otherwise. */
 typedef struct {
     int hidden;        /* H */
     int inter;         /* I: expert intermediate size */
