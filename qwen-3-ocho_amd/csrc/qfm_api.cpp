@@ -74,7 +74,7 @@ static size_t prof_event(hipStream_t s) {
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct WsLayout {
-    size_t logits, sel, wts, hidden, csr, part, total;
+    size_t logits, sel, wts, hidden, csr, xh16, part, total;
 };
 static WsLayout ws_layout(int M) {
     const Cfg &c = g_cfg;
@@ -85,6 +85,7 @@ static WsLayout ws_layout(int M) {
     w.wts = off;    off += align256((size_t)M * c.K * sizeof(float));
     w.hidden = off; off += align256((size_t)M * (c.K + 1) * c.I * sizeof(float));
     w.csr = off;    off += align256((size_t)(3 * M * c.K + 2) * sizeof(int));
+    w.xh16 = off;   off += align256((size_t)M * c.H * 2 + (size_t)M * (c.H / 16) * 8);   // fp16 activations + chunk scales
     w.part = off;   off += align256((size_t)M * (c.K + 1) * c.H * sizeof(float));   // K routed + shared slots
     w.total = off;
     return w;
@@ -286,7 +287,7 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
         float *hsh = hidden + (size_t)M * c.K * c.I;
         int rc = launch_router_shared(L->router, L->router_bias, g, sp, x, M, logits, ld, hsh, c.I, s);
         if (!rc) rc = launch_csr_forward(L->arena, L->fmt, sp, x, logits, ld, g ? 1 : 0, M, hidden, hsh, sel, wts, csr,
-                                         part, y, s);
+                                         b + w.xh16, part, y, s);
         return rc;
     }
     return launch_prefill(L, x, M, y, ws, c.gated, s);

@@ -26,16 +26,14 @@
 //                  [0, ceil(M/2)) are then the shared expert (INT8), two tokens
 //                  each: part[t*S + K][c] = gamma_t * <Wd_sh[c], hsh_t> * sd_sh[c].
 //   k_pf_combine   y[t][c] = sum over the S slots of t in slot order, bf16 out.
+#include <type_traits>
+
 #include "qfm_dev.h"
 #include "qfm_internal.h"
 
 namespace qfm {
 
 constexpr int kMaxRows = 8;
-#ifndef QFM_DOWN_ROWS
-#define QFM_DOWN_ROWS 32
-#endif
-constexpr int kDownRows = QFM_DOWN_ROWS;   // down rows per block
 constexpr int kMaxPairs = kMaxRows * 16;
 
 // ---- weight-format policies ----------------------------------------------------
@@ -115,10 +113,15 @@ __device__ __forceinline__ void csr_build_lds(CsrLds &c, int P) {
 
 // ---- top-K of all rows + routing inversion: one block, one wave per row ---------
 // Published: sel/wts [M][K]; csr = {n_exp, exp_id[P], exp_ptr[P+1], pair[P]}.
+// With xh != nullptr, threads [kTopkThreads, blockDim.x) meanwhile write the
+// activations x [M][H] (bf16) as scaled fp16 chunks for the INT8 dot:
+// xh [M][H] fp16, xci [M][H/16] = (seed, 2^-k) of each 16-value chunk.
+constexpr int kTopkThreads = 512;
 template <int EPL>
-__global__ void __launch_bounds__(512)
+__global__ void __launch_bounds__(1024)
 k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, int *__restrict__ g_sel,
-           float *__restrict__ g_wts, int *__restrict__ g_csr) {
+           float *__restrict__ g_wts, int *__restrict__ g_csr, const uint16_t *__restrict__ x, int H,
+           uint4 *__restrict__ xh, float2 *__restrict__ xci) {
     __shared__ CsrLds c;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int P = M * K;
@@ -128,15 +131,28 @@ k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, i
         float my_w;
         wave_topk<EPL>(logits + (size_t)wave * ld, K, renorm, lane, c.tk[wave], my_i, my_w);
         if (lane < K) { c.sel[wave * K + lane] = my_i; c.wts[wave * K + lane] = my_w; }
+    } else if (xh && (int)threadIdx.x >= kTopkThreads) {
+        const int nch = M * (H / 16);
+        for (int ch = threadIdx.x - kTopkThreads; ch < nch; ch += blockDim.x - kTopkThreads) {
+            const uint4 a = reinterpret_cast<const uint4 *>(x)[2 * ch], b = reinterpret_cast<const uint4 *>(x)[2 * ch + 1];
+            const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 8; i++) { v[2 * i] = bf16_lo(d[i]); v[2 * i + 1] = bf16_hi(d[i]); }
+            uint4 ha, hb;
+            xci[ch] = chunk16_to_f16(v, ha, hb);
+            xh[2 * ch] = ha;
+            xh[2 * ch + 1] = hb;
+        }
     }
     __syncthreads();
     csr_build_lds(c, P);
-    for (int i = threadIdx.x; i < P; i += 512) {
+    for (int i = threadIdx.x; i < P; i += blockDim.x) {
         g_sel[i] = c.sel[i]; g_wts[i] = c.wts[i];
         g_csr[1 + i] = c.exp_id[i];
         g_csr[1 + P + (P + 1) + i] = c.pair[i];
     }
-    for (int i = threadIdx.x; i <= P; i += 512) g_csr[1 + P + i] = c.exp_ptr[i];
+    for (int i = threadIdx.x; i <= P; i += blockDim.x) g_csr[1 + P + i] = c.exp_ptr[i];
     if (threadIdx.x == 0) g_csr[0] = c.n_exp;
 }
 
@@ -145,97 +161,213 @@ k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, i
 // were slower)
 template <class F, int H>
 constexpr int gateup_lpr() { return lpr_of(H / F::VPB / 16); }
-// One LPR-lane group per gate/up row; the row pair is loaded once and dotted
-// with the x slice of every routed token (x rows are L2-resident; each
-// 16-byte chunk's activations are converted right before use).
+#ifndef QFM_GATEUP_BPC
+#define QFM_GATEUP_BPC 2
+#endif
+constexpr int kGateupBPC = QFM_GATEUP_BPC;   // resident blocks per CU (grid = 256 * this)
+// Persistent over tiles of RPB rows: tile t = (distinct expert t / TPE, rows
+// (t % TPE) * RPB ..). Block b takes the contiguous tile range [b*n/G,
+// (b+1)*n/G) of the n = n_exp * TPE tiles, so it changes expert at most a few
+// times; at each change the activation rows of the expert's pairs are staged
+// in LDS (INT8: the scaled fp16 rows xh with their chunk (seed, 2^-k) xci,
+// dot16_i8h; NVFP4: the bf16 rows x, f4_chunk_bx). One LPR-lane group per
+// gate/up row; the weights of the tile two ahead are loaded before the current
+// tile is computed, so every wave keeps two tiles of loads in flight.
 template <class F, int H, int I>
 __global__ void __launch_bounds__(256)
 k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
              const float *__restrict__ Sg, const float *__restrict__ Su,          // INT8 row scales
              const uint8_t *__restrict__ Bg, const uint8_t *__restrict__ Bu,      // NVFP4 block scales
              const float *__restrict__ s2g, const float *__restrict__ s2u,        // NVFP4 per-expert scale
-             const uint16_t *__restrict__ x, int K, const int *__restrict__ g_csr, int P,
-             float *__restrict__ hpair) {
+             const uint16_t *__restrict__ x, const uint4 *__restrict__ xh, const float2 *__restrict__ xci,
+             int K, const int *__restrict__ g_csr, int P, float *__restrict__ hpair) {
+    constexpr bool I8 = F::VPB == 1;
     constexpr int ROWB = H / F::VPB;             // bytes per gate/up row
     constexpr int LPR = gateup_lpr<F, H>();      // lanes per row
     constexpr int NST = ROWB / (LPR * 16);
-    constexpr int RPB = 256 / LPR;               // rows per block
-    const int u = blockIdx.y;
-    const int n_exp = g_csr[0];
-    if (u >= n_exp) return;
-    const int *exp_ptr = g_csr + 1 + P, *pair = g_csr + 1 + P + P + 1;
-    const int e = g_csr[1 + u], p0 = exp_ptr[u], np = exp_ptr[u + 1] - p0;
-    const int l = threadIdx.x % LPR;
-    const int row = blockIdx.x * RPB + threadIdx.x / LPR;
-    const size_t roff = ((size_t)e * I + row) * ROWB;
-    uint4 wg[NST], wu[NST];
-#pragma unroll
-    for (int st = 0; st < NST; st++) {
-        wg[st] = ld_nt16(Wg + roff + (st * LPR + l) * 16);
-        wu[st] = ld_nt16(Wu + roff + (st * LPR + l) * 16);
-    }
-    uint32_t bg[NST], bu[NST];
-    float rsg, rsu;
-    if constexpr (F::VPB == 2) {
-        const size_t boff = ((size_t)e * I + row) * (H / 16);
+    constexpr int RPB = 256 / LPR;               // rows per tile
+    constexpr int TPE = I / RPB;                 // tiles per expert
+    constexpr int XQ = H / 8;                    // 16-byte words per staged activation row
+    constexpr int NCH = H / 16;                  // 16-value chunks per row
+    static_assert(XQ % 64 == 0 && (NCH * 2) % 64 == 0, "rows are staged in 64-lane wave loads");
+    __shared__ uint4 s_x[kMaxRows * XQ];
+    __shared__ float2 s_ci[I8 ? kMaxRows * NCH : 1];
+    const int nt = g_csr[0] * TPE;
+    const int lo = (int)((long long)blockIdx.x * nt / gridDim.x);
+    const int hi = (int)((long long)(blockIdx.x + 1) * nt / gridDim.x);
+    if (lo >= hi) return;
+    const int *exp_id = g_csr + 1, *exp_ptr = g_csr + 1 + P, *pair = g_csr + 1 + P + P + 1;
+    const int l = threadIdx.x % LPR, rg = threadIdx.x / LPR;
+    struct Tile {
+        u32x4_t g[NST], u[NST];
+        uint32_t bg[NST], bu[NST];
+        float rsg, rsu;
+    };
+    auto load = [&](Tile &w, int t, int e) __attribute__((always_inline)) {
+        const int row = (t % TPE) * RPB + rg;
+        const size_t roff = ((size_t)e * I + row) * ROWB;
 #pragma unroll
         for (int st = 0; st < NST; st++) {
-            bg[st] = *reinterpret_cast<const uint16_t *>(Bg + boff + (st * LPR + l) * 2);
-            bu[st] = *reinterpret_cast<const uint16_t *>(Bu + boff + (st * LPR + l) * 2);
+            w.g[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(Wg + roff + (st * LPR + l) * 16));
+            w.u[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(Wu + roff + (st * LPR + l) * 16));
         }
-        rsg = s2g[e]; rsu = s2u[e];
-    } else {
-        rsg = Sg[(size_t)e * I + row]; rsu = Su[(size_t)e * I + row];
-    }
-    for (int j = 0; j < np; j++) {
-        const int t = pair[p0 + j] / K;
-        const uint16_t *xt = x + (size_t)t * H;
-        float ag = 0.0f, au = 0.0f, xsum = 0.0f;
+        if constexpr (!I8) {
+            const size_t boff = ((size_t)e * I + row) * (H / 16);
 #pragma unroll
-        for (int st = 0; st < NST; st++) {
-            const uint16_t *p = xt + (st * LPR + l) * F::VPC;
-            if constexpr (F::VPB == 1) {
-                float xs[F::VPC];
-#pragma unroll
-                for (int q = 0; q < F::VPC / 8; q++) {
-                    const uint4 a = *reinterpret_cast<const uint4 *>(p + q * 8);
-                    const uint32_t d[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-                    for (int b = 0; b < 4; b++) { xs[q * 8 + 2 * b] = bf16_lo(d[b]); xs[q * 8 + 2 * b + 1] = bf16_hi(d[b]); }
-                }
-#pragma unroll
-                for (int i = 0; i < 16; i++) xsum += xs[i];
-                ag = dot16_u8(wg[st], xs, ag);
-                au = dot16_u8(wu[st], xs, au);
-            } else {
-                uint32_t xw[16];                     // the 32 bf16 activations as packed pairs
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint4 a = *reinterpret_cast<const uint4 *>(p + q * 8);
-                    xw[4 * q] = a.x; xw[4 * q + 1] = a.y; xw[4 * q + 2] = a.z; xw[4 * q + 3] = a.w;
-                }
-                ag += f4_chunk_bx(wg[st], bg[st], xw);
-                au += f4_chunk_bx(wu[st], bu[st], xw);
+            for (int st = 0; st < NST; st++) {
+                w.bg[st] = *reinterpret_cast<const uint16_t *>(Bg + boff + (st * LPR + l) * 2);
+                w.bu[st] = *reinterpret_cast<const uint16_t *>(Bu + boff + (st * LPR + l) * 2);
             }
+            w.rsg = s2g[e]; w.rsu = s2u[e];
+        } else {
+            w.rsg = Sg[(size_t)e * I + row]; w.rsu = Su[(size_t)e * I + row];
         }
-        if constexpr (F::VPB == 1) { ag = fmaf(-128.0f, xsum, ag); au = fmaf(-128.0f, xsum, au); }
-        ag = group_sum<LPR>(ag);
-        au = group_sum<LPR>(au);
-        if (l == 0) hpair[(size_t)(p0 + j) * I + row] = silu(ag * rsg) * (au * rsu);
+    };
+    const int n_exp = nt / TPE;
+    // expert ids of the current and the next expert, read at each change so the
+    // prefetch address needs no dependent load
+    int cur = -1, p0 = 0, np = 0, e_cur = 0, e_next = 0;
+    const uint4 *src = I8 ? xh : reinterpret_cast<const uint4 *>(x);
+    // tile t from w; with PF tile t + 2 is loaded into nx first
+    auto step = [&](Tile &w, Tile &nx, int t, auto pf) __attribute__((always_inline)) {
+        const int u = t / TPE;
+        if (u != cur) {                          // block-uniform: stage the expert's activation rows
+            cur = u;
+            e_cur = exp_id[u];
+            e_next = exp_id[min(u + 1, n_exp - 1)];
+            p0 = exp_ptr[u];
+            np = exp_ptr[u + 1] - p0;
+            __syncthreads();                     // the previous expert's rows are consumed
+            // straight into LDS (global_load_lds: lane i of a wave load writes base + 16 i / 4 i)
+            const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+            for (int k = wave; k < np * (XQ / 64); k += 4) {
+                const int j = k / (XQ / 64), c = k - j * (XQ / 64);
+                __builtin_amdgcn_global_load_lds(src + (size_t)(pair[p0 + j] / K) * XQ + c * 64 + lane,
+                                                 (__attribute__((address_space(3))) void *)(s_x + j * XQ + c * 64), 16,
+                                                 0, 0);
+            }
+            if constexpr (I8) {
+                constexpr int CW = NCH * 2 / 64;     // 64-dword wave loads per row of chunk data
+                const uint32_t *cs = reinterpret_cast<const uint32_t *>(xci);
+                for (int k = wave; k < np * CW; k += 4) {
+                    const int j = k / CW, c = k - j * CW;
+                    __builtin_amdgcn_global_load_lds(cs + (size_t)(pair[p0 + j] / K) * NCH * 2 + c * 64 + lane,
+                                                     (__attribute__((address_space(3))) void *)(
+                                                         reinterpret_cast<uint32_t *>(s_ci) + j * NCH * 2 + c * 64),
+                                                     4, 0, 0);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);      // this wave's LDS loads have landed
+            __syncthreads();
+        }
+        if constexpr (decltype(pf)::value) load(nx, t + 2, (t + 2) / TPE == cur ? e_cur : e_next);
+        const int row = (t - u * TPE) * RPB + rg;
+        auto pair_out = [&](int j) __attribute__((always_inline)) {
+            float ag = 0.0f, au = 0.0f;
+#pragma unroll
+            for (int st = 0; st < NST; st++) {
+                const int ch = st * LPR + l;
+                const uint4 wg = make_uint4(w.g[st].x, w.g[st].y, w.g[st].z, w.g[st].w);
+                const uint4 wu = make_uint4(w.u[st].x, w.u[st].y, w.u[st].z, w.u[st].w);
+                if constexpr (I8) {
+                    const uint4 xa = s_x[j * XQ + 2 * ch], xb = s_x[j * XQ + 2 * ch + 1];
+                    const float2 ci = s_ci[j * NCH + ch];
+                    ag = fmaf(dot16_i8h(wg, xa, xb, ci.x), ci.y, ag);
+                    au = fmaf(dot16_i8h(wu, xa, xb, ci.x), ci.y, au);
+                } else {
+                    uint32_t xw[16];                     // the 32 bf16 activations as packed pairs
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const uint4 a = s_x[j * XQ + 4 * ch + q];
+                        xw[4 * q] = a.x; xw[4 * q + 1] = a.y; xw[4 * q + 2] = a.z; xw[4 * q + 3] = a.w;
+                    }
+                    ag += f4_chunk_bx(wg, w.bg[st], xw);
+                    au += f4_chunk_bx(wu, w.bu[st], xw);
+                }
+            }
+            ag = group_sum<LPR>(ag);
+            au = group_sum<LPR>(au);
+            if (l == 0) hpair[(size_t)(p0 + j) * I + row] = silu(ag * w.rsg) * (au * w.rsu);
+        };
+        // straight-line code for the first pair (every expert has one) keeps the
+        // next tile's loads outstanding; a runtime loop would wait for them
+        pair_out(0);
+        for (int j = 1; j < np; j++) pair_out(j);
+    };
+    // Two tiles in flight ahead of the one being computed (ring of three). Every
+    // loop back-edge follows an unconditional prefetch, so the compiler's wait
+    // counts stay exact (a conditional one makes it wait for all loads).
+    using PF = std::true_type;
+    using NoPF = std::false_type;
+    Tile t0, t1, t2;
+    load(t0, lo, exp_id[lo / TPE]);
+    if (lo + 1 >= hi) { step(t0, t1, lo, NoPF{}); return; }
+    load(t1, lo + 1, exp_id[(lo + 1) / TPE]);
+    for (int t = lo;; t += 3) {
+        if (t + 2 >= hi) { step(t0, t2, t, NoPF{}); step(t1, t2, t + 1, NoPF{}); break; }
+        step(t0, t2, t, PF{});
+        if (t + 3 >= hi) { step(t1, t0, t + 1, NoPF{}); step(t2, t0, t + 2, NoPF{}); break; }
+        step(t1, t0, t + 1, PF{});
+        if (t + 4 >= hi) { step(t2, t1, t + 2, NoPF{}); step(t0, t1, t + 3, NoPF{}); break; }
+        step(t2, t1, t + 2, PF{});
     }
 }
 
+// ---- down: hidden rows staged in LDS as scaled fp16 chunks ------------------------
+// rows h[0..n) of I fp32 values, one 16-value chunk per thread and pass
+template <int I>
+__device__ __forceinline__ void stage_h16(const float *__restrict__ h, int n, uint4 *s_h16, float2 *s_hci) {
+    for (int c = threadIdx.x; c < n * (I / 16); c += 256) {
+        const float4 *hp = reinterpret_cast<const float4 *>(h) + 4 * c;
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 f = hp[q];
+            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+        }
+        uint4 ha, hb;
+        s_hci[c] = chunk16_to_f16(v, ha, hb);
+        s_h16[2 * c] = ha;
+        s_h16[2 * c + 1] = hb;
+    }
+}
+// <down row, staged hidden row j> over this lane's NST chunks: INT8 (16 codes
+// per chunk, dot16_i8h) or NVFP4 (32 codes per chunk, f4_chunk_h)
+template <class F, int I, int LPR, int NST>
+__device__ __forceinline__ float down_dot(const uint4 (&w)[NST], const uint32_t (&bs)[NST], const uint4 *s_h16,
+                                          const float2 *s_hci, int j, int l) {
+    float d = 0.0f;
+#pragma unroll
+    for (int st = 0; st < NST; st++) {
+        const int ch = st * LPR + l;
+        if constexpr (F::VPB == 1) {
+            const float2 ci = s_hci[j * (I / 16) + ch];
+            d = fmaf(dot16_i8h(w[st], s_h16[j * (I / 8) + 2 * ch], s_h16[j * (I / 8) + 2 * ch + 1], ci.x), ci.y, d);
+        } else {
+            uint32_t xw[16];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint4 a = s_h16[j * (I / 8) + 4 * ch + q];
+                xw[4 * q] = a.x; xw[4 * q + 1] = a.y; xw[4 * q + 2] = a.z; xw[4 * q + 3] = a.w;
+            }
+            d += f4_chunk_h(w[st], bs[st], xw, s_hci[j * (I / 16) + 2 * ch].y, s_hci[j * (I / 16) + 2 * ch + 1].y);
+        }
+    }
+    return d;
+}
+
 // ---- shared expert's down rows (INT8) for tokens [t0, t1): one k_csr_down block ----
-// rows [c0, c0 + ROWS); hsh rows staged in LDS (sh_h, sh_cs as in k_csr_down)
+// rows [c0, c0 + ROWS)
 template <int H, int I, int ROWS>
 __device__ __forceinline__ void csr_down_shared(const ShPtrs &sh, const float *__restrict__ hsh,
                                                 const float *__restrict__ logits, int ld, int gated, int t0,
-                                                int t1, int S, int K, int c0, float *sh_h, float *sh_cs,
+                                                int t1, int S, int K, int c0, uint4 *s_h16, float2 *s_hci,
                                                 float *__restrict__ part) {
     constexpr int CPR = I / 16, LPR = lpr_of(CPR), NST = CPR / LPR, GROUPS = 256 / LPR, RPG = ROWS / GROUPS;
     static_assert(RPG >= 1 && RPG * GROUPS == ROWS, "shared rows must tile the block");
     const int l = threadIdx.x % LPR, grp = threadIdx.x / LPR;
     uint4 w[RPG][NST];
+    uint32_t bs[NST] = {};
     float rs[RPG];
 #pragma unroll
     for (int q = 0; q < RPG; q++) {
@@ -249,15 +381,7 @@ __device__ __forceinline__ void csr_down_shared(const ShPtrs &sh, const float *_
     float gam[TS];
 #pragma unroll
     for (int t = 0; t < TS; t++) gam[t] = gated ? logits[(size_t)(t0 + (t < nt ? t : 0)) * ld + (ld - 1)] : 0.0f;
-    for (int i = threadIdx.x; i < nt * I / 4; i += 256)
-        reinterpret_cast<float4 *>(sh_h)[i] = reinterpret_cast<const float4 *>(hsh + (size_t)t0 * I)[i];
-    __syncthreads();
-    for (int i = threadIdx.x; i < nt * I / 16; i += 256) {
-        float t = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 16; q++) t += sh_h[i * 16 + q];
-        sh_cs[i] = -128.0f * t;
-    }
+    stage_h16<I>(hsh + (size_t)t0 * I, nt, s_h16, s_hci);
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < TS; t++) {
@@ -266,12 +390,7 @@ __device__ __forceinline__ void csr_down_shared(const ShPtrs &sh, const float *_
 #pragma unroll
         for (int q = 0; q < RPG; q++) {
             const int c = c0 + q * GROUPS + grp;
-            float d = 0.0f;
-#pragma unroll
-            for (int st = 0; st < NST; st++) {
-                d += sh_cs[t * (I / 16) + st * LPR + l];
-                d = dot16_u8(w[q][st], sh_h + t * I + (st * LPR + l) * 16, d);
-            }
+            float d = down_dot<FmtI8, I, LPR, NST>(w[q], bs, s_h16, s_hci, t, l);
             d = group_sum<LPR>(d);
             if (l == 0) part[((size_t)(t0 + t) * S + K) * H + c] = g * (d * rs[q]);
         }
@@ -279,9 +398,16 @@ __device__ __forceinline__ void csr_down_shared(const ShPtrs &sh, const float *_
 }
 
 // ---- down: one distinct expert x ROWS rows per block, owned partials ---------------
+#ifndef QFM_DOWN_ROWS_I8
+#define QFM_DOWN_ROWS_I8 32
+#endif
+#ifndef QFM_DOWN_ROWS_F4
+#define QFM_DOWN_ROWS_F4 32
+#endif
 template <class F, int I>
 constexpr int down_rows() {
-    return kDownRows > 256 / lpr_of(I / F::VPB / 16) ? kDownRows : 256 / lpr_of(I / F::VPB / 16);
+    constexpr int want = F::VPB == 1 ? QFM_DOWN_ROWS_I8 : QFM_DOWN_ROWS_F4;
+    return want > 256 / lpr_of(I / F::VPB / 16) ? want : 256 / lpr_of(I / F::VPB / 16);
 }
 template <class F, int H, int I>
 __global__ void __launch_bounds__(256)
@@ -295,15 +421,15 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
     constexpr int NST = CPR / LPR;
     constexpr int GROUPS = 256 / LPR;                  // row groups per block
     constexpr int ROWS = down_rows<F, I>();
-    __shared__ __align__(16) float sh_h[kMaxRows * I];
-    __shared__ float sh_cs[kMaxRows * I / 16];
+    __shared__ uint4 s_h16[kMaxRows * I / 8];
+    __shared__ float2 s_hci[kMaxRows * I / 16];
     const bool has_sh = sh.qd != nullptr;
     const int S = K + (has_sh ? 1 : 0);
     const int nsh = has_sh ? (M + 1) / 2 : 0;      // grid rows of shared blocks, two tokens each
     if ((int)blockIdx.y < nsh) {                  // dispatched first
         const int t0 = blockIdx.y * 2;
-        csr_down_shared<H, I, ROWS>(sh, hsh, logits, ld, gated, t0, min(M, t0 + 2), S, K, blockIdx.x * ROWS, sh_h,
-                                    sh_cs, part);
+        csr_down_shared<H, I, ROWS>(sh, hsh, logits, ld, gated, t0, min(M, t0 + 2), S, K, blockIdx.x * ROWS, s_h16,
+                                    s_hci, part);
         return;
     }
     const int u = blockIdx.y - nsh;
@@ -329,38 +455,20 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
             for (int st = 0; st < NST; st++) bs[q][st] = *reinterpret_cast<const uint16_t *>(Bd + boff + (st * LPR + l) * 2);
             rs[q] = s2d[e];
         } else {
+#pragma unroll
+            for (int st = 0; st < NST; st++) bs[q][st] = 0u;
             rs[q] = Sd[(size_t)e * H + c];
         }
     }
-    for (int i = threadIdx.x; i < np * I / 4; i += 256)
-        reinterpret_cast<float4 *>(sh_h)[i] = reinterpret_cast<const float4 *>(hpair + (size_t)p0 * I)[i];
+    stage_h16<I>(hpair + (size_t)p0 * I, np, s_h16, s_hci);
     __syncthreads();
-    if constexpr (F::VPB == 1) {
-        for (int i = threadIdx.x; i < np * I / 16; i += 256) {
-            float t = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 16; q++) t += sh_h[i * 16 + q];
-            sh_cs[i] = -128.0f * t;
-        }
-        __syncthreads();
-    }
     for (int j = 0; j < np; j++) {
         const int pr = pair[p0 + j];
         const float wp = g_wts[pr];
 #pragma unroll
         for (int q = 0; q < RPG; q++) {
             const int c = blockIdx.x * ROWS + q * GROUPS + grp;
-            float d = 0.0f;
-#pragma unroll
-            for (int st = 0; st < NST; st++) {
-                const int ch = st * LPR + l;
-                if constexpr (F::VPB == 1) {
-                    d += sh_cs[j * (I / 16) + ch];
-                    d = dot16_u8(w[q][st], sh_h + j * I + ch * 16, d);
-                } else {
-                    d += f4_chunk(w[q][st], bs[q][st], sh_h + j * I + ch * 32);
-                }
-            }
+            float d = down_dot<F, I, LPR, NST>(w[q], bs[q], s_h16, s_hci, j, l);
             d = group_sum<LPR>(d);
             if (l == 0) part[((size_t)(pr / K) * S + pr % K) * H + c] = wp * (d * rs[q]);
         }
@@ -370,7 +478,7 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
 // ---- launchers -------------------------------------------------------------------
 int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,
                        int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
-                       float *part, uint16_t *y, hipStream_t s) {
+                       void *xh16, float *part, uint16_t *y, hipStream_t s) {
     const int K = g_cfg.K, E = g_cfg.E, P = M * K;
     if (M < 1 || M > kMaxRows || P > kMaxPairs || E != 512) {
         set_error(-2, "csr path: needs 1 <= M <= %d, M*top_k <= %d, 512 experts", kMaxRows, kMaxPairs); return -2;
@@ -378,19 +486,26 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
     const int umax = P < E ? P : E;
     ShPtrs sp{};
     if (sh) sp = *sh;
-    const dim3 b512(512), b256(256);
+    const dim3 b256(256);
     const uint8_t *wg, *wu, *wd, *bg = nullptr, *bu = nullptr, *bd = nullptr;
+    uint4 *xh = nullptr;                           // INT8: scaled fp16 activations, then their chunk (seed, 2^-k)
+    float2 *xci = nullptr;
     if (fmt == QFM_FMT_INT8) {
         if (!a->i8_gate || !a->i8_up || !a->i8_down) { set_error(-1, "csr path: arena has no INT8 blobs"); return -1; }
+        if (!xh16) { set_error(-1, "csr path: INT8 needs the fp16 activation buffer"); return -1; }
+        xh = static_cast<uint4 *>(xh16);
+        xci = reinterpret_cast<float2 *>(xh + (size_t)M * g_cfg.H / 8);
         wg = (const uint8_t *)a->i8_gate; wu = (const uint8_t *)a->i8_up; wd = (const uint8_t *)a->i8_down;
     } else {
         if (!a->w_gate || !a->s_gate || !a->s2g_dev) { set_error(-1, "csr path: arena has no NVFP4 blobs"); return -1; }
         wg = a->w_gate; wu = a->w_up; wd = a->w_down; bg = a->s_gate; bu = a->s_up; bd = a->s_down;
     }
 #define QFM_CSR_LAUNCH(F, HH, II)                                                                                   \
-    hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), b512, 0, s, logits, ld, M, K, g_cfg.renorm, sel, wts, csr);       \
-    hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(II / (256 / gateup_lpr<F, HH>()), umax), b256, 0, s,  \
-                       wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, K, csr, P, hpair);       \
+    hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), dim3(xh ? 1024 : kTopkThreads), 0, s, logits, ld, M, K,          \
+                       g_cfg.renorm, sel, wts, csr, x, HH, xh, xci);                                             \
+    hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(256 * kGateupBPC), b256, 0, s,                         \
+                       wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, xh, xci, K, csr, P,  \
+                       hpair);                                                                                   \
     hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / down_rows<F, II>(), umax + (sh ? (M + 1) / 2 : 0)), b256, 0, s, wd,   \
                        a->i8s_down, bd, a->s2d_dev, hpair, wts, csr, P, part, K, sp, hsh, logits, ld, gated, M);   \
     launch_pf_combine(part, M, K + (sh ? 1 : 0), HH, y, s)

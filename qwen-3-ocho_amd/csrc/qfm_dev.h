@@ -42,6 +42,57 @@ __device__ __forceinline__ float dot16_u8(const uint4 w, const float *x, float a
     return acc;
 }
 
+// ---- int8 x fp16 dot of one 16-byte chunk (v_dot2_f32_f16) ------------------
+// The offset-binary code u = q ^ 0x80 = q + 128 placed in the low byte of the
+// fp16 pattern 0x6400 (1024.0) reads 1024 + u = q + 1152 exactly (fp16 has
+// unit spacing on [1024, 2048)), so one v_perm_b32 widens two codes into an
+// fp16 pair and one v_dot2_f32_f16 multiplies it with two activations, with
+// exact products (11 x 11 significant bits) and fp32 accumulation. The
+// activations are fp16 pairs in memory order (xa: values 0..7, xb: 8..15);
+// the caller seeds acc with -1152 * (sum of the 16 activations).
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f16x2_t as_h2(uint32_t v) { return __builtin_bit_cast(f16x2_t, v); }
+__device__ __forceinline__ float dot16_i8h(const uint4 w, const uint4 xa, const uint4 xb, float acc) {
+    const uint32_t d[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
+    const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        // perm selector bytes 0..3 pick bytes of the second operand, 4 the first's (0x64)
+        acc = __builtin_amdgcn_fdot2(as_h2(__builtin_amdgcn_perm(0x64646464u, d[q], 0x04010400u)), as_h2(xv[2 * q]),
+                                     acc, false);
+        acc = __builtin_amdgcn_fdot2(as_h2(__builtin_amdgcn_perm(0x64646464u, d[q], 0x04030402u)),
+                                     as_h2(xv[2 * q + 1]), acc, false);
+    }
+    return acc;
+}
+constexpr float kI8hOffset = 1152.0f;
+
+// 16 fp32 activations -> 16 fp16 scaled by 2^k, k chosen so the largest
+// magnitude lands in [2^14, 2^15) (no overflow; values with at most 11
+// significant bits, bf16 ones among them, convert exactly unless they are
+// 2^-28 below the chunk's largest). Returns (seed, 2^-k): seed = -1152 * the
+// sum of the scaled values, the dot16_i8h seed; 2^-k undoes the scaling.
+__device__ __forceinline__ float2 chunk16_to_f16(const float *v, uint4 &ha, uint4 &hb) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
+    const int e = (int)(__float_as_uint(amax) >> 23);
+    const int k = amax == 0.0f ? 0 : min(113, max(-113, 141 - e));
+    const float sc = __uint_as_float((uint32_t)(127 + k) << 23), isc = __uint_as_float((uint32_t)(127 - k) << 23);
+    uint32_t h[8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float a = v[2 * i] * sc, b = v[2 * i + 1] * sc;
+        const f16x2_t hp = {(_Float16)a, (_Float16)b};   // round to nearest even
+        h[i] = __builtin_bit_cast(uint32_t, hp);
+        sum += a + b;
+    }
+    ha = make_uint4(h[0], h[1], h[2], h[3]);
+    hb = make_uint4(h[4], h[5], h[6], h[7]);
+    return make_float2(-kI8hOffset * sum, isc);
+}
+
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_nt16(const void *p) {
     const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
@@ -50,11 +101,25 @@ __device__ __forceinline__ uint4 ld_nt16(const void *p) {
 
 // ---- cross-lane reductions -------------------------------------------------
 // Sum over aligned groups of G lanes (G a power of two <= 64); every lane of
-// the group ends with the group total.
+// the group ends with the group total. Within 16-lane rows the steps are DPP
+// adds (xor 1, xor 2, half-row mirror, row mirror: no LDS round trip); the
+// 32-lane step is one ds_swizzle (lane ^ 16), the 64-lane one a bpermute.
+// (hipcc 7.2 drops the second result of v_permlane16_swap / 32_swap, so the
+// gfx950 row swaps are not used.)
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int m = G / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, WAVE);
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group of 2^k lanes");
+    if constexpr (G >= 2)   // quad_perm [1,0,3,2]
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    if constexpr (G >= 4)   // quad_perm [2,3,0,1]
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    if constexpr (G >= 8)   // row_half_mirror
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    if constexpr (G >= 16)  // row_mirror
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    if constexpr (G >= 32)  // ds_swizzle bit-mask mode, lane ^ 16 within 32 lanes: and 0x1F, or 0, xor 0x10
+        v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    if constexpr (G >= 64) v += __shfl_xor(v, 32, WAVE);
     return v;
 }
 
@@ -260,8 +325,9 @@ __device__ __forceinline__ void load_x_slice_f32(const float *x, int l, float (&
 }
 
 // ---- silu / sigmoid ----------------------------------------------------------
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
-__device__ __forceinline__ float sigmoid(float g) { return 1.0f / (1.0f + __expf(-g)); }
+// (v_rcp_f32, 1 ulp, in place of the IEEE division sequence)
+__device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+__device__ __forceinline__ float sigmoid(float g) { return __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // ---- NVFP4 number formats -----------------------------------------------------
 // E2M1 code -> float: +-{0, .5, 1, 1.5, 2, 3, 4, 6}; built from the bit
@@ -344,6 +410,29 @@ __device__ __forceinline__ float f4_chunk_bx(uint4 w, uint32_t s2b, const uint32
     const float g0 = f4_group16_bx(w.x, w.y, xw);
     const float g1 = f4_group16_bx(w.z, w.w, xw + 8);
     return fmaf(e4m3_scale(s2b & 0xFFu), g0, e4m3_scale((s2b >> 8) & 0xFFu) * g1);
+}
+
+// NVFP4 chunk against scaled fp16 activations: 32 e2m1 codes (w), two e4m3
+// block scales (s2b), the 32 activations as 16 fp16 pairs (xw) in two
+// 16-value chunks with inverse scales isc0, isc1 (chunk16_to_f16). Codes are
+// converted to fp16 pairs (v_cvt_scalef32_pk_f16_fp4, unit scale: exact) and
+// multiplied by v_dot2_f32_f16; each 16-value group is scaled once.
+__device__ __forceinline__ float f4_group16_h(uint32_t lo, uint32_t hi, const uint32_t *xw) {
+    float a = 0.0f;
+    const uint32_t w[2] = {lo, hi};
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+        a = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w[d], 1.0f, 0), as_h2(xw[d * 4 + 0]), a, false);
+        a = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w[d], 1.0f, 1), as_h2(xw[d * 4 + 1]), a, false);
+        a = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w[d], 1.0f, 2), as_h2(xw[d * 4 + 2]), a, false);
+        a = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w[d], 1.0f, 3), as_h2(xw[d * 4 + 3]), a, false);
+    }
+    return a;
+}
+__device__ __forceinline__ float f4_chunk_h(uint4 w, uint32_t s2b, const uint32_t *xw, float isc0, float isc1) {
+    const float g0 = f4_group16_h(w.x, w.y, xw);
+    const float g1 = f4_group16_h(w.z, w.w, xw + 8);
+    return fmaf(e4m3_scale(s2b & 0xFFu) * isc0, g0, (e4m3_scale((s2b >> 8) & 0xFFu) * isc1) * g1);
 }
 
 // ---- Philox-4x32-10 (Salmon et al. 2011) ------------------------------------

@@ -49,15 +49,16 @@ int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *x
 int launch_i8_down_m1(const Qf4ExpCache *c, const float *hidden, const float *wts, const int *sel,
                       int nexp, const ShPtrs *sh, const float *gdot, float *y32, uint16_t *ybf, hipStream_t s);
 
-// Multi-row decode (1 <= M <= 8): top-K of all rows + routing inversion +
-// weight-once-per-distinct-expert gate/up (k_csr_gateup), down partials per
-// (expert, row block) (k_csr_down), combine + shared-expert down
-// (k_csr_combine). fmt: QFM_FMT_INT8 or QFM_FMT_NVFP4 for the routed experts.
-// hsh: shared hidden [M][I] (from launch_router_shared); csr: 3*M*K+2 ints;
-// part: [M*K][H] fp32; hpair: [M*K][I] fp32.
+// Multi-row decode (1 <= M <= 8): top-K of all rows + routing inversion
+// (k_topk_csr), weight-once-per-distinct-expert gate/up (k_csr_gateup), down
+// partials per (expert, row block) with the shared expert's down in the first
+// grid rows (k_csr_down), combine (k_pf_combine). fmt: QFM_FMT_INT8 or
+// QFM_FMT_NVFP4 for the routed experts. hsh: shared hidden [M][I] (from
+// launch_router_shared); csr: 3*M*K+2 ints; hpair: [M*K][I] fp32; part:
+// [M][K+1][H] fp32; xh16 (INT8): M*H*2 + M*(H/16)*8 bytes, 16-byte aligned.
 int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,
                        int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
-                       float *part, uint16_t *y, hipStream_t s);
+                       void *xh16, float *part, uint16_t *y, hipStream_t s);
 
 // Prefill (T > 8 rows): MFMA router + exact candidate selection, grouped
 // MFMA gate/up and down over the routing inversion, owned-partial combine.
