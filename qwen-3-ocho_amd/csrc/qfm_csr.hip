@@ -11,23 +11,26 @@
 // owned partials part[t][k][H] summed in k order (no atomics, deterministic).
 //
 // Launch sequence (all stream-ordered):
-//   k_topk_csr     one block, 512 threads: the top-K of all M rows (one wave
-//                  per row), then the routing inversion in LDS (O(P^2) rank
-//                  counting over P = M*K <= 128 pairs); publishes sel/wts/CSR.
+//   k_topk_csr     one block: the top-K of all M rows (one wave per row), then
+//                  the routing inversion in LDS (O(P^2) rank counting over
+//                  P = M*K <= 128 pairs); publishes sel/wts/CSR. For INT8 a
+//                  second set of waves meanwhile writes the activations as
+//                  scaled fp16 chunks (chunk16_to_f16).
 //   k_csr_gateup   grid (I/rows, min(M*K, E)), 256 threads: distinct expert
-//                  blockIdx.y. One lane group per gate/up row: the row is
-//                  loaded once, then dotted with the x slice of each routed
-//                  token (L2-resident). hidden is written per pair, in CSR
+//                  blockIdx.y. One lane group per gate/up row: the row pair is
+//                  loaded once, then dotted with the LDS-staged activation row
+//                  of each routed token. hidden is written per pair, in CSR
 //                  order.
 //   k_csr_down     grid (H/ROWS, min(M*K, E) + shared), 256 threads: expert
 //                  u's down rows [ROWS b, ROWS b + ROWS), pairs' hidden vectors
-//                  staged in LDS; writes part[t*S + k][c] = w * <Wd_e[c], h_pair>
-//                  * scale, S = K + 1 with a shared expert. Grid rows
-//                  [0, ceil(M/2)) are then the shared expert (INT8), two tokens
-//                  each: part[t*S + K][c] = gamma_t * <Wd_sh[c], hsh_t> * sd_sh[c].
+//                  staged in LDS as scaled fp16 chunks; writes
+//                  part[t*S + k][c] = w * <Wd_e[c], h_pair> * scale, S = K + 1
+//                  with a shared expert. Grid rows [0, ceil(M/2)) are then the
+//                  shared expert (INT8), two tokens each:
+//                  part[t*S + K][c] = gamma_t * <Wd_sh[c], hsh_t> * sd_sh[c].
 //   k_pf_combine   y[t][c] = sum over the S slots of t in slot order, bf16 out.
-#include <type_traits>
-
+// INT8 dots widen the codes to fp16 (dot16_i8h); NVFP4 gate/up converts e2m1
+// to bf16 pairs against the bf16 activations, NVFP4 down to fp16 pairs.
 #include "qfm_dev.h"
 #include "qfm_internal.h"
 
@@ -161,18 +164,15 @@ k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, i
 // were slower)
 template <class F, int H>
 constexpr int gateup_lpr() { return lpr_of(H / F::VPB / 16); }
-#ifndef QFM_GATEUP_BPC
-#define QFM_GATEUP_BPC 2
-#endif
-constexpr int kGateupBPC = QFM_GATEUP_BPC;   // resident blocks per CU (grid = 256 * this)
-// Persistent over tiles of RPB rows: tile t = (distinct expert t / TPE, rows
-// (t % TPE) * RPB ..). Block b takes the contiguous tile range [b*n/G,
-// (b+1)*n/G) of the n = n_exp * TPE tiles, so it changes expert at most a few
-// times; at each change the activation rows of the expert's pairs are staged
-// in LDS (INT8: the scaled fp16 rows xh with their chunk (seed, 2^-k) xci,
-// dot16_i8h; NVFP4: the bf16 rows x, f4_chunk_bx). One LPR-lane group per
-// gate/up row; the weights of the tile two ahead are loaded before the current
-// tile is computed, so every wave keeps two tiles of loads in flight.
+constexpr int kGateupPG = 2;   // routed activation rows staged in LDS at a time
+// One block per (distinct expert, RPB rows), one LPR-lane group per gate/up
+// row. The row pair's weights are loaded first (the HBM stream starts at
+// once); the activation rows of the expert's pairs are staged in LDS straight
+// from memory, kGateupPG at a time (INT8: the scaled fp16 rows xh with their
+// chunk (seed, 2^-k) xci, dot16_i8h; NVFP4: the bf16 rows x, f4_chunk_bx).
+// (A persistent form over tile ranges with two tiles of weights in flight was
+// slower: its registers allowed two waves per SIMD instead of four, and the
+// dot and reduction latencies then went unhidden.)
 template <class F, int H, int I>
 __global__ void __launch_bounds__(256)
 k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
@@ -185,95 +185,72 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
     constexpr int ROWB = H / F::VPB;             // bytes per gate/up row
     constexpr int LPR = gateup_lpr<F, H>();      // lanes per row
     constexpr int NST = ROWB / (LPR * 16);
-    constexpr int RPB = 256 / LPR;               // rows per tile
-    constexpr int TPE = I / RPB;                 // tiles per expert
+    constexpr int RPB = 256 / LPR;               // rows per block
     constexpr int XQ = H / 8;                    // 16-byte words per staged activation row
     constexpr int NCH = H / 16;                  // 16-value chunks per row
+    constexpr int PG = kGateupPG;
     static_assert(XQ % 64 == 0 && (NCH * 2) % 64 == 0, "rows are staged in 64-lane wave loads");
-    __shared__ uint4 s_x[kMaxRows * XQ];
-    __shared__ float2 s_ci[I8 ? kMaxRows * NCH : 1];
-    const int nt = g_csr[0] * TPE;
-    const int lo = (int)((long long)blockIdx.x * nt / gridDim.x);
-    const int hi = (int)((long long)(blockIdx.x + 1) * nt / gridDim.x);
-    if (lo >= hi) return;
-    const int *exp_id = g_csr + 1, *exp_ptr = g_csr + 1 + P, *pair = g_csr + 1 + P + P + 1;
-    const int l = threadIdx.x % LPR, rg = threadIdx.x / LPR;
-    struct Tile {
-        u32x4_t g[NST], u[NST];
-        uint32_t bg[NST], bu[NST];
-        float rsg, rsu;
-    };
-    auto load = [&](Tile &w, int t, int e) __attribute__((always_inline)) {
-        const int row = (t % TPE) * RPB + rg;
-        const size_t roff = ((size_t)e * I + row) * ROWB;
+    __shared__ uint4 s_x[PG * XQ];
+    __shared__ float2 s_ci[I8 ? PG * NCH : 1];
+    const int u = blockIdx.y;
+    const int n_exp = g_csr[0];
+    if (u >= n_exp) return;
+    const int *exp_ptr = g_csr + 1 + P, *pair = g_csr + 1 + P + P + 1;
+    const int e = g_csr[1 + u], p0 = exp_ptr[u], np = exp_ptr[u + 1] - p0;
+    const int l = threadIdx.x % LPR;
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR;
+    const size_t roff = ((size_t)e * I + row) * ROWB;
+    uint4 wg[NST], wu[NST];
+#pragma unroll
+    for (int st = 0; st < NST; st++) {
+        wg[st] = ld_nt16(Wg + roff + (st * LPR + l) * 16);
+        wu[st] = ld_nt16(Wu + roff + (st * LPR + l) * 16);
+    }
+    uint32_t bg[NST], bu[NST];
+    float rsg, rsu;
+    if constexpr (!I8) {
+        const size_t boff = ((size_t)e * I + row) * (H / 16);
 #pragma unroll
         for (int st = 0; st < NST; st++) {
-            w.g[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(Wg + roff + (st * LPR + l) * 16));
-            w.u[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(Wu + roff + (st * LPR + l) * 16));
+            bg[st] = *reinterpret_cast<const uint16_t *>(Bg + boff + (st * LPR + l) * 2);
+            bu[st] = *reinterpret_cast<const uint16_t *>(Bu + boff + (st * LPR + l) * 2);
         }
-        if constexpr (!I8) {
-            const size_t boff = ((size_t)e * I + row) * (H / 16);
-#pragma unroll
-            for (int st = 0; st < NST; st++) {
-                w.bg[st] = *reinterpret_cast<const uint16_t *>(Bg + boff + (st * LPR + l) * 2);
-                w.bu[st] = *reinterpret_cast<const uint16_t *>(Bu + boff + (st * LPR + l) * 2);
-            }
-            w.rsg = s2g[e]; w.rsu = s2u[e];
-        } else {
-            w.rsg = Sg[(size_t)e * I + row]; w.rsu = Su[(size_t)e * I + row];
-        }
-    };
-    const int n_exp = nt / TPE;
-    // expert ids of the current and the next expert, read at each change so the
-    // prefetch address needs no dependent load
-    int cur = -1, p0 = 0, np = 0, e_cur = 0, e_next = 0;
+        rsg = s2g[e]; rsu = s2u[e];
+    } else {
+        rsg = Sg[(size_t)e * I + row]; rsu = Su[(size_t)e * I + row];
+    }
     const uint4 *src = I8 ? xh : reinterpret_cast<const uint4 *>(x);
-    // tile t from w; with PF tile t + 2 is loaded into nx first
-    auto step = [&](Tile &w, Tile &nx, int t, auto pf) __attribute__((always_inline)) {
-        const int u = t / TPE;
-        if (u != cur) {                          // block-uniform: stage the expert's activation rows
-            cur = u;
-            e_cur = exp_id[u];
-            e_next = exp_id[min(u + 1, n_exp - 1)];
-            p0 = exp_ptr[u];
-            np = exp_ptr[u + 1] - p0;
-            __syncthreads();                     // the previous expert's rows are consumed
-            // straight into LDS (global_load_lds: lane i of a wave load writes base + 16 i / 4 i)
-            const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-            for (int k = wave; k < np * (XQ / 64); k += 4) {
-                const int j = k / (XQ / 64), c = k - j * (XQ / 64);
-                __builtin_amdgcn_global_load_lds(src + (size_t)(pair[p0 + j] / K) * XQ + c * 64 + lane,
-                                                 (__attribute__((address_space(3))) void *)(s_x + j * XQ + c * 64), 16,
-                                                 0, 0);
-            }
-            if constexpr (I8) {
-                constexpr int CW = NCH * 2 / 64;     // 64-dword wave loads per row of chunk data
-                const uint32_t *cs = reinterpret_cast<const uint32_t *>(xci);
-                for (int k = wave; k < np * CW; k += 4) {
-                    const int j = k / CW, c = k - j * CW;
-                    __builtin_amdgcn_global_load_lds(cs + (size_t)(pair[p0 + j] / K) * NCH * 2 + c * 64 + lane,
-                                                     (__attribute__((address_space(3))) void *)(
-                                                         reinterpret_cast<uint32_t *>(s_ci) + j * NCH * 2 + c * 64),
-                                                     4, 0, 0);
-                }
-            }
-            __builtin_amdgcn_s_waitcnt(0);      // this wave's LDS loads have landed
-            __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int j0 = 0; j0 < np; j0 += PG) {
+        const int ng = min(PG, np - j0);
+        if (j0 > 0) __syncthreads();             // the previous group's rows are consumed
+        // straight into LDS (global_load_lds: lane i of a wave load writes base + 16 i / 4 i)
+        for (int k = wave; k < ng * (XQ / 64); k += 4) {
+            const int j = k / (XQ / 64), c = k - j * (XQ / 64);
+            __builtin_amdgcn_global_load_lds(src + (size_t)(pair[p0 + j0 + j] / K) * XQ + c * 64 + lane,
+                                             (__attribute__((address_space(3))) void *)(s_x + j * XQ + c * 64), 16, 0, 0);
         }
-        if constexpr (decltype(pf)::value) load(nx, t + 2, (t + 2) / TPE == cur ? e_cur : e_next);
-        const int row = (t - u * TPE) * RPB + rg;
-        auto pair_out = [&](int j) __attribute__((always_inline)) {
+        if constexpr (I8) {
+            constexpr int CW = NCH * 2 / 64;
+            const uint32_t *cs = reinterpret_cast<const uint32_t *>(xci);
+            for (int k = wave; k < ng * CW; k += 4) {
+                const int j = k / CW, c = k - j * CW;
+                __builtin_amdgcn_global_load_lds(cs + (size_t)(pair[p0 + j0 + j] / K) * NCH * 2 + c * 64 + lane,
+                                                 (__attribute__((address_space(3))) void *)(reinterpret_cast<uint32_t *>(s_ci) + j * NCH * 2 + c * 64), 4, 0, 0);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);          // this wave's LDS loads (and its weights) have landed
+        __syncthreads();
+        for (int j = 0; j < ng; j++) {
             float ag = 0.0f, au = 0.0f;
 #pragma unroll
             for (int st = 0; st < NST; st++) {
                 const int ch = st * LPR + l;
-                const uint4 wg = make_uint4(w.g[st].x, w.g[st].y, w.g[st].z, w.g[st].w);
-                const uint4 wu = make_uint4(w.u[st].x, w.u[st].y, w.u[st].z, w.u[st].w);
                 if constexpr (I8) {
                     const uint4 xa = s_x[j * XQ + 2 * ch], xb = s_x[j * XQ + 2 * ch + 1];
                     const float2 ci = s_ci[j * NCH + ch];
-                    ag = fmaf(dot16_i8h(wg, xa, xb, ci.x), ci.y, ag);
-                    au = fmaf(dot16_i8h(wu, xa, xb, ci.x), ci.y, au);
+                    ag = fmaf(dot16_i8h(wg[st], xa, xb, ci.x), ci.y, ag);
+                    au = fmaf(dot16_i8h(wu[st], xa, xb, ci.x), ci.y, au);
                 } else {
                     uint32_t xw[16];                     // the 32 bf16 activations as packed pairs
 #pragma unroll
@@ -281,35 +258,14 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
                         const uint4 a = s_x[j * XQ + 4 * ch + q];
                         xw[4 * q] = a.x; xw[4 * q + 1] = a.y; xw[4 * q + 2] = a.z; xw[4 * q + 3] = a.w;
                     }
-                    ag += f4_chunk_bx(wg, w.bg[st], xw);
-                    au += f4_chunk_bx(wu, w.bu[st], xw);
+                    ag += f4_chunk_bx(wg[st], bg[st], xw);
+                    au += f4_chunk_bx(wu[st], bu[st], xw);
                 }
             }
             ag = group_sum<LPR>(ag);
             au = group_sum<LPR>(au);
-            if (l == 0) hpair[(size_t)(p0 + j) * I + row] = silu(ag * w.rsg) * (au * w.rsu);
-        };
-        // straight-line code for the first pair (every expert has one) keeps the
-        // next tile's loads outstanding; a runtime loop would wait for them
-        pair_out(0);
-        for (int j = 1; j < np; j++) pair_out(j);
-    };
-    // Two tiles in flight ahead of the one being computed (ring of three). Every
-    // loop back-edge follows an unconditional prefetch, so the compiler's wait
-    // counts stay exact (a conditional one makes it wait for all loads).
-    using PF = std::true_type;
-    using NoPF = std::false_type;
-    Tile t0, t1, t2;
-    load(t0, lo, exp_id[lo / TPE]);
-    if (lo + 1 >= hi) { step(t0, t1, lo, NoPF{}); return; }
-    load(t1, lo + 1, exp_id[(lo + 1) / TPE]);
-    for (int t = lo;; t += 3) {
-        if (t + 2 >= hi) { step(t0, t2, t, NoPF{}); step(t1, t2, t + 1, NoPF{}); break; }
-        step(t0, t2, t, PF{});
-        if (t + 3 >= hi) { step(t1, t0, t + 1, NoPF{}); step(t2, t0, t + 2, NoPF{}); break; }
-        step(t1, t0, t + 1, PF{});
-        if (t + 4 >= hi) { step(t2, t1, t + 2, NoPF{}); step(t0, t1, t + 3, NoPF{}); break; }
-        step(t2, t1, t + 2, PF{});
+            if (l == 0) hpair[(size_t)(p0 + j0 + j) * I + row] = silu(ag * rsg) * (au * rsu);
+        }
     }
 }
 
@@ -503,7 +459,7 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
 #define QFM_CSR_LAUNCH(F, HH, II)                                                                                   \
     hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), dim3(xh ? 1024 : kTopkThreads), 0, s, logits, ld, M, K,          \
                        g_cfg.renorm, sel, wts, csr, x, HH, xh, xci);                                             \
-    hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(256 * kGateupBPC), b256, 0, s,                         \
+    hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(II / (256 / gateup_lpr<F, HH>()), umax), b256, 0, s,  \
                        wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, xh, xci, K, csr, P,  \
                        hpair);                                                                                   \
     hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / down_rows<F, II>(), umax + (sh ? (M + 1) / 2 : 0)), b256, 0, s, wd,   \
