@@ -150,7 +150,7 @@ __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict_
 // Block tile (16 MW WM) x (64 WN), WM x WN waves of (16 MW) x 64 (MW x 4
 // v_mfma_f32_16x16x32_bf16 accumulators each), k-step BK2 = 64 (two 32-deep
 // MFMA steps). Two LDS buffers (the k-step being multiplied and the next one)
-// and two register stages of global loads, one barrier per k-step.
+// and NSTG (2 or 3) register stages of global loads, one barrier per k-step.
 // A rows: bf16, row r at A + arow[r] * lda (arow < 0: absent row). B rows:
 // int8 (staged as bf16 in offset-binary form u = q + 128, exact), bf16, or
 // NVFP4 (packed e2m1 at bptr[n], e4m3 block scales per 16 at sptr[n]; staged
@@ -159,10 +159,10 @@ __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict_
 // wave = WN wm + wn. Staging: 16-byte chunks, consecutive threads on
 // consecutive chunks of a row (A: 8 chunks per row, B: 4 int8 / 2 NVFP4 / 8 bf16).
 //
-// The two register stages are two named stage sets of native vector type (a
+// The register stages are named stage sets of native vector type (a
 // dynamically indexed stage array went to scratch; uint4 stage members were
 // promoted to LDS), and every k-step is one basic block: the global loads of
-// step s + 3 are clamped to the last k-step (a repeat of an address already
+// step s + NSTG + 1 are clamped to the last k-step (a repeat of an address already
 // loaded: L2 hits) and absent A rows read a present row (their results are
 // never stored), so no branch splits the step and the compiler schedules the
 // fragment reads, MFMAs, the next step's conversion, LDS writes and global
@@ -176,8 +176,9 @@ struct TileLds {
     uint16_t b[2][BNt * LDS2];
 };
 enum { kB_I8 = 0, kB_BF16 = 2, kB_F4 = 3 };
-template <int BMODE, int WM, int WN, int MW = 4>
+template <int BMODE, int WM, int WN, int MW, int NSTG>
 struct TileEngine {
+    static_assert(NSTG == 2 || NSTG == 3, "two or three register stages");
     static_assert(BMODE == kB_I8 || BMODE == kB_F4 || BMODE == kB_BF16, "int8, NVFP4 or bf16 B rows");
     // MW m-blocks of 16 rows per wave: a wave computes (16 MW) x 64
     static constexpr int BMt = 16 * MW * WM, BNt = 64 * WN, NT = 64 * WM * WN;
@@ -256,7 +257,7 @@ struct TileEngine {
         const int nk = K / BK2;
         const int lr = lane & 15, lk = (lane >> 4) * 8;
         // one k-step: MFMAs on LDS buffer s & 1, then stage `nx` (holding step
-        // s + 1) goes to the other buffer and is refilled with step s + 3
+        // s + 1) goes to the other buffer and is refilled with step s + NSTG + 1
         auto step = [&](int s, Stage &nx) __attribute__((always_inline)) {
             const int buf = s & 1;
             bf16x8_t av[2][MW], bv[2][4];
@@ -277,39 +278,60 @@ struct TileEngine {
                     for (int nb = 0; nb < 4; nb++)
                         acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[kk][mb], bv[kk][nb], acc[mb][nb], 0, 0, 0);
             sstore(buf ^ 1, nx);
-            gload(min(s + 3, nk - 1) * BK2, nx);
+            gload(min(s + NSTG + 1, nk - 1) * BK2, nx);
             __syncthreads();
         };
-        Stage s0, s1;                                  // stage (s mod 2) holds k-step s
-        gload(0, s0);
-        gload(min(1, nk - 1) * BK2, s1);
-        sstore(0, s0);
-        gload(min(2, nk - 1) * BK2, s0);
-        __syncthreads();
-        int s = 0;
-        for (; s + 2 <= nk; s += 2) {
-            step(s, s1);
-            step(s + 1, s0);
+        if constexpr (NSTG == 2) {
+            Stage s0, s1;                              // stage (s mod 2) holds k-step s
+            gload(0, s0);
+            gload(min(1, nk - 1) * BK2, s1);
+            sstore(0, s0);
+            gload(min(2, nk - 1) * BK2, s0);
+            __syncthreads();
+            int s = 0;
+            for (; s + 2 <= nk; s += 2) {
+                step(s, s1);
+                step(s + 1, s0);
+            }
+            if (s < nk) step(s, s1);
+        } else {
+            Stage s0, s1, s2;                          // stage (s mod 3) holds k-step s
+            gload(0, s0);
+            gload(min(1, nk - 1) * BK2, s1);
+            gload(min(2, nk - 1) * BK2, s2);
+            sstore(0, s0);
+            gload(min(3, nk - 1) * BK2, s0);
+            __syncthreads();
+            int s = 0;
+            for (; s + 3 <= nk; s += 3) {
+                step(s, s1);
+                step(s + 1, s2);
+                step(s + 2, s0);
+            }
+            if (s < nk) step(s, s1);
+            if (s + 1 < nk) step(s + 1, s2);
         }
-        if (s < nk) step(s, s1);
     }
 };
 
 // router GEMM: 128 x 128 tiles, 2 x 2 waves; grouped expert GEMMs: 128 x 256, 2 x 4 waves
-using RouterEngine = TileEngine<kB_BF16, 2, 2, 4>;
+using RouterEngine = TileEngine<kB_BF16, 2, 2, 4, 2>;
 // router GEMM slices along H, summed in slice order by k_pf_select (2 measured
 // 5% slower than 1 at T = 8038: the 63 m-tiles x 4 n-tiles already fill the chip)
 constexpr int kRouterKS = 1;
 // INT8 tiles: 128 x 256 in 8 waves of 64 x 64 (two waves per SIMD). Four
 // waves of 128 x 64 (MW = 8: one wave per SIMD, accumulators in AGPRs, 25%
 // fewer LDS reads per MFMA) measured 1343 / 1149 us against 797 / 719 us.
-using ExpertEngine = TileEngine<kB_I8, 2, 4, 4>;
+using ExpertEngine = TileEngine<kB_I8, 2, 4, 4, 2>;
 // INT8 down tiles: 128 x 128 in 4 waves, two blocks per CU (K = I is short, so
 // one block's prologue and epilogue overlap the other block's k-steps)
-using DownEngineI8 = TileEngine<kB_I8, 2, 2, 4>;
+using DownEngineI8 = TileEngine<kB_I8, 2, 2, 4, 2>;
 // NVFP4 launches: e2m1 tiles and the shared expert's INT8 tiles in one kernel
-using ExpertEngineF4 = TileEngine<kB_F4, 2, 4, 4>;
-using SharedEngineI8 = TileEngine<kB_I8, 2, 4, 4>;     // shared tiles inside the NVFP4 launch
+// (three register stages: loads four k-steps ahead; gate/up 831 -> 737 us.
+// The INT8 engines and the router keep two: a third measured no faster for
+// INT8 and cost the router GEMM its second wave per SIMD.)
+using ExpertEngineF4 = TileEngine<kB_F4, 2, 4, 4, 3>;
+using SharedEngineI8 = TileEngine<kB_I8, 2, 4, 4, 3>;     // shared tiles inside the NVFP4 launch
 constexpr int GBN = ExpertEngine::BNt;          // weight rows per grouped-GEMM tile
 
 // Workgroups are dispatched to the 8 XCDs round-robin (block b on XCD b % 8).
