@@ -37,12 +37,15 @@
 //                      (precomputed: x sums in the router, hidden sums in the
 //                      gate/up epilogue) times 128 is subtracted in the epilogue.
 //   k_pf_combine       y[t] = sum over the K+1 slots of t, in slot order.
+#include <type_traits>
+
 #include "qfm_dev.h"
 #include "qfm_internal.h"
 
 namespace qfm {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128;
@@ -61,6 +64,20 @@ __device__ __forceinline__ void i8_to_bf16_ob(uint4 w, uint4 &o0, uint4 &o1) {
     for (int q = 0; q < 4; q++) {
         o[2 * q] = pack_bf16_exact((float)(d[q] & 0xFFu), (float)((d[q] >> 8) & 0xFFu));
         o[2 * q + 1] = pack_bf16_exact((float)((d[q] >> 16) & 0xFFu), (float)(d[q] >> 24));
+    }
+    o0 = make_uint4(o[0], o[1], o[2], o[3]);
+    o1 = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+// 16 int8 codes -> 16 fp16 1024 + u (u = q ^ 0x80 = q + 128; exact: unit
+// spacing on [1024, 2048)), one v_perm_b32 per two codes
+__device__ __forceinline__ void i8_to_f16_ob(uint4 w, uint4 &o0, uint4 &o1) {
+    const uint32_t d[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
+    uint32_t o[8];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        o[2 * q] = __builtin_amdgcn_perm(0x64646464u, d[q], 0x04010400u);
+        o[2 * q + 1] = __builtin_amdgcn_perm(0x64646464u, d[q], 0x04030402u);
     }
     o0 = make_uint4(o[0], o[1], o[2], o[3]);
     o1 = make_uint4(o[4], o[5], o[6], o[7]);
@@ -94,7 +111,9 @@ __device__ __forceinline__ void f4_to_bf16(uint4 w, uint32_t sc2, uint4 (&o)[4])
 __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict__ W, int E, int H,
                                                          float *__restrict__ wnorm, uint16_t *__restrict__ wb,
                                                          const uint16_t *__restrict__ x, int T,
-                                                         float *__restrict__ xnorm, float *__restrict__ xsum) {
+                                                         float *__restrict__ xnorm, float *__restrict__ xsum,
+                                                         uint4 *__restrict__ x16, float *__restrict__ x16sum,
+                                                         float *__restrict__ x16isc) {
     if ((int)blockIdx.x >= E) {
         constexpr int kMaxCh = 5;                    // 16-byte chunks per lane: H / 512 <= 5
         const int lane = threadIdx.x & 63;
@@ -125,6 +144,43 @@ __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict_
         if (lane == 0) {
             xnorm[t] = (float)(sqrt(sq) * (1.0 + 1e-6));
             xsum[t] = sx;
+        }
+        if (x16) {
+            // the row as fp16 scaled by 2^k (largest magnitude in [2^14, 2^15): no
+            // overflow, bf16 values exact), with the sum of the scaled values and 2^-k
+            float amax = 0.0f;
+#pragma unroll
+            for (int q = 0; q < kMaxCh; q++) {
+                const uint32_t d[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+                for (int u = 0; u < 4; u++) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(d[u])), fabsf(bf16_hi(d[u]))));
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, WAVE));
+            const int e = (int)(__float_as_uint(amax) >> 23);
+            const int k = amax == 0.0f ? 0 : min(113, max(-113, 141 - e));
+            const float sc = __uint_as_float((uint32_t)(127 + k) << 23);
+            float hs = 0.0f;
+            uint4 *xo = x16 + (size_t)t * (H / 8);
+#pragma unroll
+            for (int q = 0; q < kMaxCh; q++) {
+                if (q >= nch) break;
+                const uint32_t d[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+                uint32_t o[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const f16x2_t hp = {(_Float16)(bf16_lo(d[u]) * sc), (_Float16)(bf16_hi(d[u]) * sc)};
+                    hs += (float)hp.x + (float)hp.y;
+                    o[u] = __builtin_bit_cast(uint32_t, hp);
+                }
+                xo[q * 64 + lane] = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) hs += __shfl_xor(hs, m, WAVE);
+            if (lane == 0) {
+                x16sum[t] = hs;
+                x16isc[t] = __uint_as_float((uint32_t)(127 - k) << 23);
+            }
         }
         return;
     }
@@ -175,14 +231,18 @@ struct TileLds {
     uint16_t a[2][BMt * LDS2];
     uint16_t b[2][BNt * LDS2];
 };
-enum { kB_I8 = 0, kB_BF16 = 2, kB_F4 = 3 };
+enum { kB_I8 = 0, kB_BF16 = 2, kB_F4 = 3, kB_I8H = 4 };
 template <int BMODE, int WM, int WN, int MW, int NSTG>
 struct TileEngine {
     static_assert(NSTG == 2 || NSTG == 3, "two or three register stages");
-    static_assert(BMODE == kB_I8 || BMODE == kB_F4 || BMODE == kB_BF16, "int8, NVFP4 or bf16 B rows");
+    using Lds = TileLds<16 * MW * WM, 64 * WN>;
+    static constexpr int WMc = WM, WNc = WN, MWc = MW, WavesPerSimd = 2;
+    static_assert(BMODE == kB_I8 || BMODE == kB_I8H || BMODE == kB_F4 || BMODE == kB_BF16,
+                  "int8 (bf16 or fp16 staging), NVFP4 or bf16 B rows");
+    static constexpr bool B8 = BMODE == kB_I8 || BMODE == kB_I8H;   // one byte per B value
     // MW m-blocks of 16 rows per wave: a wave computes (16 MW) x 64
     static constexpr int BMt = 16 * MW * WM, BNt = 64 * WN, NT = 64 * WM * WN;
-    static constexpr int BCPR = BMODE == kB_I8 ? 4 : BMODE == kB_F4 ? 2 : 8;   // 16-byte B chunks per row per k-step
+    static constexpr int BCPR = B8 ? 4 : BMODE == kB_F4 ? 2 : 8;   // 16-byte B chunks per row per k-step
     static constexpr int NA = BMt * 8 / NT, NB = BNt * BCPR / NT;      // chunks per thread
     static_assert(NA * NT == BMt * 8 && NB * NT == BNt * BCPR, "staging must divide evenly");
     struct Stage {                                // native vector types: SROA keeps them in registers
@@ -211,14 +271,14 @@ struct TileEngine {
             const int c = t + j * NT, r = c / BCPR, kc = c % BCPR;
             bp[j] = bptr[r] + kc * 16;
             sp[j] = BMODE == kB_F4 ? sptr[r] + kc * 2 : nullptr;
-            b_lds[j] = r * LDS2 + (BMODE == kB_I8 ? kc * 16 : BMODE == kB_F4 ? kc * 32 : kc * 8);
+            b_lds[j] = r * LDS2 + (B8 ? kc * 16 : BMODE == kB_F4 ? kc * 32 : kc * 8);
         }
         auto gload = [&](int k0, Stage &g) __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < NA; j++) g.a[j] = *reinterpret_cast<const u32x4_t *>(ap[j] + k0);
 #pragma unroll
             for (int j = 0; j < NB; j++) {
-                if constexpr (BMODE == kB_I8) {
+                if constexpr (B8) {
                     g.b[j] = *reinterpret_cast<const u32x4_t *>(bp[j] + k0);
                 } else if constexpr (BMODE == kB_BF16) {
                     g.b[j] = *reinterpret_cast<const u32x4_t *>(bp[j] + (size_t)k0 * 2);
@@ -237,9 +297,10 @@ struct TileEngine {
                 const uint4 bw = make_uint4(g.b[j].x, g.b[j].y, g.b[j].z, g.b[j].w);
                 if constexpr (BMODE == kB_BF16) {
                     lb[0] = bw;
-                } else if constexpr (BMODE == kB_I8) {
+                } else if constexpr (B8) {
                     uint4 o0, o1;
-                    i8_to_bf16_ob(bw, o0, o1);
+                    if constexpr (BMODE == kB_I8H) i8_to_f16_ob(bw, o0, o1);
+                    else i8_to_bf16_ob(bw, o0, o1);
                     lb[0] = o0;
                     lb[1] = o1;
                 } else {
@@ -276,7 +337,12 @@ struct TileEngine {
                 for (int mb = 0; mb < MW; mb++)
 #pragma unroll
                     for (int nb = 0; nb < 4; nb++)
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[kk][mb], bv[kk][nb], acc[mb][nb], 0, 0, 0);
+                        if constexpr (BMODE == kB_I8H)
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av[kk][mb]),
+                                                                                __builtin_bit_cast(f16x8_t, bv[kk][nb]),
+                                                                                acc[mb][nb], 0, 0, 0);
+                        else
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[kk][mb], bv[kk][nb], acc[mb][nb], 0, 0, 0);
             sstore(buf ^ 1, nx);
             gload(min(s + NSTG + 1, nk - 1) * BK2, nx);
             __syncthreads();
@@ -322,7 +388,9 @@ constexpr int kRouterKS = 1;
 // INT8 tiles: 128 x 256 in 8 waves of 64 x 64 (two waves per SIMD). Four
 // waves of 128 x 64 (MW = 8: one wave per SIMD, accumulators in AGPRs, 25%
 // fewer LDS reads per MFMA) measured 1343 / 1149 us against 797 / 719 us.
-using ExpertEngine = TileEngine<kB_I8, 2, 4, 4, 2>;
+// INT8 gate/up: int8 weights widened to fp16 while staging (one v_perm per two
+// codes instead of three ops per two for bf16) against the fp16 x rows
+using ExpertEngine = TileEngine<kB_I8H, 2, 4, 4, 2>;
 // INT8 down tiles: 128 x 128 in 4 waves, two blocks per CU (K = I is short, so
 // one block's prologue and epilogue overlap the other block's k-steps)
 using DownEngineI8 = TileEngine<kB_I8, 2, 2, 4, 2>;
@@ -667,23 +735,28 @@ struct GroupW {
 // applied in the epilogue) and the shared expert's tiles, INT8 in both formats.
 // kDownI8: INT8 down on 128 x 128 tiles (DownEngineI8).
 enum { kAllI8 = 0, kRoutedF4 = 1, kDownI8 = 2 };
+template <int MODE>
+using GemmEngine = std::conditional_t<MODE == kDownI8, DownEngineI8,
+                                      std::conditional_t<MODE == kAllI8, ExpertEngine, ExpertEngineF4>>;
 template <bool GATEUP, int MODE>
-__global__ void __launch_bounds__(MODE == kAllI8 ? ExpertEngine::NT : MODE == kDownI8 ? DownEngineI8::NT
-                                                                                      : ExpertEngineF4::NT)
-__attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(GemmEngine<MODE>::NT)
+__attribute__((amdgpu_waves_per_eu(GemmEngine<MODE>::WavesPerSimd, GemmEngine<MODE>::WavesPerSimd)))
 k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int which, const int *__restrict__ off,
           const int *__restrict__ p_tok, const int *__restrict__ p_slot, const float *__restrict__ p_wt,
           const uint16_t *__restrict__ A, int Kdim, int Nrows, GroupW g0, GroupW g1, int E,
           uint16_t *__restrict__ hid, float *__restrict__ part, int Hout, int ntiles,
-          const float *__restrict__ xsum, float *__restrict__ hsum, int nt_gu) {
+          const float *__restrict__ xsum, float *__restrict__ hsum, int nt_gu, const float *__restrict__ xisc) {
     static_assert(MODE != kDownI8 || !GATEUP, "the narrow tiles are for the down GEMM");
-    constexpr int WN = MODE == kDownI8 ? 2 : 4, TBN = 64 * WN;
-    __shared__ __align__(16) TileLds<BM, TBN> lds;
+    using Eng = GemmEngine<MODE>;
+    constexpr int WN = Eng::WNc, TBN = Eng::BNt;
+    static_assert(Eng::BMt == BM, "tiles of BM rows");
+    constexpr bool H16 = MODE == kAllI8;            // fp16 A rows (scaled per token) and fp16-widened int8
+    __shared__ __align__(16) typename Eng::Lds lds;
     __shared__ int arow[BM];
     __shared__ const char *bptr[TBN];
     constexpr bool F4 = MODE == kRoutedF4;
     __shared__ const char *sptr[F4 ? TBN : 1];
-    __shared__ float rsum[BM], hpart[WN][BM];
+    __shared__ float rsum[BM], rscl[H16 ? BM : 1], hpart[WN][BM];
     int mi, ni;
     xcd_tile(blockIdx.x, ntiles, mi, ni);
     if (mi * ntiles >= n_items[which]) return;
@@ -718,6 +791,7 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
         if (GATEUP) {
             arow[r] = r < rows ? p_tok[pbase + r] : -1;
             if (r < rows) rs = xsum[arow[r]];
+            if constexpr (H16) rscl[r] = r < rows ? xisc[arow[r]] : 0.0f;
         } else {
             arow[r] = r < rows ? pbase + r : -1;
             if (r < rows)
@@ -739,9 +813,8 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
         }
     }
     __syncthreads();
-    // engine geometry: MWv m-blocks of 16 rows per wave, WMv waves along the rows
-    constexpr int MWv = 4;
-    static_assert(ExpertEngine::BMt == 16 * MWv * 2 && DownEngineI8::BMt == 16 * MWv * 2, "2 waves x 64 rows");
+    // engine geometry: MWv m-blocks of 16 rows per wave, Eng::WMc waves along the rows
+    constexpr int MWv = Eng::MWc;
     constexpr int RPW = 16 * MWv;                   // rows per wave
     f32x4_t acc[MWv][4];
     if constexpr (F4) {
@@ -765,9 +838,11 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
                     const int o = nt * 128 + wn * 32 + nb * 16 + (lane & 15);
                     float hs = 0.0f;
                     if (r < rows) {
-                        const float cr = f4 ? 0.0f : 128.0f * rsum[r];
-                        const float gv = (acc[mb][nb][i] - cr) * (f4 ? s2a : Sb[o]);
-                        const float uv = (acc[mb][nb + 2][i] - cr) * (f4 ? s2b : Sb2[o]);
+                        // offset-binary correction: bf16 rows 128 * sum(x), fp16 rows 1152 * sum(x16)
+                        const float cr = f4 ? 0.0f : (H16 ? 1152.0f : 128.0f) * rsum[r];
+                        const float ks = H16 ? rscl[r] : 1.0f;
+                        const float gv = (acc[mb][nb][i] - cr) * ks * (f4 ? s2a : Sb[o]);
+                        const float uv = (acc[mb][nb + 2][i] - cr) * ks * (f4 ? s2b : Sb2[o]);
                         const uint16_t hb = f32_to_bf16(silu(gv) * uv);
                         hid[(size_t)(pbase + r) * Nrows + o] = hb;
                         hs = bf16_to_f32(hb);
@@ -858,6 +933,7 @@ size_t prefill_ws_bytes(int T) {
     b += al(P * c.H * 4);                  // partials
     b += al((size_t)T * 4);                // x row sums
     b += al(P * (c.I / (GBN / 2)) * 4);    // hidden row sums per gate/up n-tile
+    b += al((size_t)T * c.H * 2) + al((size_t)T * 4) * 2;   // fp16 x rows, their sums and 2^-k
     return b;
 }
 
@@ -913,13 +989,16 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     uint16_t *hid = reinterpret_cast<uint16_t *>(b); b += al(P * I * 2);
     float *part = reinterpret_cast<float *>(b); b += al(P * H * 4);
     float *xsum = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
-    float *hsum = reinterpret_cast<float *>(b);
+    float *hsum = reinterpret_cast<float *>(b); b += al(P * nt_gu * 4);
+    uint4 *x16 = reinterpret_cast<uint4 *>(b); b += al((size_t)T * H * 2);
+    float *x16sum = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
+    float *x16isc = reinterpret_cast<float *>(b);
 
     const float *g = (has_sh && gated) ? L->sh_gate_inp : nullptr;
     // zero the small counters with a fill kernel (no memset node in captured graphs)
     launch_fill_f32(reinterpret_cast<float *>(ctr), 8, 0.0f, s);
     hipLaunchKernelGGL(k_pf_router_prep, dim3((unsigned)(E + (T + 3) / 4)), dim3(256), 0, s, L->router, E, H, wnorm,
-                       wb16, x, T, xnorm, xsum);
+                       wb16, x, T, xnorm, xsum, f4 ? nullptr : x16, x16sum, x16isc);
     const int mt_router = ((T + BM - 1) / BM + 7) / 8 * 8;
     hipLaunchKernelGGL(k_pf_router_mfma, dim3(mt_router * (E / BN), kRouterKS), dim3(256), 0, s, x, T, H, wb16, E, lg);
     if (H == 2048)
@@ -947,14 +1026,15 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
         nth(f4 ? ExpertEngineF4::NT : ExpertEngine::NT), nth_dn(f4 ? ExpertEngineF4::NT : DownEngineI8::NT);
     if (f4) {
         hipLaunchKernelGGL((k_pf_gemm<true, kRoutedF4>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, off, p_tok, p_slot,
-                           p_wt, x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu);
+                           p_wt, x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu, nullptr);
         hipLaunchKernelGGL((k_pf_gemm<false, kRoutedF4>), g_dn, nth, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot,
-                           p_wt, hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu);
+                           p_wt, hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu, nullptr);
     } else {
         hipLaunchKernelGGL((k_pf_gemm<true, kAllI8>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, off, p_tok, p_slot, p_wt,
-                           x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu);
+                           reinterpret_cast<const uint16_t *>(x16), H, I, gg, gu, E, hid, part, H, nt_gu, x16sum, hsum,
+                           nt_gu, x16isc);
         hipLaunchKernelGGL((k_pf_gemm<false, kDownI8>), g_dn, nth_dn, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot, p_wt,
-                           hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu);
+                           hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu, nullptr);
     }
     launch_pf_combine(part, T, S, H, y, s);
     return check_launch("prefill");
