@@ -272,11 +272,12 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
         float *hsh = hidden + (size_t)c.K * c.I;
         // 1. router logits (+ shared gate dot): depend on x only
         int rc = 0;
-        if (mask & 1) rc = launch_router_shared(L->router, L->router_bias, g, nullptr, x, 1, logits, ld, hsh, c.I, s);
+        void *x16 = b + w.xh16;                    // x as scaled fp16 + (sum, 2^-k), written by the router launch
+        if (mask & 1) rc = launch_router_shared(L->router, L->router_bias, g, nullptr, x, 1, logits, ld, hsh, c.I, s, x16);
         if (g_prof.on) pm[1] = prof_event(s);
         // 2. top-K inside the gate/up kernel, whose last grid row computes the shared
         // expert's hidden (no selection needed there); 3. down + combine (+ shared) -> y bf16
-        if (!rc && (mask & 2)) rc = launch_i8_gateup_m1(L->arena, x, nullptr, logits, sel, wts, c.K, hidden, s, sp);
+        if (!rc && (mask & 2)) rc = launch_i8_gateup_m1(L->arena, x, nullptr, logits, sel, wts, c.K, hidden, s, sp, x16);
         if (g_prof.on) pm[2] = prof_event(s);
         if (!rc && (mask & 4))
             rc = launch_i8_down_m1(L->arena, hidden, wts, sel, c.K, sp, g ? logits + c.E : nullptr, nullptr, y, s);

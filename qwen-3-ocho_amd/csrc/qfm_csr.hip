@@ -269,24 +269,6 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
     }
 }
 
-// ---- down: hidden rows staged in LDS as scaled fp16 chunks ------------------------
-// rows h[0..n) of I fp32 values, one 16-value chunk per thread and pass
-template <int I>
-__device__ __forceinline__ void stage_h16(const float *__restrict__ h, int n, uint4 *s_h16, float2 *s_hci) {
-    for (int c = threadIdx.x; c < n * (I / 16); c += 256) {
-        const float4 *hp = reinterpret_cast<const float4 *>(h) + 4 * c;
-        float v[16];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 f = hp[q];
-            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
-        }
-        uint4 ha, hb;
-        s_hci[c] = chunk16_to_f16(v, ha, hb);
-        s_h16[2 * c] = ha;
-        s_h16[2 * c + 1] = hb;
-    }
-}
 // <down row, staged hidden row j> over this lane's NST chunks: INT8 (16 codes
 // per chunk, dot16_i8h) or NVFP4 (32 codes per chunk, f4_chunk_h)
 template <class F, int I, int LPR, int NST>

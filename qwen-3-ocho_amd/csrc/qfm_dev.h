@@ -93,6 +93,67 @@ __device__ __forceinline__ float2 chunk16_to_f16(const float *v, uint4 &ha, uint
     return make_float2(-kI8hOffset * sum, isc);
 }
 
+// ---- hidden rows staged in LDS as scaled fp16 chunks ---------------------------
+// rows h[0..n) of I fp32 values (contiguous), one 16-value chunk per thread and
+// pass of an NT-thread block: s_h16 two 16-byte words per chunk, s_hci its
+// (seed, 2^-k) (chunk16_to_f16)
+template <int I, int NT = 256>
+__device__ __forceinline__ void stage_h16(const float *__restrict__ h, int n, uint4 *s_h16, float2 *s_hci) {
+    for (int c = threadIdx.x; c < n * (I / 16); c += NT) {
+        const float4 *hp = reinterpret_cast<const float4 *>(h) + 4 * c;
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 f = hp[q];
+            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+        }
+        uint4 ha, hb;
+        s_hci[c] = chunk16_to_f16(v, ha, hb);
+        s_h16[2 * c] = ha;
+        s_h16[2 * c + 1] = hb;
+    }
+}
+// One wave converts a bf16 row of H values to fp16 scaled by 2^k (largest
+// magnitude in [2^14, 2^15): exact for bf16 values, no overflow); writes the
+// row (H / 8 16-byte words, same value order) and info = (sum of the scaled
+// values, 2^-k). (group_max / group_sum are defined further down.)
+template <int G> __device__ float group_sum(float v);
+template <int G> __device__ float group_max(float v);
+template <int H>
+__device__ __forceinline__ void wave_row_to_f16(const uint16_t *__restrict__ x, uint4 *__restrict__ xo,
+                                                float2 *__restrict__ info, int lane) {
+    constexpr int NC = H / 512;                     // 16-byte words per lane
+    uint4 v[NC];
+#pragma unroll
+    for (int q = 0; q < NC; q++) v[q] = reinterpret_cast<const uint4 *>(x)[q * 64 + lane];
+    float amax = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NC; q++) {
+        const uint32_t d[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+        for (int u = 0; u < 4; u++) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(d[u])), fabsf(bf16_hi(d[u]))));
+    }
+    amax = group_max<64>(amax);
+    const int e = (int)(__float_as_uint(amax) >> 23);
+    const int k = amax == 0.0f ? 0 : min(113, max(-113, 141 - e));
+    const float sc = __uint_as_float((uint32_t)(127 + k) << 23);
+    float hs = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NC; q++) {
+        const uint32_t d[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const f16x2_t hp = {(_Float16)(bf16_lo(d[u]) * sc), (_Float16)(bf16_hi(d[u]) * sc)};
+            hs += (float)hp.x + (float)hp.y;
+            o[u] = __builtin_bit_cast(uint32_t, hp);
+        }
+        xo[q * 64 + lane] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    hs = group_sum<64>(hs);
+    if (lane == 0) *info = make_float2(hs, __uint_as_float((uint32_t)(127 - k) << 23));
+}
+
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_nt16(const void *p) {
     const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
@@ -107,7 +168,7 @@ __device__ __forceinline__ uint4 ld_nt16(const void *p) {
 // (hipcc 7.2 drops the second result of v_permlane16_swap / 32_swap, so the
 // gfx950 row swaps are not used.)
 template <int G>
-__device__ __forceinline__ float group_sum(float v) {
+__device__ float group_sum(float v) {
     static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group of 2^k lanes");
     if constexpr (G >= 2)   // quad_perm [1,0,3,2]
         v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
@@ -120,6 +181,24 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (G >= 32)  // ds_swizzle bit-mask mode, lane ^ 16 within 32 lanes: and 0x1F, or 0, xor 0x10
         v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
     if constexpr (G >= 64) v += __shfl_xor(v, 32, WAVE);
+    return v;
+}
+
+// Max over aligned groups of G lanes (same steps as group_sum).
+template <int G>
+__device__ float group_max(float v) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group of 2^k lanes");
+    if constexpr (G >= 2)
+        v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    if constexpr (G >= 4)
+        v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    if constexpr (G >= 8)
+        v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    if constexpr (G >= 16)
+        v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+    if constexpr (G >= 32)
+        v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
+    if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32, WAVE));
     return v;
 }
 

@@ -22,9 +22,11 @@
 // routed blocks are still selecting.
 //
 // down: one LPR-lane group per output row (LPR = 32 for I = 512, 8 for
-// I = 640). Every weight load of the row is issued first (the 16-byte chunks
-// of all K + 1 expert rows), then the hidden vectors are staged in LDS with
-// the sum of every 16-element chunk (the offset-binary correction). Each
+// I = 640). The hidden vectors are loaded first, then every weight load of
+// the row is issued (the 16-byte chunks of all K + 1 expert rows), and while
+// those are in flight the hidden vectors are staged in LDS as fp16 chunks
+// scaled by powers of two (chunk16_to_f16; the codes are widened to fp16,
+// dot16_i8h). Each
 // lane accumulates sum_j w_j * sd_j[c] * <Wd_j slice, h_j slice> across all
 // jobs and the group reduces once, so every output row has one writer and a
 // fixed summation order (deterministic; y is seeded, not accumulated).
@@ -33,22 +35,26 @@
 
 namespace qfm {
 
-template <int H, int I, int EPL>
-__global__ void __launch_bounds__(256)
+// (H = 2048: three waves per SIMD, so the 11 x 64 blocks of a decode step are all resident at once)
+template <int H, int I, int EPL, bool X16>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(H == 2048 ? 3 : 1)))
 k_i8_gateup_m1(const int8_t *__restrict__ Qg, const int8_t *__restrict__ Qu,
                const float *__restrict__ Sg, const float *__restrict__ Su,
                const uint16_t *__restrict__ xb, const float *__restrict__ xf,
                const float *__restrict__ logits, int *__restrict__ sel, float *__restrict__ wts,
-               int K, int renorm, float *__restrict__ hidden, ShPtrs sh) {
+               int K, int renorm, float *__restrict__ hidden, ShPtrs sh,
+               const uint4 *__restrict__ x16, const float2 *__restrict__ x16i) {
     constexpr int NST = H / 512;
     __shared__ __align__(16) unsigned long long s_tk[4][kTopkLds];
     const int job = blockIdx.y;
     const bool shared_job = sh.qg != nullptr && job == (int)gridDim.y - 1;
     const int l = threadIdx.x & 31;
     const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
-    float xs[NST][16];
-    if (xb) load_x_slice_bf16<H>(xb, l, xs);
-    else load_x_slice_f32<H>(xf, l, xs);
+    float xs[X16 ? 1 : NST][16];
+    if constexpr (!X16) {
+        if (xb) load_x_slice_bf16<H>(xb, l, xs);
+        else load_x_slice_f32<H>(xf, l, xs);
+    }
     int e = 0;
     if (shared_job) {
         Qg = sh.qg; Qu = sh.qu; Sg = sh.sg; Su = sh.su;     // expert 0 of a one-expert arena
@@ -71,6 +77,19 @@ k_i8_gateup_m1(const int8_t *__restrict__ Qg, const int8_t *__restrict__ Qu,
     } else {
         e = sel[job];
     }
+    uint4 xh[X16 ? NST : 1][2];
+    float2 xinf = make_float2(0.0f, 1.0f);
+    if constexpr (X16) {
+        // the x slice as fp16 (scaled per row), loaded after the selection (fewer
+        // registers live through it) and before the weights (waiting for it never
+        // waits for them): values [512 st + 16 l, +16) are words 64 st + 2 l, +1
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            xh[st][0] = x16[st * 64 + 2 * l];
+            xh[st][1] = x16[st * 64 + 2 * l + 1];
+        }
+        xinf = *x16i;
+    }
     const int8_t *qg = Qg + (size_t)e * ((size_t)I * H) + (size_t)row * H + l * 16;
     const int8_t *qu = Qu + (size_t)e * ((size_t)I * H) + (size_t)row * H + l * 16;
     uint4 wg[NST], wu[NST];
@@ -80,23 +99,42 @@ k_i8_gateup_m1(const int8_t *__restrict__ Qg, const int8_t *__restrict__ Qu,
         wu[st] = ld_nt16(qu + st * 512);
     }
     const float sg = Sg[(size_t)e * I + row], su = Su[(size_t)e * I + row];
-    float xsum = 0.0f;
+    float ag, au;
+    if constexpr (X16) {
+        // fp16-widened codes (dot16_i8h); the 1152 * sum(x16) offset is removed
+        // once from the row total
+        ag = 0.0f; au = 0.0f;
 #pragma unroll
-    for (int st = 0; st < NST; st++)
+        for (int st = 0; st < NST; st++) {
+            ag = dot16_i8h(wg[st], xh[st][0], xh[st][1], ag);
+            au = dot16_i8h(wu[st], xh[st][0], xh[st][1], au);
+        }
+        ag = group_sum<32>(ag);
+        au = group_sum<32>(au);
+        ag = (ag - kI8hOffset * xinf.x) * xinf.y;
+        au = (au - kI8hOffset * xinf.x) * xinf.y;
+    } else {
+        float xsum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) xsum += xs[st][i];
-    float ag = -128.0f * xsum, au = ag;
+        for (int st = 0; st < NST; st++)
 #pragma unroll
-    for (int st = 0; st < NST; st++) {
-        ag = dot16_u8(wg[st], xs[st], ag);
-        au = dot16_u8(wu[st], xs[st], au);
+            for (int i = 0; i < 16; i++) xsum += xs[st][i];
+        ag = -128.0f * xsum; au = ag;
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            ag = dot16_u8(wg[st], xs[st], ag);
+            au = dot16_u8(wu[st], xs[st], au);
+        }
+        ag = group_sum<32>(ag);
+        au = group_sum<32>(au);
     }
-    ag = group_sum<32>(ag);
-    au = group_sum<32>(au);
     if (l == 0) hidden[(size_t)job * I + row] = silu(ag * sg) * (au * su);
 }
 
 constexpr int kMaxJobs = 17;   // top_k <= 16 plus the shared expert
+#ifndef QFM_DOWN_M1_F16
+#define QFM_DOWN_M1_F16 1
+#endif
 
 // NJ jobs (routed experts, then the shared one when HAS_SH) are a template
 // parameter so that every register array is indexed at compile time: no
@@ -111,19 +149,27 @@ k_i8_down_m1(const int8_t *__restrict__ Qd, const float *__restrict__ Sd,
     constexpr int NST = I / (16 * LPR);
     constexpr int RPB = 256 / LPR;
     constexpr int NEXP = HAS_SH ? NJ - 1 : NJ;
-    constexpr int NH4 = NJ * I / 4;
-    constexpr int NSTG = (NH4 + 255) / 256;
-    __shared__ __align__(16) float sh_h[NSTG * 256 * 4];   // padded: the fill below is unconditional
-    __shared__ float sh_cs[NJ * I / 16];
+    constexpr int NCH = NJ * I / 16;                  // 16-value hidden chunks
+    constexpr int CPT = (NCH + 255) / 256;            // chunks per thread
+#if QFM_DOWN_M1_F16
+    __shared__ uint4 s_h16[NCH * 2];                  // the hidden rows as scaled fp16 (chunk16_to_f16)
+    __shared__ float2 s_hci[NCH];
+#else
+    __shared__ __align__(16) float s_h[NCH * 16];     // the hidden rows (fp32)
+    __shared__ float s_cs[NCH];                       // -128 * each chunk's sum (offset-binary correction)
+#endif
     const int l = threadIdx.x % LPR;
     const int c = blockIdx.x * RPB + threadIdx.x / LPR;
-    // batch 1: routing, router weights, shared gate, hidden vectors (to registers)
-    float4 stg[NSTG];
+    // batch 1: routing, router weights, shared gate, this thread's hidden chunks (to registers)
+    float hv[CPT][16];
 #pragma unroll
-    for (int q = 0; q < NSTG; q++) {
-        int i = threadIdx.x + q * 256;
-        i = i < NH4 ? i : NH4 - 1;
-        stg[q] = reinterpret_cast<const float4 *>(hidden)[i];   // shared hidden follows the routed ones
+    for (int q = 0; q < CPT; q++) {
+        const int ch = min((int)threadIdx.x + q * 256, NCH - 1);   // shared hidden follows the routed ones
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const float4 f = reinterpret_cast<const float4 *>(hidden)[ch * 4 + v];
+            hv[q][4 * v] = f.x; hv[q][4 * v + 1] = f.y; hv[q][4 * v + 2] = f.z; hv[q][4 * v + 3] = f.w;
+        }
     }
     int ex[NEXP > 0 ? NEXP : 1];
     float wt[NEXP > 0 ? NEXP : 1];
@@ -146,13 +192,25 @@ k_i8_down_m1(const int8_t *__restrict__ Qd, const float *__restrict__ Sd,
         for (int st = 0; st < NST; st++) w[u][st] = ld_nt16(p + (st * LPR + l) * 16);
     }
 #pragma unroll
-    for (int q = 0; q < NSTG; q++) reinterpret_cast<float4 *>(sh_h)[threadIdx.x + q * 256] = stg[q];
-    __syncthreads();
-    for (int i = threadIdx.x; i < NJ * I / 16; i += 256) {
-        float t = 0.0f;
+    for (int q = 0; q < CPT; q++) {
+        const int ch = (int)threadIdx.x + q * 256;
+        if (ch < NCH) {
+#if QFM_DOWN_M1_F16
+            uint4 ha, hb;
+            s_hci[ch] = chunk16_to_f16(hv[q], ha, hb);
+            s_h16[2 * ch] = ha;
+            s_h16[2 * ch + 1] = hb;
+#else
+            float t = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 16; q++) t += sh_h[i * 16 + q];
-        sh_cs[i] = -128.0f * t;
+            for (int i = 0; i < 16; i++) t += hv[q][i];
+            s_cs[ch] = -128.0f * t;
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                reinterpret_cast<float4 *>(s_h)[ch * 4 + v] =
+                    make_float4(hv[q][4 * v], hv[q][4 * v + 1], hv[q][4 * v + 2], hv[q][4 * v + 3]);
+#endif
+        }
     }
     __syncthreads();
     if constexpr (HAS_SH) wsc[NJ - 1] = (gdot ? sigmoid(gd) : 1.0f) * sh_sd;
@@ -177,8 +235,14 @@ k_i8_down_m1(const int8_t *__restrict__ Qd, const float *__restrict__ Sd,
                 float d = 0.0f;
 #pragma unroll
                 for (int st = 0; st < NST; st++) {
-                    d += sh_cs[j * (I / 16) + st * LPR + l];
-                    d = dot16_u8(w[u][st], sh_h + j * I + (st * LPR + l) * 16, d);
+                    const int ch = j * (I / 16) + st * LPR + l;
+#if QFM_DOWN_M1_F16
+                    const float2 ci = s_hci[ch];
+                    d = fmaf(dot16_i8h(w[u][st], s_h16[2 * ch], s_h16[2 * ch + 1], ci.x), ci.y, d);
+#else
+                    d += s_cs[ch];
+                    d = dot16_u8(w[u][st], s_h + ch * 16, d);
+#endif
                 }
                 acc = fmaf(wsc[j], d, acc);
             }
@@ -215,11 +279,11 @@ static bool down_dispatch_nj(int nj, bool has_sh, const Qf4ExpCache *c, const fl
 }
 
 int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *xf, const float *logits, int *sel,
-                        float *wts, int nexp, float *hidden, hipStream_t s, const ShPtrs *sh) {
+                        float *wts, int nexp, float *hidden, hipStream_t s, const ShPtrs *sh, const void *x16) {
     if (!c || !c->i8_gate || !c->i8_up || !c->i8s_gate || !c->i8s_up) {
         set_error(-1, "i8_gateup_m1: arena has no INT8 gate/up"); return -1;
     }
-    if (nexp < 1 || nexp > 16 || (!xb && !xf) || !hidden || !sel || (logits && !wts)) {
+    if (nexp < 1 || nexp > 16 || (!xb && !xf && !x16) || !hidden || !sel || (logits && !wts)) {
         set_error(-1, "i8_gateup_m1: bad arguments"); return -1;
     }
     if (logits && (nexp != g_cfg.K || g_cfg.E != 512)) {
@@ -230,15 +294,19 @@ int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *x
     ShPtrs sp{};
     if (sh) sp = *sh;
     const unsigned jobs = (unsigned)nexp + (sh ? 1u : 0u);   // shared expert: last grid row, hidden row nexp
+    const uint4 *xh = static_cast<const uint4 *>(x16);
+    const float2 *xi = xh ? reinterpret_cast<const float2 *>(xh + g_cfg.H / 8) : nullptr;
+#define QFM_GU_M1(HH, II, X16)                                                                                  \
+    hipLaunchKernelGGL((k_i8_gateup_m1<HH, II, 8, X16>), dim3(II / 8, jobs), block, 0, s, c->i8_gate, c->i8_up, \
+                       c->i8s_gate, c->i8s_up, xb, xf, logits, sel, wts, K, rn, hidden, sp, xh, xi)
     if (shape_2048()) {
-        hipLaunchKernelGGL((k_i8_gateup_m1<2048, 512, 8>), dim3(512 / 8, jobs), block, 0, s, c->i8_gate, c->i8_up,
-                           c->i8s_gate, c->i8s_up, xb, xf, logits, sel, wts, K, rn, hidden, sp);
+        if (xh) QFM_GU_M1(2048, 512, true); else QFM_GU_M1(2048, 512, false);
     } else if (shape_2560()) {
-        hipLaunchKernelGGL((k_i8_gateup_m1<2560, 640, 8>), dim3(640 / 8, jobs), block, 0, s, c->i8_gate, c->i8_up,
-                           c->i8s_gate, c->i8s_up, xb, xf, logits, sel, wts, K, rn, hidden, sp);
+        if (xh) QFM_GU_M1(2560, 640, true); else QFM_GU_M1(2560, 640, false);
     } else {
         set_error(-2, "i8_gateup_m1: unsupported shape"); return -2;
     }
+#undef QFM_GU_M1
     return check_launch("i8_gateup_m1");
 }
 

@@ -30,9 +30,11 @@ struct ShPtrs { const int8_t *qg, *qu, *qd; const float *sg, *su, *sd; };
 
 // router: W_f32 [E][H] (+ row g [H] written at column E when g != nullptr)
 // and, when sh != nullptr, the shared-expert hidden hsh[m * ld_hsh + r], in one launch.
+// With x16 != nullptr (M = 1) the launch also writes x as scaled fp16 (H / 8
+// 16-byte words) followed by a float2 (sum of the scaled values, 2^-k).
 int launch_router_shared(const float *W, const float *bias, const float *g, const ShPtrs *sh,
                          const uint16_t *x, int M, float *logits, int ld_logits, float *hsh, int ld_hsh,
-                         hipStream_t s);
+                         hipStream_t s, void *x16 = nullptr);
 int launch_router_bf16w(const uint16_t *W, const float *x, float *logits, hipStream_t s);
 int launch_topk(const float *logits, int ld_logits, int M, int *sel, float *wts, hipStream_t s);
 
@@ -41,8 +43,11 @@ int launch_topk(const float *logits, int ld_logits, int M, int *sel, float *wts,
 // runs the top-K of its row of logits) and block 0 writes sel/wts; otherwise
 // sel is an input. x is bf16 (xb) or fp32 (xf). With sh != nullptr the shared
 // expert's hidden vector is computed too, into hidden row nexp.
+// With x16 != nullptr (launch_router_shared's fp16 row) x is read from there
+// and the codes are widened to fp16 (dot16_i8h); xb/xf are then unused.
 int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *xf, const float *logits,
-                        int *sel, float *wts, int nexp, float *hidden, hipStream_t s, const ShPtrs *sh = nullptr);
+                        int *sel, float *wts, int nexp, float *hidden, hipStream_t s, const ShPtrs *sh = nullptr,
+                        const void *x16 = nullptr);
 // y = sum_k wts[k] * down_k(hidden[k]) (+ gamma * shared_down(hidden[nexp]) when
 // sh != nullptr: the shared expert's hidden vector follows the routed ones),
 // gamma = sigmoid(*gdot) when gdot != nullptr, 1 otherwise. Writes y32 and/or ybf.

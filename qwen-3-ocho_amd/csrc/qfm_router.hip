@@ -47,14 +47,20 @@ __device__ __forceinline__ float canon_reduce_row(const float4 (&w)[NJ], const f
 // MR > 1 the shared-expert rows are also split over x rows: block (pair, mg)
 // computes rows [2 mg, 2 mg + 2) of x for its row pair, MG = ceil(M / 2) blocks
 // per pair, laid out so that one pair's blocks share an XCD (and its L2).
+// With x16 != nullptr one more block (the first) writes x row 0 as scaled
+// fp16 with its (sum, 2^-k) for the M = 1 gate/up kernel.
 template <int NJ, int I, int MR>
 __global__ void __launch_bounds__(64)
 k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, const float *__restrict__ g,
                 ShPtrs sh, const uint16_t *__restrict__ x, int M, int E, float *__restrict__ logits, int ld,
-                float *__restrict__ hsh, int ldh) {
+                float *__restrict__ hsh, int ldh, uint4 *__restrict__ x16, float2 *__restrict__ x16i) {
     constexpr int H = NJ * 256;
     const int lane = threadIdx.x;
-    const int b = blockIdx.x;
+    if (x16 && blockIdx.x == 0) {                   // the first block: x row 0 as scaled fp16
+        wave_row_to_f16<H>(x, x16, x16i, lane);
+        return;
+    }
+    const int b = (int)blockIdx.x - (x16 ? 1 : 0);
     const int ng = g ? 1 : 0;
     if (b < E + ng) {
         const bool is_g = b == E;
@@ -185,22 +191,26 @@ k_topk(const float *__restrict__ logits, int ld, int M, int K, int renorm,
 }
 
 int launch_router_shared(const float *W, const float *bias, const float *g, const ShPtrs *sh,
-                         const uint16_t *x, int M, float *logits, int ld, float *hsh, int ldh, hipStream_t s) {
+                         const uint16_t *x, int M, float *logits, int ld, float *hsh, int ldh, hipStream_t s,
+                         void *x16) {
     const int E = g_cfg.E, I = g_cfg.I;
     if (sh && !hsh) { set_error(-1, "router: shared rows need an output"); return -1; }
+    if (x16 && M != 1) { set_error(-1, "router: the fp16 x row is for M = 1"); return -1; }
     ShPtrs sp{};
     if (sh) sp = *sh;
-    const int nblk = E + (g ? 1 : 0) + (sh ? (I / 2) * (M == 1 ? 1 : (M + 1) / 2) : 0);
+    uint4 *xh = static_cast<uint4 *>(x16);
+    float2 *xi = xh ? reinterpret_cast<float2 *>(xh + g_cfg.H / 8) : nullptr;
+    const int nblk = E + (g ? 1 : 0) + (sh ? (I / 2) * (M == 1 ? 1 : (M + 1) / 2) : 0) + (xh ? 1 : 0);
     if (shape_2048()) {
         if (M == 1)
-            hipLaunchKernelGGL((k_router_shared<8, 512, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
+            hipLaunchKernelGGL((k_router_shared<8, 512, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
         else
-            hipLaunchKernelGGL((k_router_shared<8, 512, 4>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
+            hipLaunchKernelGGL((k_router_shared<8, 512, 4>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
     } else if (shape_2560()) {
         if (M == 1)
-            hipLaunchKernelGGL((k_router_shared<10, 640, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
+            hipLaunchKernelGGL((k_router_shared<10, 640, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
         else
-            hipLaunchKernelGGL((k_router_shared<10, 640, 4>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh);
+            hipLaunchKernelGGL((k_router_shared<10, 640, 4>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
     } else {
         set_error(-2, "router: unsupported shape"); return -2;
     }

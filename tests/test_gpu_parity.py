@@ -191,7 +191,11 @@ def test_i8_m1_reference_entry_points(lib, H, I):
         href, ye = orc.i8_expert(x.astype(np.float64), *_oracle_expert(seed, layer, int(e), H, I))
         assert _rel(h[k], href) < 1e-5, k
         yref += float(wts[k]) * ye
-    assert _rel(y, yref) < 1e-5
+    # The down kernel stages the hidden vectors in LDS as fp16 (11 significant
+    # bits, a power-of-two scale per 16 values): |dy| / max|y| ~ 1e-3, against the
+    # reference's int8 re-quantization of the hidden vector (~4e-3) and the
+    # north-star bound of 1e-2. The gate/up with fp32 x above stays fp32-exact.
+    assert _rel(y, yref) < 2e-3
     lib.qfm_arena_free(C.byref(arena))
     st.destroy()
     _cfg(lib)
