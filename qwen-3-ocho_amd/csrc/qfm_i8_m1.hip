@@ -11,9 +11,13 @@
 // st = 0..H/512-1, so a half-wave reads 512 contiguous bytes per step and
 // all H/256 weight loads of a row pair (gate + up) are in flight before the
 // first multiply. The activation slice a lane needs is the same for every
-// row, so it is held in registers as fp32 (no LDS). Each code q is used in
-// offset-binary form q + 128 (one v_cvt_f32_ubyte per code) and the
-// accumulator starts at -128 * sum(x_slice). When the launch carries the
+// row, so it is held in registers (no LDS). In the fused forward x arrives as
+// fp16 scaled per row (written by the router launch) and each code is widened
+// to fp16 (dot16_i8h: 1024 + (q ^ 0x80), one v_perm per two codes), the
+// 1152 * sum(x16) offset removed from the row total; with fp32 or bf16 x (the
+// reference-named entry) each code is used in offset-binary form q + 128 (one
+// v_cvt_f32_ubyte per code) and the accumulator starts at -128 * sum(x_slice).
+// When the launch carries the
 // router logits, every wave runs the top-K selection itself (the 2 KiB row of
 // logits is L2-resident), which removes a dependent launch from the decode
 // chain; block (0, 0) publishes sel/wts for the down kernel. With a shared
@@ -26,8 +30,7 @@
 // the row is issued (the 16-byte chunks of all K + 1 expert rows), and while
 // those are in flight the hidden vectors are staged in LDS as fp16 chunks
 // scaled by powers of two (chunk16_to_f16; the codes are widened to fp16,
-// dot16_i8h). Each
-// lane accumulates sum_j w_j * sd_j[c] * <Wd_j slice, h_j slice> across all
+// dot16_i8h). Each lane accumulates sum_j w_j * sd_j[c] * <Wd_j slice, h_j slice> across all
 // jobs and the group reduces once, so every output row has one writer and a
 // fixed summation order (deterministic; y is seeded, not accumulated).
 #include "qfm_dev.h"
@@ -132,9 +135,6 @@ k_i8_gateup_m1(const int8_t *__restrict__ Qg, const int8_t *__restrict__ Qu,
 }
 
 constexpr int kMaxJobs = 17;   // top_k <= 16 plus the shared expert
-#ifndef QFM_DOWN_M1_F16
-#define QFM_DOWN_M1_F16 1
-#endif
 
 // NJ jobs (routed experts, then the shared one when HAS_SH) are a template
 // parameter so that every register array is indexed at compile time: no
@@ -151,13 +151,8 @@ k_i8_down_m1(const int8_t *__restrict__ Qd, const float *__restrict__ Sd,
     constexpr int NEXP = HAS_SH ? NJ - 1 : NJ;
     constexpr int NCH = NJ * I / 16;                  // 16-value hidden chunks
     constexpr int CPT = (NCH + 255) / 256;            // chunks per thread
-#if QFM_DOWN_M1_F16
     __shared__ uint4 s_h16[NCH * 2];                  // the hidden rows as scaled fp16 (chunk16_to_f16)
     __shared__ float2 s_hci[NCH];
-#else
-    __shared__ __align__(16) float s_h[NCH * 16];     // the hidden rows (fp32)
-    __shared__ float s_cs[NCH];                       // -128 * each chunk's sum (offset-binary correction)
-#endif
     const int l = threadIdx.x % LPR;
     const int c = blockIdx.x * RPB + threadIdx.x / LPR;
     // batch 1: routing, router weights, shared gate, this thread's hidden chunks (to registers)
@@ -195,21 +190,10 @@ k_i8_down_m1(const int8_t *__restrict__ Qd, const float *__restrict__ Sd,
     for (int q = 0; q < CPT; q++) {
         const int ch = (int)threadIdx.x + q * 256;
         if (ch < NCH) {
-#if QFM_DOWN_M1_F16
             uint4 ha, hb;
             s_hci[ch] = chunk16_to_f16(hv[q], ha, hb);
             s_h16[2 * ch] = ha;
             s_h16[2 * ch + 1] = hb;
-#else
-            float t = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; i++) t += hv[q][i];
-            s_cs[ch] = -128.0f * t;
-#pragma unroll
-            for (int v = 0; v < 4; v++)
-                reinterpret_cast<float4 *>(s_h)[ch * 4 + v] =
-                    make_float4(hv[q][4 * v], hv[q][4 * v + 1], hv[q][4 * v + 2], hv[q][4 * v + 3]);
-#endif
         }
     }
     __syncthreads();
@@ -236,13 +220,8 @@ k_i8_down_m1(const int8_t *__restrict__ Qd, const float *__restrict__ Sd,
 #pragma unroll
                 for (int st = 0; st < NST; st++) {
                     const int ch = j * (I / 16) + st * LPR + l;
-#if QFM_DOWN_M1_F16
                     const float2 ci = s_hci[ch];
                     d = fmaf(dot16_i8h(w[u][st], s_h16[2 * ch], s_h16[2 * ch + 1], ci.x), ci.y, d);
-#else
-                    d += s_cs[ch];
-                    d = dot16_u8(w[u][st], s_h + ch * 16, d);
-#endif
                 }
                 acc = fmaf(wsc[j], d, acc);
             }
