@@ -35,9 +35,13 @@ HBM_PEAK_GBS = 8000.0
 SEC_NAMES = ["k_router_shared (router logits + shared gate logit)",
              "k_i8_gateup_m1 (top-K + routed and shared gate/up)",
              "k_i8_down_m1 (routed + shared down, combine)"]
+# router: W fp32, gate vector, x in, logits out, x out as scaled fp16 + (sum, 2^-k);
+# gate/up: 11 experts' gate/up rows + row scales, the fp16 x row + its 8 bytes,
+# logits, hidden out, sel/wts out; down: 11 experts' down rows + scales, hidden,
+# y out, sel/wts, gate logit
 SEC_BYTES = [
-    E * H * 4 + H * 4 + H * 2 + (E + 1) * 4,
-    (K + 1) * (2 * I * H + 2 * I * 4) + H * 2 + E * 4 + (K + 1) * I * 4 + 2 * K * 4,
+    E * H * 4 + H * 4 + H * 2 + (E + 1) * 4 + H * 2 + 8,
+    (K + 1) * (2 * I * H + 2 * I * 4) + H * 2 + 8 + E * 4 + (K + 1) * I * 4 + 2 * K * 4,
     (K + 1) * (H * I + H * 4) + (K + 1) * I * 4 + H * 2 + 2 * K * 4 + 4,
 ]
 
