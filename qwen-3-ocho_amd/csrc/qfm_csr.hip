@@ -206,14 +206,14 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
         wg[st] = ld_nt16(Wg + roff + (st * LPR + l) * 16);
         wu[st] = ld_nt16(Wu + roff + (st * LPR + l) * 16);
     }
-    uint32_t bg[NST], bu[NST];
+    uint32_t bs[2 * NST];                         // NVFP4 block-scale pairs: gate chunks, then up chunks
     float rsg, rsu;
     if constexpr (!I8) {
         const size_t boff = ((size_t)e * I + row) * (H / 16);
 #pragma unroll
         for (int st = 0; st < NST; st++) {
-            bg[st] = *reinterpret_cast<const uint16_t *>(Bg + boff + (st * LPR + l) * 2);
-            bu[st] = *reinterpret_cast<const uint16_t *>(Bu + boff + (st * LPR + l) * 2);
+            bs[st] = *reinterpret_cast<const uint16_t *>(Bg + boff + (st * LPR + l) * 2);
+            bs[NST + st] = *reinterpret_cast<const uint16_t *>(Bu + boff + (st * LPR + l) * 2);
         }
         rsg = s2g[e]; rsu = s2u[e];
     } else {
@@ -241,6 +241,7 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
         }
         __builtin_amdgcn_s_waitcnt(0);          // this wave's LDS loads (and its weights) have landed
         __syncthreads();
+
         for (int j = 0; j < ng; j++) {
             float ag = 0.0f, au = 0.0f;
 #pragma unroll
@@ -258,8 +259,8 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
                         const uint4 a = s_x[j * XQ + 4 * ch + q];
                         xw[4 * q] = a.x; xw[4 * q + 1] = a.y; xw[4 * q + 2] = a.z; xw[4 * q + 3] = a.w;
                     }
-                    ag += f4_chunk_bx(wg[st], bg[st], xw);
-                    au += f4_chunk_bx(wu[st], bu[st], xw);
+                    ag += f4_chunk_bx(wg[st], bs[st], xw);        // (the hardware scale convert
+                    au += f4_chunk_bx(wu[st], bs[NST + st], xw);  // measured slower here: 24.9 vs 22.5 us)
                 }
             }
             ag = group_sum<LPR>(ag);
@@ -272,7 +273,7 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
 // <down row, staged hidden row j> over this lane's NST chunks: INT8 (16 codes
 // per chunk, dot16_i8h) or NVFP4 (32 codes per chunk, f4_chunk_h)
 template <class F, int I, int LPR, int NST>
-__device__ __forceinline__ float down_dot(const uint4 (&w)[NST], const uint32_t (&bs)[NST], const uint4 *s_h16,
+__device__ __forceinline__ float down_dot(const uint4 (&w)[NST], const f32x2_t (&bs)[NST], const uint4 *s_h16,
                                           const float2 *s_hci, int j, int l) {
     float d = 0.0f;
 #pragma unroll
@@ -305,7 +306,7 @@ __device__ __forceinline__ void csr_down_shared(const ShPtrs &sh, const float *_
     static_assert(RPG >= 1 && RPG * GROUPS == ROWS, "shared rows must tile the block");
     const int l = threadIdx.x % LPR, grp = threadIdx.x / LPR;
     uint4 w[RPG][NST];
-    uint32_t bs[NST] = {};
+    f32x2_t bs[NST] = {};
     float rs[RPG];
 #pragma unroll
     for (int q = 0; q < RPG; q++) {
@@ -379,7 +380,8 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
     // weights for this thread's rows first (ROWS/GROUPS rows per group)
     constexpr int RPG = ROWS / GROUPS;
     uint4 w[RPG][NST];
-    uint32_t bs[RPG][NST];
+    uint32_t braw[RPG * NST];                    // NVFP4 block-scale pairs
+    f32x2_t bs[RPG][NST];
     float rs[RPG];
 #pragma unroll
     for (int q = 0; q < RPG; q++) {
@@ -390,16 +392,24 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
         if constexpr (F::VPB == 2) {
             const size_t boff = ((size_t)e * H + c) * (I / 16);
 #pragma unroll
-            for (int st = 0; st < NST; st++) bs[q][st] = *reinterpret_cast<const uint16_t *>(Bd + boff + (st * LPR + l) * 2);
+            for (int st = 0; st < NST; st++) braw[q * NST + st] = *reinterpret_cast<const uint16_t *>(Bd + boff + (st * LPR + l) * 2);
             rs[q] = s2d[e];
         } else {
 #pragma unroll
-            for (int st = 0; st < NST; st++) bs[q][st] = 0u;
+            for (int st = 0; st < NST; st++) braw[q * NST + st] = 0u;
             rs[q] = Sd[(size_t)e * H + c];
         }
     }
     stage_h16<I>(hpair + (size_t)p0 * I, np, s_h16, s_hci);
     __syncthreads();
+    if constexpr (F::VPB == 2) {
+        f32x2_t dec[RPG * NST];
+        e4m3_pairs(braw, dec);
+#pragma unroll
+        for (int q = 0; q < RPG; q++)
+#pragma unroll
+            for (int st = 0; st < NST; st++) bs[q][st] = dec[q * NST + st];
+    }
     for (int j = 0; j < np; j++) {
         const int pr = pair[p0 + j];
         const float wp = g_wts[pr];

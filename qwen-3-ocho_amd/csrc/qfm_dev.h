@@ -456,6 +456,29 @@ __device__ __forceinline__ float e4m3_scale(uint32_t b) {
     const uint32_t bits = b == 0x7Fu ? 0x7F800000u : ((e + 120u) << 23) | (m << 20);
     return e ? __uint_as_float(bits) : (float)m * 0x1p-9f;
 }
+// Both e4m3 block scales of a 16-bit pair (byte 0 low). The gfx950 OCP E4M3
+// convert (v_cvt_pk_f32_fp8, one op for the pair) gives the same fp32 bits as
+// e4m3_scale for bytes 0x00..0x7E (checked on the box over all 256 bytes);
+// bytes >= 0x7F differ (0x7F: +inf here, NaN there; bit 7 set: large
+// unsigned scales here, negative values there) and take e4m3_scale.
+// e4m3_pairs decodes NS pairs with the convert when no lane of the wave holds
+// such a byte (a wave-uniform choice), otherwise with e4m3_scale.
+__device__ __forceinline__ bool e4m3_pair_hw_ok(uint32_t s2b) {
+    return ((s2b | (s2b + 0x0101u)) & 0x8080u) == 0;   // both bytes < 0x7F (a carry out of byte 0 means byte 0 >= 0xFF)
+}
+template <int NS>
+__device__ __forceinline__ void e4m3_pairs(const uint32_t (&s2b)[NS], f32x2_t (&out)[NS]) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < NS; i++) ok = ok && e4m3_pair_hw_ok(s2b[i]);
+    if (__builtin_amdgcn_ballot_w64(!ok) == 0) {
+#pragma unroll
+        for (int i = 0; i < NS; i++) out[i] = __builtin_amdgcn_cvt_pk_f32_fp8(s2b[i], false);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NS; i++) out[i] = f32x2_t{e4m3_scale(s2b[i] & 0xFFu), e4m3_scale((s2b[i] >> 8) & 0xFFu)};
+    }
+}
 __device__ __forceinline__ float f4_chunk(uint4 w, uint32_t s2b, const float *x) {
     const float g0 = f4_group16(w.x, w.y, x);
     const float g1 = f4_group16(w.z, w.w, x + 16);
@@ -490,6 +513,12 @@ __device__ __forceinline__ float f4_chunk_bx(uint4 w, uint32_t s2b, const uint32
     const float g1 = f4_group16_bx(w.z, w.w, xw + 8);
     return fmaf(e4m3_scale(s2b & 0xFFu), g0, e4m3_scale((s2b >> 8) & 0xFFu) * g1);
 }
+// with the two block scales already decoded (sc.x: values 0..15, sc.y: 16..31)
+__device__ __forceinline__ float f4_chunk_bx(uint4 w, f32x2_t sc, const uint32_t *xw) {
+    const float g0 = f4_group16_bx(w.x, w.y, xw);
+    const float g1 = f4_group16_bx(w.z, w.w, xw + 8);
+    return fmaf(sc.x, g0, sc.y * g1);
+}
 
 // NVFP4 chunk against scaled fp16 activations: 32 e2m1 codes (w), two e4m3
 // block scales (s2b), the 32 activations as 16 fp16 pairs (xw) in two
@@ -508,10 +537,10 @@ __device__ __forceinline__ float f4_group16_h(uint32_t lo, uint32_t hi, const ui
     }
     return a;
 }
-__device__ __forceinline__ float f4_chunk_h(uint4 w, uint32_t s2b, const uint32_t *xw, float isc0, float isc1) {
+__device__ __forceinline__ float f4_chunk_h(uint4 w, f32x2_t sc, const uint32_t *xw, float isc0, float isc1) {
     const float g0 = f4_group16_h(w.x, w.y, xw);
     const float g1 = f4_group16_h(w.z, w.w, xw + 8);
-    return fmaf(e4m3_scale(s2b & 0xFFu) * isc0, g0, (e4m3_scale((s2b >> 8) & 0xFFu) * isc1) * g1);
+    return fmaf(sc.x * isc0, g0, (sc.y * isc1) * g1);
 }
 
 // ---- Philox-4x32-10 (Salmon et al. 2011) ------------------------------------
