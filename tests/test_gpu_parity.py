@@ -201,6 +201,70 @@ def test_i8_m1_reference_entry_points(lib, H, I):
     _cfg(lib)
 
 
+# ------------------------------------------------------------------ NVFP4 scale bytes >= 0x80
+@pytest.mark.gpu
+def test_nvfp4_fork_rows_high_scale_bytes(lib):
+    """NVFP4 fork rows whose selected experts carry down-projection block-scale
+    bytes >= 0x80: the reference decodes them as large unsigned scales
+    (e = byte >> 3, ocho/amd_server/qf_nvfp4_wave64.hip:68-73) where the
+    hardware E4M3 convert reads bit 7 as a sign, so the down kernel must take
+    the integer decode for those tiles. The bytes are planted in device memory
+    after a first forward (routing does not depend on expert weights); the
+    result is checked against the oracle expert on the arrays read back from
+    the device, with the shared expert left out."""
+    _say("nvfp4 high scale bytes")
+    M, seed, layer, H, I = 2, 3, 11, 2048, 512
+    st = qfm.Stream()
+    L = qfm.SynthLayer(qfm.QFM_FMT_NVFP4, seed, layer, stream=st)
+    lay = qfm.QfmLayer.from_buffer_copy(L.s.layer)
+    lay.sh_gate, lay.sh_up, lay.sh_down, lay.sh_gate_inp = qfm.Qf8I8Mat(), qfm.Qf8I8Mat(), qfm.Qf8I8Mat(), None
+    dx, dy = qfm.DevBuf(M * H * 2), qfm.DevBuf(M * H * 2)
+    qfm.check(lib.qfm_gen_input_rows(dx.ptr, M, seed, 40, 0, st.h), "x")
+    wsb = lib.qfm_workspace_bytes(M)
+    ws = qfm.DevBuf(wsb)
+    qfm.check(lib.qfm_moe_forward(C.byref(lay), dx.ptr, M, dy.ptr, ws.ptr, wsb, st.h), "forward")
+    st.sync()
+    view = qfm.QfmWsView()
+    lib.qfm_workspace_view(ws.ptr, M, C.byref(view))
+    sel = qfm.d2h(view.sel, np.int32, (M, 10))
+    wts = qfm.d2h(view.wts, np.float32, (M, 10))
+    a = L.s.arena
+    GS = H * I // 16                                  # down scale bytes per expert
+    planted = 0
+    for e in sorted(set(sel.ravel().tolist())):
+        sd = qfm.d2h(a.s_down + e * GS, np.uint8, GS).copy()
+        idx = np.arange(e % 7, GS, 7)
+        sd[idx] = (0x80 + (idx % 8)).astype(np.uint8)   # scales 2^9 * (1 + m/8)
+        planted += idx.size
+        qfm.check(lib.qfm_memcpy_h2d(a.s_down + e * GS, sd.ctypes.data, sd.nbytes), "plant")
+    assert planted > 0
+    qfm.check(lib.qfm_moe_forward(C.byref(lay), dx.ptr, M, dy.ptr, ws.ptr, wsb, st.h), "forward")
+    st.sync()
+    qfm.status_check("high scale bytes")
+    y = orc.bf16_to_f32(dy.download(np.uint16, (M, H)))
+    x = orc.bf16_to_f32(dx.download(np.uint16, (M, H)))
+    s2 = [qfm.d2h(p, np.float32, 512) for p in (a.s2g_dev, a.s2u_dev, a.s2d_dev)]
+    GW, DW, GSg = I * H // 2, H * I // 2, I * H // 16
+    for t in range(M):
+        yref = np.zeros(H)
+        for k in range(10):
+            e = int(sel[t, k])
+            Fg = qfm.d2h(a.w_gate + e * GW, np.uint8, (I, H // 2))
+            Fu = qfm.d2h(a.w_up + e * GW, np.uint8, (I, H // 2))
+            Fd = qfm.d2h(a.w_down + e * DW, np.uint8, (H, I // 2))
+            Sg = qfm.d2h(a.s_gate + e * GSg, np.uint8, (I, H // 16))
+            Su = qfm.d2h(a.s_up + e * GSg, np.uint8, (I, H // 16))
+            Sd = qfm.d2h(a.s_down + e * GS, np.uint8, (H, I // 16))
+            _, ye = orc.nvfp4_expert(x[t].astype(np.float64), Fg, Sg, float(s2[0][e]), Fu, Su, float(s2[1][e]),
+                                     Fd, Sd, float(s2[2][e]), H, I)
+            yref += float(wts[t, k]) * ye
+        rel = _rel(y[t], yref)
+        _say("  row", t, "max rel err", rel)
+        assert rel <= 1e-2, (t, rel)
+    L.destroy()
+    st.destroy()
+
+
 # ------------------------------------------------------------------ fused layer
 def _run_layer(lib, M, seed, layer, x_layer, fmt=qfm.QFM_FMT_INT8, bias=False):
     st = qfm.Stream()
