@@ -158,7 +158,7 @@ float orc_bf16_to_f32(uint16_t h) {
 /* Router logits in the canonical fp32 order (the order the HIP router
    kernels execute): 64 lane partials, partial l = sequential fma over
    k = j*256 + 4l + c for j = 0..H/256-1, c = 0..3; then a butterfly
-   p[l] = p[l] + p[l ^ m] for m = 32, 16, 8, 4, 2, 1. H % 256 == 0.
+   p[l] = p[l] + p[l ^ m] for m = 1, 2, 4, 8, 16, 32. H % 256 == 0.
    Bias (prefill skew) is added last with one rounding. The reference's
    router is a plain fp32 dot (qf_router_wave64.hip:42-51); the order is
    fixed here so that GPU and CPU logits are bit-identical. */
@@ -173,7 +173,7 @@ static float canon_dot(const float *w, const float *xf, int H) {
             }
         p[l] = a;
     }
-    for (int s = 32; s >= 1; s >>= 1) {
+    for (int s = 1; s <= 32; s <<= 1) {
         for (int l = 0; l < 64; l++) q[l] = p[l] + p[l ^ s];
         memcpy(p, q, sizeof p);
     }

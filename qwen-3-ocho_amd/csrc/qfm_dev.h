@@ -184,6 +184,22 @@ __device__ float group_sum(float v) {
     return v;
 }
 
+// The canonical router reduction of 64 lane partials: p[l] + p[l ^ m] for
+// m = 1, 2, 4, 8, 16, 32, each step one fp32 rounding (the oracle's
+// canon_dot). After the xor-1 and xor-2 steps every quad holds one value, so
+// the half-row mirror partner (l ^ 7) carries the value of l ^ 4; after the
+// xor-4 step every 8-lane group does, so the row mirror (l ^ 15) carries that
+// of l ^ 8: four DPP adds reproduce the first four steps exactly, a ds_swizzle
+// (l ^ 16) and one bpermute (l ^ 32) the last two. Every lane ends with the sum.
+__device__ __forceinline__ float canon_butterfly(float a) {
+    a = __fadd_rn(a, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), 0xB1, 0xF, 0xF, false)));
+    a = __fadd_rn(a, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), 0x4E, 0xF, 0xF, false)));
+    a = __fadd_rn(a, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), 0x141, 0xF, 0xF, false)));
+    a = __fadd_rn(a, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), 0x140, 0xF, 0xF, false)));
+    a = __fadd_rn(a, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, a), 0x401F)));
+    return __fadd_rn(a, __shfl_xor(a, 32, WAVE));
+}
+
 // Max over aligned groups of G lanes (same steps as group_sum).
 template <int G>
 __device__ float group_max(float v) {

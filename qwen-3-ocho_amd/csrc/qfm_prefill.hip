@@ -455,9 +455,7 @@ __device__ __forceinline__ float canon_dot_wave(const float *__restrict__ w, con
         a = __fmaf_rn(wv.z, bf16_lo(p.y), a);
         a = __fmaf_rn(wv.w, bf16_hi(p.y), a);
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) a = __fadd_rn(a, __shfl_xor(a, m, WAVE));
-    return a;
+    return canon_butterfly(a);
 }
 
 // The same canonical dot for CB router rows at once (x held in registers):
@@ -485,9 +483,7 @@ __device__ __forceinline__ void canon_dot_wave_batch(const float *__restrict__ W
         out[c] = a;
     }
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1)
-#pragma unroll
-        for (int c = 0; c < CB; c++) out[c] = __fadd_rn(out[c], __shfl_xor(out[c], m, WAVE));
+    for (int c = 0; c < CB; c++) out[c] = canon_butterfly(out[c]);
 }
 
 // Error-bound constant per unit of ||w_e|| ||x_t||: bf16 rounding of W

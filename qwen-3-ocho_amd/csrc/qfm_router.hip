@@ -7,7 +7,8 @@
 // restatement reproduces them bit for bit: lane l of a wave owns elements
 // k = j*256 + 4l + c (j = 0..H/256-1, c = 0..3) of the row and accumulates
 // them with a sequential fmaf chain in (j, c) order; the 64 lane partials
-// are then combined by an xor butterfly p[l] = p[l] + p[l ^ m], m = 32..1.
+// are then combined by an xor butterfly p[l] = p[l] + p[l ^ m], m = 1..32
+// (canon_butterfly: DPP for the first four steps).
 // Each lane's weights arrive as H/256 coalesced 16-byte loads (1 KiB per
 // wave per load), so a router row is one wave and E rows are E waves.
 //
@@ -31,9 +32,7 @@ __device__ __forceinline__ float canon_reduce_row(const float4 (&w)[NJ], const f
         a = __fmaf_rn(w[j].z, x[j][2], a);
         a = __fmaf_rn(w[j].w, x[j][3], a);
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) a = __fadd_rn(a, __shfl_xor(a, m, WAVE));
-    return a;
+    return canon_butterfly(a);
 }
 
 // One wave per block. Blocks [0, E): router rows of W fp32 [E][H]; block E
@@ -90,9 +89,7 @@ k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, con
                 }
             }
 #pragma unroll
-            for (int m = 32; m >= 1; m >>= 1)
-#pragma unroll
-                for (int r = 0; r < MR; r++) a[r] = __fadd_rn(a[r], __shfl_xor(a[r], m, WAVE));
+            for (int r = 0; r < MR; r++) a[r] = canon_butterfly(a[r]);
 #pragma unroll
             for (int r = 0; r < MR; r++) {
                 float v = a[r];

@@ -71,7 +71,7 @@ def test_router_canonical_order_is_the_documented_one():
                 a = rnd(Fraction(float(w[k])) * Fraction(float(xf[k])) + Fraction(float(a)))
         p.append(a)
     p = np.array(p, np.float32)
-    for m in (32, 16, 8, 4, 2, 1):
+    for m in (1, 2, 4, 8, 16, 32):
         p = (p + p[np.arange(64) ^ m]).astype(np.float32)
     lg = orc.router_logits(w[None, :], x[None, :])
     assert lg[0, 0] == p[0]
