@@ -753,6 +753,8 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     constexpr bool F4 = MODE == kRoutedF4;
     __shared__ const char *sptr[F4 ? TBN : 1];
     __shared__ float rsum[BM], rscl[H16 ? BM : 1], hpart[WN][BM];
+    __shared__ int rslot[GATEUP ? 1 : BM];          // down: the owned partial slot of each row
+    __shared__ float rwt[GATEUP ? 1 : BM];          // down: the routing weight of each row
     int mi, ni;
     xcd_tile(blockIdx.x, ntiles, mi, ni);
     if (mi * ntiles >= n_items[which]) return;
@@ -790,8 +792,11 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
             if constexpr (H16) rscl[r] = r < rows ? xisc[arow[r]] : 0.0f;
         } else {
             arow[r] = r < rows ? pbase + r : -1;
-            if (r < rows)
+            if (r < rows) {
                 for (int q = 0; q < nt_gu; q++) rs += hsum[(size_t)(pbase + r) * nt_gu + q];
+                rslot[r] = p_slot[pbase + r];
+                rwt[r] = p_wt[pbase + r];
+            }
         }
         rsum[r] = rs;
     }
@@ -822,29 +827,39 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
         ExpertEngine::run(A, Kdim, arow, bptr, Kdim, lds, acc);
     }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave / WN, wn = wave % WN;
+    // epilogues: the column scales are loaded once per lane and the per-row
+    // values come from the LDS tables filled above (no per-element global loads)
     if (GATEUP) {
+        const int o0 = nt * 128 + wn * 32 + (lane & 15);
+        float sgv[2], suv[2];
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++) {
+            sgv[nb] = f4 ? s2a : Sb[o0 + nb * 16];
+            suv[nb] = f4 ? s2b : Sb2[o0 + nb * 16];
+        }
         float hsacc[MWv][4] = {};
 #pragma unroll
         for (int mb = 0; mb < MWv; mb++)
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int r = wm * RPW + mb * 16 + (lane >> 4) * 4 + i;
-                    const int o = nt * 128 + wn * 32 + nb * 16 + (lane & 15);
+            for (int i = 0; i < 4; i++) {
+                const int r = wm * RPW + mb * 16 + (lane >> 4) * 4 + i;
+                if (r < rows) {
+                    // offset-binary correction: bf16 rows 128 * sum(x), fp16 rows 1152 * sum(x16)
+                    const float cr = f4 ? 0.0f : (H16 ? 1152.0f : 128.0f) * rsum[r];
+                    const float ks = H16 ? rscl[r] : 1.0f;
+                    uint16_t *dst = hid + (size_t)(pbase + r) * Nrows + o0;
                     float hs = 0.0f;
-                    if (r < rows) {
-                        // offset-binary correction: bf16 rows 128 * sum(x), fp16 rows 1152 * sum(x16)
-                        const float cr = f4 ? 0.0f : (H16 ? 1152.0f : 128.0f) * rsum[r];
-                        const float ks = H16 ? rscl[r] : 1.0f;
-                        const float gv = (acc[mb][nb][i] - cr) * ks * (f4 ? s2a : Sb[o]);
-                        const float uv = (acc[mb][nb + 2][i] - cr) * ks * (f4 ? s2b : Sb2[o]);
+#pragma unroll
+                    for (int nb = 0; nb < 2; nb++) {
+                        const float gv = (acc[mb][nb][i] - cr) * ks * sgv[nb];
+                        const float uv = (acc[mb][nb + 2][i] - cr) * ks * suv[nb];
                         const uint16_t hb = f32_to_bf16(silu(gv) * uv);
-                        hid[(size_t)(pbase + r) * Nrows + o] = hb;
-                        hs = bf16_to_f32(hb);
+                        dst[nb * 16] = hb;
+                        hs += bf16_to_f32(hb);
                     }
-                    hsacc[mb][i] += hs;
+                    hsacc[mb][i] = hs;
                 }
+            }
         // per-row sum of this tile's 128 bf16 hidden values: 16 columns in the
         // lanes of a row group, two n-blocks here, the rest in the other WN - 1
         // waves of the row; summed in wave order (deterministic)
@@ -865,20 +880,22 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
             hsum[(size_t)(pbase + threadIdx.x) * nt_gu + nt] = v;
         }
     } else {
+        const int c0 = nt * TBN + wn * 64 + (lane & 15);
+        float sbv[4];
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) sbv[nb] = f4 ? s2a : Sb[c0 + nb * 16];
 #pragma unroll
         for (int mb = 0; mb < MWv; mb++)
 #pragma unroll
-            for (int nb = 0; nb < 4; nb++)
+            for (int i = 0; i < 4; i++) {
+                const int r = wm * RPW + mb * 16 + (lane >> 4) * 4 + i;
+                if (r < rows) {
+                    const float cr = f4 ? 0.0f : 128.0f * rsum[r], w = rwt[r];
+                    float *dst = part + (size_t)rslot[r] * Hout + c0;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int r = wm * RPW + mb * 16 + (lane >> 4) * 4 + i;
-                    const int c = nt * TBN + wn * 64 + nb * 16 + (lane & 15);
-                    if (r < rows) {
-                        const int p = pbase + r;
-                        const float v = f4 ? acc[mb][nb][i] * s2a : (acc[mb][nb][i] - 128.0f * rsum[r]) * Sb[c];
-                        part[(size_t)p_slot[p] * Hout + c] = p_wt[p] * v;
-                    }
+                    for (int nb = 0; nb < 4; nb++) dst[nb * 16] = w * ((acc[mb][nb][i] - cr) * sbv[nb]);
                 }
+            }
     }
 }
 
@@ -893,7 +910,10 @@ k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__re
     float4 v[kMaxS];
 #pragma unroll
     for (int k = 0; k < kMaxS; k++)
-        if (k < S) v[k] = *reinterpret_cast<const float4 *>(part + (t * S + k) * H + c);
+        if (k < S) {
+            const f32x4_t q = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t *>(part + (t * S + k) * H + c));
+            v[k] = make_float4(q.x, q.y, q.z, q.w);
+        }
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int k = 0; k < kMaxS; k++)
