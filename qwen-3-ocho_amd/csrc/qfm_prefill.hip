@@ -225,7 +225,13 @@ __global__ void __launch_bounds__(256) k_pf_router_prep(const float *__restrict_
 // loads of a step together (explicit scheduling-group patterns measured
 // slower than the compiler's own order).
 constexpr int BK2 = 64;
-constexpr int LDS2 = BK2 + 8;                  // bf16 elements per LDS row (144 bytes)
+// LDS rows of BK2 16-bit elements (128 bytes, eight 16-byte chunks), chunk q
+// of row r stored at chunk position q ^ (r & 7). The MFMA fragment reads (16
+// rows at one chunk per 16 lanes) and the staging writes are then free of
+// bank conflicts; rows padded to 144 bytes cost four conflict cycles per
+// fragment read (measured with SQ_LDS_BANK_CONFLICT on ds_read_b128).
+constexpr int LDS2 = BK2;
+__device__ __forceinline__ int lds_swz(int r, int q) { return r * LDS2 + ((q ^ (r & 7)) << 3); }
 template <int BMt, int BNt>
 struct TileLds {
     uint16_t a[2][BMt * LDS2];
@@ -262,7 +268,7 @@ struct TileEngine {
             const int c = t + j * NT, r = c >> 3, kc = c & 7;
             const int ar = arow[r];
             ap[j] = A + (long)(ar >= 0 ? ar : a0) * lda + kc * 8;
-            a_lds[j] = r * LDS2 + kc * 8;
+            a_lds[j] = lds_swz(r, kc);
         }
         const char *bp[NB], *sp[NB];
         int b_lds[NB];
@@ -271,7 +277,9 @@ struct TileEngine {
             const int c = t + j * NT, r = c / BCPR, kc = c % BCPR;
             bp[j] = bptr[r] + kc * 16;
             sp[j] = BMODE == kB_F4 ? sptr[r] + kc * 2 : nullptr;
-            b_lds[j] = r * LDS2 + (B8 ? kc * 16 : BMODE == kB_F4 ? kc * 32 : kc * 8);
+            // first 16-byte chunk of the thread's 1, 2 (int8) or 4 (NVFP4)
+            // consecutive chunks; chunk h of them is at b_lds[j] ^ (8 h)
+            b_lds[j] = lds_swz(r, B8 ? kc * 2 : BMODE == kB_F4 ? kc * 4 : kc);
         }
         auto gload = [&](int k0, Stage &g) __attribute__((always_inline)) {
 #pragma unroll
@@ -293,21 +301,22 @@ struct TileEngine {
             for (int j = 0; j < NA; j++) *reinterpret_cast<u32x4_t *>(&L.a[buf][a_lds[j]]) = g.a[j];
 #pragma unroll
             for (int j = 0; j < NB; j++) {
-                uint4 *lb = reinterpret_cast<uint4 *>(&L.b[buf][b_lds[j]]);
+                uint16_t *lb = L.b[buf];
+                const int bo = b_lds[j];
                 const uint4 bw = make_uint4(g.b[j].x, g.b[j].y, g.b[j].z, g.b[j].w);
                 if constexpr (BMODE == kB_BF16) {
-                    lb[0] = bw;
+                    *reinterpret_cast<uint4 *>(lb + bo) = bw;
                 } else if constexpr (B8) {
                     uint4 o0, o1;
                     if constexpr (BMODE == kB_I8H) i8_to_f16_ob(bw, o0, o1);
                     else i8_to_bf16_ob(bw, o0, o1);
-                    lb[0] = o0;
-                    lb[1] = o1;
+                    *reinterpret_cast<uint4 *>(lb + bo) = o0;
+                    *reinterpret_cast<uint4 *>(lb + (bo ^ 8)) = o1;
                 } else {
                     uint4 o[4];
                     f4_to_bf16(bw, g.sc[j], o);
 #pragma unroll
-                    for (int q = 0; q < 4; q++) lb[q] = o[q];
+                    for (int q = 0; q < 4; q++) *reinterpret_cast<uint4 *>(lb + (bo ^ (8 * q))) = o[q];
                 }
             }
         };
@@ -316,7 +325,8 @@ struct TileEngine {
 #pragma unroll
             for (int nb = 0; nb < 4; nb++) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         const int nk = K / BK2;
-        const int lr = lane & 15, lk = (lane >> 4) * 8;
+        // fragment rows start at multiples of 16, so row & 7 == lr & 7
+        const int lr = lane & 15, fq0 = ((lane >> 4) ^ (lr & 7)) << 3;   // chunk position of kk = 0; kk = 1: ^ 32
         // one k-step: MFMAs on LDS buffer s & 1, then stage `nx` (holding step
         // s + 1) goes to the other buffer and is refilled with step s + NSTG + 1
         auto step = [&](int s, Stage &nx) __attribute__((always_inline)) {
@@ -326,10 +336,10 @@ struct TileEngine {
             for (int kk = 0; kk < 2; kk++) {
 #pragma unroll
                 for (int mb = 0; mb < MW; mb++)
-                    av[kk][mb] = *reinterpret_cast<const bf16x8_t *>(&L.a[buf][(wm * 16 * MW + mb * 16 + lr) * LDS2 + kk * 32 + lk]);
+                    av[kk][mb] = *reinterpret_cast<const bf16x8_t *>(&L.a[buf][(wm * 16 * MW + mb * 16 + lr) * LDS2 + (fq0 ^ (kk * 32))]);
 #pragma unroll
                 for (int nb = 0; nb < 4; nb++)
-                    bv[kk][nb] = *reinterpret_cast<const bf16x8_t *>(&L.b[buf][(wn * 64 + nb * 16 + lr) * LDS2 + kk * 32 + lk]);
+                    bv[kk][nb] = *reinterpret_cast<const bf16x8_t *>(&L.b[buf][(wn * 64 + nb * 16 + lr) * LDS2 + (fq0 ^ (kk * 32))]);
             }
 #pragma unroll
             for (int kk = 0; kk < 2; kk++)
