@@ -73,46 +73,74 @@ struct CsrLds {
     int pair[kMaxPairs];      // CSR position -> original pair index t*K + k
     int exp_id[kMaxPairs];
     int exp_ptr[kMaxPairs + 1];
-    uint32_t bits[512 / 32];  // bitmap of selected experts (E == 512)
+    uint32_t tbits[kMaxRows][512 / 32];   // per row: bitmap of its selected experts (E == 512)
+    int tpre[kMaxRows][512 / 32];         // per row: its selected experts in bitmap words [0, w)
+    uint32_t bits[512 / 32];              // union of the rows' bitmaps
+    int gpre[512 / 32 + 1];               // distinct experts in words [0, w); [16] = all
     int n_exp;
     alignas(16) unsigned long long tk[8][kTopkLds];
 };
 
-// Called by all threads of the block after sel of the P pairs is in LDS and
-// bits[] is zero. Position of pair p in (expert, token, k) order =
-// #{q: e_q < e_p} + #{q < p: e_q == e_p}; an expert's distinct index =
-// #{distinct e' < e_p}, read from the selected-expert bitmap.
-__device__ __forceinline__ void csr_build_lds(CsrLds &c, int P) {
-    const int p = threadIdx.x;
-    const int e = p < P ? c.sel[p] : 0;
-    if (p < P) atomicOr(&c.bits[e >> 5], 1u << (e & 31));
-    int less = 0, before = 0;
-    if (p < P) {
-#pragma unroll 8
-        for (int q = 0; q < P; q++) {
-            const int f = c.sel[q];
-            less += f < e;
-            before += (f == e) & (q < p);
+// Called by all threads of the block after sel of the P = M K pairs is in LDS
+// and tbits is zero; the K experts of a row are distinct (top-K). Position of
+// pair p = (t, k) with expert e in (expert, token, k) order
+//   #{q: e_q < e} + #{q < p: e_q == e}
+//   = sum over rows u of #{experts of u below e} + #{rows u < t selecting e},
+// and e's distinct index = #{distinct experts below e}: both read from the
+// per-row bitmaps and their word prefix counts (no scan over the pairs).
+__device__ __forceinline__ void csr_build_lds(CsrLds &c, int M, int K) {
+    const int P = M * K, i = threadIdx.x, wave = i >> 6, lane = i & 63;
+    if (i < P) {
+        const int e = c.sel[i];
+        atomicOr(&c.tbits[i / K][e >> 5], 1u << (e & 31));
+    }
+    __syncthreads();
+    if (wave < M && lane < 32) {
+        // lanes 0-15: row `wave`'s word w; lanes 16-31: the union's word w;
+        // exclusive prefix sums of the popcounts over the 16 words
+        const int w = lane & 15;
+        uint32_t b = 0u;
+        if (lane < 16) {
+            b = c.tbits[wave][w];
+        } else {
+            for (int u = 0; u < M; u++) b |= c.tbits[u][w];
+        }
+        const int pc = __popc(b);
+        int inc = pc;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) {
+            const int o = __shfl_up(inc, d, 16);
+            if (w >= d) inc += o;
+        }
+        if (lane < 16) {
+            c.tpre[wave][w] = inc - pc;
+        } else if (wave == 0) {
+            c.bits[w] = b;
+            c.gpre[w] = inc - pc;
+            if (w == 15) c.gpre[16] = inc;
         }
     }
     __syncthreads();
-    if (p < P) {
-        int first_less = __popc(c.bits[e >> 5] & ((1u << (e & 31)) - 1u));
-#pragma unroll
-        for (int w = 0; w < 16; w++) first_less += w < (e >> 5) ? __popc(c.bits[w]) : 0;
-        c.pair[less + before] = p;
+    if (i < P) {
+        const int e = c.sel[i], t = i / K, w = e >> 5, sh = e & 31;
+        const uint32_t below = (1u << sh) - 1u;
+        int less = 0, before = 0;
+        for (int u = 0; u < M; u++) {
+            const uint32_t b = c.tbits[u][w];
+            less += c.tpre[u][w] + __popc(b & below);
+            before += u < t ? (int)((b >> sh) & 1u) : 0;
+        }
+        const int first_less = c.gpre[w] + __popc(c.bits[w] & below);
+        c.pair[less + before] = i;
         if (before == 0) { c.exp_id[first_less] = e; c.exp_ptr[first_less] = less; }
     }
-    if (threadIdx.x == 0) {
-        int n = 0;
-#pragma unroll
-        for (int w = 0; w < 16; w++) n += __popc(c.bits[w]);
+    if (i == 0) {
+        const int n = c.gpre[16];
         c.n_exp = n;
         c.exp_ptr[n] = P;
     }
     __syncthreads();
 }
-
 
 // ---- top-K of all rows + routing inversion: one block, one wave per row ---------
 // Published: sel/wts [M][K]; csr = {n_exp, exp_id[P], exp_ptr[P+1], pair[P]}.
@@ -128,7 +156,7 @@ k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, i
     __shared__ CsrLds c;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int P = M * K;
-    if (threadIdx.x < 16) c.bits[threadIdx.x] = 0u;
+    if (threadIdx.x < kMaxRows * 16) (&c.tbits[0][0])[threadIdx.x] = 0u;
     if (wave < M) {
         int my_i;
         float my_w;
@@ -149,7 +177,7 @@ k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, i
         }
     }
     __syncthreads();
-    csr_build_lds(c, P);
+    csr_build_lds(c, M, K);
     for (int i = threadIdx.x; i < P; i += blockDim.x) {
         g_sel[i] = c.sel[i]; g_wts[i] = c.wts[i];
         g_csr[1 + i] = c.exp_id[i];
