@@ -410,7 +410,9 @@ using DownEngineI8 = TileEngine<kB_I8, 2, 2, 4, 2>;
 // INT8 and cost the router GEMM its second wave per SIMD.)
 using ExpertEngineF4 = TileEngine<kB_F4, 2, 4, 4, 3>;
 using SharedEngineI8 = TileEngine<kB_I8, 2, 4, 4, 3>;     // shared tiles inside the NVFP4 launch
-constexpr int GBN = ExpertEngine::BNt;          // weight rows per grouped-GEMM tile
+// weight rows per grouped-GEMM tile (gate/up: half gate, half up rows)
+constexpr int GBN_I8 = ExpertEngine::BNt, GBN_F4 = ExpertEngineF4::BNt;
+constexpr int GBN_MIN = GBN_I8 < GBN_F4 ? GBN_I8 : GBN_F4;
 
 // Workgroups are dispatched to the 8 XCDs round-robin (block b on XCD b % 8).
 // Map block b to tile (m, n) so that the nt n-tiles of one m-tile run back to
@@ -813,9 +815,9 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     if (threadIdx.x < TBN) {
         const int n = threadIdx.x;
         if (GATEUP) {
-            // wave column wn = n / 64 holds intermediate rows [128 nt + 32 wn, +32):
+            // wave column wn = n / 64 holds intermediate rows [(TBN / 2) nt + 32 wn, +32):
             // its n-blocks 0, 1 are their gate rows and n-blocks 2, 3 the same up rows
-            const int wn = n >> 6, q = (n >> 4) & 3, o = nt * 128 + wn * 32 + (q & 1) * 16 + (n & 15);
+            const int wn = n >> 6, q = (n >> 4) & 3, o = nt * (TBN / 2) + wn * 32 + (q & 1) * 16 + (n & 15);
             bptr[n] = reinterpret_cast<const char *>((q < 2 ? Wb : Wb2) + (size_t)o * rowb);
             if (F4 && f4) sptr[n] = reinterpret_cast<const char *>((q < 2 ? Cb : Cb2) + (size_t)o * (Kdim / 16));
         } else {
@@ -840,7 +842,7 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     // epilogues: the column scales are loaded once per lane and the per-row
     // values come from the LDS tables filled above (no per-element global loads)
     if (GATEUP) {
-        const int o0 = nt * 128 + wn * 32 + (lane & 15);
+        const int o0 = nt * (TBN / 2) + wn * 32 + (lane & 15);
         float sgv[2], suv[2];
 #pragma unroll
         for (int nb = 0; nb < 2; nb++) {
@@ -953,12 +955,12 @@ size_t prefill_ws_bytes(int T) {
     b += al((size_t)(c.E + 2) * 4);        // off
     b += al((size_t)((size_t)T * c.K + kPairsPerBlk - 1) / kPairsPerBlk * c.E * 4);   // per-block counts
     const size_t max_mt = (P / BM + c.E + 2 + 7) / 8 * 8;
-    b += al(max_mt * (c.I / (GBN / 2)) * 16) + al(max_mt * (c.H / DownEngineI8::BNt) * 16);   // item lists
+    b += al(max_mt * (c.I / (GBN_MIN / 2)) * 16) + al(max_mt * (c.H / DownEngineI8::BNt) * 16);   // item lists
     b += al(P * 4) * 3;                    // p_tok, p_slot, p_wt
     b += al(P * c.I * 2);                  // hidden bf16
     b += al(P * c.H * 4);                  // partials
     b += al((size_t)T * 4);                // x row sums
-    b += al(P * (c.I / (GBN / 2)) * 4);    // hidden row sums per gate/up n-tile
+    b += al(P * (c.I / (GBN_MIN / 2)) * 4);    // hidden row sums per gate/up n-tile
     b += al((size_t)T * c.H * 2) + al((size_t)T * 4) * 2;   // fp16 x rows, their sums and 2^-k
     return b;
 }
@@ -1006,7 +1008,7 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     const int nblk = (int)(((size_t)T * K + kPairsPerBlk - 1) / kPairsPerBlk);
     int *blk = reinterpret_cast<int *>(b); b += al((size_t)nblk * E * 4);
     const size_t max_mt = (P / BM + E + 2 + 7) / 8 * 8;   // bound on m-tiles, a multiple of 8
-    const int nt_gu = I / (GBN / 2), nt_dn = H / (f4 ? GBN : DownEngineI8::BNt);
+    const int nt_gu = I / ((f4 ? GBN_F4 : GBN_I8) / 2), nt_dn = H / (f4 ? GBN_F4 : DownEngineI8::BNt);
     int4 *items_gu = reinterpret_cast<int4 *>(b); b += al(max_mt * nt_gu * 16);
     int4 *items_dn = reinterpret_cast<int4 *>(b); b += al(max_mt * (H / DownEngineI8::BNt) * 16);
     int *p_tok = reinterpret_cast<int *>(b); b += al(P * 4);
