@@ -30,12 +30,16 @@
 //                      so y does not depend on it) and the GEMM work lists.
 //   k_pf_gemm<GATEUP>  hidden[p][n] = silu(sg (x_p . Wg_n)) * (su (x_p . Wu_n))
 //   k_pf_gemm<DOWN>    part[slot_p][c] = w_p * sd_c * (h_p . Wd_c)
-//                      Both: BM=128 rows x BN=256 weight rows x BK=64, 2 x 4
-//                      waves of 64 x 64, v_mfma_f32_16x16x32_bf16; int8 weights are
-//                      staged to LDS as bf16 in offset-binary form
-//                      (u = q + 128 is exact in bf16) and the row sum of A
-//                      (precomputed: x sums in the router, hidden sums in the
-//                      gate/up epilogue) times 128 is subtracted in the epilogue.
+//                      BM=128 rows x BK=64, waves of 64 x 64 on 16x16x32 MFMAs.
+//                      INT8 gate/up (128 x 256 tiles, 8 waves): x rows as fp16
+//                      scaled by 2^k per token, weights kept as int8 in LDS and
+//                      widened at the fragment read to fp16 1024 + u
+//                      (u = q + 128), f16 MFMA, 1152 * sum(x16) removed and 2^-k
+//                      applied in the epilogue. INT8 down (128 x 128 tiles, 4
+//                      waves, two blocks per CU): bf16 hidden rows, weights
+//                      staged as bf16 u (exact), bf16 MFMA, 128 * sum(h) removed
+//                      (the hidden sums come from the gate/up epilogue). NVFP4:
+//                      e2m1 times its e4m3 block scale staged as bf16 (exact).
 //   k_pf_combine       y[t] = sum over the K+1 slots of t, in slot order.
 #include <type_traits>
 
@@ -232,20 +236,37 @@ constexpr int BK2 = 64;
 // fragment read (measured with SQ_LDS_BANK_CONFLICT on ds_read_b128).
 constexpr int LDS2 = BK2;
 __device__ __forceinline__ int lds_swz(int r, int q) { return r * LDS2 + ((q ^ (r & 7)) << 3); }
-template <int BMt, int BNt>
+template <int BMt, int BNt, int BROW = LDS2>
 struct TileLds {
     uint16_t a[2][BMt * LDS2];
-    uint16_t b[2][BNt * LDS2];
+    uint16_t b[2][BNt * BROW];                 // BROW 16-bit units per B row
 };
-enum { kB_I8 = 0, kB_BF16 = 2, kB_F4 = 3, kB_I8H = 4 };
+// B row modes: int8 staged as bf16 (offset binary) or as fp16 (1024 + u), bf16,
+// NVFP4 staged as bf16, or int8 kept as int8 in LDS (64-byte rows) and widened
+// to fp16 at the fragment read (half the LDS bytes written and read for B).
+enum { kB_I8 = 0, kB_BF16 = 2, kB_F4 = 3, kB_I8H = 4, kB_I8HL = 5 };
+// int8 B rows in LDS: 8-byte chunk c of row r at chunk position c ^ (2 ((r >> 2) & 3)).
+// A fragment read (16 rows at one chunk per 16 lanes, ds_read_b64) is then free
+// of bank conflicts (6 conflict cycles per instruction unswizzled), and the two
+// chunks a staging thread writes stay one aligned 16-byte pair.
+__device__ __forceinline__ int lds_swz8(int r, int c) { return r * (LDS2 / 2) + ((c ^ (2 * ((r >> 2) & 3))) << 2); }
+// 8 int8 codes -> 8 fp16 1024 + u (as i8_to_f16_ob)
+__device__ __forceinline__ f16x8_t i8x8_to_f16_ob(uint32_t w0, uint32_t w1) {
+    const uint32_t d0 = w0 ^ 0x80808080u, d1 = w1 ^ 0x80808080u;
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const u32x4v o = {__builtin_amdgcn_perm(0x64646464u, d0, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, d0, 0x04030402u),
+                      __builtin_amdgcn_perm(0x64646464u, d1, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, d1, 0x04030402u)};
+    return __builtin_bit_cast(f16x8_t, o);
+}
 template <int BMODE, int WM, int WN, int MW, int NSTG>
 struct TileEngine {
     static_assert(NSTG == 2 || NSTG == 3, "two or three register stages");
-    using Lds = TileLds<16 * MW * WM, 64 * WN>;
+    static constexpr bool BL8 = BMODE == kB_I8HL;                  // int8 B rows in LDS
+    using Lds = TileLds<16 * MW * WM, 64 * WN, BL8 ? LDS2 / 2 : LDS2>;
     static constexpr int WMc = WM, WNc = WN, MWc = MW, WavesPerSimd = 2;
-    static_assert(BMODE == kB_I8 || BMODE == kB_I8H || BMODE == kB_F4 || BMODE == kB_BF16,
-                  "int8 (bf16 or fp16 staging), NVFP4 or bf16 B rows");
-    static constexpr bool B8 = BMODE == kB_I8 || BMODE == kB_I8H;   // one byte per B value
+    static_assert(BMODE == kB_I8 || BMODE == kB_I8H || BMODE == kB_I8HL || BMODE == kB_F4 || BMODE == kB_BF16,
+                  "int8 (bf16 or fp16 staging, or int8 in LDS), NVFP4 or bf16 B rows");
+    static constexpr bool B8 = BMODE == kB_I8 || BMODE == kB_I8H || BL8;   // one byte per B value
     // MW m-blocks of 16 rows per wave: a wave computes (16 MW) x 64
     static constexpr int BMt = 16 * MW * WM, BNt = 64 * WN, NT = 64 * WM * WN;
     static constexpr int BCPR = B8 ? 4 : BMODE == kB_F4 ? 2 : 8;   // 16-byte B chunks per row per k-step
@@ -256,7 +277,7 @@ struct TileEngine {
         uint32_t sc[NB];
     };
     __device__ static void run(const uint16_t *__restrict__ A, long lda, const int *arow,
-                               const char *const *bptr, int K, TileLds<BMt, BNt> &L, f32x4_t (&acc)[MW][4],
+                               const char *const *bptr, int K, Lds &L, f32x4_t (&acc)[MW][4],
                                const char *const *sptr = nullptr) {
         const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
         const int wm = wave / WN, wn = wave % WN;
@@ -279,7 +300,7 @@ struct TileEngine {
             sp[j] = BMODE == kB_F4 ? sptr[r] + kc * 2 : nullptr;
             // first 16-byte chunk of the thread's 1, 2 (int8) or 4 (NVFP4)
             // consecutive chunks; chunk h of them is at b_lds[j] ^ (8 h)
-            b_lds[j] = lds_swz(r, B8 ? kc * 2 : BMODE == kB_F4 ? kc * 4 : kc);
+            b_lds[j] = BL8 ? lds_swz8(r, kc * 2) : lds_swz(r, B8 ? kc * 2 : BMODE == kB_F4 ? kc * 4 : kc);
         }
         auto gload = [&](int k0, Stage &g) __attribute__((always_inline)) {
 #pragma unroll
@@ -304,7 +325,7 @@ struct TileEngine {
                 uint16_t *lb = L.b[buf];
                 const int bo = b_lds[j];
                 const uint4 bw = make_uint4(g.b[j].x, g.b[j].y, g.b[j].z, g.b[j].w);
-                if constexpr (BMODE == kB_BF16) {
+                if constexpr (BMODE == kB_BF16 || BL8) {
                     *reinterpret_cast<uint4 *>(lb + bo) = bw;
                 } else if constexpr (B8) {
                     uint4 o0, o1;
@@ -327,6 +348,7 @@ struct TileEngine {
         const int nk = K / BK2;
         // fragment rows start at multiples of 16, so row & 7 == lr & 7
         const int lr = lane & 15, fq0 = ((lane >> 4) ^ (lr & 7)) << 3;   // chunk position of kk = 0; kk = 1: ^ 32
+        const int fb0 = ((lane >> 4) ^ (2 * ((lr >> 2) & 3))) << 2;      // int8 B rows: kk = 0; kk = 1: ^ 16
         // one k-step: MFMAs on LDS buffer s & 1, then stage `nx` (holding step
         // s + 1) goes to the other buffer and is refilled with step s + NSTG + 1
         auto step = [&](int s, Stage &nx) __attribute__((always_inline)) {
@@ -338,8 +360,14 @@ struct TileEngine {
                 for (int mb = 0; mb < MW; mb++)
                     av[kk][mb] = *reinterpret_cast<const bf16x8_t *>(&L.a[buf][(wm * 16 * MW + mb * 16 + lr) * LDS2 + (fq0 ^ (kk * 32))]);
 #pragma unroll
-                for (int nb = 0; nb < 4; nb++)
-                    bv[kk][nb] = *reinterpret_cast<const bf16x8_t *>(&L.b[buf][(wn * 64 + nb * 16 + lr) * LDS2 + (fq0 ^ (kk * 32))]);
+                for (int nb = 0; nb < 4; nb++) {
+                    if constexpr (BL8) {
+                        const uint2 w8 = *reinterpret_cast<const uint2 *>(&L.b[buf][(wn * 64 + nb * 16 + lr) * (LDS2 / 2) + (fb0 ^ (kk * 16))]);
+                        bv[kk][nb] = __builtin_bit_cast(bf16x8_t, i8x8_to_f16_ob(w8.x, w8.y));
+                    } else {
+                        bv[kk][nb] = *reinterpret_cast<const bf16x8_t *>(&L.b[buf][(wn * 64 + nb * 16 + lr) * LDS2 + (fq0 ^ (kk * 32))]);
+                    }
+                }
             }
 #pragma unroll
             for (int kk = 0; kk < 2; kk++)
@@ -347,7 +375,7 @@ struct TileEngine {
                 for (int mb = 0; mb < MW; mb++)
 #pragma unroll
                     for (int nb = 0; nb < 4; nb++)
-                        if constexpr (BMODE == kB_I8H)
+                        if constexpr (BMODE == kB_I8H || BL8)
                             acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av[kk][mb]),
                                                                                 __builtin_bit_cast(f16x8_t, bv[kk][nb]),
                                                                                 acc[mb][nb], 0, 0, 0);
@@ -398,9 +426,10 @@ constexpr int kRouterKS = 1;
 // INT8 tiles: 128 x 256 in 8 waves of 64 x 64 (two waves per SIMD). Four
 // waves of 128 x 64 (MW = 8: one wave per SIMD, accumulators in AGPRs, 25%
 // fewer LDS reads per MFMA) measured 1343 / 1149 us against 797 / 719 us.
-// INT8 gate/up: int8 weights widened to fp16 while staging (one v_perm per two
-// codes instead of three ops per two for bf16) against the fp16 x rows
-using ExpertEngine = TileEngine<kB_I8H, 2, 4, 4, 2>;
+// INT8 gate/up: int8 weights kept as int8 in LDS and widened to fp16 at the
+// fragment read (one v_perm per two codes) against the fp16 x rows; widening
+// while staging (fp16 B rows in LDS) measured 677 vs 639 us
+using ExpertEngine = TileEngine<kB_I8HL, 2, 4, 4, 2>;
 // INT8 down tiles: 128 x 128 in 4 waves, two blocks per CU (K = I is short, so
 // one block's prologue and epilogue overlap the other block's k-steps)
 using DownEngineI8 = TileEngine<kB_I8, 2, 2, 4, 2>;
