@@ -431,7 +431,10 @@ constexpr int kRouterKS = 1;
 // while staging (fp16 B rows in LDS) measured 677 vs 639 us
 using ExpertEngine = TileEngine<kB_I8HL, 2, 4, 4, 2>;
 // INT8 down tiles: 128 x 128 in 4 waves, two blocks per CU (K = I is short, so
-// one block's prologue and epilogue overlap the other block's k-steps)
+// one block's prologue and epilogue overlap the other block's k-steps). The
+// weights are widened to bf16 while staging: int8 in LDS widened at the
+// fragment read to bf16 (seven operations per four codes, done by both wave
+// rows) measured 551 vs 542 us.
 using DownEngineI8 = TileEngine<kB_I8, 2, 2, 4, 2>;
 // NVFP4 launches: e2m1 tiles and the shared expert's INT8 tiles in one kernel
 // (three register stages: loads four k-steps ahead; gate/up 831 -> 737 us.
