@@ -224,6 +224,13 @@ void qf5_m8_downacc(const uint8_t *Wd, const uint8_t *Sd, const float *s2d_res,
 void qf5_m8_build_csr(const int *sel_dev, const float *wt_dev, int M, int K,
                       int card, int epc, int il, int *exp_slot, int *exp_ptr,
                       int *pair_tok, float *pair_wt, int *counts, hipStream_t s);
+/* Four-card combine of fp32 partials already in this device's memory:
+ * y_out[i] = ((y0[i] + y1[i]) + y2[i]) + y3[i], i < n (n = M*H). y_out may be
+ * one of the inputs. Replaces qf5_m8_reduce4
+ * (ocho/amd_server/qf_moe_m8_wave64.h:72-75; kernel k_m8_reduce4,
+ * qf_moe_m8_wave64.hip:216-221). */
+void qf5_m8_reduce4(float *y_out, const float *y0, const float *y1,
+                    const float *y2, const float *y3, int n, hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* INT8 shared expert on X8 rows: eg = silu(gate.x) * up.x, eu = up.x,

@@ -327,6 +327,16 @@ void orc_nvfp4_to_i8(const uint8_t *W, const uint8_t *S, float s2, int rows, int
     free(v);
 }
 
+/* Four-card combine: y[i] = ((y0[i] + y1[i]) + y2[i]) + y3[i], fp32, the
+   left-to-right order of k_m8_reduce4 (qf_moe_m8_wave64.hip:216-221). */
+void orc_m8_reduce4(float *y, const float *y0, const float *y1, const float *y2, const float *y3, long n) {
+    for (long i = 0; i < n; i++) {
+        float a = y0[i] + y1[i];
+        a = a + y2[i];
+        y[i] = a + y3[i];
+    }
+}
+
 /* Routing inversion: experts ascending; within an expert, pairs in (token, k)
    order (qf8_moe_i8.hip:323-358; qf_moe_m8_wave64.hip:261-299). */
 int orc_csr_build(const int *sel, const float *wt, int T, int K, int E,

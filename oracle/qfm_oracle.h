@@ -35,6 +35,8 @@
  *   orc_nvfp4_expert       numpy fp64 matmul after an independent numpy dequant
  *   orc_csr_build          invariants (permutation, ascending ids, token order)
  *   orc_x8_quant           numpy restatement + invariants (|q| <= 127, q*s ~ v)
+ *   orc_m8_reduce4         exact integer sums; an order-sensitive case whose
+ *                          result differs for every other association
  *   orc_nvfp4_to_i8        closed forms: the row maximum maps to +-127, an
  *                          all-zero row keeps scale 1, constant rows, codes
  *                          reconstruct within scale/2, 5-bit exponent field
@@ -106,6 +108,9 @@ void orc_nvfp4_to_i8(const uint8_t *W, const uint8_t *S, float s2, int rows, int
 
 /* ---- X8 activation quantizer (reference's lossy activation mode) ---- */
 void orc_x8_quant(const float *v, int n, int8_t *q, float *s);
+
+/* ---- four-card combine of fp32 partials ---- */
+void orc_m8_reduce4(float *y, const float *y0, const float *y1, const float *y2, const float *y3, long n);
 
 /* ---- routing inversion ---- */
 int orc_csr_build(const int *sel, const float *wt, int T, int K, int E,

@@ -266,6 +266,29 @@ k_cx_combine(const float *__restrict__ part, int K, int H, float *__restrict__ y
     y[(size_t)t * H + i] = a;
 }
 
+// Four-card combine: y[i] = ((y0[i] + y1[i]) + y2[i]) + y3[i] (the
+// left-to-right sum of k_m8_reduce4, qf_moe_m8_wave64.hip:216-221). VEC: four
+// elements per thread in 16-byte accesses (every pointer 16-byte aligned);
+// the n % 4 tail elements are done by the first threads of the vector grid.
+template <bool VEC>
+__global__ void __launch_bounds__(256)
+k_cx_reduce4(float *y, const float *y0, const float *y1, const float *y2, const float *y3, int n) {   // y may alias an input
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if constexpr (VEC) {
+        const int n4 = n >> 2;
+        if (i < n4) {
+            const float4 a = reinterpret_cast<const float4 *>(y0)[i], b = reinterpret_cast<const float4 *>(y1)[i];
+            const float4 c = reinterpret_cast<const float4 *>(y2)[i], d = reinterpret_cast<const float4 *>(y3)[i];
+            reinterpret_cast<float4 *>(y)[i] = make_float4(((a.x + b.x) + c.x) + d.x, ((a.y + b.y) + c.y) + d.y,
+                                                           ((a.z + b.z) + c.z) + d.z, ((a.w + b.w) + c.w) + d.w);
+        }
+        const int t = n4 * 4 + i;
+        if (i < (n & 3)) y[t] = ((y0[t] + y1[t]) + y2[t]) + y3[t];
+    } else {
+        if (i < n) y[i] = ((y0[i] + y1[i]) + y2[i]) + y3[i];
+    }
+}
+
 // ---- NVFP4 weights x fp32 activations -------------------------------------------
 // Pair groups: group g covers pairs [ptr[g], ptr[g+1]) of weight slot slot[g];
 // ptr == nullptr makes group g the single pair g on activation row 0 (the M=1
@@ -639,6 +662,23 @@ void qf5_m8_downacc(const uint8_t *Wd, const uint8_t *Sd, const float *s2d_res, 
                                           rt->n_exp_max), dim3(256), 0, stream, Wd, Sd, s2d_res, hidden, rt->pair_wt,
                                           y_partial, pg));
     check_launch("qf5_m8_downacc");
+}
+
+void qf5_m8_reduce4(float *y_out, const float *y0, const float *y1, const float *y2, const float *y3, int n,
+                    hipStream_t s) {
+    if (n < 0 || (n > 0 && (!y_out || !y0 || !y1 || !y2 || !y3))) { set_error(-1, "qf5_m8_reduce4: bad arguments"); return; }
+    if (n == 0) return;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(y_out) | reinterpret_cast<uintptr_t>(y0) |
+                         reinterpret_cast<uintptr_t>(y1) | reinterpret_cast<uintptr_t>(y2) |
+                         reinterpret_cast<uintptr_t>(y3);
+    if ((al & 15) == 0) {
+        const int n4 = n >> 2, nb = (n4 > (n & 3) ? n4 : (n & 3)) + 255;
+        hipLaunchKernelGGL(k_cx_reduce4<true>, dim3((unsigned)(nb / 256)), dim3(256), 0, s, y_out, y0, y1, y2, y3, n);
+    } else {
+        hipLaunchKernelGGL(k_cx_reduce4<false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y_out, y0, y1, y2,
+                           y3, n);
+    }
+    check_launch("qf5_m8_reduce4");
 }
 
 void qf5_m8_build_csr(const int *sel_dev, const float *wt_dev, int M, int K, int card, int epc, int il, int *exp_slot,

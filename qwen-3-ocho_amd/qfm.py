@@ -95,6 +95,7 @@ _SIGS = {
     "qf5_m8_gateup": (None, [vp] * 8 + [C.POINTER(Qf5M8Route), vp]),
     "qf5_m8_downacc": (None, [vp] * 5 + [C.POINTER(Qf5M8Route), vp]),
     "qf5_m8_build_csr": (None, [vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp, vp]),
+    "qf5_m8_reduce4": (None, [vp, vp, vp, vp, vp, C.c_int, vp]),
     "qf8_i8_shexp_m1": (None, [C.POINTER(Qf8I8Mat)] * 4 + [vp] * 9 + [vp]),
     "qf8_i8_shexp_rows": (C.c_int, [C.POINTER(Qf8I8Mat)] * 4 + [vp] * 9 + [C.c_int, vp]),
     "qfm_workspace_bytes": (C.c_size_t, [C.c_int]),

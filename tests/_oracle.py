@@ -60,6 +60,7 @@ _SIGS = {
     "orc_x8_quant": (None, [vp, C.c_int, vp, vp]),
     "orc_nvfp4_to_i8": (None, [vp, vp, C.c_float, C.c_int, C.c_int, vp, vp]),
     "orc_csr_build": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp, vp]),
+    "orc_m8_reduce4": (None, [vp, vp, vp, vp, vp, C.c_long]),
     "orc_moe_layer": (C.c_int, [C.POINTER(LayerCfg), C.c_int, vp, vp, vp, vp, vp, vp]),
     "orc_cpu_moe_layer_fast": (None, [C.POINTER(HostLayer), C.c_int, C.c_int, C.c_int, C.c_int,
                                       vp, C.c_int, vp, C.c_int]),
@@ -188,6 +189,14 @@ def x8_quant(v):
     s = np.empty(v.shape[0] // 32, np.float32)
     lib.orc_x8_quant(ptr(v), v.shape[0], ptr(q), ptr(s))
     return q, s
+
+
+def m8_reduce4(y0, y1, y2, y3):
+    lib = load()
+    ys = [np.ascontiguousarray(v, np.float32) for v in (y0, y1, y2, y3)]
+    out = np.empty_like(ys[0])
+    lib.orc_m8_reduce4(ptr(out), *[ptr(v) for v in ys], out.size)
+    return out
 
 
 def csr_build(sel, wt, E):

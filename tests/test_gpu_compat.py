@@ -330,3 +330,29 @@ def test_i8_build_bit_exact(lib):
         assert np.array_equal(bufs[3 + j].download(np.float32, rows, offset=3 * rows * 4),
                               bufs[3 + j].download(np.float32, rows, offset=17 * rows * 4))
     L.destroy()
+
+
+def test_m8_reduce4(lib):
+    """qf5_m8_reduce4: bit-exact against the oracle's left-to-right fp32 sum, on
+    the 16-byte path (aligned, n % 4 == 0 and ragged), the element path
+    (pointers 4 bytes off alignment), in place (y_out == y0) and n == 0."""
+    rng = np.random.default_rng(17)
+    for n, off, inplace in ((8 * H, 0, False), (8 * H + 3, 0, False), (1001, 1, False), (7, 3, False),
+                            (4 * H, 0, True), (5, 0, True)):
+        _say("m8_reduce4", n, off, inplace)
+        ys = [(rng.standard_normal(n) * 10.0 ** rng.uniform(-3, 3, n)).astype(np.float32) for _ in range(4)]
+        if n >= 4:                                   # the order-sensitive case in the first lanes
+            ys[0][:2], ys[1][:2], ys[2][:2], ys[3][:2] = (2.0 ** 24, 1.0), (1.0, 1.0), (1.0, 1.0), (1.0, 2.0 ** 24)
+        bufs = [_dev(np.concatenate([np.zeros(off, np.float32), v])) for v in ys]
+        ptrs = [b.ptr + 4 * off for b in bufs]
+        out = bufs[0] if inplace else qfm.DevBuf(4 * (n + off))
+        optr = ptrs[0] if inplace else out.ptr + 4 * off
+        lib.qf5_m8_reduce4(optr, *ptrs, n, None)
+        _sync(lib)
+        got = out.download(np.float32, n + off)[off:]
+        ref = orc.m8_reduce4(*ys)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        if n >= 4:
+            assert got[0] == 2.0 ** 24 and got[1] == 2.0 ** 24 + 4
+    lib.qf5_m8_reduce4(None, None, None, None, None, 0, None)   # nothing to do, no error
+    _sync(lib)

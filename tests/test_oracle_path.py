@@ -221,6 +221,22 @@ def test_x8_quant_properties():
     assert not q[64:96].any()
 
 
+def test_m8_reduce4_exact_and_order():
+    """orc_m8_reduce4 (qf_moe_m8_wave64.hip:216-221): y0 + y1 + y2 + y3 left to right in fp32."""
+    rng = np.random.default_rng(5)
+    ys = [rng.integers(-2 ** 20, 2 ** 20, 4099).astype(np.float32) for _ in range(4)]
+    exact = sum(v.astype(np.int64) for v in ys)                     # every partial sum < 2^24: exact
+    assert np.array_equal(orc.m8_reduce4(*ys), exact.astype(np.float32))
+    # 2^24 + 1 + 1 + 1 left to right stays 2^24 (each +1 is a tie, to even); every
+    # other association of the four gives 2^24 + 2 or 2^24 + 4, and the reversed
+    # order 1 + 1 + 1 + 2^24 gives 2^24 + 4
+    big, one = np.float32([2 ** 24]), np.float32([1.0])
+    assert orc.m8_reduce4(big, one, one, one)[0] == 2 ** 24
+    assert orc.m8_reduce4(one, one, one, big)[0] == 2 ** 24 + 4
+    z = np.zeros(0, np.float32)
+    assert orc.m8_reduce4(z, z, z, z).size == 0
+
+
 def test_csr_invariants_and_order():
     T, K, E = 257, 10, 512
     sel = np.stack([RNG.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32)
