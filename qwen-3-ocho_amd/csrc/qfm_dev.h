@@ -200,6 +200,53 @@ __device__ __forceinline__ float canon_butterfly(float a) {
     return __fadd_rn(a, __shfl_xor(a, 32, WAVE));
 }
 
+// v from lane l ^ M (M = 1, 2: DPP quad permutes; 4, 8, 16: ds_swizzle in
+// bitmask mode; 32: bpermute)
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "lane xor of a power of two");
+    if constexpr (M == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    else if constexpr (M == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    else if constexpr (M < 32) return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), (M << 10) | 0x1F));
+    else return __shfl_xor(v, 32, WAVE);
+}
+
+// The canonical reduction (canon_butterfly's addition tree: level m adds the
+// partial sums of lanes l and l ^ m) of R rows at once, R = 2, 4 or 8,
+// computed reduce-scatter style: at the levels m < R, lane l keeps the rows
+// whose bit matches bit m of l and trades the others with lane l ^ m (which
+// holds the same rows), so every addition still combines the partial sums of
+// lanes l and l ^ m of one row; the levels m >= R are a plain butterfly.
+// R - 1 + 6 - log2(R) cross-lane steps instead of 6 R. Lane l returns the
+// sum of row l & (R - 1).
+template <int R, int M = 1>
+__device__ __forceinline__ float canon_scatter_level(const float (&v)[R], int lane) {
+    if constexpr (R == 1) {
+        float s = v[0];
+        if constexpr (M <= 1) s = __fadd_rn(s, lane_xor<1>(s));
+        if constexpr (M <= 2) s = __fadd_rn(s, lane_xor<2>(s));
+        if constexpr (M <= 4) s = __fadd_rn(s, lane_xor<4>(s));
+        if constexpr (M <= 8) s = __fadd_rn(s, lane_xor<8>(s));
+        if constexpr (M <= 16) s = __fadd_rn(s, lane_xor<16>(s));
+        return __fadd_rn(s, lane_xor<32>(s));
+    } else {
+        const bool hi = (lane & M) != 0;
+        float n[R / 2];
+#pragma unroll
+        for (int j = 0; j < R / 2; j++) {
+            const float keep = hi ? v[2 * j + 1] : v[2 * j];
+            const float send = hi ? v[2 * j] : v[2 * j + 1];
+            n[j] = __fadd_rn(keep, lane_xor<M>(send));
+        }
+        return canon_scatter_level<R / 2, 2 * M>(n, lane);
+    }
+}
+template <int R>
+__device__ __forceinline__ float canon_reduce_rows(const float (&a)[R], int lane) {
+    static_assert(R == 2 || R == 4 || R == 8, "2, 4 or 8 rows");
+    return canon_scatter_level<R, 1>(a, lane);
+}
+
 // Max over aligned groups of G lanes (same steps as group_sum).
 template <int G>
 __device__ float group_max(float v) {

@@ -41,8 +41,9 @@ __device__ __forceinline__ float canon_reduce_row(const float4 (&w)[NJ], const f
 // two shared-expert gate/up rows each, one per half-wave, giving
 // hsh[m][r] = silu(sg_r <Qg_r, x_m>) * (su_r <Qu_r, x_m>). x is bf16 [M][H],
 // logits [M][ld]. Every output depends on x only, so one launch covers all.
-// MR rows of x are processed together: their fma chains and butterflies are
-// independent, so they overlap (each row keeps the canonical order). With
+// MR rows of x are processed together: their fma chains are independent and
+// their canonical reductions share cross-lane steps (canon_reduce_rows; each
+// row keeps the canonical order). With
 // MR > 1 the shared-expert rows are also split over x rows: block (pair, mg)
 // computes rows [2 mg, 2 mg + 2) of x for its row pair, MG = ceil(M / 2) blocks
 // per pair, laid out so that one pair's blocks share an XCD (and its L2).
@@ -88,13 +89,15 @@ k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, con
                     a[r] = __fmaf_rn(w[j].w, bf16_hi(xp[r][j].y), a[r]);
                 }
             }
-#pragma unroll
-            for (int r = 0; r < MR; r++) a[r] = canon_butterfly(a[r]);
-#pragma unroll
-            for (int r = 0; r < MR; r++) {
-                float v = a[r];
+            if constexpr (MR == 1) {
+                float v = canon_butterfly(a[0]);
                 if (bias && !is_g) v = __fadd_rn(v, bb);
-                if (lane == 0 && m0 + r < M) logits[(size_t)(m0 + r) * ld + b] = v;
+                if (lane == 0 && m0 < M) logits[(size_t)m0 * ld + b] = v;
+            } else {
+                // lane r < MR ends with row m0 + r (the same addition tree per row)
+                float v = canon_reduce_rows<MR>(a, lane);
+                if (bias && !is_g) v = __fadd_rn(v, bb);
+                if (lane < MR && m0 + lane < M) logits[(size_t)(m0 + lane) * ld + b] = v;
             }
         }
         return;
@@ -201,8 +204,10 @@ int launch_router_shared(const float *W, const float *bias, const float *g, cons
     if (shape_2048()) {
         if (M == 1)
             hipLaunchKernelGGL((k_router_shared<8, 512, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
-        else
+        else if (M <= 4)
             hipLaunchKernelGGL((k_router_shared<8, 512, 4>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
+        else
+            hipLaunchKernelGGL((k_router_shared<8, 512, 8>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
     } else if (shape_2560()) {
         if (M == 1)
             hipLaunchKernelGGL((k_router_shared<10, 640, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);

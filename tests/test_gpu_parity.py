@@ -75,7 +75,8 @@ def test_generator_bit_exact(lib, kind, tensor, n0, cnt, scale):
 
 
 # ------------------------------------------------------------------ router
-@pytest.mark.parametrize("H,M,bias", [(2048, 1, False), (2048, 8, False), (2048, 37, True), (2560, 8, True)])
+@pytest.mark.parametrize("H,M,bias", [(2048, 1, False), (2048, 3, True), (2048, 5, False), (2048, 8, False),
+                                      (2048, 37, True), (2560, 8, True)])
 def test_router_logits_bit_exact(lib, H, M, bias):
     _say("router", H, M, bias)
     _cfg(lib, H=H, I=512 if H == 2048 else 640)
