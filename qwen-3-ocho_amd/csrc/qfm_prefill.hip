@@ -716,19 +716,18 @@ k_pf_plan(int *__restrict__ blk, int nblk, int E, int has_sh, int T, int nt_gu, 
     __syncthreads();
     const int mtot = s_mt[G];
     if (g == 0) { n_items[0] = mtot * nt_gu; n_items[1] = mtot * nt_dn; }
-    for (int pass = 0; pass < 2; pass++) {
-        const int nt = pass ? nt_dn : nt_gu, mx = pass ? max_dn : max_gu;
-        int4 *items = pass ? items_dn : items_gu;
-        for (int it = g; it < mtot * nt && it < mx; it += 1024) {
-            const int m = it / nt, n = it - m * nt;
-            int lo = 0, hi = G - 1;                  // last group whose first m-tile is <= m
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (s_mt[mid] <= m) lo = mid; else hi = mid - 1;
-            }
-            const int row0 = (m - s_mt[lo]) * BM;
-            items[it] = make_int4(lo, row0, min(BM, s_cnt[lo] - row0), n);
+    // one thread per m-tile: its group (one search), then its n-tiles' items of both lists
+    for (int m = g; m < mtot; m += 1024) {
+        int lo = 0, hi = G - 1;                      // last group whose first m-tile is <= m
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_mt[mid] <= m) lo = mid; else hi = mid - 1;
         }
+        const int row0 = (m - s_mt[lo]) * BM, rows = min(BM, s_cnt[lo] - row0);
+        for (int n = 0; n < nt_gu; n++)
+            if (m * nt_gu + n < max_gu) items_gu[m * nt_gu + n] = make_int4(lo, row0, rows, n);
+        for (int n = 0; n < nt_dn; n++)
+            if (m * nt_dn + n < max_dn) items_dn[m * nt_dn + n] = make_int4(lo, row0, rows, n);
     }
 }
 
