@@ -12,8 +12,9 @@
 //
 // Launch sequence (all stream-ordered):
 //   k_topk_csr     one block: the top-K of all M rows (one wave per row), then
-//                  the routing inversion in LDS (O(P^2) rank counting over
-//                  P = M*K <= 128 pairs); publishes sel/wts/CSR. For INT8 a
+//                  the routing inversion in LDS (per-row expert bitmaps and
+//                  their word prefix counts, P = M*K <= 128 pairs); publishes
+//                  sel/wts/CSR. For INT8 a
 //                  second set of waves meanwhile writes the activations as
 //                  scaled fp16 chunks (chunk16_to_f16).
 //   k_csr_gateup   grid (I/rows, min(M*K, E)), 256 threads: distinct expert

@@ -564,7 +564,7 @@ k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, 
         lo[i] = l - b;
         hi[i] = l + b;
     }
-    // tau = K-th largest lower bound: rank counting over the E values
+    // tau = K-th largest lower bound (K rounds of a wave-wide maximum)
     float tau;
     {
         // K-th largest of lo[] by repeated wave max (K <= 16, values need not be distinct)
