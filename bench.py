@@ -308,14 +308,16 @@ def main():
     log(f"step {ms_step:.3f} ms ({us_layer:.2f} us/layer, {gbs:.0f} GB/s), host wall {t_host:.2f}s")
 
     # per-launch durations: each section of the step captured alone (48
-    # launches of one kernel, reading the workspace a full pass left) and replayed
+    # launches of one kernel, reading the workspace a full pass left) and
+    # replayed; the median of three timed replays of each
     sec_us = []
     for sec in range(3):
         def enq_sec(sec=sec):
             for l in range(nl):
                 qfm.check(lib.qfm_moe_forward_sections(C.byref(arr[l]), x.ptr + l * H * 2, 1, y.ptr + l * H * 2,
                                                        ws.ptr, wsb, 1 << sec, st.h), "section")
-        sec_us.append(time_graph(lib, st, enq_sec, args.steps, args.warmup) * 1000.0 / nl)
+        reps = sorted(time_graph(lib, st, enq_sec, args.steps, args.warmup) * 1000.0 / nl for _ in range(3))
+        sec_us.append(reps[1])
     dom = max(range(3), key=lambda i: sec_us[i])
     dom_gbs = SEC_BYTES[dom] / (sec_us[dom] * 1e-6) / 1e9
     log("sections (us/launch, one-kernel graphs): " + ", ".join(f"{SEC_NAMES[i].split()[0]}={sec_us[i]:.2f}" for i in range(3)))
