@@ -456,6 +456,21 @@ __device__ __forceinline__ void xcd_tile(int b, int nt, int &m, int &n) {
     n = slot - (slot / nt) * nt;
 }
 
+// Gate/up GEMM order: XCD x takes the contiguous m-tile range [x c, (x + 1) c),
+// c = ceil(mtot / 8), each m-tile's nt n-tiles back to back, so the m-tiles of
+// one expert (which read the same weight tiles) share one XCD's L2: 621 vs
+// 634 us against xcd_tile in interleaved runs (the down GEMM, whose weight
+// tiles are a quarter the size, measured 542 vs 538 us and keeps xcd_tile).
+// False for the blocks past the XCD's range (the grid is sized for a bound on
+// the m-tiles).
+__device__ __forceinline__ bool xcd_tile_contig(int b, int nt, int mtot, int &m, int &n) {
+    const int x = b & 7, slot = b >> 3, c = (mtot + 7) >> 3;
+    const int ml = slot / nt;
+    n = slot - ml * nt;
+    m = x * c + ml;
+    return ml < c && m < mtot;
+}
+
 // ---- router GEMM: logits~ [T][E] --------------------------------------------------
 __global__ void __launch_bounds__(256)
 k_pf_router_mfma(const uint16_t *__restrict__ x, int T, int H, const uint16_t *__restrict__ Wb, int E,
@@ -799,8 +814,12 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     __shared__ int rslot[GATEUP ? 1 : BM];          // down: the owned partial slot of each row
     __shared__ float rwt[GATEUP ? 1 : BM];          // down: the routing weight of each row
     int mi, ni;
-    xcd_tile(blockIdx.x, ntiles, mi, ni);
-    if (mi * ntiles >= n_items[which]) return;
+    if constexpr (GATEUP) {
+        if (!xcd_tile_contig(blockIdx.x, ntiles, n_items[which] / ntiles, mi, ni)) return;
+    } else {
+        xcd_tile(blockIdx.x, ntiles, mi, ni);
+        if (mi * ntiles >= n_items[which]) return;
+    }
     const int4 it = items[mi * ntiles + ni];
     const int grp = it.x, r0 = it.y, rows = it.z, nt = it.w;
     const int pbase = off[grp] + r0;
