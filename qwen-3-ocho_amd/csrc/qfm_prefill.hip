@@ -51,6 +51,7 @@ namespace qfm {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 128, BN = 128;
 constexpr int kCandMax = 64;
@@ -572,9 +573,11 @@ k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, 
         const int e = i * 64 + lane;
         float l = 0.0f;
 #pragma unroll
-        for (int q = 0; q < kRouterKS; q++) l += lg_approx[((size_t)q * T + t) * E + e];   // slice order
+        for (int q = 0; q < kRouterKS; q++) l += __builtin_nontemporal_load(&lg_approx[((size_t)q * T + t) * E + e]);   // slice order
         if (bias) l += bias[e];
-        lg_approx[(size_t)t * E + e] = l;          // the view's approximate logits
+        // the approximate logits, the x row and their write-back are touched once per
+        // token: nontemporal, so the router rows of the candidates stay in L2
+        __builtin_nontemporal_store(l, &lg_approx[(size_t)t * E + e]);          // the view's approximate logits
         const float b = cB * wnorm[e] + 1e-6f * (fabsf(l) + (bias ? fabsf(bias[e]) : 0.0f) + 1.0f);
         lo[i] = l - b;
         hi[i] = l + b;
@@ -625,7 +628,7 @@ k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, 
     float xv[NJ][4];                                // this token's x slice, canonical lane layout
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const uint2 p = *reinterpret_cast<const uint2 *>(xt + j * 256 + lane * 4);
+        const u32x2_t p = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(xt + j * 256 + lane * 4));
         xv[j][0] = bf16_lo(p.x); xv[j][1] = bf16_hi(p.x); xv[j][2] = bf16_lo(p.y); xv[j][3] = bf16_hi(p.y);
     }
     constexpr int CB = 4;                           // candidates per batch of loads
@@ -664,7 +667,10 @@ k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, 
         wts[(size_t)t * K + lane] = ek / denom;
     }
     if (g) {
-        const float gd = canon_dot_wave<NJ>(g, xt, lane);
+        const int e0[1] = {0};
+        float gdv[1];
+        canon_dot_wave_batch<NJ, 1>(g, H, e0, xv, lane, gdv);   // x from registers
+        const float gd = gdv[0];
         if (lane == 0) gam[t] = sigmoid(gd);
     }
 }
