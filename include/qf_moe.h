@@ -37,10 +37,8 @@ extern "C" {
  * QF5_NEMBD / QF5_NFF / QF5_NEXP / QF5_NEXPUSED (ocho/amd_server/
  * qf_nvfp4_wave64.h:54-57) and QF5_K (qf8_moe_i8.hip:5-7). Supported:
  * (hidden, inter) = (2048, 512) [benchmark shape] and (2560, 640) [reference
- * checkpoint]; n_experts in {64, 128, 256, 512, 1024}; 1 <= top_k <= 16.
- * The router and top-K entry points run at every accepted expert count; the
- * fused layer forward (qfm_moe_forward*, every M) needs n_experts == 512, the
- * reference's value, and returns -2 with a message otherwise. */
+ * checkpoint]; n_experts == 512 (the reference's QF5_NEXP, which every path
+ * here is built for; other counts are rejected); 1 <= top_k <= 16. */
 typedef struct {
     int hidden;        /* H */
     int inter;         /* I: expert intermediate size */
@@ -135,14 +133,18 @@ int qfm_topk(const float *logits, int M, int *sel, float *wts, hipStream_t s);
 /* ------------------------------------------------------------------------ */
 /* INT8 routed experts, one row (M=1). */
 /* hidden[k][I] = silu(sg * Wg.x) * (su * Wu.x) for the nexp experts sel_ids[0..nexp).
- * x: fp32 [H]. x8q/x8s are accepted for signature compatibility and not
- * written: this library dequantizes the weights in registers against the
- * exact activations (no activation quantization).
+ * The activations are X8 rows, as in the reference (qf8_moe_i8.hip:416-421):
+ * x8q int8 [H] codes with x8s fp32 [H/32] block scales (value = code * scale,
+ * dequantized in registers). quant_x != 0: x (fp32 [H]) is quantized into
+ * x8q/x8s first (qf8_i8_x8's rule); quant_x == 0: x8q/x8s already hold the
+ * caller's X8 row and x is not read (may be NULL).
  * Replaces qf8_i8_gateup_m1 (ocho/amd_server/qf8_moe_i8.h:41-42). */
 void qf8_i8_gateup_m1(const Qf4ExpCache *c, const float *x, int8_t *x8q, float *x8s,
                       float *hidden, const int *sel_ids, int nexp, int quant_x, hipStream_t s);
 /* y[H] = sum_k wts[k] * sd * Wd.hidden[k] in fixed k order; y is SEEDED
- * (overwritten, one writer per row). h8q/h8s unused as above.
+ * (overwritten, one writer per row). h8q/h8s are accepted and not written:
+ * the hidden vectors stay fp32 (staged as fp16 chunks with a power-of-two
+ * scale per 16 values) instead of the reference's X8 re-quantization.
  * Replaces qf8_i8_down_m1 (qf8_moe_i8.h:45-46). */
 void qf8_i8_down_m1(const Qf4ExpCache *c, const float *hidden, int8_t *h8q, float *h8s,
                     const float *wts, const int *sel_ids, float *y, int nexp, hipStream_t s);
@@ -248,6 +250,50 @@ int qf8_i8_shexp_rows(const Qf8I8Mat *gate, const Qf8I8Mat *up, const Qf8I8Mat *
                       int T, hipStream_t s);
 
 /* ------------------------------------------------------------------------ */
+/* Validated twins of the reference's void launchers (the error convention of
+ * ocho/amd_server/qf8_moe_i8.h:34-37 extended to every launcher): the same
+ * arguments and work, returning 0, -1 (a rejected argument: nothing was
+ * launched), -2 (unsupported shape configuration) or -3 (launch failure). The
+ * void forms call these and leave the code in the error latch. */
+int qf_rtr_gemv_launch_ex(const uint16_t *router, const float *x, float *logits, hipStream_t s);
+int qf_rtr_topk10_launch_ex(const float *logits, int *sel_ids, float *wts, hipStream_t s);
+int qf_rtr_topk10_rows_launch_ex(const float *logits, int *sel_ids, float *wts, int T, hipStream_t s);
+int qf8_i8_gateup_m1_ex(const Qf4ExpCache *c, const float *x, int8_t *x8q, float *x8s,
+                        float *hidden, const int *sel_ids, int nexp, int quant_x, hipStream_t s);
+int qf8_i8_down_m1_ex(const Qf4ExpCache *c, const float *hidden, int8_t *h8q, float *h8s,
+                      const float *wts, const int *sel_ids, float *y, int nexp, hipStream_t s);
+int qf8_i8_x8_ex(const float *x, int8_t *q, float *sc, int n, hipStream_t s);
+int qf8_i8_csr_build_ex(const int *sel, const float *wt, int T, int *exp_slot, int *exp_ptr,
+                        int *pair_tok, float *pair_wt, int *counts, hipStream_t s);
+int qf8_i8_experts_chunk_ex(const Qf4ExpCache *c, const int8_t *xq, const float *xs,
+                            float *hidden, int8_t *h8q, float *h8s,
+                            const int *exp_slot, const int *exp_ptr, const int *pair_tok,
+                            const float *pair_wt, const int *n_exp_dev, int n_exp_max,
+                            int n_pairs_max, const int *sel, float *part, int T, float *y, hipStream_t s);
+int qf5_nvfp4_moe_all_ex(const uint8_t *Wg, const uint8_t *Sg, const uint8_t *Wu, const uint8_t *Su,
+                         const uint8_t *Wd, const uint8_t *Sd, const float *x, float *hidden, float *y,
+                         const float *s2g_dev, const float *s2u_dev, const float *s2d_dev, const float *wts,
+                         const int *sel_ids, const int *slot_ids, int nexp, hipStream_t stream);
+int qf5_nvfp4_gateup_all_launch_ex(const uint8_t *Wg, const uint8_t *Sg, const uint8_t *Wu, const uint8_t *Su,
+                                   const float *x, float *hidden, const float *s2g_dev, const float *s2u_dev,
+                                   const int *sel_ids, const int *slot_ids, int nexp, hipStream_t stream);
+int qf5_nvfp4_downacc_all_launch_ex(const uint8_t *Wd, const uint8_t *Sd, const float *hidden, const float *wts,
+                                    float *y, const float *s2d_dev, const int *sel_ids, const int *slot_ids,
+                                    int nexp, hipStream_t stream);
+int qf5_m8_gateup_ex(const uint8_t *Wg, const uint8_t *Sg, const uint8_t *Wu, const uint8_t *Su,
+                     const float *s2g_res, const float *s2u_res, const float *x, float *hidden,
+                     const Qf5M8Route *rt, hipStream_t stream);
+int qf5_m8_downacc_ex(const uint8_t *Wd, const uint8_t *Sd, const float *s2d_res, const float *hidden,
+                      float *y_partial, const Qf5M8Route *rt, hipStream_t stream);
+int qf5_m8_build_csr_ex(const int *sel_dev, const float *wt_dev, int M, int K, int card, int epc, int il,
+                        int *exp_slot, int *exp_ptr, int *pair_tok, float *pair_wt, int *counts, hipStream_t s);
+int qf5_m8_reduce4_ex(float *y_out, const float *y0, const float *y1, const float *y2, const float *y3,
+                      int n, hipStream_t stream);
+int qf8_i8_shexp_m1_ex(const Qf8I8Mat *gate, const Qf8I8Mat *up, const Qf8I8Mat *gate_inp,
+                       const Qf8I8Mat *down, const int8_t *xq, const float *xs, float *eg, float *eu,
+                       float *g1, float *ed, int8_t *e8q, float *e8s, float *y2560, hipStream_t s);
+
+/* ------------------------------------------------------------------------ */
 /* Fused MoE layer (this library's entry point for the whole path). */
 enum { QFM_FMT_INT8 = 0, QFM_FMT_NVFP4 = 1 };
 typedef struct {
@@ -262,13 +308,16 @@ typedef struct {
 /* Workspace for M rows (device memory, caller-owned, >= 256-byte aligned). */
 size_t qfm_workspace_bytes(int M);
 /* For M > 8 (prefill) logits is [M][E] of the MFMA router GEMM (the exact
- * canonical logits are computed only for the selection candidates) and
- * hidden is NULL. */
+ * canonical logits are computed only for the selection candidates), hidden is
+ * NULL and counters points at {tokens whose candidate set overflowed and had
+ * every logit recomputed, gate/up work items, down work items} (int, device
+ * memory; NULL for M <= 8). */
 typedef struct {
     float *logits;   /* [M][E+1]: router logits; column E = <sh_gate_inp, x> */
     int   *sel;      /* [M][K] */
     float *wts;      /* [M][K] */
     float *hidden;   /* routed / shared intermediate activations */
+    int   *counters; /* prefill: {n_fallback, n_items_gateup, n_items_down}; else NULL */
 } qfm_ws_view;
 int qfm_workspace_view(void *ws, int M, qfm_ws_view *v);
 

@@ -122,7 +122,7 @@ int qfm_init(const qfm_config *cfg) {
     if (!cfg) { set_error(-1, "qfm_init: null config"); return -1; }
     const bool shape = (cfg->hidden == 2048 && cfg->inter == 512) || (cfg->hidden == 2560 && cfg->inter == 640);
     const int E = cfg->n_experts;
-    const bool e_ok = E == 64 || E == 128 || E == 256 || E == 512 || E == 1024;
+    const bool e_ok = E == 512;   // the reference's expert count; every path is built for it
     if (!shape || !e_ok || cfg->top_k < 1 || cfg->top_k > 16 || cfg->top_k > E) {
         set_error(-1, "qfm_init: unsupported configuration H=%d I=%d E=%d K=%d", cfg->hidden, cfg->inter, E, cfg->top_k);
         return -1;
@@ -168,17 +168,29 @@ size_t qfm_sizeof(int which) {
 }
 
 // ---- router ----------------------------------------------------------------
+// Every reference-named void launcher has an _ex twin returning 0 or a
+// negative code (-1 rejected argument, -2 unsupported shape, -3 launch
+// failure); the void form calls it and leaves the code in the error latch.
+int qf_rtr_gemv_launch_ex(const uint16_t *router, const float *x, float *logits, hipStream_t s) {
+    if (!router || !x || !logits) { set_error(-1, "qf_rtr_gemv_launch: null pointer"); return -1; }
+    return launch_router_bf16w(router, x, logits, s);
+}
 void qf_rtr_gemv_launch(const uint16_t *router, const float *x, float *logits, hipStream_t s) {
-    if (!router || !x || !logits) { set_error(-1, "qf_rtr_gemv_launch: null pointer"); return; }
-    launch_router_bf16w(router, x, logits, s);
+    (void)qf_rtr_gemv_launch_ex(router, x, logits, s);
+}
+int qf_rtr_topk10_launch_ex(const float *logits, int *sel_ids, float *wts, hipStream_t s) {
+    if (!logits || !sel_ids || !wts) { set_error(-1, "qf_rtr_topk10_launch: null pointer"); return -1; }
+    return launch_topk(logits, g_cfg.E, 1, sel_ids, wts, s);
 }
 void qf_rtr_topk10_launch(const float *logits, int *sel_ids, float *wts, hipStream_t s) {
-    if (!logits || !sel_ids || !wts) { set_error(-1, "qf_rtr_topk10_launch: null pointer"); return; }
-    launch_topk(logits, g_cfg.E, 1, sel_ids, wts, s);
+    (void)qf_rtr_topk10_launch_ex(logits, sel_ids, wts, s);
+}
+int qf_rtr_topk10_rows_launch_ex(const float *logits, int *sel_ids, float *wts, int T, hipStream_t s) {
+    if (!logits || !sel_ids || !wts || T < 1) { set_error(-1, "qf_rtr_topk10_rows_launch: bad arguments"); return -1; }
+    return launch_topk(logits, g_cfg.E, T, sel_ids, wts, s);
 }
 void qf_rtr_topk10_rows_launch(const float *logits, int *sel_ids, float *wts, int T, hipStream_t s) {
-    if (!logits || !sel_ids || !wts || T < 1) { set_error(-1, "qf_rtr_topk10_rows_launch: bad arguments"); return; }
-    launch_topk(logits, g_cfg.E, T, sel_ids, wts, s);
+    (void)qf_rtr_topk10_rows_launch_ex(logits, sel_ids, wts, T, s);
 }
 int qfm_router_logits(const float *W, const float *bias, const uint16_t *x, int M, float *logits, hipStream_t s) {
     if (!W || !x || !logits || M < 1) { set_error(-1, "qfm_router_logits: bad arguments"); return -1; }
@@ -190,16 +202,34 @@ int qfm_topk(const float *logits, int M, int *sel, float *wts, hipStream_t s) {
 }
 
 // ---- INT8 M=1 (reference signatures) ------------------------------------------
+// gate/up reads its activations as X8 rows (x8q: H int8 codes, x8s: H/32 fp32
+// scales), as the reference does (qf8_moe_i8.hip:416-421): quant_x != 0
+// quantizes x into them first, quant_x == 0 uses what the caller left there
+// (x is not read and may be null).
+int qf8_i8_gateup_m1_ex(const Qf4ExpCache *c, const float *x, int8_t *x8q, float *x8s, float *hidden,
+                        const int *sel_ids, int nexp, int quant_x, hipStream_t s) {
+    if (!x8q || !x8s || (quant_x && !x)) {
+        set_error(-1, "qf8_i8_gateup_m1: needs x8q/x8s (and x when quant_x)"); return -1;
+    }
+    if (quant_x) {
+        const int rc = launch_x8(x, x8q, x8s, g_cfg.H, s);
+        if (rc) return rc;
+    }
+    return launch_i8_gateup_m1(c, nullptr, nullptr, nullptr, const_cast<int *>(sel_ids), nullptr, nexp, hidden, s,
+                               nullptr, nullptr, x8q, x8s);
+}
 void qf8_i8_gateup_m1(const Qf4ExpCache *c, const float *x, int8_t *x8q, float *x8s, float *hidden,
                       const int *sel_ids, int nexp, int quant_x, hipStream_t s) {
-    (void)x8q; (void)x8s; (void)quant_x;
-    if (!x) { set_error(-1, "qf8_i8_gateup_m1: null x"); return; }
-    launch_i8_gateup_m1(c, nullptr, x, nullptr, const_cast<int *>(sel_ids), nullptr, nexp, hidden, s);
+    (void)qf8_i8_gateup_m1_ex(c, x, x8q, x8s, hidden, sel_ids, nexp, quant_x, s);
+}
+int qf8_i8_down_m1_ex(const Qf4ExpCache *c, const float *hidden, int8_t *h8q, float *h8s, const float *wts,
+                      const int *sel_ids, float *y, int nexp, hipStream_t s) {
+    (void)h8q; (void)h8s;
+    return launch_i8_down_m1(c, hidden, wts, sel_ids, nexp, nullptr, nullptr, y, nullptr, s);
 }
 void qf8_i8_down_m1(const Qf4ExpCache *c, const float *hidden, int8_t *h8q, float *h8s, const float *wts,
                     const int *sel_ids, float *y, int nexp, hipStream_t s) {
-    (void)h8q; (void)h8s;
-    launch_i8_down_m1(c, hidden, wts, sel_ids, nexp, nullptr, nullptr, y, nullptr, s);
+    (void)qf8_i8_down_m1_ex(c, hidden, h8q, h8s, wts, sel_ids, y, nexp, s);
 }
 
 // ---- fused layer ---------------------------------------------------------------
@@ -211,7 +241,7 @@ size_t qfm_workspace_bytes(int M) {
 int qfm_workspace_view(void *ws, int M, qfm_ws_view *v) {
     if (!ws || !v || M < 1) return -1;
     if (M > 8) {
-        prefill_ws_view(ws, M, &v->logits, &v->sel, &v->wts);
+        prefill_ws_view(ws, M, &v->logits, &v->sel, &v->wts, &v->counters);
         v->hidden = nullptr;
         return 0;
     }
@@ -221,6 +251,7 @@ int qfm_workspace_view(void *ws, int M, qfm_ws_view *v) {
     v->sel = reinterpret_cast<int *>(b + w.sel);
     v->wts = reinterpret_cast<float *>(b + w.wts);
     v->hidden = reinterpret_cast<float *>(b + w.hidden);
+    v->counters = nullptr;
     return 0;
 }
 
@@ -245,6 +276,10 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
     if (ws_bytes < qfm_workspace_bytes(M)) {
         set_error(-1, "qfm_moe_forward: workspace too small (%zu < %zu)", ws_bytes, qfm_workspace_bytes(M)); return -1;
     }
+    // a gated shared expert needs its gate vector on every path (prefill included)
+    if (L->sh_gate.w && g_cfg.gated && !L->sh_gate_inp) {
+        set_error(-1, "qfm_moe_forward: gated shared expert needs sh_gate_inp"); return -1;
+    }
     if (M > 8) return launch_prefill(L, x, M, y, ws, g_cfg.gated, s);
     const WsLayout w = ws_layout(M);
     const Cfg &c = g_cfg;
@@ -256,8 +291,7 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
     int *csr = reinterpret_cast<int *>(b + w.csr);
     float *part = reinterpret_cast<float *>(b + w.part);
     const bool has_sh = L->sh_gate.w != nullptr;
-    const float *g = (has_sh && c.gated && L->sh_gate_inp) ? L->sh_gate_inp : nullptr;
-    if (has_sh && c.gated && !g) { set_error(-1, "qfm_moe_forward: gated shared expert needs sh_gate_inp"); return -1; }
+    const float *g = (has_sh && c.gated) ? L->sh_gate_inp : nullptr;
     ShPtrs shp{};
     if (has_sh) {
         shp.qg = L->sh_gate.w; shp.qu = L->sh_up.w; shp.qd = L->sh_down.w;

@@ -9,9 +9,13 @@
 // Differences from the reference, all in the direction of more exact
 // arithmetic: hidden vectors are kept in fp32 between gate/up and down (the
 // reference re-quantizes them to X8; h8q/h8s/e8q/e8s are accepted and not
-// written), and E4M3 block scales are decoded by the gfx950 fp8 convert
-// instruction (0x7F decodes to NaN there, +Inf in the reference; checkpoints
-// never store 0x7F).
+// written). E4M3 block scales are decoded from the byte with integer ops
+// exactly as the reference does (e4m3_scale: e = byte >> 3, so bytes >= 0x80
+// are large unsigned scales, and 0x7F is +inf), not by the OCP fp8 convert.
+//
+// Every reference-named void launcher has an _ex twin that returns 0, -1 (a
+// rejected argument: nothing launched), -2 (unsupported shape) or -3 (launch
+// failure); the void form calls it and leaves the code in the error latch.
 #include "qfm_dev.h"
 #include "qfm_internal.h"
 
@@ -494,53 +498,83 @@ k_cx_shexp_down(Qf8I8Mat down, const float *__restrict__ eg, const float *__rest
     }
 }
 
-// ---- NVFP4 -> INT8 arena conversion (qf8_moe_i8.hip:146-195): value k of a row
-// = e2m1(nibble k) * ue4m3(scale byte k/16) * s2 (in that order), per-row scale
-// absmax * (1/127) (1 for an all-zero row), code rint(v * (1/scale)) clamped to
-// +-127. grid (rows, slots), K <= 2560.
+// ---- NVFP4 -> INT8 arena conversion (semantics of qf8_moe_i8.hip:146-195):
+// value k of a row = e2m1(code k) * ue4m3(block scale k/16) * s2, in that
+// order; row scale = absmax * (1/127) (1 for an all-zero row); code =
+// rint(value * (1/scale)) clamped to +-127. One wave per row: lane l takes the
+// 16-byte chunks l, l + 64, ... of the packed row (32 codes and their two
+// block scales each), decodes them with the gfx950 fp4 convert at unit scale
+// (exact e2m1 values), reduces the row maximum with DPP and writes 32 codes
+// per chunk as two 16-byte stores. CPL = chunks per lane (K <= 2048: 1).
+template <int CPL>
 __global__ void __launch_bounds__(256)
-k_cx_nvfp4_to_i8(const uint8_t *__restrict__ W, const uint8_t *__restrict__ S, const float *__restrict__ s2,
-                 int rows, int K, int8_t *__restrict__ Wo, float *__restrict__ So) {
-    constexpr int NV = 10;
-    __shared__ float red[4];
-    const int slot = blockIdx.y, row = blockIdx.x;
-    const uint8_t *wr = W + (size_t)slot * ((size_t)rows * K / 2) + (size_t)row * (K / 2);
-    const uint8_t *sr = S + (size_t)slot * ((size_t)rows * K / 16) + (size_t)row * (K / 16);
-    const float sc2 = s2[slot];
-    float v[NV];
-    float mx = 0.0f;
+k_f4_rows_to_i8(const uint8_t *__restrict__ W, const uint8_t *__restrict__ S, const float *__restrict__ s2,
+                int rows, int K, int8_t *__restrict__ Wo, float *__restrict__ So) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), slot = blockIdx.y;
+    if (row >= rows) return;                              // wave-uniform
+    const size_t rs = (size_t)slot * rows + row;          // row index in the slot-major arena
+    const int nch = K / 32;
+    const float gsc = s2[slot];
+    float val[CPL][32];
+    float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int k = threadIdx.x + i * 256;
-        v[i] = 0.0f;
-        if (k < K) {
-            const uint32_t byte = wr[k >> 1];
-            const uint32_t nib = (k & 1) ? (byte >> 4) : (byte & 15u);
-            v[i] = e2m1(nib) * e4m3_scale(sr[k >> 4]) * sc2;
-            mx = fmaxf(mx, fabsf(v[i]));
+    for (int c = 0; c < CPL; c++) {
+        const int ch = c * 64 + lane;
+        if (ch < nch) {
+            const uint4 w = *reinterpret_cast<const uint4 *>(W + rs * (K / 2) + (size_t)ch * 16);
+            const uint32_t sb = *reinterpret_cast<const uint16_t *>(S + rs * (K / 16) + (size_t)ch * 2);
+            const float bs[2] = {e4m3_scale(sb & 0xFFu), e4m3_scale(sb >> 8)};
+            const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {                 // word q holds codes 8q .. 8q + 7
+                const f32x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd[q], 1.0f, 0);
+                const f32x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd[q], 1.0f, 1);
+                const f32x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd[q], 1.0f, 2);
+                const f32x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd[q], 1.0f, 3);
+                const float e[8] = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+                const float b = bs[q >> 1];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const float v = (e[u] * b) * gsc;
+                    val[c][8 * q + u] = v;
+                    amax = fmaxf(amax, fabsf(v));
+                }
+            }
         }
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, WAVE));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    const float bm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float scale = bm > 0.0f ? bm * (1.0f / 127.0f) : 1.0f;
+    amax = group_max<64>(amax);
+    const float scale = amax > 0.0f ? amax * (1.0f / 127.0f) : 1.0f;
     const float inv = 1.0f / scale;
-    int8_t *wo = Wo + (size_t)slot * ((size_t)rows * K) + (size_t)row * K;
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int k = threadIdx.x + i * 256;
-        if (k < K) {
-            int q = (int)rintf(v[i] * inv);
-            q = q > 127 ? 127 : (q < -127 ? -127 : q);
-            wo[k] = (int8_t)q;
+    for (int c = 0; c < CPL; c++) {
+        const int ch = c * 64 + lane;
+        if (ch < nch) {
+            uint32_t pk[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int code = min(127, max(-127, (int)rintf(val[c][4 * q + u] * inv)));
+                    word |= ((uint32_t)code & 0xFFu) << (8 * u);
+                }
+                pk[q] = word;
+            }
+            uint4 *dst = reinterpret_cast<uint4 *>(Wo + rs * K + (size_t)ch * 32);
+            dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
         }
     }
-    if (threadIdx.x == 0) So[(size_t)slot * rows + row] = scale;
+    if (lane == 0) So[rs] = scale;
 }
 
 // ---- host helpers ------------------------------------------------------------------
+int launch_x8(const float *x, int8_t *q, float *sc, int n, hipStream_t s) {
+    hipLaunchKernelGGL(k_x8, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, q, sc, n);
+    return check_launch("qf8_i8_x8");
+}
+
 static bool shape_ok(const char *who) {
     if (shape_2048() || shape_2560()) return true;
     set_error(-2, "%s: (hidden, inter) must be (2048, 512) or (2560, 640)", who);
@@ -558,36 +592,44 @@ using namespace qfm;
 
 extern "C" {
 
-void qf8_i8_x8(const float *x, int8_t *q, float *sc, int n, hipStream_t s) {
-    if (!x || !q || !sc || n < 32 || n % 32) { set_error(-1, "qf8_i8_x8: need n a positive multiple of 32"); return; }
-    hipLaunchKernelGGL(k_x8, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, q, sc, n);
-    check_launch("qf8_i8_x8");
+int qf8_i8_x8_ex(const float *x, int8_t *q, float *sc, int n, hipStream_t s) {
+    if (!x || !q || !sc || n < 32 || n % 32) { set_error(-1, "qf8_i8_x8: need n a positive multiple of 32"); return -1; }
+    return launch_x8(x, q, sc, n, s);
 }
 
-void qf8_i8_csr_build(const int *sel, const float *wt, int T, int *exp_slot, int *exp_ptr, int *pair_tok,
-                      float *pair_wt, int *counts, hipStream_t s) {
+void qf8_i8_x8(const float *x, int8_t *q, float *sc, int n, hipStream_t s) {
+    (void)qf8_i8_x8_ex(x, q, sc, n, s);
+}
+
+int qf8_i8_csr_build_ex(const int *sel, const float *wt, int T, int *exp_slot, int *exp_ptr, int *pair_tok,
+                         float *pair_wt, int *counts, hipStream_t s) {
     const int K = g_cfg.K, E = g_cfg.E;
     if (!sel || !wt || !exp_slot || !exp_ptr || !pair_tok || !pair_wt || !counts || T < 1 || E > 1024 ||
         (long)T * K > (1L << 30)) {
-        set_error(-1, "qf8_i8_csr_build: bad arguments"); return;
+        set_error(-1, "qf8_i8_csr_build: bad arguments"); return -1;
     }
     const int P = T * K;
     hipLaunchKernelGGL(k_cb_count, dim3(1), dim3(1024), 0, s, sel, P, E, exp_slot, exp_ptr, counts);
     hipLaunchKernelGGL(k_cb_scatter, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, s, sel, wt, P, K, E, exp_slot,
                        exp_ptr, counts, pair_tok, pair_wt);
-    check_launch("qf8_i8_csr_build");
+    return check_launch("qf8_i8_csr_build");
 }
 
-void qf8_i8_experts_chunk(const Qf4ExpCache *c, const int8_t *xq, const float *xs, float *hidden, int8_t *h8q,
-                          float *h8s, const int *exp_slot, const int *exp_ptr, const int *pair_tok,
-                          const float *pair_wt, const int *n_exp_dev, int n_exp_max, int n_pairs_max, const int *sel,
-                          float *part, int T, float *y, hipStream_t s) {
+void qf8_i8_csr_build(const int *sel, const float *wt, int T, int *exp_slot, int *exp_ptr, int *pair_tok,
+                      float *pair_wt, int *counts, hipStream_t s) {
+    (void)qf8_i8_csr_build_ex(sel, wt, T, exp_slot, exp_ptr, pair_tok, pair_wt, counts, s);
+}
+
+int qf8_i8_experts_chunk_ex(const Qf4ExpCache *c, const int8_t *xq, const float *xs, float *hidden, int8_t *h8q,
+                             float *h8s, const int *exp_slot, const int *exp_ptr, const int *pair_tok,
+                             const float *pair_wt, const int *n_exp_dev, int n_exp_max, int n_pairs_max, const int *sel,
+                             float *part, int T, float *y, hipStream_t s) {
     (void)h8q; (void)h8s; (void)n_pairs_max;
-    if (!shape_ok("qf8_i8_experts_chunk")) return;
+    if (!shape_ok("qf8_i8_experts_chunk")) return -2;
     if (!c || !c->i8_gate || !c->i8_up || !c->i8_down || !xq || !xs || !hidden || !exp_slot || !exp_ptr ||
         !pair_tok || !pair_wt || !n_exp_dev || !sel || !part || !y || T < 1 || n_exp_max < 1 ||
         n_exp_max > c->slots) {
-        set_error(-1, "qf8_i8_experts_chunk: bad arguments"); return;
+        set_error(-1, "qf8_i8_experts_chunk: bad arguments"); return -1;
     }
     const int K = g_cfg.K;
     QFM_SHAPE_DISPATCH({
@@ -599,75 +641,114 @@ void qf8_i8_experts_chunk(const Qf4ExpCache *c, const int8_t *xq, const float *x
                            K, part);
         hipLaunchKernelGGL(k_cx_combine, dim3((HH + 255) / 256, T), dim3(256), 0, s, part, K, HH, y);
     });
-    check_launch("qf8_i8_experts_chunk");
+    return check_launch("qf8_i8_experts_chunk");
+}
+
+void qf8_i8_experts_chunk(const Qf4ExpCache *c, const int8_t *xq, const float *xs, float *hidden, int8_t *h8q,
+                          float *h8s, const int *exp_slot, const int *exp_ptr, const int *pair_tok,
+                          const float *pair_wt, const int *n_exp_dev, int n_exp_max, int n_pairs_max, const int *sel,
+                          float *part, int T, float *y, hipStream_t s) {
+    (void)qf8_i8_experts_chunk_ex(c, xq, xs, hidden, h8q, h8s, exp_slot, exp_ptr, pair_tok, pair_wt, n_exp_dev, n_exp_max, n_pairs_max, sel, part, T, y, s);
+}
+
+int qf5_nvfp4_gateup_all_launch_ex(const uint8_t *Wg, const uint8_t *Sg, const uint8_t *Wu, const uint8_t *Su,
+                                    const float *x, float *hidden, const float *s2g_dev, const float *s2u_dev,
+                                    const int *sel_ids, const int *slot_ids, int nexp, hipStream_t stream) {
+    if (!shape_ok("qf5_nvfp4_gateup_all_launch")) return -2;
+    if (!Wg || !Sg || !Wu || !Su || !x || !hidden || !s2g_dev || !s2u_dev || !sel_ids || !slot_ids || nexp < 1 ||
+        nexp > kMaxSel) {
+        set_error(-1, "qf5_nvfp4_gateup_all_launch: bad arguments"); return -1;
+    }
+    const PairGroups pg{slot_ids, nullptr, nullptr, nullptr, sel_ids};
+    QFM_SHAPE_DISPATCH(hipLaunchKernelGGL((k_cx_gateup_f4<HH, II>), dim3(II / (256 / lpr_of(HH / 32)), nexp),
+                                          dim3(256), 0, stream, Wg, Sg, Wu, Su, s2g_dev, s2u_dev, x, hidden, pg));
+    return check_launch("qf5_nvfp4_gateup_all_launch");
 }
 
 void qf5_nvfp4_gateup_all_launch(const uint8_t *Wg, const uint8_t *Sg, const uint8_t *Wu, const uint8_t *Su,
                                  const float *x, float *hidden, const float *s2g_dev, const float *s2u_dev,
                                  const int *sel_ids, const int *slot_ids, int nexp, hipStream_t stream) {
-    if (!shape_ok("qf5_nvfp4_gateup_all_launch")) return;
-    if (!Wg || !Sg || !Wu || !Su || !x || !hidden || !s2g_dev || !s2u_dev || !sel_ids || !slot_ids || nexp < 1 ||
-        nexp > kMaxSel) {
-        set_error(-1, "qf5_nvfp4_gateup_all_launch: bad arguments"); return;
+    (void)qf5_nvfp4_gateup_all_launch_ex(Wg, Sg, Wu, Su, x, hidden, s2g_dev, s2u_dev, sel_ids, slot_ids, nexp, stream);
+}
+
+int qf5_nvfp4_downacc_all_launch_ex(const uint8_t *Wd, const uint8_t *Sd, const float *hidden, const float *wts,
+                                     float *y, const float *s2d_dev, const int *sel_ids, const int *slot_ids, int nexp,
+                                     hipStream_t stream) {
+    if (!shape_ok("qf5_nvfp4_downacc_all_launch")) return -2;
+    if (!Wd || !Sd || !hidden || !wts || !y || !s2d_dev || !sel_ids || !slot_ids || nexp < 1 || nexp > kMaxSel) {
+        set_error(-1, "qf5_nvfp4_downacc_all_launch: bad arguments"); return -1;
     }
-    const PairGroups pg{slot_ids, nullptr, nullptr, nullptr, sel_ids};
-    QFM_SHAPE_DISPATCH(hipLaunchKernelGGL((k_cx_gateup_f4<HH, II>), dim3(II / (256 / lpr_of(HH / 32)), nexp),
-                                          dim3(256), 0, stream, Wg, Sg, Wu, Su, s2g_dev, s2u_dev, x, hidden, pg));
-    check_launch("qf5_nvfp4_gateup_all_launch");
+    QFM_SHAPE_DISPATCH(hipLaunchKernelGGL((k_cx_down_seed_f4<HH, II>), dim3(HH / (256 / lpr_of(II / 32))), dim3(256),
+                                          0, stream, Wd, Sd, s2d_dev, hidden, wts, y, sel_ids, slot_ids, nexp));
+    return check_launch("qf5_nvfp4_downacc_all_launch");
 }
 
 void qf5_nvfp4_downacc_all_launch(const uint8_t *Wd, const uint8_t *Sd, const float *hidden, const float *wts,
                                   float *y, const float *s2d_dev, const int *sel_ids, const int *slot_ids, int nexp,
                                   hipStream_t stream) {
-    if (!shape_ok("qf5_nvfp4_downacc_all_launch")) return;
-    if (!Wd || !Sd || !hidden || !wts || !y || !s2d_dev || !sel_ids || !slot_ids || nexp < 1 || nexp > kMaxSel) {
-        set_error(-1, "qf5_nvfp4_downacc_all_launch: bad arguments"); return;
-    }
-    QFM_SHAPE_DISPATCH(hipLaunchKernelGGL((k_cx_down_seed_f4<HH, II>), dim3(HH / (256 / lpr_of(II / 32))), dim3(256),
-                                          0, stream, Wd, Sd, s2d_dev, hidden, wts, y, sel_ids, slot_ids, nexp));
-    check_launch("qf5_nvfp4_downacc_all_launch");
+    (void)qf5_nvfp4_downacc_all_launch_ex(Wd, Sd, hidden, wts, y, s2d_dev, sel_ids, slot_ids, nexp, stream);
+}
+
+int qf5_nvfp4_moe_all_ex(const uint8_t *Wg, const uint8_t *Sg, const uint8_t *Wu, const uint8_t *Su,
+                          const uint8_t *Wd, const uint8_t *Sd, const float *x, float *hidden, float *y,
+                          const float *s2g_dev, const float *s2u_dev, const float *s2d_dev, const float *wts,
+                          const int *sel_ids, const int *slot_ids, int nexp, hipStream_t stream) {
+    const int rc = qf5_nvfp4_gateup_all_launch_ex(Wg, Sg, Wu, Su, x, hidden, s2g_dev, s2u_dev, sel_ids, slot_ids, nexp,
+                                                  stream);
+    if (rc) return rc;
+    return qf5_nvfp4_downacc_all_launch_ex(Wd, Sd, hidden, wts, y, s2d_dev, sel_ids, slot_ids, nexp, stream);
 }
 
 void qf5_nvfp4_moe_all(const uint8_t *Wg, const uint8_t *Sg, const uint8_t *Wu, const uint8_t *Su,
                        const uint8_t *Wd, const uint8_t *Sd, const float *x, float *hidden, float *y,
                        const float *s2g_dev, const float *s2u_dev, const float *s2d_dev, const float *wts,
                        const int *sel_ids, const int *slot_ids, int nexp, hipStream_t stream) {
-    qf5_nvfp4_gateup_all_launch(Wg, Sg, Wu, Su, x, hidden, s2g_dev, s2u_dev, sel_ids, slot_ids, nexp, stream);
-    qf5_nvfp4_downacc_all_launch(Wd, Sd, hidden, wts, y, s2d_dev, sel_ids, slot_ids, nexp, stream);
+    (void)qf5_nvfp4_moe_all_ex(Wg, Sg, Wu, Su, Wd, Sd, x, hidden, y, s2g_dev, s2u_dev, s2d_dev, wts, sel_ids, slot_ids, nexp, stream);
+}
+
+int qf5_m8_gateup_ex(const uint8_t *Wg, const uint8_t *Sg, const uint8_t *Wu, const uint8_t *Su,
+                      const float *s2g_res, const float *s2u_res, const float *x, float *hidden, const Qf5M8Route *rt,
+                      hipStream_t stream) {
+    if (!shape_ok("qf5_m8_gateup")) return -2;
+    if (!Wg || !Sg || !Wu || !Su || !s2g_res || !s2u_res || !x || !hidden || !rt || !rt->n_exp_dev ||
+        !rt->exp_slot || !rt->exp_ptr || !rt->pair_tok || rt->n_exp_max < 1 || rt->n_exp_max > 65535) {
+        set_error(-1, "qf5_m8_gateup: bad arguments"); return -1;
+    }
+    const PairGroups pg{rt->exp_slot, rt->exp_ptr, rt->pair_tok, rt->n_exp_dev, nullptr};
+    QFM_SHAPE_DISPATCH(hipLaunchKernelGGL((k_cx_gateup_f4<HH, II>), dim3(II / (256 / lpr_of(HH / 32)), rt->n_exp_max),
+                                          dim3(256), 0, stream, Wg, Sg, Wu, Su, s2g_res, s2u_res, x, hidden, pg));
+    return check_launch("qf5_m8_gateup");
 }
 
 void qf5_m8_gateup(const uint8_t *Wg, const uint8_t *Sg, const uint8_t *Wu, const uint8_t *Su,
                    const float *s2g_res, const float *s2u_res, const float *x, float *hidden, const Qf5M8Route *rt,
                    hipStream_t stream) {
-    if (!shape_ok("qf5_m8_gateup")) return;
-    if (!Wg || !Sg || !Wu || !Su || !s2g_res || !s2u_res || !x || !hidden || !rt || !rt->n_exp_dev ||
-        !rt->exp_slot || !rt->exp_ptr || !rt->pair_tok || rt->n_exp_max < 1 || rt->n_exp_max > 65535) {
-        set_error(-1, "qf5_m8_gateup: bad arguments"); return;
-    }
-    const PairGroups pg{rt->exp_slot, rt->exp_ptr, rt->pair_tok, rt->n_exp_dev, nullptr};
-    QFM_SHAPE_DISPATCH(hipLaunchKernelGGL((k_cx_gateup_f4<HH, II>), dim3(II / (256 / lpr_of(HH / 32)), rt->n_exp_max),
-                                          dim3(256), 0, stream, Wg, Sg, Wu, Su, s2g_res, s2u_res, x, hidden, pg));
-    check_launch("qf5_m8_gateup");
+    (void)qf5_m8_gateup_ex(Wg, Sg, Wu, Su, s2g_res, s2u_res, x, hidden, rt, stream);
 }
 
-void qf5_m8_downacc(const uint8_t *Wd, const uint8_t *Sd, const float *s2d_res, const float *hidden,
-                    float *y_partial, const Qf5M8Route *rt, hipStream_t stream) {
-    if (!shape_ok("qf5_m8_downacc")) return;
+int qf5_m8_downacc_ex(const uint8_t *Wd, const uint8_t *Sd, const float *s2d_res, const float *hidden,
+                       float *y_partial, const Qf5M8Route *rt, hipStream_t stream) {
+    if (!shape_ok("qf5_m8_downacc")) return -2;
     if (!Wd || !Sd || !s2d_res || !hidden || !y_partial || !rt || !rt->n_exp_dev || !rt->exp_slot || !rt->exp_ptr ||
         !rt->pair_tok || !rt->pair_wt || rt->n_exp_max < 1 || rt->n_exp_max > 65535) {
-        set_error(-1, "qf5_m8_downacc: bad arguments"); return;
+        set_error(-1, "qf5_m8_downacc: bad arguments"); return -1;
     }
     const PairGroups pg{rt->exp_slot, rt->exp_ptr, rt->pair_tok, rt->n_exp_dev, nullptr};
     QFM_SHAPE_DISPATCH(hipLaunchKernelGGL((k_cx_down_atomic_f4<HH, II>), dim3(HH / (256 / lpr_of(II / 32)),
                                           rt->n_exp_max), dim3(256), 0, stream, Wd, Sd, s2d_res, hidden, rt->pair_wt,
                                           y_partial, pg));
-    check_launch("qf5_m8_downacc");
+    return check_launch("qf5_m8_downacc");
 }
 
-void qf5_m8_reduce4(float *y_out, const float *y0, const float *y1, const float *y2, const float *y3, int n,
-                    hipStream_t s) {
-    if (n < 0 || (n > 0 && (!y_out || !y0 || !y1 || !y2 || !y3))) { set_error(-1, "qf5_m8_reduce4: bad arguments"); return; }
-    if (n == 0) return;
+void qf5_m8_downacc(const uint8_t *Wd, const uint8_t *Sd, const float *s2d_res, const float *hidden,
+                    float *y_partial, const Qf5M8Route *rt, hipStream_t stream) {
+    (void)qf5_m8_downacc_ex(Wd, Sd, s2d_res, hidden, y_partial, rt, stream);
+}
+
+int qf5_m8_reduce4_ex(float *y_out, const float *y0, const float *y1, const float *y2, const float *y3, int n,
+                       hipStream_t s) {
+    if (n < 0 || (n > 0 && (!y_out || !y0 || !y1 || !y2 || !y3))) { set_error(-1, "qf5_m8_reduce4: bad arguments"); return -1; }
+    if (n == 0) return 0;
     const uintptr_t al = reinterpret_cast<uintptr_t>(y_out) | reinterpret_cast<uintptr_t>(y0) |
                          reinterpret_cast<uintptr_t>(y1) | reinterpret_cast<uintptr_t>(y2) |
                          reinterpret_cast<uintptr_t>(y3);
@@ -678,18 +759,28 @@ void qf5_m8_reduce4(float *y_out, const float *y0, const float *y1, const float 
         hipLaunchKernelGGL(k_cx_reduce4<false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y_out, y0, y1, y2,
                            y3, n);
     }
-    check_launch("qf5_m8_reduce4");
+    return check_launch("qf5_m8_reduce4");
+}
+
+void qf5_m8_reduce4(float *y_out, const float *y0, const float *y1, const float *y2, const float *y3, int n,
+                    hipStream_t s) {
+    (void)qf5_m8_reduce4_ex(y_out, y0, y1, y2, y3, n, s);
+}
+
+int qf5_m8_build_csr_ex(const int *sel_dev, const float *wt_dev, int M, int K, int card, int epc, int il, int *exp_slot,
+                         int *exp_ptr, int *pair_tok, float *pair_wt, int *counts, hipStream_t s) {
+    if (!sel_dev || !wt_dev || !exp_slot || !exp_ptr || !pair_tok || !pair_wt || !counts || M < 1 || K < 1 ||
+        M * K > 1024 || card < 0 || epc < 1 || il < 0 || (card + 1) * epc > 1024) {
+        set_error(-1, "qf5_m8_build_csr: bad arguments (M*K <= 1024, experts < 1024)"); return -1;
+    }
+    hipLaunchKernelGGL(k_m8_csr, dim3(1), dim3(1024), 0, s, sel_dev, wt_dev, M * K, K, card * epc, card * epc + epc,
+                       il * epc, exp_slot, exp_ptr, pair_tok, pair_wt, counts);
+    return check_launch("qf5_m8_build_csr");
 }
 
 void qf5_m8_build_csr(const int *sel_dev, const float *wt_dev, int M, int K, int card, int epc, int il, int *exp_slot,
                       int *exp_ptr, int *pair_tok, float *pair_wt, int *counts, hipStream_t s) {
-    if (!sel_dev || !wt_dev || !exp_slot || !exp_ptr || !pair_tok || !pair_wt || !counts || M < 1 || K < 1 ||
-        M * K > 1024 || card < 0 || epc < 1 || il < 0 || (card + 1) * epc > 1024) {
-        set_error(-1, "qf5_m8_build_csr: bad arguments (M*K <= 1024, experts < 1024)"); return;
-    }
-    hipLaunchKernelGGL(k_m8_csr, dim3(1), dim3(1024), 0, s, sel_dev, wt_dev, M * K, K, card * epc, card * epc + epc,
-                       il * epc, exp_slot, exp_ptr, pair_tok, pair_wt, counts);
-    check_launch("qf5_m8_build_csr");
+    (void)qf5_m8_build_csr_ex(sel_dev, wt_dev, M, K, card, epc, il, exp_slot, exp_ptr, pair_tok, pair_wt, counts, s);
 }
 
 static bool mat_ok(const Qf8I8Mat *m, int rows, int K) {
@@ -715,24 +806,35 @@ int qf8_i8_shexp_rows(const Qf8I8Mat *gate, const Qf8I8Mat *up, const Qf8I8Mat *
     return check_launch("qf8_i8_shexp_rows");
 }
 
+int qf8_i8_shexp_m1_ex(const Qf8I8Mat *gate, const Qf8I8Mat *up, const Qf8I8Mat *gate_inp, const Qf8I8Mat *down,
+                        const int8_t *xq, const float *xs, float *eg, float *eu, float *g1, float *ed, int8_t *e8q,
+                        float *e8s, float *y2560, hipStream_t s) {
+    return qf8_i8_shexp_rows(gate, up, gate_inp, down, xq, xs, eg, eu, g1, ed, e8q, e8s, y2560, 1, s);
+}
+
 void qf8_i8_shexp_m1(const Qf8I8Mat *gate, const Qf8I8Mat *up, const Qf8I8Mat *gate_inp, const Qf8I8Mat *down,
                      const int8_t *xq, const float *xs, float *eg, float *eu, float *g1, float *ed, int8_t *e8q,
                      float *e8s, float *y2560, hipStream_t s) {
-    qf8_i8_shexp_rows(gate, up, gate_inp, down, xq, xs, eg, eu, g1, ed, e8q, e8s, y2560, 1, s);
+    (void)qf8_i8_shexp_m1_ex(gate, up, gate_inp, down, xq, xs, eg, eu, g1, ed, e8q, e8s, y2560, s);
+}
+
+// one matrix of nslots slots: rows of K codes, four rows per block
+static void f4_rows_to_i8(const uint8_t *W, const uint8_t *S, const float *s2, int rows, int K, int nslots,
+                          int8_t *Wo, float *So, hipStream_t s) {
+    const dim3 grid((unsigned)((rows + 3) / 4), (unsigned)nslots);
+    if (K / 32 <= 64) hipLaunchKernelGGL(k_f4_rows_to_i8<1>, grid, dim3(256), 0, s, W, S, s2, rows, K, Wo, So);
+    else hipLaunchKernelGGL(k_f4_rows_to_i8<2>, grid, dim3(256), 0, s, W, S, s2, rows, K, Wo, So);
 }
 
 static int i8_build_range(Qf4ExpCache *c, int src_slot, int dst_slot, int s2_index, int nslots, hipStream_t s) {
     const int H = g_cfg.H, I = g_cfg.I;
     const size_t gw = (size_t)I * H;                 // elements per matrix (all three)
-    hipLaunchKernelGGL(k_cx_nvfp4_to_i8, dim3(I, nslots), dim3(256), 0, s, c->w_gate + src_slot * (gw / 2),
-                       c->s_gate + src_slot * (gw / 16), c->s2g_dev + s2_index, I, H, c->i8_gate + dst_slot * gw,
-                       c->i8s_gate + (size_t)dst_slot * I);
-    hipLaunchKernelGGL(k_cx_nvfp4_to_i8, dim3(I, nslots), dim3(256), 0, s, c->w_up + src_slot * (gw / 2),
-                       c->s_up + src_slot * (gw / 16), c->s2u_dev + s2_index, I, H, c->i8_up + dst_slot * gw,
-                       c->i8s_up + (size_t)dst_slot * I);
-    hipLaunchKernelGGL(k_cx_nvfp4_to_i8, dim3(H, nslots), dim3(256), 0, s, c->w_down + src_slot * (gw / 2),
-                       c->s_down + src_slot * (gw / 16), c->s2d_dev + s2_index, H, I, c->i8_down + dst_slot * gw,
-                       c->i8s_down + (size_t)dst_slot * H);
+    f4_rows_to_i8(c->w_gate + src_slot * (gw / 2), c->s_gate + src_slot * (gw / 16), c->s2g_dev + s2_index, I, H,
+                  nslots, c->i8_gate + dst_slot * gw, c->i8s_gate + (size_t)dst_slot * I, s);
+    f4_rows_to_i8(c->w_up + src_slot * (gw / 2), c->s_up + src_slot * (gw / 16), c->s2u_dev + s2_index, I, H, nslots,
+                  c->i8_up + dst_slot * gw, c->i8s_up + (size_t)dst_slot * I, s);
+    f4_rows_to_i8(c->w_down + src_slot * (gw / 2), c->s_down + src_slot * (gw / 16), c->s2d_dev + s2_index, H, I,
+                  nslots, c->i8_down + dst_slot * gw, c->i8s_down + (size_t)dst_slot * H, s);
     return check_launch("qf8_i8_build") ? -1 : 0;
 }
 

@@ -2,9 +2,10 @@
 //
 // Reference behaviour: k_i8_gateup_all / k_i8_downacc_all
 // (ocho/amd_server/qf8_moe_i8.hip:72-144) and the int8 shared expert
-// qf8_i8_shexp_m1 (ocho/amd_server/qf8_dense_i8.hip:346-358), with the
-// activations kept exact (bf16/fp32) instead of the reference's X8 int8
-// re-quantization.
+// qf8_i8_shexp_m1 (ocho/amd_server/qf8_dense_i8.hip:346-358). The fused
+// forward keeps the activations exact (bf16 x, fp16-chunked hidden) instead of
+// the reference's X8 int8 re-quantization; the reference-named gate/up entry
+// takes X8 rows as the reference does (qf8_moe_i8.hip:416-421).
 //
 // gate/up: grid (I/8, K), 256 threads; one 32-lane half-wave per weight
 // row. Lane l owns bytes [st*512 + 16l, +16) of the H-byte row for
@@ -14,9 +15,11 @@
 // row, so it is held in registers (no LDS). In the fused forward x arrives as
 // fp16 scaled per row (written by the router launch) and each code is widened
 // to fp16 (dot16_i8h: 1024 + (q ^ 0x80), one v_perm per two codes), the
-// 1152 * sum(x16) offset removed from the row total; with fp32 or bf16 x (the
-// reference-named entry) each code is used in offset-binary form q + 128 (one
-// v_cvt_f32_ubyte per code) and the accumulator starts at -128 * sum(x_slice).
+// 1152 * sum(x16) offset removed from the row total; with fp32 or bf16 x, or
+// X8 rows (int8 codes with one fp32 scale per 32 values, the reference-named
+// entry's input, dequantized in registers), each code is used in offset-binary
+// form q + 128 (one v_cvt_f32_ubyte per code) and the accumulator starts at
+// -128 * sum(x_slice).
 // When the launch carries the
 // router logits, every wave runs the top-K selection itself (the 2 KiB row of
 // logits is L2-resident), which removes a dependent launch from the decode
@@ -46,7 +49,8 @@ k_i8_gateup_m1(const int8_t *__restrict__ Qg, const int8_t *__restrict__ Qu,
                const uint16_t *__restrict__ xb, const float *__restrict__ xf,
                const float *__restrict__ logits, int *__restrict__ sel, float *__restrict__ wts,
                int K, int renorm, float *__restrict__ hidden, ShPtrs sh,
-               const uint4 *__restrict__ x16, const float2 *__restrict__ x16i) {
+               const uint4 *__restrict__ x16, const float2 *__restrict__ x16i,
+               const int8_t *__restrict__ x8q, const float *__restrict__ x8s) {
     constexpr int NST = H / 512;
     __shared__ __align__(16) unsigned long long s_tk[4][kTopkLds];
     const int job = blockIdx.y;
@@ -55,8 +59,23 @@ k_i8_gateup_m1(const int8_t *__restrict__ Qg, const int8_t *__restrict__ Qu,
     const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
     float xs[X16 ? 1 : NST][16];
     if constexpr (!X16) {
-        if (xb) load_x_slice_bf16<H>(xb, l, xs);
-        else load_x_slice_f32<H>(xf, l, xs);
+        if (x8q) {
+            // X8 rows: values [512 st + 16 l, +16) are codes of one 32-value block
+#pragma unroll
+            for (int st = 0; st < NST; st++) {
+                const int k0 = st * 512 + l * 16;
+                const uint4 q = *reinterpret_cast<const uint4 *>(x8q + k0);
+                const float sc = x8s[k0 >> 5];
+                // offset-binary widening (u - 128, exact), not a sign-extend + convert pair
+                const uint32_t d[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+#pragma unroll
+                for (int i = 0; i < 16; i++) xs[st][i] = ((float)((d[i >> 2] >> (8 * (i & 3))) & 0xFFu) - 128.0f) * sc;
+            }
+        } else if (xb) {
+            load_x_slice_bf16<H>(xb, l, xs);
+        } else {
+            load_x_slice_f32<H>(xf, l, xs);
+        }
     }
     int e = 0;
     if (shared_job) {
@@ -258,11 +277,12 @@ static bool down_dispatch_nj(int nj, bool has_sh, const Qf4ExpCache *c, const fl
 }
 
 int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *xf, const float *logits, int *sel,
-                        float *wts, int nexp, float *hidden, hipStream_t s, const ShPtrs *sh, const void *x16) {
+                        float *wts, int nexp, float *hidden, hipStream_t s, const ShPtrs *sh, const void *x16,
+                        const int8_t *x8q, const float *x8s) {
     if (!c || !c->i8_gate || !c->i8_up || !c->i8s_gate || !c->i8s_up) {
         set_error(-1, "i8_gateup_m1: arena has no INT8 gate/up"); return -1;
     }
-    if (nexp < 1 || nexp > 16 || (!xb && !xf && !x16) || !hidden || !sel || (logits && !wts)) {
+    if (nexp < 1 || nexp > 16 || (!xb && !xf && !x16 && !(x8q && x8s)) || !hidden || !sel || (logits && !wts)) {
         set_error(-1, "i8_gateup_m1: bad arguments"); return -1;
     }
     if (logits && (nexp != g_cfg.K || g_cfg.E != 512)) {
@@ -277,7 +297,7 @@ int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *x
     const float2 *xi = xh ? reinterpret_cast<const float2 *>(xh + g_cfg.H / 8) : nullptr;
 #define QFM_GU_M1(HH, II, X16)                                                                                  \
     hipLaunchKernelGGL((k_i8_gateup_m1<HH, II, 8, X16>), dim3(II / 8, jobs), block, 0, s, c->i8_gate, c->i8_up, \
-                       c->i8s_gate, c->i8s_up, xb, xf, logits, sel, wts, K, rn, hidden, sp, xh, xi)
+                       c->i8s_gate, c->i8s_up, xb, xf, logits, sel, wts, K, rn, hidden, sp, xh, xi, x8q, x8s)
     if (shape_2048()) {
         if (xh) QFM_GU_M1(2048, 512, true); else QFM_GU_M1(2048, 512, false);
     } else if (shape_2560()) {

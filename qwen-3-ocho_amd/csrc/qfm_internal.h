@@ -45,9 +45,13 @@ int launch_topk(const float *logits, int ld_logits, int M, int *sel, float *wts,
 // expert's hidden vector is computed too, into hidden row nexp.
 // With x16 != nullptr (launch_router_shared's fp16 row) x is read from there
 // and the codes are widened to fp16 (dot16_i8h); xb/xf are then unused.
+// With x8q/x8s != nullptr (X8 rows: int8 codes, one fp32 scale per 32 values)
+// x is read from there, dequantized in registers (value = code * scale).
 int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *xf, const float *logits,
                         int *sel, float *wts, int nexp, float *hidden, hipStream_t s, const ShPtrs *sh = nullptr,
-                        const void *x16 = nullptr);
+                        const void *x16 = nullptr, const int8_t *x8q = nullptr, const float *x8s = nullptr);
+// X8 quantizer (qf8_i8_x8): n a positive multiple of 32
+int launch_x8(const float *x, int8_t *q, float *sc, int n, hipStream_t s);
 // y = sum_k wts[k] * down_k(hidden[k]) (+ gamma * shared_down(hidden[nexp]) when
 // sh != nullptr: the shared expert's hidden vector follows the routed ones),
 // gamma = sigmoid(*gdot) when gdot != nullptr, 1 otherwise. Writes y32 and/or ybf.
@@ -70,7 +74,8 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
 size_t prefill_ws_bytes(int T);
 // y[t] = sum of the S owned partial slots part[t*S + k][H] in slot order (bf16 out)
 void launch_pf_combine(const float *part, int T, int S, int H, uint16_t *y, hipStream_t s);
-void prefill_ws_view(void *ws, int T, float **lg_approx, int **sel, float **wts);
+// ctr: {candidate overflows (tokens whose logits were all recomputed), gate/up items, down items}
+void prefill_ws_view(void *ws, int T, float **lg_approx, int **sel, float **wts, int **ctr);
 int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, void *ws, int gated, hipStream_t s);
 
 }  // namespace qfm

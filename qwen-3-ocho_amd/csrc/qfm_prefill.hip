@@ -612,12 +612,16 @@ k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, 
         off += __popcll(bb & ltm) << bt;
         total += __popcll(bb) << bt;
     }
-    const bool full = total > kCandMax;
+    // Without renormalization the weights divide by the softmax denominator over
+    // all E logits, so every logit is recomputed exactly (the M <= 8 path's
+    // denominator, bit for bit); a candidate overflow also takes every expert.
+    const bool overflow = total > kCandMax;
+    const bool full = overflow || !renorm;
     if (!full) {
 #pragma unroll
         for (int i = 0; i < EPL; i++)
             if (hi[i] >= tau) s_cand[wave][off++] = i * 64 + lane;
-    } else if (lane == 0) {
+    } else if (overflow && lane == 0) {
         atomicAdd(n_fallback, 1);
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -632,6 +636,9 @@ k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, 
         xv[j][0] = bf16_lo(p.x); xv[j][1] = bf16_hi(p.x); xv[j][2] = bf16_lo(p.y); xv[j][3] = bf16_hi(p.y);
     }
     constexpr int CB = 4;                           // candidates per batch of loads
+    float exl[EPL];                                 // full: exact logit of expert i * 64 + lane
+#pragma unroll
+    for (int i = 0; i < EPL; i++) exl[i] = 0.0f;
     for (int c0 = 0; c0 < nc; c0 += CB) {
         int eb[CB];
 #pragma unroll
@@ -646,6 +653,11 @@ k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, 
             if (c0 + q >= nc) break;
             float l = lb[q];
             if (bias) l = __fadd_rn(l, bias[eb[q]]);
+            if (full) {                             // keep it in the lane that owns expert eb[q]
+#pragma unroll
+                for (int i = 0; i < EPL; i++)
+                    if (eb[q] == i * 64 + lane) exl[i] = l;
+            }
             const unsigned long long key = topk_key(l, eb[q]);
             // insert into the sorted lane list: lanes with a smaller key shift down
             const unsigned long long prev = __shfl_up(best, 1, WAVE);
@@ -656,10 +668,10 @@ k_pf_select(const uint16_t *__restrict__ x, int T, const float *__restrict__ W, 
     const float mx = topk_key_value(__shfl(best, 0, WAVE));
     const float ek = lane < K ? __expf(topk_key_value(best) - mx) : 0.0f;
     float denom = __ockl_wfred_add_f32(ek);
-    if (!renorm) {
+    if (!renorm) {                                  // every logit is exact here (full)
         float s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < EPL; i++) s += __expf(lg_approx[(size_t)t * E + i * 64 + lane] - mx);
+        for (int i = 0; i < EPL; i++) s += __expf(exl[i] - mx);
         denom = __ockl_wfred_add_f32(s);
     }
     if (lane < K) {
@@ -1021,7 +1033,7 @@ size_t prefill_ws_bytes(int T) {
     return b;
 }
 
-void prefill_ws_view(void *ws, int T, float **lg, int **sel, float **wts) {
+void prefill_ws_view(void *ws, int T, float **lg, int **sel, float **wts, int **ctr) {
     const Cfg &c = g_cfg;
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     char *b = static_cast<char *>(ws);
@@ -1030,7 +1042,9 @@ void prefill_ws_view(void *ws, int T, float **lg, int **sel, float **wts) {
     b += al((size_t)c.E * 4);
     b += al((size_t)c.E * c.H * 2);
     *sel = reinterpret_cast<int *>(b); b += al((size_t)T * c.K * 4);
-    *wts = reinterpret_cast<float *>(b);
+    *wts = reinterpret_cast<float *>(b); b += al((size_t)T * c.K * 4);
+    b += al((size_t)T * 4);                // gam
+    *ctr = reinterpret_cast<int *>(b);     // {candidate overflows, gate/up items, down items}
 }
 
 int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, void *ws, int gated, hipStream_t s) {

@@ -65,7 +65,7 @@ class QfmSynthLayer(C.Structure):
 
 
 class QfmWsView(C.Structure):
-    _fields_ = [("logits", vp), ("sel", vp), ("wts", vp), ("hidden", vp)]
+    _fields_ = [("logits", vp), ("sel", vp), ("wts", vp), ("hidden", vp), ("counters", vp)]
 
 
 # name -> (restype, argtypes)
@@ -98,6 +98,23 @@ _SIGS = {
     "qf5_m8_reduce4": (None, [vp, vp, vp, vp, vp, C.c_int, vp]),
     "qf8_i8_shexp_m1": (None, [C.POINTER(Qf8I8Mat)] * 4 + [vp] * 9 + [vp]),
     "qf8_i8_shexp_rows": (C.c_int, [C.POINTER(Qf8I8Mat)] * 4 + [vp] * 9 + [C.c_int, vp]),
+    "qf_rtr_gemv_launch_ex": (C.c_int, [vp, vp, vp, vp]),
+    "qf_rtr_topk10_launch_ex": (C.c_int, [vp, vp, vp, vp]),
+    "qf_rtr_topk10_rows_launch_ex": (C.c_int, [vp, vp, vp, C.c_int, vp]),
+    "qf8_i8_gateup_m1_ex": (C.c_int, [C.POINTER(Qf4ExpCache), vp, vp, vp, vp, vp, C.c_int, C.c_int, vp]),
+    "qf8_i8_down_m1_ex": (C.c_int, [C.POINTER(Qf4ExpCache), vp, vp, vp, vp, vp, vp, C.c_int, vp]),
+    "qf8_i8_x8_ex": (C.c_int, [vp, vp, vp, C.c_int, vp]),
+    "qf8_i8_csr_build_ex": (C.c_int, [vp, vp, C.c_int, vp, vp, vp, vp, vp, vp]),
+    "qf8_i8_experts_chunk_ex": (C.c_int, [C.POINTER(Qf4ExpCache), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                          C.c_int, C.c_int, vp, vp, C.c_int, vp, vp]),
+    "qf5_nvfp4_moe_all_ex": (C.c_int, [vp] * 15 + [C.c_int, vp]),
+    "qf5_nvfp4_gateup_all_launch_ex": (C.c_int, [vp] * 10 + [C.c_int, vp]),
+    "qf5_nvfp4_downacc_all_launch_ex": (C.c_int, [vp] * 8 + [C.c_int, vp]),
+    "qf5_m8_gateup_ex": (C.c_int, [vp] * 8 + [C.POINTER(Qf5M8Route), vp]),
+    "qf5_m8_downacc_ex": (C.c_int, [vp] * 5 + [C.POINTER(Qf5M8Route), vp]),
+    "qf5_m8_build_csr_ex": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp, vp]),
+    "qf5_m8_reduce4_ex": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, vp]),
+    "qf8_i8_shexp_m1_ex": (C.c_int, [C.POINTER(Qf8I8Mat)] * 4 + [vp] * 9 + [vp]),
     "qfm_workspace_bytes": (C.c_size_t, [C.c_int]),
     "qfm_workspace_view": (C.c_int, [vp, C.c_int, C.POINTER(QfmWsView)]),
     "qfm_moe_forward": (C.c_int, [C.POINTER(QfmLayer), vp, C.c_int, vp, vp, C.c_size_t, vp]),

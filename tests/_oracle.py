@@ -229,3 +229,69 @@ def moe_layer(H, I, E, K, M, seed, layer, x_layer, x_row0=0, fmt=0, gated=1, ren
     rc = lib.orc_moe_layer(C.byref(cfg), M, ptr(x), ptr(logits), ptr(sel), ptr(w64), ptr(y64), ptr(ybf))
     assert rc == 0
     return dict(x=x, logits=logits, sel=sel, w=w64, y=y64, ybf=ybf)
+
+
+def _i8_expert_arrays(seed, layer, e, H, I):
+    """Generator arrays of INT8 expert e (the shared expert is e = E)."""
+    Qg = fill("i8", seed, layer, T_QG, e * I * H, I * H).reshape(I, H)
+    Qu = fill("i8", seed, layer, T_QU, e * I * H, I * H).reshape(I, H)
+    Qd = fill("i8", seed, layer, T_QD, e * H * I, H * I).reshape(H, I)
+    sg = fill("rowscale", seed, layer, T_SG, e * I, I)
+    su = fill("rowscale", seed, layer, T_SU, e * I, I)
+    sd = fill("rowscale", seed, layer, T_SD, e * H, H)
+    return Qg, sg, Qu, su, Qd, sd
+
+
+def _expert_fp64(seed, layer, e, H, I, fmt):
+    """Expert e's gate, up, down weights as fp64 matrices (exact values:
+    int8 * row scale, or e2m1 * e4m3 * s2 through orc_nvfp4_dequant)."""
+    if fmt == 0:
+        Qg, sg, Qu, su, Qd, sd = _i8_expert_arrays(seed, layer, e, H, I)
+        return (Qg.astype(np.float64) * sg.astype(np.float64)[:, None],
+                Qu.astype(np.float64) * su.astype(np.float64)[:, None],
+                Qd.astype(np.float64) * sd.astype(np.float64)[:, None])
+    IH = I * H
+    Fg = fill("fp4byte", seed, layer, T_FG, e * IH // 2, IH // 2)
+    Fu = fill("fp4byte", seed, layer, T_FU, e * IH // 2, IH // 2)
+    Fd = fill("fp4byte", seed, layer, T_FD, e * IH // 2, IH // 2)
+    Sg = fill("e4m3scale", seed, layer, T_FSG, e * IH // 16, IH // 16)
+    Su = fill("e4m3scale", seed, layer, T_FSU, e * IH // 16, IH // 16)
+    Sd = fill("e4m3scale", seed, layer, T_FSD, e * IH // 16, IH // 16)
+    return (nvfp4_dequant(Fg, Sg, 0.01, I, H), nvfp4_dequant(Fu, Su, 0.01, I, H), nvfp4_dequant(Fd, Sd, 0.01, H, I))
+
+
+def moe_layer_grouped(H, I, E, K, M, seed, layer, x_layer, x_row0=0, fmt=0, gated=1, renorm=1, use_bias=0, x=None,
+                      router=None):
+    """The whole layer (orc_moe_layer's definition) evaluated expert by expert:
+    every distinct expert's weights are dequantized once (the oracle's own
+    dequantization, exact in fp64) and applied to all of its tokens with fp64
+    matrix products, so a T = 8038 prefill is checked in seconds. Routing comes
+    from the oracle's router and top-K. x (bf16 bits [M][H]) overrides the
+    generated input rows and router (fp32 [E][H]) the generated router weights.
+    Same arithmetic as orc_moe_layer up to the order of fp64 summation (pinned
+    against it in tests/test_oracle_path.py)."""
+    if x is None:
+        x = fill("gauss_bf16", seed, x_layer, T_X, x_row0 * H, M * H).reshape(M, H)
+    W = fill("gauss", seed, layer, T_ROUTER, 0, E * H, 0.02).reshape(E, H) if router is None else router
+    b = fill("gauss", seed, layer, T_BIAS, 0, E, 1.5) if use_bias else None
+    logits = router_logits(W, x, b)
+    sel, w64, _ = topk(logits, K, renorm)
+    X = bf16_to_f32(x).astype(np.float64)
+    y = np.zeros((M, H), np.float64)
+
+    def expert_out(Wg, Wu, Wd, Xe):
+        g = Xe @ Wg.T
+        u = Xe @ Wu.T
+        return (g / (1.0 + np.exp(-g)) * u) @ Wd.T
+
+    for e in np.unique(sel):
+        rows, ks = np.nonzero(sel == e)
+        Wg, Wu, Wd = _expert_fp64(seed, layer, int(e), H, I, fmt)
+        y[rows] += w64[rows, ks][:, None] * expert_out(Wg, Wu, Wd, X[rows])
+    Wg, Wu, Wd = _expert_fp64(seed, layer, E, H, I, 0)          # shared expert: INT8, index E
+    ys = expert_out(Wg, Wu, Wd, X)
+    if gated:
+        g = fill("gauss", seed, layer, T_SHGATE, 0, H, 0.02).astype(np.float64)
+        ys *= (1.0 / (1.0 + np.exp(-(X @ g))))[:, None]
+    y += ys
+    return dict(x=x, logits=logits, sel=sel, w=w64, y=y)

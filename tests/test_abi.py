@@ -81,7 +81,7 @@ def test_config_validation_without_gpu(built):
     assert lib.qfm_init(C.byref(bad)) != 0
     assert b"unsupported" in lib.qfm_last_error()
     assert lib.qfm_last_error() == b""              # reading clears the latch
-    for cfg in [(2048, 512, 512, 10, 1, 1), (2560, 640, 512, 10, 1, 1), (2048, 512, 64, 4, 0, 0)]:
+    for cfg in [(2048, 512, 512, 10, 1, 1), (2560, 640, 512, 10, 1, 1), (2048, 512, 512, 4, 0, 0)]:
         c = qfm.QfmConfig(*cfg)
         assert lib.qfm_init(C.byref(c)) == 0
         out = qfm.QfmConfig()
@@ -89,6 +89,10 @@ def test_config_validation_without_gpu(built):
         assert (out.hidden, out.inter, out.n_experts, out.top_k) == cfg[:4]
     assert lib.qfm_init(C.byref(qfm.QfmConfig(2048, 512, 512, 17, 1, 1))) != 0
     lib.qfm_last_error()
+    # every path is built for the reference's 512 experts: other counts are rejected
+    for e in (64, 256, 1024):
+        assert lib.qfm_init(C.byref(qfm.QfmConfig(2048, 512, e, 4, 1, 1))) != 0
+        assert b"unsupported" in lib.qfm_last_error()
     lib.qfm_init(C.byref(qfm.QfmConfig(2048, 512, 512, 10, 1, 1)))
 
 
@@ -103,3 +107,62 @@ def test_argument_rejection_without_gpu(built):
     assert lib.qfm_gen_fill(None, 0, 0, 10, 0, 0, 1, 0.0, None) != 0
     lib.qfm_last_error()
     assert lib.qfm_workspace_bytes(1) > 0 and lib.qfm_workspace_bytes(0) == 0
+
+
+def test_validated_twins_reject_without_launching(built):
+    """Every reference-named void launcher has an _ex twin returning a code; bad
+    arguments come back as -1 with a message and nothing is launched (so this
+    runs without a GPU)."""
+    import qfm
+    lib = qfm.load()
+    lib.qfm_init(C.byref(qfm.QfmConfig(2048, 512, 512, 10, 1, 1)))
+    calls = {
+        "qf_rtr_gemv_launch_ex": (None, None, None, None),
+        "qf_rtr_topk10_launch_ex": (None, None, None, None),
+        "qf_rtr_topk10_rows_launch_ex": (None, None, None, 0, None),
+        "qf8_i8_gateup_m1_ex": (None, None, None, None, None, None, 10, 1, None),
+        "qf8_i8_down_m1_ex": (None, None, None, None, None, None, None, 10, None),
+        "qf8_i8_x8_ex": (None, None, None, 30, None),
+        "qf8_i8_csr_build_ex": (None, None, 0, None, None, None, None, None, None),
+        "qf8_i8_experts_chunk_ex": (None,) * 11 + (0, 0, None, None, 0, None, None),
+        "qf5_nvfp4_moe_all_ex": (None,) * 15 + (0, None),
+        "qf5_nvfp4_gateup_all_launch_ex": (None,) * 10 + (0, None),
+        "qf5_nvfp4_downacc_all_launch_ex": (None,) * 8 + (0, None),
+        "qf5_m8_gateup_ex": (None,) * 8 + (None, None),
+        "qf5_m8_downacc_ex": (None,) * 5 + (None, None),
+        "qf5_m8_build_csr_ex": (None, None, 0, 0, 0, 0, 0, None, None, None, None, None, None),
+        "qf5_m8_reduce4_ex": (None, None, None, None, None, 8, None),
+        "qf8_i8_shexp_m1_ex": (None,) * 4 + (None,) * 9 + (None,),
+    }
+    for name, args in calls.items():
+        rc = getattr(lib, name)(*args)
+        assert rc == -1, (name, rc)
+        assert lib.qfm_last_error() != b"", name
+    # the void forms latch the same error
+    lib.qf8_i8_x8(None, None, None, 30, None)
+    assert lib.qfm_status() == -1
+    assert b"multiple of 32" in lib.qfm_last_error()
+
+
+def test_gated_shared_expert_needs_gate_vector_on_every_path(built):
+    """A gated shared expert without sh_gate_inp is rejected for decode rows and
+    for prefill alike (checked before any launch: no GPU needed)."""
+    import qfm
+    lib = qfm.load()
+    lib.qfm_init(C.byref(qfm.QfmConfig(2048, 512, 512, 10, 1, 1)))
+    arena = qfm.Qf4ExpCache()
+    for f in ("i8_gate", "i8_up", "i8_down", "i8s_gate", "i8s_up", "i8s_down"):
+        setattr(arena, f, 0x1000)
+    lay = qfm.QfmLayer()
+    lay.arena = C.pointer(arena)
+    lay.fmt = qfm.QFM_FMT_INT8
+    lay.router = 0x2000
+    lay.sh_gate = qfm.Qf8I8Mat(0x3000, 0x3100, 512, 2048)
+    lay.sh_up = qfm.Qf8I8Mat(0x4000, 0x4100, 512, 2048)
+    lay.sh_down = qfm.Qf8I8Mat(0x5000, 0x5100, 2048, 512)
+    lay.sh_gate_inp = None
+    for M in (1, 8, 9, 300):
+        wsb = lib.qfm_workspace_bytes(M)
+        rc = lib.qfm_moe_forward(C.byref(lay), 0x6000, M, 0x7000, 0x100000, wsb, None)
+        assert rc == -1, (M, rc)
+        assert b"sh_gate_inp" in lib.qfm_last_error(), M

@@ -180,22 +180,42 @@ def test_i8_m1_reference_entry_points(lib, H, I):
     wts /= wts.sum()
     x = orc.bf16_to_f32(orc.fill("gauss_bf16", seed, 9, orc.T_X, 0, H))
     dx, dsel, dw = qfm.DevBuf.from_array(x), qfm.DevBuf.from_array(sel), qfm.DevBuf.from_array(wts)
+    dq, ds = qfm.DevBuf(H), qfm.DevBuf(H // 32 * 4)
     dh, dy = qfm.DevBuf(10 * I * 4), qfm.DevBuf(H * 4)
-    lib.qf8_i8_gateup_m1(C.byref(arena), dx.ptr, None, None, dh.ptr, dsel.ptr, 10, 0, st.h)
-    lib.qf8_i8_down_m1(C.byref(arena), dh.ptr, None, None, dw.ptr, dsel.ptr, dy.ptr, 10, st.h)
-    qfm.status_check("i8 m1")
+    # quant_x = 1: x is quantized into x8q/x8s (X8, as the reference does) and read from there
+    qfm.check(lib.qf8_i8_gateup_m1_ex(C.byref(arena), dx.ptr, dq.ptr, ds.ptr, dh.ptr, dsel.ptr, 10, 1, st.h), "gu")
+    qfm.check(lib.qf8_i8_down_m1_ex(C.byref(arena), dh.ptr, None, None, dw.ptr, dsel.ptr, dy.ptr, 10, st.h), "dn")
     st.sync()
     h = dh.download(np.float32, (10, I))
     y = dy.download(np.float32, H)
+    q, s = orc.x8_quant(x)
+    assert np.array_equal(dq.download(np.int8, H), q)
+    assert np.array_equal(ds.download(np.float32, H // 32).view(np.uint32), s.view(np.uint32))
+    # the activations the kernel multiplies: code * scale, rounded to fp32 as in the kernel
+    xq = (q.astype(np.float32) * np.repeat(s, 32)).astype(np.float64)
     yref = np.zeros(H)
     for k, e in enumerate(sel):
-        href, ye = orc.i8_expert(x.astype(np.float64), *_oracle_expert(seed, layer, int(e), H, I))
+        href, ye = orc.i8_expert(xq, *_oracle_expert(seed, layer, int(e), H, I))
         assert _rel(h[k], href) < 1e-5, k
         yref += float(wts[k]) * ye
+    # quant_x = 0 reads the caller's x8q/x8s and never x: a stale x (here garbage,
+    # then no x at all) gives the same hidden vectors bit for bit
+    dx.upload(np.full(H, 123.0, np.float32))
+    dh2 = qfm.DevBuf(10 * I * 4)
+    qfm.check(lib.qf8_i8_gateup_m1_ex(C.byref(arena), dx.ptr, dq.ptr, ds.ptr, dh2.ptr, dsel.ptr, 10, 0, st.h), "gu0")
+    st.sync()
+    assert np.array_equal(dh2.download(np.float32, (10, I)).view(np.uint32), h.view(np.uint32))
+    lib.qf8_i8_gateup_m1(C.byref(arena), None, dq.ptr, ds.ptr, dh2.ptr, dsel.ptr, 10, 0, st.h)
+    qfm.status_check("gateup without x")
+    st.sync()
+    assert np.array_equal(dh2.download(np.float32, (10, I)).view(np.uint32), h.view(np.uint32))
+    # missing X8 buffers are rejected (nothing launched)
+    assert lib.qf8_i8_gateup_m1_ex(C.byref(arena), dx.ptr, None, None, dh2.ptr, dsel.ptr, 10, 1, st.h) == -1
+    lib.qfm_last_error()
     # The down kernel stages the hidden vectors in LDS as fp16 (11 significant
     # bits, a power-of-two scale per 16 values): |dy| / max|y| ~ 1e-3, against the
     # reference's int8 re-quantization of the hidden vector (~4e-3) and the
-    # north-star bound of 1e-2. The gate/up with fp32 x above stays fp32-exact.
+    # north-star bound of 1e-2. The gate/up on the X8 row above is fp32-exact.
     assert _rel(y, yref) < 2e-3
     lib.qfm_arena_free(C.byref(arena))
     st.destroy()
@@ -349,15 +369,18 @@ def _run_prefill(lib, T, seed, layer, x_layer, bias=True, fmt=qfm.QFM_FMT_INT8, 
     return out
 
 
-@pytest.mark.parametrize("T,bias,fmt", [(37, True, 0), (300, True, 0), (129, False, 0), (37, True, 1), (300, True, 1),
-                                        (9, False, 1)])
-def test_prefill_small(lib, T, bias, fmt):
+@pytest.mark.parametrize("T,bias,fmt,renorm", [(37, True, 0, 1), (300, True, 0, 1), (129, False, 0, 1), (37, True, 1, 1),
+                                               (300, True, 1, 1), (9, False, 1, 1), (37, True, 0, 0), (129, False, 1, 0)])
+def test_prefill_small(lib, T, bias, fmt, renorm):
     """Prefill path (T > 8): MFMA router + exact candidate selection, grouped GEMMs
-    on INT8 (fmt 0) or NVFP4 (fmt 1) routed experts (the shared expert is INT8)."""
-    _say("prefill", T, bias, "int8" if fmt == 0 else "nvfp4")
-    _cfg(lib)
+    on INT8 (fmt 0) or NVFP4 (fmt 1) routed experts (the shared expert is INT8).
+    renorm 0 divides by the softmax denominator over all 512 logits, which the
+    selection recomputes exactly (weights at the same 2e-6 as renorm 1)."""
+    _say("prefill", T, bias, "int8" if fmt == 0 else "nvfp4", "renorm", renorm)
+    _cfg(lib, renorm=renorm)
     g = _run_prefill(lib, T, 1, 2, 600 + T, bias, fmt)
-    r = orc.moe_layer(2048, 512, 512, 10, T, 1, 2, 600 + T, use_bias=int(bias), fmt=fmt)
+    _cfg(lib)
+    r = orc.moe_layer(2048, 512, 512, 10, T, 1, 2, 600 + T, use_bias=int(bias), fmt=fmt, renorm=renorm)
     assert np.array_equal(g["x"], r["x"])
     assert np.array_equal(g["sel"], r["sel"])
     assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
@@ -404,21 +427,22 @@ def test_prefill_reference_shape(lib, T, fmt, gated):
     assert rel <= TOL
 
 
-def test_prefill_config4_nvfp4_sample(lib):
+def test_prefill_config4_nvfp4_all_rows(lib):
     """Config 4's prefill (T=8038, skewed router bias) on an NVFP4 arena: routing
-    of every token, outputs of a 1024-token window against the fp64 oracle (the
-    NVFP4 oracle over all 8038 tokens takes ~3 minutes on the test host; it
-    passed at 5.3e-3 when run once)."""
+    of every token bit-exact, and the outputs of every token (all tokens of the
+    hottest and the coldest expert among them) against the fp64 layer, evaluated
+    expert by expert on the oracle's dequantized weights (moe_layer_grouped)."""
     T, seed, layer, xl = 8038, 0, 3, 700
     _say("prefill config4 nvfp4", T)
     _cfg(lib)
     g = _run_prefill(lib, T, seed, layer, xl, True, qfm.QFM_FMT_NVFP4)
-    E, H = 512, 2048
-    W = orc.fill("gauss", seed, layer, orc.T_ROUTER, 0, E * H, 0.02).reshape(E, H)
-    b = orc.fill("gauss", seed, layer, orc.T_BIAS, 0, E, 1.5)
-    sel, w64, _ = orc.topk(orc.router_logits(W, g["x"], b), 10)
-    assert np.array_equal(g["sel"], sel)
-    r = orc.moe_layer(2048, 512, 512, 10, 1024, seed, layer, xl, x_row0=3000, use_bias=1, fmt=1)
-    rel = np.abs(g["y"][3000:4024] - r["y"]).max(axis=1) / np.abs(r["y"]).max(axis=1)
-    _say("  rows 3000..4023 max rel err", float(rel.max()))
+    r = orc.moe_layer_grouped(2048, 512, 512, 10, T, seed, layer, xl, use_bias=1, fmt=1)
+    assert np.array_equal(g["x"], r["x"])
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    cnt = np.bincount(g["sel"].ravel(), minlength=512)
+    hot, cold = int(cnt.argmax()), int(np.where(cnt > 0, cnt, 1 << 30).argmin())
+    _say("  hottest expert", hot, cnt[hot], "coldest", cold, cnt[cold])
+    rel = np.abs(g["y"] - r["y"]).max(axis=1) / np.abs(r["y"]).max(axis=1)
+    _say("  max rel err over all rows", float(rel.max()))
     assert float(rel.max()) <= TOL

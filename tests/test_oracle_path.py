@@ -5,6 +5,8 @@ its formula: numpy fp64 matmuls of independently dequantized weights,
 brute-force selection by a stable sort, exact-arithmetic special cases,
 closed forms (one-hot weights) and structural invariants.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -325,3 +327,64 @@ def test_nvfp4_to_i8_closed_forms():
     q1, s1 = orc.nvfp4_to_i8(F1, S1, 1.0, 1, 64)
     assert s1[0] == np.float32(np.float32((1 + 0 / 8) * 2.0 ** 16) * np.float32(1 / 127))
     assert np.all(q1[0, :16] == 127) and np.all(q1[0, 16:] == 0)
+
+
+def test_x8_exact_ties_round_half_to_even():
+    """X8 uses rintf (ties to even, qf8_moe_i8.hip:66), not roundf (ties away).
+    With absmax 127 the scale is exactly 1.0 (fl(127 * fl(1/127)) = 1), so
+    v = k + 1/2 lands exactly on a tie."""
+    v = np.zeros(64, np.float32)
+    v[0] = 127.0
+    ties = np.array([0.5, 1.5, 2.5, 3.5, -0.5, -1.5, -2.5, 126.5, -126.5, 5.5, 6.5, -7.5], np.float32)
+    v[1:1 + ties.size] = ties
+    v[32] = -127.0                                    # second block: absmax 127 again, negative
+    v[33:33 + ties.size] = -ties
+    q, s = orc.x8_quant(v)
+    assert s[0] == 1.0 and s[1] == 1.0
+    want = np.rint(ties).astype(np.int32)            # numpy rounds half to even
+    assert np.array_equal(q[1:1 + ties.size], want)
+    assert np.array_equal(q[33:33 + ties.size], -want)
+    away = np.sign(ties) * np.floor(np.abs(ties) + 0.5)
+    assert not np.array_equal(want, away)            # the case separates the two rules
+    assert q[0] == 127 and q[32] == -127
+
+
+@pytest.mark.parametrize("fmt,bias,renorm,gated", [(0, 1, 1, 1), (1, 1, 1, 1), (0, 0, 0, 0), (1, 0, 0, 1)])
+def test_grouped_layer_matches_per_token_oracle(fmt, bias, renorm, gated):
+    """The expert-grouped fp64 layer (the checker used for all 8038 prefill
+    tokens) reproduces orc_moe_layer's per-token evaluation."""
+    H, I, E, K, M = 2048, 512, 512, 10, 8
+    r = orc.moe_layer(H, I, E, K, M, 4, 6, 60, fmt=fmt, use_bias=bias, renorm=renorm, gated=gated)
+    g = orc.moe_layer_grouped(H, I, E, K, M, 4, 6, 60, fmt=fmt, use_bias=bias, renorm=renorm, gated=gated)
+    assert np.array_equal(g["x"], r["x"])
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.array_equal(g["w"], r["w"])
+    rel = np.abs(g["y"] - r["y"]).max() / np.abs(r["y"]).max()
+    assert rel < 1e-12, rel
+
+
+def test_cpu_baseline_path_matches_oracle():
+    """orc_cpu_moe_layer_fast (the fp32 path bench.py times as the CPU baseline)
+    against the fp64 oracle layer on the same generated layer: identical
+    routing, outputs within the parity bound."""
+    H, I, E, K, M, seed, layer, xl = 2048, 512, 512, 10, 3, 0, 5, 1005
+    lib = orc.load()
+    r = orc.moe_layer(H, I, E, K, M, seed, layer, xl)
+    router = orc.fill("gauss", seed, layer, orc.T_ROUTER, 0, E * H, 0.02)
+    g = orc.fill("gauss", seed, layer, orc.T_SHGATE, 0, H, 0.02)
+    qg = np.zeros((E + 1) * I * H, np.int8); qu = np.zeros_like(qg); qd = np.zeros_like(qg)
+    sg = np.zeros((E + 1) * I, np.float32); su = np.zeros_like(sg); sd = np.zeros((E + 1) * H, np.float32)
+    for e in sorted(set(r["sel"].ravel().tolist())) + [E]:
+        Qg, s_g, Qu, s_u, Qd, s_d = orc._i8_expert_arrays(seed, layer, e, H, I)
+        qg[e * I * H:(e + 1) * I * H] = Qg.ravel(); qu[e * I * H:(e + 1) * I * H] = Qu.ravel()
+        qd[e * H * I:(e + 1) * H * I] = Qd.ravel()
+        sg[e * I:(e + 1) * I] = s_g; su[e * I:(e + 1) * I] = s_u; sd[e * H:(e + 1) * H] = s_d
+    hl = orc.HostLayer(router.ctypes.data, qg.ctypes.data, qu.ctypes.data, qd.ctypes.data,
+                       sg.ctypes.data, su.ctypes.data, sd.ctypes.data, g.ctypes.data)
+    y = np.empty((M, H), np.float32)
+    x = np.ascontiguousarray(r["x"])
+    lib.orc_cpu_moe_layer_fast(C.byref(hl), H, I, E, K, x.ctypes.data, M, y.ctypes.data, 4)
+    for m in range(M):
+        rel = np.abs(y[m] - r["y"][m]).max() / np.abs(r["y"][m]).max()
+        assert rel <= 1e-2, (m, rel)
+        assert rel < 1e-4, (m, rel)                  # fp32 accumulation: far inside the bound
