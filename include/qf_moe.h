@@ -325,6 +325,19 @@ int qfm_workspace_view(void *ws, int M, qfm_ws_view *v);
 int qfm_moe_forward(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y,
                     void *ws, size_t ws_bytes, hipStream_t s);
 
+/* qfm_moe_forward for callers that cannot allocate or pass a workspace (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The workspace is a 2 MiB
+ * device array inside the library (one per GPU, held until the process ends),
+ * which serves 1 <= M <= 8 rows at either supported shape; larger M is
+ * rejected with -1 and a message (prefill needs qfm_moe_forward and a caller
+ * workspace). Allocates nothing, same kernels and results as qfm_moe_forward.
+ * The array's address is resolved by qfm_init for the device current then, or
+ * by the first call on another device: make that first call outside a stream
+ * capture. Calls that overlap on one GPU (two streams or host threads) share
+ * the array and race: serialize them. */
+int qfm_moe_forward_noalloc(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, hipStream_t s);
+
 /* Profiling form of the M=1 forward: launches only the sections in mask
  * (bit 0 router + shared gate/up, bit 1 top-K + routed gate/up, bit 2 down +
  * combine), reading the workspace the earlier sections left behind. */

@@ -129,6 +129,7 @@ int qfm_init(const qfm_config *cfg) {
     }
     g_cfg.H = cfg->hidden; g_cfg.I = cfg->inter; g_cfg.E = E; g_cfg.K = cfg->top_k;
     g_cfg.renorm = cfg->renorm ? 1 : 0; g_cfg.gated = cfg->shared_gated ? 1 : 0;
+    noalloc_prepare_current_device();
     return 0;
 }
 
@@ -256,7 +257,8 @@ int qfm_workspace_view(void *ws, int M, qfm_ws_view *v) {
 }
 
 static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
-                        int mask, hipStream_t s);
+                        int mask, hipStream_t s, bool prof = true);
+
 
 int qfm_moe_forward(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
                     hipStream_t s) {
@@ -270,7 +272,7 @@ int qfm_moe_forward_sections(const qfm_layer *L, const uint16_t *x, int M, uint1
 }
 
 static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
-                        int mask, hipStream_t s) {
+                        int mask, hipStream_t s, bool prof) {
     if (!layer_ok(L) || !x || !y || !ws || M < 1) { set_error(-1, "qfm_moe_forward: bad arguments"); return -1; }
     if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) { set_error(-1, "qfm_moe_forward: workspace not 256-byte aligned"); return -1; }
     if (ws_bytes < qfm_workspace_bytes(M)) {
@@ -300,7 +302,8 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
     const ShPtrs *sp = has_sh ? &shp : nullptr;
     const int ld = c.E + 1;
     std::array<size_t, 4> pm{};
-    if (g_prof.on) pm[0] = prof_event(s);
+    const bool marks = prof && g_prof.on;
+    if (marks) pm[0] = prof_event(s);
     if (M == 1 && L->fmt == QFM_FMT_INT8 && c.E == 512) {
         // per row: K routed hidden vectors, then the shared one (read as one block by the down kernel)
         float *hsh = hidden + (size_t)c.K * c.I;
@@ -308,14 +311,14 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
         int rc = 0;
         void *x16 = b + w.xh16;                    // x as scaled fp16 + (sum, 2^-k), written by the router launch
         if (mask & 1) rc = launch_router_shared(L->router, L->router_bias, g, nullptr, x, 1, logits, ld, hsh, c.I, s, x16);
-        if (g_prof.on) pm[1] = prof_event(s);
+        if (marks) pm[1] = prof_event(s);
         // 2. top-K inside the gate/up kernel, whose last grid row computes the shared
         // expert's hidden (no selection needed there); 3. down + combine (+ shared) -> y bf16
         if (!rc && (mask & 2)) rc = launch_i8_gateup_m1(L->arena, x, nullptr, logits, sel, wts, c.K, hidden, s, sp, x16);
-        if (g_prof.on) pm[2] = prof_event(s);
+        if (marks) pm[2] = prof_event(s);
         if (!rc && (mask & 4))
             rc = launch_i8_down_m1(L->arena, hidden, wts, sel, c.K, sp, g ? logits + c.E : nullptr, nullptr, y, s);
-        if (g_prof.on) { pm[3] = prof_event(s); g_prof.marks.push_back(pm); }
+        if (marks) { pm[3] = prof_event(s); g_prof.marks.push_back(pm); }
         return rc;
     }
     if (M <= 8) {
@@ -446,3 +449,10 @@ int qfm_device_info(char *name, int name_len, int *n_cu, size_t *mem_bytes, int 
 }
 
 }  // extern "C"
+
+// the forward on a workspace the caller vouches for, never touching the
+// section profiler (whose event pool may create events): the no-allocation entry
+int qfm::forward_on_workspace(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
+                              hipStream_t s) {
+    return forward_impl(L, x, M, y, ws, ws_bytes, 7, s, false);
+}

@@ -69,6 +69,14 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
                        int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
                        void *xh16, float *part, uint16_t *y, hipStream_t s);
 
+// The fused forward on a caller-vouched workspace, without the section
+// profiler (qfm_moe_forward minus its event marks): the no-allocation entry.
+int forward_on_workspace(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
+                         hipStream_t s);
+
+// Resolve the no-allocation entry's device array for the current device (qfm_init).
+void noalloc_prepare_current_device();
+
 // Prefill (T > 8 rows): MFMA router + exact candidate selection, grouped
 // MFMA gate/up and down over the routing inversion, owned-partial combine.
 size_t prefill_ws_bytes(int T);

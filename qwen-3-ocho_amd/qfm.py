@@ -118,6 +118,7 @@ _SIGS = {
     "qfm_workspace_bytes": (C.c_size_t, [C.c_int]),
     "qfm_workspace_view": (C.c_int, [vp, C.c_int, C.POINTER(QfmWsView)]),
     "qfm_moe_forward": (C.c_int, [C.POINTER(QfmLayer), vp, C.c_int, vp, vp, C.c_size_t, vp]),
+    "qfm_moe_forward_noalloc": (C.c_int, [C.POINTER(QfmLayer), vp, C.c_int, vp, vp]),
     "qfm_moe_forward_sections": (C.c_int, [C.POINTER(QfmLayer), vp, C.c_int, vp, vp, C.c_size_t, C.c_int, vp]),
     "qfm_moe_forward_layers": (C.c_int, [C.POINTER(QfmLayer), C.c_int, vp, C.c_long, C.c_int, vp, C.c_long,
                                          vp, C.c_size_t, vp]),
