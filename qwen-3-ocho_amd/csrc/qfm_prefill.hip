@@ -45,6 +45,7 @@
 
 #include "qfm_dev.h"
 #include "qfm_internal.h"
+#include "qfm_prefill_layout.h"
 
 namespace qfm {
 
@@ -445,7 +446,6 @@ using ExpertEngineF4 = TileEngine<kB_F4, 2, 4, 4, 3>;
 using SharedEngineI8 = TileEngine<kB_I8, 2, 4, 4, 3>;     // shared tiles inside the NVFP4 launch
 // weight rows per grouped-GEMM tile (gate/up: half gate, half up rows)
 constexpr int GBN_I8 = ExpertEngine::BNt, GBN_F4 = ExpertEngineF4::BNt;
-constexpr int GBN_MIN = GBN_I8 < GBN_F4 ? GBN_I8 : GBN_F4;
 
 // Workgroups are dispatched to the 8 XCDs round-robin (block b on XCD b % 8).
 // Map block b to tile (m, n) so that the nt n-tiles of one m-tile run back to
@@ -1009,42 +1009,28 @@ void launch_pf_combine(const float *part, int T, int S, int H, uint16_t *y, hipS
 }
 
 // ---- launcher -------------------------------------------------------------------------
-size_t prefill_ws_bytes(int T) {
+// The carve-up of one configuration (qfm_prefill_layout.h): gate/up tiles of
+// GBN_F4 / GBN_I8 weight rows, down tiles of GBN_F4 (NVFP4) or
+// DownEngineI8::BNt (INT8) output columns.
+static PfLayout layout_of(int T, bool f4, bool has_sh) {
     const Cfg &c = g_cfg;
-    const size_t P = (size_t)T * (c.K + 1);
-    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    size_t b = 0;
-    b += al((size_t)kRouterKS * T * c.E * 4);   // router GEMM slices (slice 0 ends as lg_approx)
-    b += al((size_t)T * 4) + al((size_t)c.E * 4);   // xnorm, wnorm
-    b += al((size_t)c.E * c.H * 2);        // bf16 router weights
-    b += al((size_t)T * c.K * 4) * 2;      // sel, wts
-    b += al((size_t)T * 4);                // gam
-    b += al(4 * 8);                        // counters
-    b += al((size_t)(c.E + 2) * 4);        // off
-    b += al((size_t)((size_t)T * c.K + kPairsPerBlk - 1) / kPairsPerBlk * c.E * 4);   // per-block counts
-    const size_t max_mt = (P / BM + c.E + 2 + 7) / 8 * 8;
-    b += al(max_mt * (c.I / (GBN_MIN / 2)) * 16) + al(max_mt * (c.H / DownEngineI8::BNt) * 16);   // item lists
-    b += al(P * 4) * 3;                    // p_tok, p_slot, p_wt
-    b += al(P * c.I * 2);                  // hidden bf16
-    b += al(P * c.H * 4);                  // partials
-    b += al((size_t)T * 4);                // x row sums
-    b += al(P * (c.I / (GBN_MIN / 2)) * 4);    // hidden row sums per gate/up n-tile
-    b += al((size_t)T * c.H * 2) + al((size_t)T * 4) * 2;   // fp16 x rows, their sums and 2^-k
-    return b;
+    return pf_layout(T, c.H, c.I, c.E, c.K, has_sh, f4 ? GBN_F4 : GBN_I8, f4 ? GBN_F4 : DownEngineI8::BNt, BM,
+                     kRouterKS, kPairsPerBlk);
+}
+
+size_t prefill_ws_bytes(int T) {
+    // the larger of the two arena formats, with the shared expert
+    const size_t a = layout_of(T, false, true).total, b = layout_of(T, true, true).total;
+    return a > b ? a : b;
 }
 
 void prefill_ws_view(void *ws, int T, float **lg, int **sel, float **wts, int **ctr) {
-    const Cfg &c = g_cfg;
-    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    const PfLayout Lw = layout_of(T, false, true);    // these regions do not depend on the format
     char *b = static_cast<char *>(ws);
-    *lg = reinterpret_cast<float *>(b); b += al((size_t)kRouterKS * T * c.E * 4);
-    b += al((size_t)T * 4);
-    b += al((size_t)c.E * 4);
-    b += al((size_t)c.E * c.H * 2);
-    *sel = reinterpret_cast<int *>(b); b += al((size_t)T * c.K * 4);
-    *wts = reinterpret_cast<float *>(b); b += al((size_t)T * c.K * 4);
-    b += al((size_t)T * 4);                // gam
-    *ctr = reinterpret_cast<int *>(b);     // {candidate overflows, gate/up items, down items}
+    *lg = reinterpret_cast<float *>(b + Lw.off[kPfLg]);
+    *sel = reinterpret_cast<int *>(b + Lw.off[kPfSel]);
+    *wts = reinterpret_cast<float *>(b + Lw.off[kPfWts]);
+    *ctr = reinterpret_cast<int *>(b + Lw.off[kPfCtr]);   // {candidate overflows, gate/up items, down items}
 }
 
 int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, void *ws, int gated, hipStream_t s) {
@@ -1063,34 +1049,34 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     }
     const bool has_sh = L->sh_gate.w != nullptr;
     const int S = K + (has_sh ? 1 : 0);      // partial slots per token: K routed (+ shared)
-    const size_t P = (size_t)T * S;
-    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    const PfLayout Lw = layout_of(T, f4, has_sh);
     char *b = static_cast<char *>(ws);
-    float *lg = reinterpret_cast<float *>(b); b += al((size_t)kRouterKS * T * E * 4);
-    float *xnorm = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
-    float *wnorm = reinterpret_cast<float *>(b); b += al((size_t)E * 4);
-    uint16_t *wb16 = reinterpret_cast<uint16_t *>(b); b += al((size_t)E * H * 2);
-    int *sel = reinterpret_cast<int *>(b); b += al((size_t)T * K * 4);
-    float *wts = reinterpret_cast<float *>(b); b += al((size_t)T * K * 4);
-    float *gam = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
-    int *ctr = reinterpret_cast<int *>(b); b += al(4 * 8);
-    int *off = reinterpret_cast<int *>(b); b += al((size_t)(E + 2) * 4);
-    const int nblk = (int)(((size_t)T * K + kPairsPerBlk - 1) / kPairsPerBlk);
-    int *blk = reinterpret_cast<int *>(b); b += al((size_t)nblk * E * 4);
-    const size_t max_mt = (P / BM + E + 2 + 7) / 8 * 8;   // bound on m-tiles, a multiple of 8
-    const int nt_gu = I / ((f4 ? GBN_F4 : GBN_I8) / 2), nt_dn = H / (f4 ? GBN_F4 : DownEngineI8::BNt);
-    int4 *items_gu = reinterpret_cast<int4 *>(b); b += al(max_mt * nt_gu * 16);
-    int4 *items_dn = reinterpret_cast<int4 *>(b); b += al(max_mt * (H / DownEngineI8::BNt) * 16);
-    int *p_tok = reinterpret_cast<int *>(b); b += al(P * 4);
-    int *p_slot = reinterpret_cast<int *>(b); b += al(P * 4);
-    float *p_wt = reinterpret_cast<float *>(b); b += al(P * 4);
-    uint16_t *hid = reinterpret_cast<uint16_t *>(b); b += al(P * I * 2);
-    float *part = reinterpret_cast<float *>(b); b += al(P * H * 4);
-    float *xsum = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
-    float *hsum = reinterpret_cast<float *>(b); b += al(P * nt_gu * 4);
-    uint4 *x16 = reinterpret_cast<uint4 *>(b); b += al((size_t)T * H * 2);
-    float *x16sum = reinterpret_cast<float *>(b); b += al((size_t)T * 4);
-    float *x16isc = reinterpret_cast<float *>(b);
+    auto at = [&](PfRegion r) { return static_cast<void *>(b + Lw.off[r]); };
+    float *lg = static_cast<float *>(at(kPfLg));
+    float *xnorm = static_cast<float *>(at(kPfXnorm));
+    float *wnorm = static_cast<float *>(at(kPfWnorm));
+    uint16_t *wb16 = static_cast<uint16_t *>(at(kPfWb16));
+    int *sel = static_cast<int *>(at(kPfSel));
+    float *wts = static_cast<float *>(at(kPfWts));
+    float *gam = static_cast<float *>(at(kPfGam));
+    int *ctr = static_cast<int *>(at(kPfCtr));
+    int *off = static_cast<int *>(at(kPfOff));
+    const int nblk = Lw.nblk;
+    int *blk = static_cast<int *>(at(kPfBlk));
+    const size_t max_mt = Lw.max_mt;                 // bound on m-tiles, a multiple of 8
+    const int nt_gu = Lw.nt_gu, nt_dn = Lw.nt_dn;
+    int4 *items_gu = static_cast<int4 *>(at(kPfItemsGu));
+    int4 *items_dn = static_cast<int4 *>(at(kPfItemsDn));
+    int *p_tok = static_cast<int *>(at(kPfTok));
+    int *p_slot = static_cast<int *>(at(kPfSlot));
+    float *p_wt = static_cast<float *>(at(kPfPwt));
+    uint16_t *hid = static_cast<uint16_t *>(at(kPfHid));
+    float *part = static_cast<float *>(at(kPfPart));
+    float *xsum = static_cast<float *>(at(kPfXsum));
+    float *hsum = static_cast<float *>(at(kPfHsum));
+    uint4 *x16 = static_cast<uint4 *>(at(kPfX16));
+    float *x16sum = static_cast<float *>(at(kPfX16sum));
+    float *x16isc = static_cast<float *>(at(kPfX16isc));
 
     const float *g = (has_sh && gated) ? L->sh_gate_inp : nullptr;
     // zero the small counters with a fill kernel (no memset node in captured graphs)
