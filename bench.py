@@ -16,6 +16,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -50,7 +51,40 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(n_layers, seconds, threads):
+def host_cpu():
+    """The host's CPU model and core counts: nproc (os.cpu_count), the cores
+    this process may run on (its affinity mask), OMP_NUM_THREADS, and the thread
+    count used for the CPU baseline (the affinity count, capped by
+    OMP_NUM_THREADS when that is set: the machine's share for this job)."""
+    model = "unknown"
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for ln in out.splitlines():
+            if ln.startswith("Model name:"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except Exception:
+        pass
+    if model == "unknown":
+        try:
+            with open("/proc/cpuinfo") as f:
+                for ln in f:
+                    if ln.startswith("model name"):
+                        model = ln.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    nproc = os.cpu_count() or 1
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = nproc
+    omp = os.environ.get("OMP_NUM_THREADS")
+    use = min(aff, int(omp)) if omp and omp.isdigit() and int(omp) > 0 else aff
+    return {"model": model, "nproc": nproc, "affinity": aff, "omp_num_threads": omp, "threads": use}
+
+
+def cpu_baseline(n_layers, seconds, threads, cpu):
     """Time the oracle's fp32 CPU path on n_layers x 1 token of the same workload."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import _oracle as orc
@@ -90,7 +124,70 @@ def cpu_baseline(n_layers, seconds, threads):
     us = el * 1e6 / (reps * n_layers)
     return {"value": round(us, 2), "unit": "us/token/layer", "cores": threads, "kind": "port",
             "sample": f"{n_layers} distinct layers x 1 token (config-1 shapes), {reps} passes, "
-                      f"fp32-accumulate oracle path, OpenMP {threads} threads"}
+                      f"fp32-accumulate oracle path (orc_cpu_moe_layer_fast), OpenMP {threads} threads",
+            "cpu_model": cpu["model"], "nproc": cpu["nproc"], "affinity_cores": cpu["affinity"],
+            "omp_num_threads": cpu["omp_num_threads"]}
+
+
+def run_config0(lib, st, args, cpu):
+    """one INT8 SwiGLU expert at M=1 through the reference-named
+    M=1 entry points (qf8_i8_gateup_m1 with quant_x=1: X8 activations as in the
+    reference, then qf8_i8_down_m1), one expert of each of 48 distinct arenas per
+    replay so every expert streams from HBM; and the oracle's fp64 expert on the
+    host (orc_i8_expert, one thread) on the same expert."""
+    import qfm
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import _oracle as orc
+    nl = 48
+    arenas = []
+    for l in range(nl):
+        a = qfm.Qf4ExpCache()
+        qfm.check(lib.qfm_arena_init(C.byref(a), qfm.QFM_FMT_INT8, 500 + l), "arena")
+        arenas.append(a)
+    # only expert 0 of each arena is read: generate just its bytes
+    for l, a in enumerate(arenas):
+        for ptr, kind, tensor, cnt in ((a.i8_gate, 0, 1, I * H), (a.i8_up, 0, 2, I * H), (a.i8_down, 0, 3, H * I),
+                                       (a.i8s_gate, 1, 4, I), (a.i8s_up, 1, 5, I), (a.i8s_down, 1, 6, H)):
+            qfm.check(lib.qfm_gen_fill(ptr, kind, 0, cnt, 0, 500 + l, tensor, 0.0, st.h), "gen")
+    x = qfm.DevBuf(H * 4)
+    xb = orc.bf16_to_f32(orc.fill("gauss_bf16", 0, 1, orc.T_X, 0, H)).astype(np.float32)
+    x.upload(xb)
+    q, sc, hid, y = qfm.DevBuf(H), qfm.DevBuf(H // 32 * 4), qfm.DevBuf(I * 4), qfm.DevBuf(H * 4)
+    sel, wt = qfm.DevBuf.from_array(np.zeros(1, np.int32)), qfm.DevBuf.from_array(np.ones(1, np.float32))
+    st.sync()
+
+    def enq():
+        for a in arenas:
+            qfm.check(lib.qf8_i8_gateup_m1_ex(C.byref(a), x.ptr, q.ptr, sc.ptr, hid.ptr, sel.ptr, 1, 1, st.h), "gu")
+            qfm.check(lib.qf8_i8_down_m1_ex(C.byref(a), hid.ptr, None, None, wt.ptr, sel.ptr, y.ptr, 1, st.h), "dn")
+    ms = time_graph(lib, st, enq, args.steps, args.warmup)
+    us = ms * 1000.0 / nl
+    nbytes = EXPERT_BYTES + H * 4 + H * 4           # weights + scales, x fp32 in, y fp32 out
+    # host: the oracle's fp64 expert on the same expert, single thread
+    Qg = orc.fill("i8", 0, 500, orc.T_QG, 0, I * H).reshape(I, H)
+    Qu = orc.fill("i8", 0, 500, orc.T_QU, 0, I * H).reshape(I, H)
+    Qd = orc.fill("i8", 0, 500, orc.T_QD, 0, H * I).reshape(H, I)
+    sg = orc.fill("rowscale", 0, 500, orc.T_SG, 0, I)
+    su = orc.fill("rowscale", 0, 500, orc.T_SU, 0, I)
+    sd = orc.fill("rowscale", 0, 500, orc.T_SD, 0, H)
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < min(args.cpu_seconds, 3.0) or reps < 3:
+        orc.i8_expert(xb.astype(np.float64), Qg, sg, Qu, su, Qd, sd)
+        reps += 1
+    cpu_us = (time.perf_counter() - t0) * 1e6 / reps
+    for a in arenas:
+        lib.qfm_arena_free(C.byref(a))
+    log(f"BASELINE config 0: single INT8 expert M=1: {us:.2f} us/expert on the GPU "
+        f"({nbytes / (us * 1e-6) / 1e9:.0f} GB/s), CPU oracle expert {cpu_us:.0f} us (1 thread)")
+    return {"workload": "BASELINE config 0: single INT8 SwiGLU expert, M=1 (reference-named M=1 entry points, "
+                        "X8 activations as in the reference; 48 distinct experts per replay)",
+            "us_per_expert": round(us, 3), "algorithmic_bytes": nbytes,
+            "roofline": {"bound": "hbm", "achieved": round(nbytes / (us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "note": "three dependent launches (x8 quant, gate/up, down) for 3.2 MB: latency-bound"},
+            "cpu_baseline": {"value": round(cpu_us, 1), "unit": "us/expert", "cores": 1, "kind": "port",
+                             "sample": f"orc_i8_expert (fp64) on expert 0 of arena 500, {reps} runs",
+                             "cpu_model": cpu["model"]}}
 
 
 def time_graph(lib, st, enqueue, steps, warmup):
@@ -153,7 +250,10 @@ def run_rows(lib, st, layers, nl, M, args, label, fmt_bytes=EXPERT_BYTES):
     log(f"{label}: {us_layer:.2f} us/layer ({us_layer / M:.2f} us/token/layer), {gbs:.0f} GB/s, mean distinct experts {U:.1f}")
     return {"workload": label, "rows": M, "us_per_layer": round(us_layer, 3), "us_per_token_layer": round(us_layer / M, 3),
             "achieved_GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "mean_distinct_experts": round(U, 2), "algorithmic_bytes_per_step": nbytes}
+            "mean_distinct_experts": round(U, 2), "algorithmic_bytes_per_step": nbytes,
+            "roofline": {"bound": "hbm", "level": "layer (every launch of the step)", "achieved": round(gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": None}}
 
 
 NVFP4_EXPERT_BYTES = 3 * (H * I // 2 + H * I // 16) + 3 * 4     # codes + e4m3 block scales + 3 fp32 global scales
@@ -218,7 +318,10 @@ def run_prefill(lib, st, args, T=8038, nl=4, fmt=0):
             "flops_per_layer": flops, "achieved_TFLOPs": round(tflops, 1),
             "mfma_util": round(tflops / MFMA_PEAK_TFLOPS, 4), "weight_act_bytes_per_layer": wbytes,
             "achieved_GBps": round(gbs, 1), "experts_touched": float(np.mean(touched)),
-            "max_expert_load": max(max_load)}
+            "max_expert_load": max(max_load),
+            "roofline": {"bound": "mfma", "level": "layer (every launch of the step)", "achieved": round(tflops, 1),
+                         "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                         "traffic": None}}
 
 
 def main():
@@ -231,7 +334,7 @@ def main():
     ap.add_argument("--cpu-layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the M=8 INT8 / NVFP4 / prefill lines")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config 0 / M=8 INT8 / NVFP4 / prefill lines")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="before the timed region, one device-to-device copy of this many MiB (the "
                          "known-size copy that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -322,8 +425,11 @@ def main():
     dom_gbs = SEC_BYTES[dom] / (sec_us[dom] * 1e-6) / 1e9
     log("sections (us/launch, one-kernel graphs): " + ", ".join(f"{SEC_NAMES[i].split()[0]}={sec_us[i]:.2f}" for i in range(3)))
 
+    cpu_info = host_cpu()
+    log("host cpu", cpu_info)
     extra = {}
     if not args.no_extra:
+        extra["config0_single_expert"] = run_config0(lib, st, args, cpu_info)
         extra["config2_int8_m8"] = run_rows(lib, st, layers, nl, 8, args, "BASELINE config 2: M=8 INT8 fork rows")
         for L in layers:
             L.destroy()
@@ -334,9 +440,9 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        log(f"cpu baseline: {args.cpu_layers} layers, ~{args.cpu_seconds}s, {threads} threads")
-        cpu = cpu_baseline(args.cpu_layers, args.cpu_seconds, threads)
+        threads = cpu_info["threads"]
+        log(f"cpu baseline: {args.cpu_layers} layers, ~{args.cpu_seconds}s, {threads} threads ({cpu_info['model']})")
+        cpu = cpu_baseline(args.cpu_layers, args.cpu_seconds, threads, cpu_info)
         log("cpu baseline", cpu)
 
     # HBM bytes per launch of the dominant kernel, from the committed rocprofv3
