@@ -54,7 +54,8 @@ const char *qfm_last_error(void);   /* "" when no error is latched; reading clea
 int         qfm_status(void);       /* 0, or the latched error code; also polls hipGetLastError */
 const char *qfm_version(void);
 /* sizeof of the ABI structs (0 Qf4ExpCache, 1 qfm_layer, 2 qfm_synth_layer,
-   3 Qf8I8Mat, 4 Qf5M8Route, 5 qfm_config, 6 qfm_ws_view) for FFI layout checks. */
+   3 Qf8I8Mat, 4 Qf5M8Route, 5 qfm_config, 6 qfm_ws_view, 7 QfEntry, 8 QfStore,
+   9 Qf4ExpXfer, 10 QfRouteMailbox) for FFI layout checks. */
 size_t      qfm_sizeof(int which);
 
 /* ------------------------------------------------------------------------ */

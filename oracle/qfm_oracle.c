@@ -327,6 +327,105 @@ void orc_nvfp4_to_i8(const uint8_t *W, const uint8_t *S, float s2, int rows, int
     free(v);
 }
 
+/* Dense bf16 -> INT8 per-row (qf8_dense_i8.hip:41-60): scale = absmax / 127
+   (IEEE division; 1 for an all-zero row), inv = 1 / scale, code =
+   rint(w * inv) clamped to +-127. */
+void orc_i8_quant_bf16(const uint16_t *W, int rows, int K, int8_t *Wo, float *So) {
+    for (int r = 0; r < rows; r++) {
+        float mx = 0.0f;
+        for (int k = 0; k < K; k++) mx = fmaxf(mx, fabsf(orc_bf16_to_f32(W[(size_t)r * K + k])));
+        const float scale = mx > 0.0f ? mx / 127.0f : 1.0f;
+        const float inv = 1.0f / scale;
+        for (int k = 0; k < K; k++) {
+            int q = (int)rintf(orc_bf16_to_f32(W[(size_t)r * K + k]) * inv);
+            q = q > 127 ? 127 : (q < -127 ? -127 : q);
+            Wo[(size_t)r * K + k] = (int8_t)q;
+        }
+        So[r] = scale;
+    }
+}
+
+/* FP8 lane-chunk format (qf8_moe_fp8.hip:19-37, :217-246).
+   Decode: sign bit 7, exponent bits 6..3 (bias 7), mantissa bits 2..0;
+   exponent 0 is m * 2^-9; no NaN or infinity (0x7F reads 480).
+   Encode: |v| < 2^-9 (unbiased exponent < -9) -> signed zero; exponent >= 8
+   -> 0x7E (448) with the sign; exponents -9..-7 -> subnormal code, mantissa
+   truncated; otherwise 3-bit mantissa rounded to nearest even, a carry into
+   exponent 8 saturating to 0x7E. */
+float orc_f8_decode(uint8_t b) {
+    const uint32_t x = b, sgn = (x & 0x80u) << 24, e = (x >> 3) & 0xFu, m = x & 7u;
+    float v;
+    if (e == 0) {
+        v = (float)m * 0.001953125f;
+        uint32_t u;
+        memcpy(&u, &v, 4);
+        u |= sgn;
+        memcpy(&v, &u, 4);
+        return v;
+    }
+    const uint32_t u = sgn | ((e + 120u) << 23) | (m << 20);
+    memcpy(&v, &u, 4);
+    return v;
+}
+
+uint8_t orc_f8_encode(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    const uint32_t sgn = (u >> 24) & 0x80u;
+    int e = (int)((u >> 23) & 0xFFu) - 127;
+    const uint32_t m = u & 0x7FFFFFu;
+    if (e < -9) return (uint8_t)sgn;
+    if (e >= 8) return (uint8_t)(sgn | 0x7Eu);
+    if (e < -6) {
+        const int sh = -6 - e;
+        return (uint8_t)(sgn | (((m | 0x800000u) >> (sh + 20)) & 7u));
+    }
+    uint32_t mm = m >> 20;
+    const uint32_t rem = m & 0xFFFFFu;
+    if (rem > 0x80000u || (rem == 0x80000u && (mm & 1u))) {
+        mm++;
+        if (mm == 8u) {
+            mm = 0;
+            e++;
+            if (e >= 8) return (uint8_t)(sgn | 0x7Eu);
+        }
+    }
+    return (uint8_t)(sgn | (uint32_t)((e + 7) << 3) | (mm & 7u));
+}
+
+/* The packer's block-scale decode (qf8_moe_fp8.hip:231-234): e = b >> 3 (five
+   bits), m = b & 7; e == 0 -> m * 2^-9, else (1 + m/8) * 2^(e-7). Unlike
+   orc_e4m3 there is no infinity: 0x7F reads 480. */
+static float orc_f8_block_scale(uint32_t b) {
+    const uint32_t e = (b & 0xFFu) >> 3, m = b & 7u;
+    return e ? ldexpf(1.0f + (float)m / 8.0f, (int)e - 7) : ldexpf((float)m, -9);
+}
+
+/* NVFP4 expert matrix rows x in -> lane-chunk E4M3: chunk l of row r holds
+   values v = e2m1(nibble) * (block scale * s2) (orc_f8_block_scale), sc[r][l]
+   = max|v| / 448 (1 for an all-zero chunk), code = orc_f8_encode(v / sc). */
+void orc_fp8_pack_expert(const uint8_t *W, const uint8_t *S, float s2, int rows, int in, uint8_t *w8, float *sc) {
+    const int ch = in / 64;
+    float *v = (float *)malloc((size_t)ch * sizeof(float));
+    for (int r = 0; r < rows; r++)
+        for (int l = 0; l < 64; l++) {
+            float mx = 0.0f;
+            for (int c = 0; c < ch; c++) {
+                const int k = l * ch + c;
+                const uint32_t byte = W[(size_t)r * (in / 2) + k / 2];
+                const uint32_t nib = (k & 1) ? (byte >> 4) : (byte & 15u);
+                const float bs = orc_f8_block_scale(S[(size_t)r * (in / 16) + k / 16]);
+                v[c] = orc_e2m1(nib) * (bs * s2);
+                const float a = fabsf(v[c]);
+                if (a > mx) mx = a;
+            }
+            const float scale = mx > 0.0f ? mx / 448.0f : 1.0f;
+            sc[(size_t)r * 64 + l] = scale;
+            for (int c = 0; c < ch; c++) w8[(size_t)r * in + (size_t)l * ch + c] = orc_f8_encode(v[c] / scale);
+        }
+    free(v);
+}
+
 /* Four-card combine: y[i] = ((y0[i] + y1[i]) + y2[i]) + y3[i], fp32, the
    left-to-right order of k_m8_reduce4 (qf_moe_m8_wave64.hip:216-221). */
 void orc_m8_reduce4(float *y, const float *y0, const float *y1, const float *y2, const float *y3, long n) {

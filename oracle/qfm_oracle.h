@@ -11,6 +11,8 @@
  *                                    ocho/engine_spark/cuda/qf.cu:1184-1271
  *   INT8 expert (exact + X8 modes)   ocho/amd_server/qf8_moe_i8.hip:58-144
  *   NVFP4 -> INT8 arena build        ocho/amd_server/qf8_moe_i8.hip:146-195
+ *   dense bf16 -> INT8 per row       ocho/amd_server/qf8_dense_i8.hip:41-60
+ *   FP8 lane-chunk format            ocho/amd_server/qf8_moe_fp8.hip:19-37, :217-246
  *   NVFP4 decode / expert            ocho/amd_server/qf_nvfp4_wave64.hip:10-21, 62-101,
  *                                    :175-216, :406-454
  *   routing inversion (CSR)          ocho/amd_server/qf8_moe_i8.hip:323-358,
@@ -40,6 +42,15 @@
  *   orc_nvfp4_to_i8        closed forms: the row maximum maps to +-127, an
  *                          all-zero row keeps scale 1, constant rows, codes
  *                          reconstruct within scale/2, 5-bit exponent field
+ *   orc_i8_quant_bf16      closed forms: row maximum -> +-127, all-zero row keeps
+ *                          scale 1, exact half-way ties round to even (rint,
+ *                          not round), clamp; numpy restatement on random rows
+ *   orc_f8_decode          all 256 codes vs torch float8_e4m3fn (0x7F / 0xFF: closed form 480)
+ *   orc_f8_encode          round trip over every code it emits; nearest-even vs torch on the
+ *                          normal range; closed forms for the truncated subnormals, the flush
+ *                          below 2^-9 and the saturation from 2^8 up
+ *   orc_fp8_pack_expert    chunk maximum -> 0x7E, zero chunk keeps scale 1, numpy
+ *                          restatement of the value formula on random experts
  *   orc_moe_layer          recomposition from the pieces with numpy fp64 experts
  */
 #ifndef QFM_ORACLE_H
@@ -105,6 +116,12 @@ void orc_nvfp4_dequant(const uint8_t *F, const uint8_t *S, float s2, int rows, i
 
 /* ---- NVFP4 -> INT8 arena conversion (bit-exact restatement) ---- */
 void orc_nvfp4_to_i8(const uint8_t *W, const uint8_t *S, float s2, int rows, int K, int8_t *Wo, float *So);
+/* dense bf16 [rows][K] -> per-row INT8 codes + fp32 scales (qf8_i8_quant_bf16's rule) */
+void orc_i8_quant_bf16(const uint16_t *W, int rows, int K, int8_t *Wo, float *So);
+/* FP8 lane-chunk format: E4M3 decode / encode of the reference's packer and the pack itself */
+float   orc_f8_decode(uint8_t b);
+uint8_t orc_f8_encode(float v);
+void    orc_fp8_pack_expert(const uint8_t *W, const uint8_t *S, float s2, int rows, int in, uint8_t *w8, float *sc);
 
 /* ---- X8 activation quantizer (reference's lossy activation mode) ---- */
 void orc_x8_quant(const float *v, int n, int8_t *q, float *s);

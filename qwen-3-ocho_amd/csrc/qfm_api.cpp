@@ -2,6 +2,7 @@
 // reference-named launchers, the fused per-layer forward and the harness
 // utilities. Host code only; every kernel lives in the .hip files.
 #include "qfm_internal.h"
+#include "../../include/qf_store.h"
 
 #include <array>
 #include <cstdarg>
@@ -94,11 +95,17 @@ static WsLayout ws_layout(int M) {
 static bool layer_ok(const qfm_layer *L) {
     if (!L || !L->arena || !L->router) return false;
     const Qf4ExpCache *a = L->arena;
+    // the fused forward addresses expert e at slot e: every expert resident
+    if (a->slots < g_cfg.E || !a->fully_resident) {
+        set_error(-1, "qfm_moe_forward: the arena must be fully resident (slots %d of %d, fully_resident %d)", a->slots,
+                  g_cfg.E, a->fully_resident);
+        return false;
+    }
     if (L->fmt == QFM_FMT_INT8) {
         if (!a->i8_gate || !a->i8_up || !a->i8_down || !a->i8s_gate || !a->i8s_up || !a->i8s_down) return false;
     } else if (L->fmt == QFM_FMT_NVFP4) {
         if (!a->w_gate || !a->w_up || !a->w_down || !a->s_gate || !a->s_up || !a->s_down || !a->s2g_dev ||
-            !a->s2u_dev || !a->s2d_dev)
+            !a->s2u_dev || !a->s2d_dev || a->nv_ring)   // a staging ring holds only nv_ring NVFP4 slots
             return false;
     } else {
         return false;
@@ -164,6 +171,10 @@ size_t qfm_sizeof(int which) {
     case 4: return sizeof(Qf5M8Route);
     case 5: return sizeof(qfm_config);
     case 6: return sizeof(qfm_ws_view);
+    case 7: return sizeof(QfEntry);
+    case 8: return sizeof(QfStore);
+    case 9: return sizeof(Qf4ExpXfer);
+    case 10: return sizeof(QfRouteMailbox);
     default: return 0;
     }
 }

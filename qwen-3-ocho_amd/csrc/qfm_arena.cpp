@@ -8,6 +8,7 @@
 // function of (seed, L, t, n), with n the row-major index over the whole
 // [experts][rows][cols] blob and the shared expert at expert index E.
 #include "qfm_internal.h"
+#include "../../include/qf_store.h"
 
 #include <cstring>
 #include <type_traits>
@@ -68,14 +69,8 @@ int qfm_arena_init(Qf4ExpCache *c, int fmt, int layer) {
     return 0;
 }
 
-void qfm_arena_free(Qf4ExpCache *c) {
-    if (!c) return;
-    dfree(&c->i8_gate); dfree(&c->i8_up); dfree(&c->i8_down);
-    dfree(&c->i8s_gate); dfree(&c->i8s_up); dfree(&c->i8s_down);
-    dfree(&c->w_gate); dfree(&c->w_up); dfree(&c->w_down);
-    dfree(&c->s_gate); dfree(&c->s_up); dfree(&c->s_down);
-    dfree(&c->s2g_dev); dfree(&c->s2u_dev); dfree(&c->s2d_dev);
-}
+// also releases what qfm_expcache_init allocates (host maps, routing state, mailbox)
+void qfm_arena_free(Qf4ExpCache *c) { qf4_expcache_free(c); }
 
 int qfm_arena_generate(Qf4ExpCache *c, uint32_t seed, uint32_t layer, hipStream_t s) {
     if (!c) { set_error(-1, "qfm_arena_generate: null arena"); return -1; }

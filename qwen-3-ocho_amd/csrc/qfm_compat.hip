@@ -843,13 +843,19 @@ int qf8_i8_build(Qf4ExpCache *c, hipStream_t s) {
         !c->s_gate || !c->s_up || !c->s_down || !c->s2u_dev || !c->s2d_dev || c->slots < 1 || c->slots > 65535 ||
         !shape_ok("qf8_i8_build"))
         return -1;
+    if (c->nv_ring) {   // the NVFP4 arrays hold only the staging ring, not every slot
+        set_error(-1, "qf8_i8_build: the arena's NVFP4 arrays are a %d-slot staging ring; use qf8_i8_build_slot",
+                  c->nv_ring);
+        return -1;
+    }
     return i8_build_range(c, 0, 0, 0, c->slots, s);
 }
 
 int qf8_i8_build_slot(Qf4ExpCache *c, int src_slot, int dst_slot, int expert, hipStream_t s) {
     if (!c || !c->i8_gate || !c->w_gate || !c->s2g_dev || !c->i8_up || !c->i8_down || !c->w_up || !c->w_down ||
         !c->s_gate || !c->s_up || !c->s_down || !c->s2u_dev || !c->s2d_dev || src_slot < 0 || dst_slot < 0 ||
-        src_slot >= c->slots || dst_slot >= c->slots || expert < 0 || expert >= g_cfg.E || !shape_ok("qf8_i8_build_slot"))
+        src_slot >= (c->nv_ring ? c->nv_ring : c->slots) || dst_slot >= c->slots || expert < 0 || expert >= g_cfg.E ||
+        !shape_ok("qf8_i8_build_slot"))
         return -1;
     return i8_build_range(c, src_slot, dst_slot, expert, 1, s);
 }

@@ -1,0 +1,249 @@
+// qfm_fp8.hip -- MoE over the FP8 lane-chunk arena (format and contract in
+// include/qf_fp8.h; semantics of ocho/amd_server/qf8_moe_fp8.hip:45-213).
+//
+// k_fp8_build_desc: one wave. The selected experts are marked in an LDS
+// bitmap, enumerated in ascending id, and for each the wave finds its rows
+// (lane t checks token t, a ballot orders them).
+// k_fp8_gateup / k_fp8_downacc: a fixed grid of 256-thread workgroups; wave w
+// of workgroup b takes items b*4 + w, then strides by 4 * gridDim.x, until
+// the device-side item count ctl[0] * tiles is exhausted (every wave reaches
+// that bound). An item is (descriptor, tile of output rows); the wave loads
+// all of the tile's weight chunks first (lane l owns chunk l of every row),
+// decodes them with the gfx950 E4M3 convert, then for each of the
+// descriptor's rows forms the chunk dot products, scales by the chunk scale
+// and sums across the wave (DPP). Gate/up writes silu(g) * u; down adds
+// wt * a into y with one atomic per (row, output).
+#include "qfm_internal.h"
+#include "qfm_dev.h"
+#include "../../include/qf_fp8.h"
+
+namespace qfm {
+
+constexpr int kF8Grid = 1024;          // workgroups of the item walks (4 per CU)
+constexpr int kF8MaxExperts = 512;
+constexpr int kF8RowsGu = 4;           // gate/up output rows per item
+constexpr int kF8RowsDn = 8;           // down output rows per item
+
+__global__ void __launch_bounds__(64)
+k_fp8_build_desc(const int *__restrict__ sel, const float *__restrict__ wt, int M, int K, int slot_base,
+                 Qf8MoeDesc *__restrict__ desc, int *__restrict__ ctl, int n_experts) {
+    __shared__ unsigned bits[kF8MaxExperts / 32];
+    const int lane = threadIdx.x;
+    const int nw = (n_experts + 31) / 32;
+    for (int i = lane; i < nw; i += 64) bits[i] = 0u;
+    __syncthreads();
+    for (int i = lane; i < M * K; i += 64) {
+        const int e = sel[i];
+        if (e >= 0 && e < n_experts) atomicOr(&bits[e >> 5], 1u << (e & 31));
+    }
+    __syncthreads();
+    int n = 0;
+    for (int w = 0; w < nw; w++) {
+        unsigned b = bits[w];
+        while (b) {
+            const int e = w * 32 + __builtin_ctz(b);
+            b &= b - 1u;
+            int nrow = 0;
+            for (int t0 = 0; t0 < M && nrow < QF8_FP8_MAXROW; t0 += 64) {
+                const int t = t0 + lane;
+                int kf = -1;
+                if (t < M)
+                    for (int k = 0; k < K; k++)
+                        if (sel[t * K + k] == e) { kf = k; break; }
+                const unsigned long long bal = __ballot(kf >= 0);
+                const int rank = __popcll(bal & ((1ull << lane) - 1ull));
+                if (kf >= 0 && nrow + rank < QF8_FP8_MAXROW) {
+                    desc[n].row[nrow + rank] = t;
+                    desc[n].wt[nrow + rank] = wt[t * K + kf];
+                }
+                nrow += __popcll(bal);
+            }
+            if (lane == 0) {
+                desc[n].slot = slot_base + e;
+                desc[n].nrow = min(nrow, QF8_FP8_MAXROW);
+            }
+            n++;
+        }
+    }
+    if (lane == 0) {
+        ctl[0] = n;
+        ctl[1] = 0;
+        ctl[2] = 0;
+    }
+}
+
+// decode 8 E4M3 codes (one uint2) into out[0..7]
+__device__ __forceinline__ void f8x8(uint2 q, float *out) {
+    const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8(q.x, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(q.x, true);
+    const f32x2_t c = __builtin_amdgcn_cvt_pk_f32_fp8(q.y, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(q.y, true);
+    out[0] = a.x; out[1] = a.y; out[2] = b.x; out[3] = b.y;
+    out[4] = c.x; out[5] = c.y; out[6] = d.x; out[7] = d.y;
+}
+
+// CH = H / 64 code bytes per lane and row (32 at H 2048, 40 at H 2560)
+template <int CH>
+__global__ void __launch_bounds__(256)
+k_fp8_gateup(const uint8_t *__restrict__ Wg, const float *__restrict__ Sg, const uint8_t *__restrict__ Wu,
+             const float *__restrict__ Su, const float *__restrict__ x, float *__restrict__ hidden,
+             const Qf8MoeDesc *__restrict__ desc, const int *__restrict__ ctl, int I) {
+    constexpr int H = CH * 64, NW = CH / 8, R = kF8RowsGu;
+    const int lane = threadIdx.x & 63;
+    const int tiles = I / R;
+    const int total = ctl[0] * tiles;
+    for (int item = blockIdx.x * 4 + (threadIdx.x >> 6); item < total; item += gridDim.x * 4) {
+        const int di = item / tiles, o0 = (item % tiles) * R;
+        const int slot = desc[di].slot, nrow = desc[di].nrow;
+        const size_t wb = (size_t)slot * I * H + (size_t)o0 * H + (size_t)lane * CH;
+        const size_t sb = ((size_t)slot * I + o0) * 64 + lane;
+        uint2 gq[R][NW], uq[R][NW];
+        float sg[R], su[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint2 *pg = reinterpret_cast<const uint2 *>(Wg + wb + (size_t)r * H);
+            const uint2 *pu = reinterpret_cast<const uint2 *>(Wu + wb + (size_t)r * H);
+#pragma unroll
+            for (int j = 0; j < NW; j++) {
+                gq[r][j] = pg[j];
+                uq[r][j] = pu[j];
+            }
+            sg[r] = Sg[sb + r * 64];
+            su[r] = Su[sb + r * 64];
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float gv[CH], uv[CH];
+#pragma unroll
+            for (int j = 0; j < NW; j++) {
+                f8x8(gq[r][j], gv + 8 * j);
+                f8x8(uq[r][j], uv + 8 * j);
+            }
+            for (int t = 0; t < nrow; t++) {
+                const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)desc[di].row[t] * H + (size_t)lane * CH);
+                float ag = 0.0f, au = 0.0f;
+#pragma unroll
+                for (int j = 0; j < CH / 4; j++) {
+                    const float4 xv = xr[j];
+                    ag = fmaf(gv[4 * j + 3], xv.w, fmaf(gv[4 * j + 2], xv.z, fmaf(gv[4 * j + 1], xv.y, fmaf(gv[4 * j], xv.x, ag))));
+                    au = fmaf(uv[4 * j + 3], xv.w, fmaf(uv[4 * j + 2], xv.z, fmaf(uv[4 * j + 1], xv.y, fmaf(uv[4 * j], xv.x, au))));
+                }
+                const float g = group_sum<64>(ag * sg[r]), u = group_sum<64>(au * su[r]);
+                if (lane == 0) hidden[((size_t)di * QF8_FP8_MAXROW + t) * I + o0 + r] = silu(g) * u;
+            }
+        }
+    }
+}
+
+// CHD = I / 64 code bytes per lane and row (8 at I 512, 10 at I 640)
+template <int CHD>
+__global__ void __launch_bounds__(256)
+k_fp8_downacc(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const float *__restrict__ hidden,
+              float *__restrict__ y, const Qf8MoeDesc *__restrict__ desc, const int *__restrict__ ctl, int H) {
+    constexpr int I = CHD * 64, R = kF8RowsDn;
+    const int lane = threadIdx.x & 63;
+    const int tiles = H / R;
+    const int total = ctl[0] * tiles;
+    for (int item = blockIdx.x * 4 + (threadIdx.x >> 6); item < total; item += gridDim.x * 4) {
+        const int di = item / tiles, o0 = (item % tiles) * R;
+        const int slot = desc[di].slot, nrow = desc[di].nrow;
+        const size_t wb = (size_t)slot * H * I + (size_t)o0 * I + (size_t)lane * CHD;
+        const size_t sb = ((size_t)slot * H + o0) * 64 + lane;
+        float w[R][CHD], sd[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if constexpr (CHD == 8) {
+                f8x8(*reinterpret_cast<const uint2 *>(Wd + wb + (size_t)r * I), w[r]);
+            } else {
+                const uint16_t *p = reinterpret_cast<const uint16_t *>(Wd + wb + (size_t)r * I);
+#pragma unroll
+                for (int j = 0; j < CHD / 2; j++) {
+                    const f32x2_t v = __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)p[j], false);
+                    w[r][2 * j] = v.x;
+                    w[r][2 * j + 1] = v.y;
+                }
+            }
+            sd[r] = Sd[sb + r * 64];
+        }
+        for (int t = 0; t < nrow; t++) {
+            const float *hr = hidden + ((size_t)di * QF8_FP8_MAXROW + t) * I + (size_t)lane * CHD;
+            float h[CHD];
+#pragma unroll
+            for (int j = 0; j < CHD / 2; j++) {
+                const float2 v = reinterpret_cast<const float2 *>(hr)[j];
+                h[2 * j] = v.x;
+                h[2 * j + 1] = v.y;
+            }
+            const int yrow = desc[di].row[t];
+            const float wt = desc[di].wt[t];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float a = 0.0f;
+#pragma unroll
+                for (int j = 0; j < CHD; j++) a = fmaf(w[r][j], h[j], a);
+                a = group_sum<64>(a * sd[r]);
+                if (lane == 0) atomicAdd(&y[(size_t)yrow * H + o0 + r], wt * a);
+            }
+        }
+    }
+}
+
+static bool fp8_shape_ok(const char *who) {
+    if (!shape_2048() && !shape_2560()) {
+        set_error(-2, "%s: unsupported shape H %d I %d", who, g_cfg.H, g_cfg.I);
+        return false;
+    }
+    return true;
+}
+
+}  // namespace qfm
+
+using namespace qfm;
+
+extern "C" {
+
+int qf8_fp8_build_desc_ex(const int *sel_dev, const float *wt_dev, int M, int K, int slot_base, Qf8MoeDesc *desc,
+                          int *ctl, hipStream_t s) {
+    if (!sel_dev || !wt_dev || !desc || !ctl) { set_error(-1, "qf8_fp8_build_desc: null argument"); return -1; }
+    if (M < 1 || K < 1 || K > 64 || M > (1 << 20) / K || slot_base < 0 || g_cfg.E > kF8MaxExperts) {
+        set_error(-2, "qf8_fp8_build_desc: M %d, K %d, slot_base %d out of range", M, K, slot_base);
+        return -2;
+    }
+    hipLaunchKernelGGL(k_fp8_build_desc, dim3(1), dim3(64), 0, s, sel_dev, wt_dev, M, K, slot_base, desc, ctl, g_cfg.E);
+    return check_launch("qf8_fp8_build_desc") ? -3 : 0;
+}
+
+int qf8_fp8_gateup_ex(const uint8_t *Wg, const float *Sg, const uint8_t *Wu, const float *Su, const float *x,
+                      float *hidden, const Qf8MoeDesc *desc, int *ctl, hipStream_t s) {
+    if (!Wg || !Sg || !Wu || !Su || !x || !hidden || !desc || !ctl) { set_error(-1, "qf8_fp8_gateup: null argument"); return -1; }
+    if (!fp8_shape_ok("qf8_fp8_gateup")) return -2;
+    if (shape_2048())
+        hipLaunchKernelGGL(k_fp8_gateup<32>, dim3(kF8Grid), dim3(256), 0, s, Wg, Sg, Wu, Su, x, hidden, desc, ctl, g_cfg.I);
+    else
+        hipLaunchKernelGGL(k_fp8_gateup<40>, dim3(kF8Grid), dim3(256), 0, s, Wg, Sg, Wu, Su, x, hidden, desc, ctl, g_cfg.I);
+    return check_launch("qf8_fp8_gateup") ? -3 : 0;
+}
+
+int qf8_fp8_downacc_ex(const uint8_t *Wd, const float *Sd, const float *hidden, float *y, const Qf8MoeDesc *desc,
+                       int *ctl, hipStream_t s) {
+    if (!Wd || !Sd || !hidden || !y || !desc || !ctl) { set_error(-1, "qf8_fp8_downacc: null argument"); return -1; }
+    if (!fp8_shape_ok("qf8_fp8_downacc")) return -2;
+    if (shape_2048())
+        hipLaunchKernelGGL(k_fp8_downacc<8>, dim3(kF8Grid), dim3(256), 0, s, Wd, Sd, hidden, y, desc, ctl, g_cfg.H);
+    else
+        hipLaunchKernelGGL(k_fp8_downacc<10>, dim3(kF8Grid), dim3(256), 0, s, Wd, Sd, hidden, y, desc, ctl, g_cfg.H);
+    return check_launch("qf8_fp8_downacc") ? -3 : 0;
+}
+
+void qf8_fp8_build_desc(const int *sel_dev, const float *wt_dev, int M, int K, int slot_base, Qf8MoeDesc *desc,
+                        int *ctl, hipStream_t s) {
+    (void)qf8_fp8_build_desc_ex(sel_dev, wt_dev, M, K, slot_base, desc, ctl, s);
+}
+void qf8_fp8_gateup(const uint8_t *Wg, const float *Sg, const uint8_t *Wu, const float *Su, const float *x,
+                    float *hidden, const Qf8MoeDesc *desc, int *ctl, hipStream_t s) {
+    (void)qf8_fp8_gateup_ex(Wg, Sg, Wu, Su, x, hidden, desc, ctl, s);
+}
+void qf8_fp8_downacc(const uint8_t *Wd, const float *Sd, const float *hidden, float *y, const Qf8MoeDesc *desc,
+                     int *ctl, hipStream_t s) {
+    (void)qf8_fp8_downacc_ex(Wd, Sd, hidden, y, desc, ctl, s);
+}
+
+}  // extern "C"

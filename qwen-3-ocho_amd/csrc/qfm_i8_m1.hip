@@ -282,6 +282,9 @@ int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *x
     if (!c || !c->i8_gate || !c->i8_up || !c->i8s_gate || !c->i8s_up) {
         set_error(-1, "i8_gateup_m1: arena has no INT8 gate/up"); return -1;
     }
+    if (c->slots < g_cfg.E) {   // expert ids address slots directly
+        set_error(-1, "i8_gateup_m1: the INT8 arena holds %d slots, not all %d experts", c->slots, g_cfg.E); return -1;
+    }
     if (nexp < 1 || nexp > 16 || (!xb && !xf && !x16 && !(x8q && x8s)) || !hidden || !sel || (logits && !wts)) {
         set_error(-1, "i8_gateup_m1: bad arguments"); return -1;
     }
@@ -312,6 +315,9 @@ int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *x
 int launch_i8_down_m1(const Qf4ExpCache *c, const float *hidden, const float *wts, const int *sel, int nexp,
                       const ShPtrs *sh, const float *gdot, float *y32, uint16_t *ybf, hipStream_t s) {
     if (!c || !c->i8_down || !c->i8s_down) { set_error(-1, "i8_down_m1: arena has no INT8 down"); return -1; }
+    if (c->slots < g_cfg.E) {   // expert ids address slots directly
+        set_error(-1, "i8_down_m1: the INT8 arena holds %d slots, not all %d experts", c->slots, g_cfg.E); return -1;
+    }
     if (nexp < 0 || nexp > 16 || (!y32 && !ybf) || !hidden || (nexp && (!sel || !wts))) {
         set_error(-1, "i8_down_m1: bad arguments"); return -1;
     }

@@ -64,6 +64,47 @@ class QfmSynthLayer(C.Structure):
     _fields_ = [("layer", QfmLayer), ("arena", Qf4ExpCache)]
 
 
+class QfRec(C.Structure):
+    """Byte-compatible with the reference's QfRec (ocho/amd_server/qwenflash.h:12-24)."""
+    _fields_ = [("file_idx", C.c_uint32), ("dtype", C.c_uint32), ("ne", C.c_uint64 * 4),
+                ("data_off", C.c_uint64), ("nbytes", C.c_uint64), ("scale2_off", C.c_uint64),
+                ("input_off", C.c_uint64), ("scale2_file", C.c_uint32), ("input_file", C.c_uint32),
+                ("flags", C.c_uint32)]
+
+
+class QfEntry(C.Structure):
+    """One 512-byte manifest record (qwenflash.h:26-30)."""
+    _fields_ = [("name", C.c_char * 256), ("rec", QfRec), ("_pad", C.c_uint8 * 168)]
+
+
+class QfStore(C.Structure):
+    """The opened store (qwenflash.h:32-39)."""
+    _fields_ = [("n_shards", C.c_int), ("shard_paths", vp), ("shard_fds", C.POINTER(C.c_int)),
+                ("shard_maps", C.POINTER(vp)), ("shard_sizes", C.POINTER(C.c_size_t)),
+                ("entries", C.POINTER(QfEntry)), ("n_entries", C.c_int)]
+
+
+class Qf4ExpXfer(C.Structure):
+    """Per-GPU transfer context (qf_nvfp4_wave64.h:178-183)."""
+    _fields_ = [("buf", vp * 2), ("ev", vp * 2), ("cur", C.c_int), ("xfer", vp)]
+
+
+class QfRouteMailbox(C.Structure):
+    """Miss mailbox (qwenflash.h:73-83)."""
+    _fields_ = [("seq", C.c_uint32), ("miss_n", C.c_uint32), ("miss_expert", C.c_int32 * 16),
+                ("miss_slot", C.c_int32 * 16)]
+
+
+class Qf8MoeDesc(C.Structure):
+    """FP8 path expert descriptor (qf8_moe_fp8.h:37-44)."""
+    _fields_ = [("slot", C.c_int), ("nrow", C.c_int), ("row", C.c_int * 16), ("wt", C.c_float * 16)]
+
+
+DTYPE_CODES = {"BF16": 1, "F32": 2, "U8": 3, "F8_E4M3": 4, "I64": 5, "F16": 6, "I8": 7, "I32": 8,
+               "F64": 9, "F8_E5M2": 10, "I16": 11, "U16": 12, "U32": 13, "U64": 14, "BOOL": 15}
+EXPCACHE_NVFP4, EXPCACHE_INT8, EXPCACHE_INT8_ONLY, EXPCACHE_FP8 = 1, 2, 4, 8
+
+
 class QfmWsView(C.Structure):
     _fields_ = [("logits", vp), ("sel", vp), ("wts", vp), ("hidden", vp), ("counters", vp)]
 
@@ -136,6 +177,36 @@ _SIGS = {
     "qfm_arena_free": (None, [C.POINTER(Qf4ExpCache)]),
     "qfm_synth_layer_create": (C.c_int, [C.POINTER(QfmSynthLayer), C.c_int, C.c_uint32, C.c_uint32, C.c_int, vp]),
     "qfm_synth_layer_destroy": (None, [C.POINTER(QfmSynthLayer)]),
+    "qf_store_open": (C.c_int, [C.POINTER(QfStore), C.c_char_p]),
+    "qf_find": (C.POINTER(QfEntry), [C.POINTER(QfStore), C.c_char_p]),
+    "qf_store_close": (None, [C.POINTER(QfStore)]),
+    "qfm_store_data": (vp, [C.POINTER(QfStore), C.POINTER(QfEntry)]),
+    "qf4_expxfer_init": (C.c_int, [C.POINTER(Qf4ExpXfer)]),
+    "qf4_expxfer_free": (None, [C.POINTER(Qf4ExpXfer)]),
+    "qf4_expcache_init": (C.c_int, [C.POINTER(Qf4ExpCache), C.POINTER(QfStore), C.c_int, C.c_int]),
+    "qfm_expcache_init": (C.c_int, [C.POINTER(Qf4ExpCache), C.POINTER(QfStore), C.c_int, C.c_int, C.c_int]),
+    "qf4_expcache_free": (None, [C.POINTER(Qf4ExpCache)]),
+    "qf4_expcache_prefill": (C.c_int, [C.POINTER(Qf4ExpCache), C.POINTER(QfStore), C.POINTER(Qf4ExpXfer), vp]),
+    "qf4_expcache_prepare": (C.c_int, [C.POINTER(Qf4ExpCache), C.POINTER(QfStore), C.POINTER(Qf4ExpXfer),
+                                       C.c_int, vp]),
+    "qf4_expcache_service": (C.c_int, [C.POINTER(Qf4ExpCache), C.POINTER(QfStore), C.POINTER(Qf4ExpXfer), vp]),
+    "qf4_expcache_stats": (None, [C.POINTER(C.c_ulonglong)] * 3),
+    "qf8_fp8_pack_expert": (C.c_int, [vp, vp, C.c_float, C.c_int, C.c_int, vp, vp]),
+    "qf8_i8_quant_bf16": (C.c_int, [vp, C.c_int, C.c_int, C.POINTER(Qf8I8Mat), vp]),
+    "qf8_i8_quant_bf16_host": (C.c_int, [vp, C.c_int, C.c_int, C.POINTER(Qf8I8Mat), vp]),
+    "qfm_layer_load": (C.c_int, [C.POINTER(QfmSynthLayer), C.POINTER(QfStore), C.c_int, C.c_int,
+                                 C.POINTER(Qf4ExpXfer), vp]),
+    "qfm_store_check_layer": (C.c_int, [C.POINTER(QfStore), C.c_int]),
+    "qf_rtr_dispatch_launch": (None, [vp] * 7 + [C.c_uint32, C.c_int, vp]),
+    "qf_rtr_dispatch_launch_ex": (C.c_int, [vp] * 7 + [C.c_uint32, C.c_int, vp]),
+    "qf_rtr_hist_launch": (None, [vp, vp, vp]),
+    "qf_rtr_hist_launch_ex": (C.c_int, [vp, vp, vp]),
+    "qf8_fp8_build_desc": (None, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp]),
+    "qf8_fp8_build_desc_ex": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp]),
+    "qf8_fp8_gateup": (None, [vp] * 9),
+    "qf8_fp8_gateup_ex": (C.c_int, [vp] * 9),
+    "qf8_fp8_downacc": (None, [vp] * 7),
+    "qf8_fp8_downacc_ex": (C.c_int, [vp] * 7),
     "qfm_gen_input_rows": (C.c_int, [vp, C.c_int, C.c_uint32, C.c_uint32, C.c_int, vp]),
     "qfm_dev_malloc": (vp, [C.c_size_t]),
     "qfm_dev_free": (C.c_int, [vp]),
@@ -311,3 +382,64 @@ class SynthLayer:
             self.destroy()
         except Exception:
             pass
+
+
+class Store:
+    """An opened weight store (qf_store_open): the reference's manifest
+    directory, one .safetensors file, or a directory of them."""
+
+    def __init__(self, path):
+        self.lib = load()
+        self.st = QfStore()
+        check(self.lib.qf_store_open(C.byref(self.st), str(path).encode()), f"qf_store_open({path})")
+
+    def find(self, name):
+        p = self.lib.qf_find(C.byref(self.st), name.encode())
+        return p.contents if p else None
+
+    def names(self):
+        return [self.st.entries[i].name.decode() for i in range(self.st.n_entries)]
+
+    def data(self, entry):
+        """The entry's bytes (a copy out of the mapping)."""
+        ptr = self.lib.qfm_store_data(C.byref(self.st), C.byref(entry))
+        return C.string_at(ptr, entry.rec.nbytes) if entry.rec.nbytes else b""
+
+    def close(self):
+        if self.st.entries or self.st.n_shards:
+            self.lib.qf_store_close(C.byref(self.st))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class ExpXfer:
+    """Pinned double-buffered transfer context (qf4_expxfer_init)."""
+
+    def __init__(self):
+        self.lib = load()
+        self.x = Qf4ExpXfer()
+        check(self.lib.qf4_expxfer_init(C.byref(self.x)), "qf4_expxfer_init")
+
+    def free(self):
+        if self.x.xfer:
+            self.lib.qf4_expxfer_free(C.byref(self.x))
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class LoadedLayer(SynthLayer):
+    """A MoE layer read from a weight store (qfm_layer_load)."""
+
+    def __init__(self, store, layer, fmt, xfer, stream=None):
+        self.lib = load()
+        self.s = QfmSynthLayer()
+        check(self.lib.qfm_layer_load(C.byref(self.s), C.byref(store.st), layer, fmt, C.byref(xfer.x),
+                                      stream.h if stream else None), f"qfm_layer_load(layer {layer})")

@@ -59,6 +59,10 @@ _SIGS = {
     "orc_nvfp4_dequant": (None, [vp, vp, C.c_float, C.c_int, C.c_int, vp]),
     "orc_x8_quant": (None, [vp, C.c_int, vp, vp]),
     "orc_nvfp4_to_i8": (None, [vp, vp, C.c_float, C.c_int, C.c_int, vp, vp]),
+    "orc_i8_quant_bf16": (None, [vp, C.c_int, C.c_int, vp, vp]),
+    "orc_f8_decode": (C.c_float, [C.c_uint8]),
+    "orc_f8_encode": (C.c_uint8, [C.c_float]),
+    "orc_fp8_pack_expert": (None, [vp, vp, C.c_float, C.c_int, C.c_int, vp, vp]),
     "orc_csr_build": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp, vp]),
     "orc_m8_reduce4": (None, [vp, vp, vp, vp, vp, C.c_long]),
     "orc_moe_layer": (C.c_int, [C.POINTER(LayerCfg), C.c_int, vp, vp, vp, vp, vp, vp]),
@@ -182,6 +186,41 @@ def nvfp4_to_i8(F, S, s2, rows, K):
     return q, sc
 
 
+def i8_quant_bf16(W):
+    """bf16 bits [rows][K] -> (int8 codes, fp32 row scales) by orc_i8_quant_bf16."""
+    lib = load()
+    W = np.ascontiguousarray(W, np.uint16)
+    rows, K = W.shape
+    q = np.empty((rows, K), np.int8)
+    sc = np.empty(rows, np.float32)
+    lib.orc_i8_quant_bf16(ptr(W), rows, K, ptr(q), ptr(sc))
+    return q, sc
+
+
+def f8_decode_table():
+    """fp32 value of every FP8 lane-chunk code (orc_f8_decode), [256]."""
+    lib = load()
+    return np.array([lib.orc_f8_decode(b) for b in range(256)], np.float32)
+
+
+def fp8_pack_expert(W, S, s2, rows, n_in):
+    """NVFP4 matrix -> (E4M3 codes [rows][in], fp32 chunk scales [rows][64]) by orc_fp8_pack_expert."""
+    lib = load()
+    w8 = np.empty((rows, n_in), np.uint8)
+    sc = np.empty((rows, 64), np.float32)
+    lib.orc_fp8_pack_expert(ptr(np.ascontiguousarray(W, np.uint8)), ptr(np.ascontiguousarray(S, np.uint8)),
+                            float(s2), rows, n_in, ptr(w8), ptr(sc))
+    return w8, sc
+
+
+def fp8_dequant(w8, sc):
+    """fp64 weights of a lane-chunk matrix: decode(code) * chunk scale."""
+    rows, n_in = w8.shape
+    ch = n_in // 64
+    v = f8_decode_table().astype(np.float64)[w8]
+    return v * np.repeat(sc.astype(np.float64), ch, axis=1)
+
+
 def x8_quant(v):
     lib = load()
     v = np.ascontiguousarray(v, np.float32)
@@ -261,13 +300,15 @@ def _expert_fp64(seed, layer, e, H, I, fmt):
 
 
 def moe_layer_grouped(H, I, E, K, M, seed, layer, x_layer, x_row0=0, fmt=0, gated=1, renorm=1, use_bias=0, x=None,
-                      router=None):
+                      router=None, expert_fn=None, shared=None, gate_vec=None):
     """The whole layer (orc_moe_layer's definition) evaluated expert by expert:
     every distinct expert's weights are dequantized once (the oracle's own
     dequantization, exact in fp64) and applied to all of its tokens with fp64
     matrix products, so a T = 8038 prefill is checked in seconds. Routing comes
     from the oracle's router and top-K. x (bf16 bits [M][H]) overrides the
-    generated input rows and router (fp32 [E][H]) the generated router weights.
+    generated input rows and router (fp32 [E][H]) the generated router weights;
+    expert_fn(e) -> (Wg, Wu, Wd) fp64 overrides the routed experts, shared
+    (Wg, Wu, Wd) the shared expert and gate_vec (fp32 [H]) its gate vector.
     Same arithmetic as orc_moe_layer up to the order of fp64 summation (pinned
     against it in tests/test_oracle_path.py)."""
     if x is None:
@@ -286,12 +327,13 @@ def moe_layer_grouped(H, I, E, K, M, seed, layer, x_layer, x_row0=0, fmt=0, gate
 
     for e in np.unique(sel):
         rows, ks = np.nonzero(sel == e)
-        Wg, Wu, Wd = _expert_fp64(seed, layer, int(e), H, I, fmt)
+        Wg, Wu, Wd = _expert_fp64(seed, layer, int(e), H, I, fmt) if expert_fn is None else expert_fn(int(e))
         y[rows] += w64[rows, ks][:, None] * expert_out(Wg, Wu, Wd, X[rows])
-    Wg, Wu, Wd = _expert_fp64(seed, layer, E, H, I, 0)          # shared expert: INT8, index E
+    # shared expert: generator INT8 expert index E unless given
+    Wg, Wu, Wd = _expert_fp64(seed, layer, E, H, I, 0) if shared is None else shared
     ys = expert_out(Wg, Wu, Wd, X)
     if gated:
-        g = fill("gauss", seed, layer, T_SHGATE, 0, H, 0.02).astype(np.float64)
+        g = (fill("gauss", seed, layer, T_SHGATE, 0, H, 0.02) if gate_vec is None else gate_vec).astype(np.float64)
         ys *= (1.0 / (1.0 + np.exp(-(X @ g))))[:, None]
     y += ys
     return dict(x=x, logits=logits, sel=sel, w=w64, y=y)

@@ -1,5 +1,5 @@
 """C-ABI checks that need no GPU: the library loads, exports every entry
-point include/qf_moe.h declares, and the FFI struct layouts agree."""
+point the headers under include/ declare, and the FFI struct layouts agree."""
 import ctypes as C
 import os
 import re
@@ -8,12 +8,13 @@ import subprocess
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "qf_moe.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if h.endswith(".h")]
 LIB = os.path.join(ROOT, "qwen-3-ocho_amd", "libqfm.so")
 
 
 def _declared_functions():
-    src = open(HEADER).read()
+    src = "\n".join(open(h).read() for h in HEADERS)
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     src = re.sub(r"//[^\n]*", "", src)
     names = set()
@@ -69,6 +70,10 @@ def test_library_loads_without_gpu_and_struct_sizes_match(built):
     assert lib.qfm_sizeof(4) == C.sizeof(qfm.Qf5M8Route) == 56
     assert lib.qfm_sizeof(5) == C.sizeof(qfm.QfmConfig)
     assert lib.qfm_sizeof(6) == C.sizeof(qfm.QfmWsView)
+    assert lib.qfm_sizeof(7) == C.sizeof(qfm.QfEntry) == 512
+    assert lib.qfm_sizeof(8) == C.sizeof(qfm.QfStore) == 56
+    assert lib.qfm_sizeof(9) == C.sizeof(qfm.Qf4ExpXfer) == 48
+    assert lib.qfm_sizeof(10) == C.sizeof(qfm.QfRouteMailbox) == 136
     # reference field offsets of the arena (qf_nvfp4_wave64.h:133-173 on LP64)
     assert qfm.Qf4ExpCache.i8_gate.offset == 80 and qfm.Qf4ExpCache.s_gate.offset == 136
     assert qfm.Qf4ExpCache.s2g_dev.offset == 256 and qfm.Qf4ExpCache.expected_seq.offset == 304
@@ -133,6 +138,11 @@ def test_validated_twins_reject_without_launching(built):
         "qf5_m8_build_csr_ex": (None, None, 0, 0, 0, 0, 0, None, None, None, None, None, None),
         "qf5_m8_reduce4_ex": (None, None, None, None, None, 8, None),
         "qf8_i8_shexp_m1_ex": (None,) * 4 + (None,) * 9 + (None,),
+        "qf_rtr_dispatch_launch_ex": (None,) * 7 + (1, 16, None),
+        "qf_rtr_hist_launch_ex": (None, None, None),
+        "qf8_fp8_build_desc_ex": (None, None, 1, 10, 0, None, None, None),
+        "qf8_fp8_gateup_ex": (None,) * 9,
+        "qf8_fp8_downacc_ex": (None,) * 7,
     }
     for name, args in calls.items():
         rc = getattr(lib, name)(*args)
@@ -153,6 +163,7 @@ def test_gated_shared_expert_needs_gate_vector_on_every_path(built):
     arena = qfm.Qf4ExpCache()
     for f in ("i8_gate", "i8_up", "i8_down", "i8s_gate", "i8s_up", "i8s_down"):
         setattr(arena, f, 0x1000)
+    arena.slots, arena.fully_resident = 512, 1
     lay = qfm.QfmLayer()
     lay.arena = C.pointer(arena)
     lay.fmt = qfm.QFM_FMT_INT8
@@ -166,3 +177,27 @@ def test_gated_shared_expert_needs_gate_vector_on_every_path(built):
         rc = lib.qfm_moe_forward(C.byref(lay), 0x6000, M, 0x7000, 0x100000, wsb, None)
         assert rc == -1, (M, rc)
         assert b"sh_gate_inp" in lib.qfm_last_error(), M
+
+
+def test_fused_forward_needs_a_fully_resident_arena(built):
+    """The fused forward addresses expert e at slot e: a partly resident cache
+    or an NVFP4 staging ring is rejected before any launch."""
+    import qfm
+    lib = qfm.load()
+    lib.qfm_init(C.byref(qfm.QfmConfig(2048, 512, 512, 10, 1, 0)))
+    arena = qfm.Qf4ExpCache()
+    for f in ("i8_gate", "i8_up", "i8_down", "i8s_gate", "i8s_up", "i8s_down", "w_gate", "w_up", "w_down",
+              "s_gate", "s_up", "s_down", "s2g_dev", "s2u_dev", "s2d_dev"):
+        setattr(arena, f, 0x1000)
+    lay = qfm.QfmLayer()
+    lay.arena = C.pointer(arena)
+    lay.router = 0x2000
+    wsb = lib.qfm_workspace_bytes(1)
+    for slots, resident, ring, fmt in ((192, 0, 0, qfm.QFM_FMT_INT8), (512, 0, 0, qfm.QFM_FMT_INT8),
+                                       (512, 1, 2, qfm.QFM_FMT_NVFP4)):
+        arena.slots, arena.fully_resident, arena.nv_ring = slots, resident, ring
+        lay.fmt = fmt
+        lib.qfm_last_error()
+        assert lib.qfm_moe_forward(C.byref(lay), 0x6000, 1, 0x7000, 0x100000, wsb, None) == -1
+        assert lib.qfm_last_error()
+    lib.qfm_init(C.byref(qfm.QfmConfig(2048, 512, 512, 10, 1, 1)))

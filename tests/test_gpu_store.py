@@ -1,0 +1,463 @@
+"""GPU: expert arenas read from a weight store, and the non-resident arena.
+
+The store is written from the device generator's NVFP4 arena for (SEED,
+LAYER) (bytes pinned to the CPU generator elsewhere) with the reference
+checkpoint's tensor names (tests/golden/make_store.py), in both on-disk forms.
+Bars: arena bytes, slot maps and INT8 conversions bit-exact; layer outputs
+within max|y - r| / max|r| <= 1e-2 of the fp64 oracle (bf16 out); the
+non-resident path bit-exact against the fully resident one (same kernel,
+same bytes, slots remapped); FP8 lane-chunk outputs within 1e-4 (fp32 out)
+of fp64 products of the packed weights."""
+import ctypes as C
+import os
+import shutil
+import sys
+
+import numpy as np
+import pytest
+
+import _oracle as orc
+import qfm
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+import make_store as ms  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+H, I, E, K = 2048, 512, 512, 10
+SEED, LAYER = 11, 2
+IH = I * H
+TOL = 1e-2
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _rel(y, r):
+    return float(np.abs(y - r).max() / np.abs(r).max())
+
+
+@pytest.fixture(scope="module")
+def lib():
+    L = qfm.load()
+    qfm.init(H, I, E, K, 1, 1)
+    info = qfm.device_info()
+    _say("device", info)
+    assert info["arch"].startswith("gfx950"), info
+    return L
+
+
+NV = (("w_gate", IH // 2), ("w_up", IH // 2), ("w_down", IH // 2),
+      ("s_gate", IH // 16), ("s_up", IH // 16), ("s_down", IH // 16))
+
+
+def _nv_arrays(c, nslots):
+    out = {nm: qfm.d2h(getattr(c, nm), np.uint8, (nslots, n)) for nm, n in NV}
+    for nm in ("s2g_dev", "s2u_dev", "s2d_dev"):
+        out[nm] = qfm.d2h(getattr(c, nm), np.float32, (E,))
+    return out
+
+
+@pytest.fixture(scope="module")
+def gen(lib):
+    """The device generator's NVFP4 arena for (SEED, LAYER), read back."""
+    st = qfm.Stream()
+    a = qfm.Qf4ExpCache()
+    qfm.check(lib.qfm_arena_init(C.byref(a), qfm.QFM_FMT_NVFP4, LAYER), "arena init")
+    qfm.check(lib.qfm_arena_generate(C.byref(a), SEED, LAYER, st.h), "arena generate")
+    st.sync()
+    arrs = _nv_arrays(a, E)
+    lib.qfm_arena_free(C.byref(a))
+    st.destroy()
+    return arrs
+
+
+@pytest.fixture(scope="module")
+def store(lib, gen, tmp_path_factory):
+    d = tmp_path_factory.mktemp("store")
+    _say("store dir", d, "free bytes", shutil.disk_usage(str(d)).free)
+    g = lambda t, n, sc: ms.bf16_rne(orc.fill("gauss", SEED, LAYER, t, 0, n, sc))
+    dense = dict(router=g(orc.T_ROUTER, E * H, 0.02), shared=(g(101, IH, 0.05), g(102, IH, 0.05), g(103, IH, 0.05)),
+                 gate_vec=g(orc.T_SHGATE, H, 0.02))
+    paths, per = [], (E + 2) // 3
+    for sh in range(3):
+        ts = []
+        for e in range(sh * per, min(E, (sh + 1) * per)):
+            ts += ms.expert_tensors(LAYER, e, H, I, [gen["w_gate"][e], gen["w_up"][e], gen["w_down"][e]],
+                                    [gen["s_gate"][e], gen["s_up"][e], gen["s_down"][e]])
+        if sh == 2:
+            ts += ms.dense_tensors(LAYER, H, I, E, **dense)
+        p = str(d / f"model-{sh + 1:05d}-of-00003.safetensors")
+        ms.write_safetensors(p, ts, metadata={"format": "pt"})
+        paths.append(p)
+    ms.manifest_from_safetensors(str(d / "index"), paths)
+    _say("store written", paths)
+    return dict(dir=d, dense=dense)
+
+
+@pytest.fixture(scope="module")
+def xfer(lib):
+    x = qfm.ExpXfer()
+    yield x
+    x.free()
+
+
+def _store(store, form):
+    return qfm.Store(store["dir"] if form == "safetensors" else store["dir"] / "index")
+
+
+def _cache(lib, st, slots, modes):
+    c = qfm.Qf4ExpCache()
+    qfm.check(lib.qfm_expcache_init(C.byref(c), C.byref(st.st), LAYER, slots, modes), "qfm_expcache_init")
+    return c
+
+
+# ------------------------------------------------------------------ dense quantizer
+@pytest.mark.parametrize("rows,Kd", [(512, 2048), (2048, 512), (640, 2560)])
+def test_quant_bf16_bit_exact(lib, rows, Kd):
+    _say("quant", rows, Kd)
+    rng = np.random.default_rng(rows)
+    W = ms.bf16_rne(rng.standard_normal((rows, Kd)).astype(np.float32) * 0.05)
+    W[1] = 0
+    W[2, :4] = ms.bf16_rne(np.array([127.0, 2.5, 3.5, -0.5], np.float32))
+    W[2, 4:] = 0
+    q_ref, s_ref = orc.i8_quant_bf16(W)
+    st = qfm.Stream()
+    dW = qfm.DevBuf.from_array(W)
+    for host in (False, True):
+        m = qfm.Qf8I8Mat()
+        fn = lib.qf8_i8_quant_bf16_host if host else lib.qf8_i8_quant_bf16
+        qfm.check(fn(W.ctypes.data if host else dW.ptr, rows, Kd, C.byref(m), st.h), "quant")
+        st.sync()
+        assert (m.rows, m.K) == (rows, Kd)
+        assert np.array_equal(qfm.d2h(m.w, np.int8, (rows, Kd)), q_ref)
+        assert np.array_equal(qfm.d2h(m.s, np.float32, (rows,)).view(np.uint32), s_ref.view(np.uint32))
+        lib.qfm_dev_free(m.w)
+        lib.qfm_dev_free(m.s)
+    st.destroy()
+
+
+# ------------------------------------------------------------------ full residency
+@pytest.mark.parametrize("form", ["safetensors", "manifest"])
+def test_full_residency_bit_exact(lib, gen, store, xfer, form):
+    _say("full residency from", form)
+    st = _store(store, form)
+    lib.qfm_last_error()
+    assert lib.qfm_store_check_layer(C.byref(st.st), LAYER) == 0, lib.qfm_last_error().decode()
+    s = qfm.Stream()
+    c = _cache(lib, st, E, qfm.EXPCACHE_NVFP4)
+    assert lib.qf4_expcache_prefill(C.byref(c), C.byref(st.st), C.byref(xfer.x), s.h) == 1
+    s.sync()
+    got = _nv_arrays(c, E)
+    for nm, _ in NV:
+        assert np.array_equal(got[nm], gen[nm]), nm
+    for nm in ("s2g_dev", "s2u_dev", "s2d_dev"):
+        assert np.all(got[nm] == np.float32(0.01)), nm
+    assert c.fully_resident == 1
+    assert np.array_equal(qfm.d2h(c.slot_for_expert_dev, np.int32, (E,)), np.arange(E))
+    assert np.array_equal(qfm.d2h(c.expert_in_slot_dev, np.int32, (E,)), np.arange(E))
+    lib.qf4_expcache_free(C.byref(c))
+    s.destroy()
+
+
+def test_int8_only_ring_matches_full_build(lib, gen, store, xfer):
+    _say("int8-only ring vs full build")
+    st = _store(store, "safetensors")
+    s = qfm.Stream()
+    ring = _cache(lib, st, E, qfm.EXPCACHE_NVFP4 | qfm.EXPCACHE_INT8 | qfm.EXPCACHE_INT8_ONLY)
+    assert ring.nv_ring == 2
+    assert lib.qf4_expcache_prefill(C.byref(ring), C.byref(st.st), C.byref(xfer.x), s.h) == 1
+    assert lib.qf8_i8_build(C.byref(ring), s.h) == -1          # the NVFP4 arrays are only the ring
+    lib.qfm_last_error()
+    full = _cache(lib, st, E, qfm.EXPCACHE_NVFP4 | qfm.EXPCACHE_INT8)
+    assert lib.qf4_expcache_prefill(C.byref(full), C.byref(st.st), C.byref(xfer.x), s.h) == 1
+    qfm.check(lib.qf8_i8_build(C.byref(full), s.h), "qf8_i8_build")
+    s.sync()
+    for nm, rows in (("i8_gate", I), ("i8_up", I), ("i8_down", H)):
+        a = qfm.d2h(getattr(ring, nm), np.int8, (E, IH))
+        b = qfm.d2h(getattr(full, nm), np.int8, (E, IH))
+        assert np.array_equal(a, b), nm
+        sa = qfm.d2h(getattr(ring, nm.replace("i8_", "i8s_")), np.float32, (E, rows))
+        sb = qfm.d2h(getattr(full, nm.replace("i8_", "i8s_")), np.float32, (E, rows))
+        assert np.array_equal(sa.view(np.uint32), sb.view(np.uint32)), nm
+        # and against the oracle's conversion for a few experts
+        src, sc_src = {"i8_gate": ("w_gate", "s_gate"), "i8_up": ("w_up", "s_up"), "i8_down": ("w_down", "s_down")}[nm]
+        cols = IH // rows
+        for e in (0, 311, 511):
+            q, sc = orc.nvfp4_to_i8(gen[src][e], gen[sc_src][e], 0.01, rows, cols)
+            assert np.array_equal(a[e].reshape(rows, cols), q), (nm, e)
+            assert np.array_equal(sa[e].view(np.uint32), sc.view(np.uint32)), (nm, e)
+    lib.qf4_expcache_free(C.byref(ring))
+    lib.qf4_expcache_free(C.byref(full))
+    s.destroy()
+
+
+# ------------------------------------------------------------------ whole layer
+def _oracle_expert_fn(fmt):
+    def fn(e):
+        if fmt == qfm.QFM_FMT_NVFP4:
+            return orc._expert_fp64(SEED, LAYER, e, H, I, 1)
+        out = []
+        for tf, ts, rows, cols in ((orc.T_FG, orc.T_FSG, I, H), (orc.T_FU, orc.T_FSU, I, H), (orc.T_FD, orc.T_FSD, H, I)):
+            F = orc.fill("fp4byte", SEED, LAYER, tf, e * IH // 2, IH // 2)
+            S = orc.fill("e4m3scale", SEED, LAYER, ts, e * IH // 16, IH // 16)
+            q, sc = orc.nvfp4_to_i8(F, S, 0.01, rows, cols)
+            out.append(q.astype(np.float64) * sc.astype(np.float64)[:, None])
+        return tuple(out)
+    return fn
+
+
+@pytest.mark.parametrize("fmt", [qfm.QFM_FMT_INT8, qfm.QFM_FMT_NVFP4])
+def test_layer_load_and_forward(lib, store, xfer, fmt):
+    _say("layer load", "int8" if fmt == qfm.QFM_FMT_INT8 else "nvfp4")
+    st = _store(store, "manifest")
+    s = qfm.Stream()
+    L = qfm.LoadedLayer(st, LAYER, fmt, xfer, stream=s)
+    dn = store["dense"]
+    router = orc.bf16_to_f32(dn["router"]).reshape(E, H)
+    gvec = orc.bf16_to_f32(dn["gate_vec"])
+    assert np.array_equal(qfm.d2h(L.layer.router, np.float32, (E, H)).view(np.uint32), router.view(np.uint32))
+    assert np.array_equal(qfm.d2h(L.layer.sh_gate_inp, np.float32, (H,)).view(np.uint32), gvec.view(np.uint32))
+    shared = []
+    for mat, bits, rows, cols in ((L.layer.sh_gate, dn["shared"][0], I, H), (L.layer.sh_up, dn["shared"][1], I, H),
+                                  (L.layer.sh_down, dn["shared"][2], H, I)):
+        q, sc = orc.i8_quant_bf16(bits.reshape(rows, cols))
+        assert np.array_equal(qfm.d2h(mat.w, np.int8, (rows, cols)), q)
+        assert np.array_equal(qfm.d2h(mat.s, np.float32, (rows,)).view(np.uint32), sc.view(np.uint32))
+        shared.append(q.astype(np.float64) * sc.astype(np.float64)[:, None])
+    efn = _oracle_expert_fn(fmt)
+    for M in (1, 4, 37):
+        x_layer = 300 + M
+        dx, dy = qfm.DevBuf(M * H * 2), qfm.DevBuf(M * H * 2)
+        qfm.check(lib.qfm_gen_input_rows(dx.ptr, M, SEED, x_layer, 0, s.h), "x")
+        wsb = lib.qfm_workspace_bytes(M)
+        ws = qfm.DevBuf(wsb)
+        qfm.check(lib.qfm_moe_forward(C.byref(L.s.layer), dx.ptr, M, dy.ptr, ws.ptr, wsb, s.h), "forward")
+        s.sync()
+        y = orc.bf16_to_f32(dy.download(np.uint16, (M, H)))
+        view = qfm.QfmWsView()
+        lib.qfm_workspace_view(ws.ptr, M, C.byref(view))
+        sel = qfm.d2h(view.sel, np.int32, (M, K))
+        r = orc.moe_layer_grouped(H, I, E, K, M, SEED, LAYER, x_layer, router=router, expert_fn=efn,
+                                  shared=tuple(shared), gate_vec=gvec)
+        assert np.array_equal(sel, r["sel"]), M
+        worst = max(_rel(y[m], r["y"][m]) for m in range(M))
+        _say("  M", M, "worst row rel err", worst)
+        assert worst <= TOL
+    L.destroy()
+    s.destroy()
+
+
+# ------------------------------------------------------------------ host LRU
+class _Lru:
+    """The reference's LRU rules (qf_expert_slots.cpp:367-391, qf_router_wave64.hip:183-256)."""
+
+    def __init__(self, slots):
+        self.sfe = {}
+        self.eis = [-1] * slots
+        self.age = [0] * slots
+        self.clock = 0
+
+    def host_prepare(self, e):
+        if e in self.sfe:
+            self.clock += 1
+            self.age[self.sfe[e]] = self.clock
+            return self.sfe[e], False
+        slot = 0
+        for i in range(len(self.eis)):
+            if self.eis[i] < 0:
+                slot = i
+                break
+            if self.age[i] < self.age[slot]:
+                slot = i
+        return self._take(e, slot), True
+
+    def device_step(self, e):
+        if e in self.sfe:
+            self.clock += 1
+            self.age[self.sfe[e]] = self.clock
+            return self.sfe[e], False
+        slot = min(range(len(self.eis)), key=lambda i: (self.age[i], i))
+        return self._take(e, slot), True
+
+    def _take(self, e, slot):
+        ev = self.eis[slot]
+        if ev >= 0:
+            del self.sfe[ev]
+        self.eis[slot] = e
+        self.sfe[e] = slot
+        self.clock += 1
+        self.age[slot] = self.clock
+        return slot
+
+
+def test_host_lru_prepare(lib, gen, store, xfer):
+    _say("host LRU")
+    st = _store(store, "safetensors")
+    s = qfm.Stream()
+    slots = K
+    c = _cache(lib, st, slots, qfm.EXPCACHE_NVFP4)
+    model = _Lru(slots)
+    seq = [5, 7, 5, 100, 200, 300, 400, 500, 1, 2, 3, 7, 9, 10, 11, 5, 300, 12, 13, 14, 5]
+    for e in seq:
+        got = lib.qf4_expcache_prepare(C.byref(c), C.byref(st.st), C.byref(xfer.x), e, s.h)
+        want, _ = model.host_prepare(e)
+        assert got == want, (e, got, want)
+    s.sync()
+    arr = _nv_arrays(c, slots)
+    for slot, e in enumerate(model.eis):
+        for nm, _ in NV:
+            assert np.array_equal(arr[nm][slot], gen[nm][e]), (slot, e, nm)
+    lib.qf4_expcache_free(C.byref(c))
+    s.destroy()
+
+
+# ------------------------------------------------------------------ device dispatch
+def test_device_dispatch_and_service(lib, gen, store, xfer):
+    _say("device dispatch + mailbox service")
+    st = _store(store, "safetensors")
+    s = qfm.Stream()
+    slots = 16
+    c = _cache(lib, st, slots, qfm.EXPCACHE_NVFP4)
+    full = qfm.Qf4ExpCache()
+    qfm.check(lib.qfm_arena_init(C.byref(full), qfm.QFM_FMT_NVFP4, LAYER), "full arena")
+    qfm.check(lib.qfm_arena_generate(C.byref(full), SEED, LAYER, s.h), "full arena generate")
+    rng = np.random.default_rng(9)
+    pool = rng.choice(E, 30, replace=False)
+    model = _Lru(slots)
+    d_sel, d_wts = qfm.DevBuf(K * 4), qfm.DevBuf(K * 4)
+    d_x, d_h, d_y, d_yref = qfm.DevBuf(H * 4), qfm.DevBuf(K * I * 4), qfm.DevBuf(H * 4), qfm.DevBuf(H * 4)
+    calls0, miss0, bytes0 = C.c_ulonglong(), C.c_ulonglong(), C.c_ulonglong()
+    lib.qf4_expcache_stats(C.byref(calls0), C.byref(miss0), C.byref(bytes0))
+    total_miss = 0
+    for tok in range(8):
+        sel = rng.choice(pool, K, replace=False).astype(np.int32)
+        w = rng.random(K).astype(np.float32)
+        w /= w.sum()
+        d_sel.upload(sel)
+        d_wts.upload(w)
+        d_x.upload(rng.standard_normal(H).astype(np.float32))
+        c.expected_seq += 1
+        assert lib.qf_rtr_dispatch_launch_ex(d_sel.ptr, c.slot_for_expert_dev, c.expert_in_slot_dev, c.age_dev,
+                                             c.clock_dev, c.route_slot_dev, c.mb_dev, c.expected_seq, c.slots,
+                                             s.h) == 0
+        assert lib.qf4_expcache_service(C.byref(c), C.byref(st.st), C.byref(xfer.x), s.h) == 0, \
+            lib.qfm_last_error().decode()
+        lib.qf5_nvfp4_moe_all(c.w_gate, c.s_gate, c.w_up, c.s_up, c.w_down, c.s_down, d_x.ptr, d_h.ptr, d_y.ptr,
+                              c.s2g_dev, c.s2u_dev, c.s2d_dev, d_wts.ptr, d_sel.ptr, c.route_slot_dev, K, s.h)
+        lib.qf5_nvfp4_moe_all(full.w_gate, full.s_gate, full.w_up, full.s_up, full.w_down, full.s_down, d_x.ptr,
+                              d_h.ptr, d_yref.ptr, full.s2g_dev, full.s2u_dev, full.s2d_dev, d_wts.ptr, d_sel.ptr,
+                              d_sel.ptr, K, s.h)
+        s.sync()
+        qfm.status_check("dispatch token")
+        want = [model.device_step(int(e)) for e in sel]
+        nmiss = sum(m for _, m in want)
+        total_miss += nmiss
+        route = qfm.d2h(c.route_slot_dev, np.int32, (K,))
+        assert list(route) == [sl for sl, _ in want], tok
+        assert np.array_equal(d_y.download(np.float32, (H,)).view(np.uint32),
+                              d_yref.download(np.float32, (H,)).view(np.uint32)), tok
+        sfe = qfm.d2h(c.slot_for_expert_dev, np.int32, (E,))
+        assert all(sfe[e] == model.sfe.get(e, -1) for e in range(E)), tok
+        assert list(qfm.d2h(c.expert_in_slot_dev, np.int32, (slots,))) == model.eis, tok
+        assert list(qfm.d2h(c.age_dev, np.uint64, (slots,))) == model.age, tok
+        assert int(qfm.d2h(c.clock_dev, np.uint64, (1,))[0]) == model.clock, tok
+        mb = qfm.QfRouteMailbox.from_address(c.mb_host)
+        assert mb.seq == c.expected_seq and mb.miss_n == 0
+        _say("  token", tok, "misses", nmiss)
+    calls1, miss1, bytes1 = C.c_ulonglong(), C.c_ulonglong(), C.c_ulonglong()
+    lib.qf4_expcache_stats(C.byref(calls1), C.byref(miss1), C.byref(bytes1))
+    assert calls1.value - calls0.value == 8 * K
+    assert miss1.value - miss0.value == total_miss
+    assert bytes1.value - bytes0.value == total_miss * 3 * (IH // 2 + IH // 16)
+    lib.qf4_expcache_free(C.byref(c))
+    lib.qfm_arena_free(C.byref(full))
+    s.destroy()
+
+
+def test_selection_histogram(lib):
+    s = qfm.Stream()
+    hist = qfm.DevBuf(E * 4)
+    hist.zero()
+    d_sel = qfm.DevBuf(K * 4)
+    want = np.zeros(E, np.int64)
+    rng = np.random.default_rng(3)
+    for _ in range(3):
+        sel = rng.choice(E, K, replace=False).astype(np.int32)
+        d_sel.upload(sel)
+        assert lib.qf_rtr_hist_launch_ex(d_sel.ptr, hist.ptr, s.h) == 0
+        s.sync()
+        want[sel] += 1
+    assert np.array_equal(hist.download(np.uint32, (E,)), want)
+    s.destroy()
+
+
+# ------------------------------------------------------------------ FP8 lane-chunk arena
+def _desc_model(sel, wt):
+    out = []
+    for e in sorted(set(int(v) for v in sel.ravel())):
+        rows = [(t, int(np.nonzero(sel[t] == e)[0][0])) for t in range(sel.shape[0]) if (sel[t] == e).any()][:16]
+        out.append((e, [t for t, _ in rows], [float(wt[t, k]) for t, k in rows]))
+    return out
+
+
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_fp8_arena_and_kernels(lib, gen, store, xfer, M):
+    _say("fp8 lane-chunk M", M)
+    st = _store(store, "safetensors")
+    s = qfm.Stream()
+    slots = 16
+    c = _cache(lib, st, slots, qfm.EXPCACHE_FP8)
+    for e in range(slots):     # first empty slot first: expert e lands in slot e
+        assert lib.qf4_expcache_prepare(C.byref(c), C.byref(st.st), C.byref(xfer.x), e, s.h) == e
+    s.sync()
+    dq = {}
+    for nm, snm, rows, cols, wsrc, ssrc in (("w8_gate", "sc_gate", I, H, "w_gate", "s_gate"),
+                                            ("w8_up", "sc_up", I, H, "w_up", "s_up"),
+                                            ("w8_down", "sc_down", H, I, "w_down", "s_down")):
+        w8 = qfm.d2h(getattr(c, nm), np.uint8, (slots, rows, cols))
+        sc = qfm.d2h(getattr(c, snm), np.float32, (slots, rows, 64))
+        for e in range(slots):
+            rw, rs = orc.fp8_pack_expert(gen[wsrc][e], gen[ssrc][e], 0.01, rows, cols)
+            assert np.array_equal(w8[e], rw) and np.array_equal(sc[e].view(np.uint32), rs.view(np.uint32)), (nm, e)
+        dq[nm] = [orc.fp8_dequant(w8[e], sc[e]) for e in range(slots)]
+    rng = np.random.default_rng(M)
+    sel = np.stack([rng.choice(slots, K, replace=False) for _ in range(M)]).astype(np.int32)
+    wt = rng.random((M, K)).astype(np.float32)
+    x = rng.standard_normal((M, H)).astype(np.float32)
+    nd_max = min(M * K, E)
+    d_sel, d_wt, d_x = qfm.DevBuf.from_array(sel), qfm.DevBuf.from_array(wt), qfm.DevBuf.from_array(x)
+    d_desc = qfm.DevBuf(nd_max * C.sizeof(qfm.Qf8MoeDesc))
+    d_ctl = qfm.DevBuf(16)
+    d_h = qfm.DevBuf(nd_max * 16 * I * 4)
+    d_y = qfm.DevBuf(M * H * 4)
+    d_y.zero()
+    assert lib.qf8_fp8_build_desc_ex(d_sel.ptr, d_wt.ptr, M, K, 0, d_desc.ptr, d_ctl.ptr, s.h) == 0
+    assert lib.qf8_fp8_gateup_ex(c.w8_gate, c.sc_gate, c.w8_up, c.sc_up, d_x.ptr, d_h.ptr, d_desc.ptr, d_ctl.ptr,
+                                 s.h) == 0
+    assert lib.qf8_fp8_downacc_ex(c.w8_down, c.sc_down, d_h.ptr, d_y.ptr, d_desc.ptr, d_ctl.ptr, s.h) == 0
+    s.sync()
+    model = _desc_model(sel, wt)
+    ctl = d_ctl.download(np.int32, (4,))
+    assert ctl[0] == len(model) and ctl[1] == 0 and ctl[2] == 0
+    raw = d_desc.download(np.uint8, (nd_max * C.sizeof(qfm.Qf8MoeDesc),))
+    descs = (qfm.Qf8MoeDesc * nd_max).from_buffer_copy(raw.tobytes())
+    hidden = d_h.download(np.float32, (nd_max, 16, I))
+    x64 = x.astype(np.float64)
+    y_ref = np.zeros((M, H))
+    for di, (e, rows, wts) in enumerate(model):
+        d = descs[di]
+        assert (d.slot, d.nrow) == (e, len(rows)) and list(d.row[:d.nrow]) == rows
+        assert np.array_equal(np.array(d.wt[:d.nrow], np.float32), np.array(wts, np.float32))
+        g = x64[rows] @ dq["w8_gate"][e].T
+        u = x64[rows] @ dq["w8_up"][e].T
+        h = g / (1.0 + np.exp(-g)) * u
+        assert _rel(hidden[di, :len(rows)], h) <= 1e-4, (di, e)
+        y_ref[rows] += np.array(wts)[:, None] * (h @ dq["w8_down"][e].T)
+    y = d_y.download(np.float32, (M, H))
+    worst = _rel(y, y_ref)
+    _say("  fp8 y rel err", worst)
+    assert worst <= 1e-4
+    lib.qf4_expcache_free(C.byref(c))
+    s.destroy()

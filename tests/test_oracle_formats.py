@@ -150,3 +150,31 @@ def test_bf16_rne_vs_torch():
     z = orc.fill("gauss", 3, 4, orc.T_X, 100, 5000, 1.0)
     zb = orc.fill("gauss_bf16", 3, 4, orc.T_X, 100, 5000)
     assert np.array_equal(zb, torch.from_numpy(z).to(torch.bfloat16).view(torch.uint16).numpy())
+
+
+def test_i8_quant_bf16_closed_forms_and_restatement():
+    """orc_i8_quant_bf16 (qf8_dense_i8.hip:41-60): scale = absmax / 127, codes
+    rint(w * (1/scale)) clamped; ties round to even, a zero row keeps scale 1."""
+    def bf(vals):   # fp32 -> bf16 bits, nearest even (inputs here are finite)
+        u = np.asarray(vals, np.float32).view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    K = 32
+    rows = np.zeros((4, K), np.uint16)
+    rows[0] = bf([127.0, 2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5, 126.5] + [0.0] * (K - 9))   # scale exactly 1
+    rows[1] = 0                                                                              # zero row
+    rows[2] = bf(np.linspace(-3, 3, K))
+    rows[3] = bf([-1e-3] + [5e-4] * (K - 1))
+    q, s = orc.i8_quant_bf16(rows)
+    assert s[0] == 1.0 and list(q[0, :9]) == [127, 2, 4, -2, -4, 0, 2, 0, 126]            # rint, not round
+    assert s[1] == 1.0 and not q[1].any()
+    assert q[2, 0] == -127 and q[2, -1] == 127 and q[3, 0] == -127
+    rng = np.random.default_rng(4)
+    W = bf(rng.standard_normal((64, 2048)) * 0.05)
+    q, s = orc.i8_quant_bf16(W)
+    w = orc.bf16_to_f32(W)
+    amax = np.abs(w).max(axis=1)
+    sc = np.where(amax > 0, amax / np.float32(127), np.float32(1)).astype(np.float32)
+    inv = (np.float32(1) / sc).astype(np.float32)
+    ref = np.clip(np.rint(w * inv[:, None]), -127, 127).astype(np.int8)
+    assert np.array_equal(s.view(np.uint32), sc.view(np.uint32))
+    assert np.array_equal(q, ref)
