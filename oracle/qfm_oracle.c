@@ -426,6 +426,52 @@ void orc_fp8_pack_expert(const uint8_t *W, const uint8_t *S, float s2, int rows,
     free(v);
 }
 
+/* INT8 x X8 GEMV (qf8_dense_i8.hip:78-103): y[r] = act(s[r] * sum_b xs[b] *
+   (W[r] . xq)[32-block b]); each block dot is an exact integer, the sum over
+   blocks is taken in fp64 here. act 0 none, 1 silu(v/4), 2 2*sigmoid(v/4). */
+void orc_i8_gemv(const int8_t *W, const float *s, int rows, int K, const int8_t *xq, const float *xs, int act,
+                 double *y) {
+    for (int r = 0; r < rows; r++) {
+        double acc = 0.0;
+        for (int b = 0; b < K / 32; b++) {
+            long d = 0;
+            for (int k = b * 32; k < b * 32 + 32; k++) d += (long)W[(size_t)r * K + k] * (long)xq[k];
+            acc += (double)d * (double)xs[b];
+        }
+        double v = acc * (double)s[r];
+        if (act == 1) v = (v * 0.25) / (1.0 + exp(-v * 0.25));
+        else if (act == 2) v = 2.0 / (1.0 + exp(-v * 0.25));
+        y[r] = v;
+    }
+}
+
+/* Zero-centered grouped RMS norm of the hyper-connection (qf8_dense_i8.hip:
+   109-149), one stream of H values, fp64: normed = R * rstd * (1 + w),
+   rstd = 1 / sqrt(mean(R^2) + 1e-6), w bf16. */
+void orc_hc_norm(const float *R, const uint16_t *w, int H, double *normed) {
+    double ss = 0.0;
+    for (int i = 0; i < H; i++) ss += (double)R[i] * (double)R[i];
+    const double rstd = 1.0 / sqrt(ss / H + 1e-6);
+    for (int i = 0; i < H; i++) normed[i] = (double)R[i] * rstd * (1.0 + (double)orc_bf16_to_f32(w[i]));
+}
+
+/* Stream combine (qf8_dense_i8.hip:151-175), fp64: mixed[j] = 1/4 sum_c
+   sigmoid(hcy[c*H + j]) * normed[c*H + j]. */
+void orc_hc_combine(const float *hcy, const float *normed, int H, double *mixed) {
+    for (int j = 0; j < H; j++) {
+        double sum = 0.0;
+        for (int c = 0; c < 4; c++) sum += (1.0 / (1.0 + exp(-(double)hcy[c * H + j]))) * (double)normed[c * H + j];
+        mixed[j] = 0.25 * sum;
+    }
+}
+
+/* Residual-stream inject (qf8_hc.hip:99-103): R[c*H + i] += inj[c] * y[i],
+   one fused multiply-add (the compiled form of the reference expression). */
+void orc_stream_inject(float *R, const float *y, const float *inj, int H) {
+    for (int c = 0; c < 4; c++)
+        for (int i = 0; i < H; i++) R[c * H + i] = fmaf(inj[c], y[i], R[c * H + i]);
+}
+
 /* Four-card combine: y[i] = ((y0[i] + y1[i]) + y2[i]) + y3[i], fp32, the
    left-to-right order of k_m8_reduce4 (qf_moe_m8_wave64.hip:216-221). */
 void orc_m8_reduce4(float *y, const float *y0, const float *y1, const float *y2, const float *y3, long n) {

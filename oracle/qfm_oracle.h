@@ -13,6 +13,7 @@
  *   NVFP4 -> INT8 arena build        ocho/amd_server/qf8_moe_i8.hip:146-195
  *   dense bf16 -> INT8 per row       ocho/amd_server/qf8_dense_i8.hip:41-60
  *   FP8 lane-chunk format            ocho/amd_server/qf8_moe_fp8.hip:19-37, :217-246
+ *   INT8 x X8 GEMV, hyper-connection ocho/amd_server/qf8_dense_i8.hip:78-175, qf8_hc.hip:99-103
  *   NVFP4 decode / expert            ocho/amd_server/qf_nvfp4_wave64.hip:10-21, 62-101,
  *                                    :175-216, :406-454
  *   routing inversion (CSR)          ocho/amd_server/qf8_moe_i8.hip:323-358,
@@ -51,6 +52,11 @@
  *                          below 2^-9 and the saturation from 2^8 up
  *   orc_fp8_pack_expert    chunk maximum -> 0x7E, zero chunk keeps scale 1, numpy
  *                          restatement of the value formula on random experts
+ *   orc_i8_gemv            numpy fp64 matmul of codes x dequantized X8 rows; closed forms of
+ *                          the two activations; one-hot rows
+ *   orc_hc_norm            numpy restatement; unit-RMS rows give normed = R * (1 + w)
+ *   orc_hc_combine         numpy restatement; equal streams reduce to sigmoid * normed
+ *   orc_stream_inject      numpy float32 fma restatement (np.float32 products rounded once)
  *   orc_moe_layer          recomposition from the pieces with numpy fp64 experts
  */
 #ifndef QFM_ORACLE_H
@@ -122,6 +128,11 @@ void orc_i8_quant_bf16(const uint16_t *W, int rows, int K, int8_t *Wo, float *So
 float   orc_f8_decode(uint8_t b);
 uint8_t orc_f8_encode(float v);
 void    orc_fp8_pack_expert(const uint8_t *W, const uint8_t *S, float s2, int rows, int in, uint8_t *w8, float *sc);
+/* dense INT8 x X8 GEMV, hyper-connection norm / combine, stream inject */
+void orc_i8_gemv(const int8_t *W, const float *s, int rows, int K, const int8_t *xq, const float *xs, int act, double *y);
+void orc_hc_norm(const float *R, const uint16_t *w, int H, double *normed);
+void orc_hc_combine(const float *hcy, const float *normed, int H, double *mixed);
+void orc_stream_inject(float *R, const float *y, const float *inj, int H);
 
 /* ---- X8 activation quantizer (reference's lossy activation mode) ---- */
 void orc_x8_quant(const float *v, int n, int8_t *q, float *s);

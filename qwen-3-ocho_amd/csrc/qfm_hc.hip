@@ -1,0 +1,338 @@
+// qfm_hc.hip -- dense INT8 x X8 projections, the FFN-side hyper-connection
+// pre-mixer and the residual-stream inject (contracts in include/qf_dense.h).
+//
+// k_gemv_i8x8<LPR, NST>: LPR lanes per weight row, NST 16-byte steps per
+// lane (K = 16 * LPR * NST); each lane keeps its NST weight words in
+// registers and reuses them for every activation row of its block's token
+// tile. Block dots are exact int32 (sdot4), scaled by the 32-value block
+// scale and accumulated in fp32, then summed over the LPR lanes with DPP.
+//
+// The pre-mixer runs in three launches:
+//   k_hc_norm_x8    one block per (stream, row): the fused inject of the
+//                   previous mixer, the zero-centered RMS norm and X8(normed);
+//   k_gemv_i8x8     down (silu(v/4)) and inject (2 sigmoid(v/4)) rows;
+//   k_hc_up_combine one block per 32 outputs j: X8(hc_d) into LDS (every
+//                   block; block 0 also stores it), the 4 x 32 up rows
+//                   {c*H + j} of the up GEMV, then the sigmoid-weighted mean
+//                   over the 4 streams and X8(mixed) of the 32 values.
+#include "qfm_internal.h"
+#include "qfm_dev.h"
+#include "../../include/qf_dense.h"
+
+namespace qfm {
+
+struct GemvMat {
+    const int8_t *w;
+    const float *s;
+    float *y;
+    int rows, act;
+};
+struct GemvBatch {
+    GemvMat d[4];
+    int n, K;
+};
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int dot16_i8i8(const i32x4 w, const i32x4 x) {
+    int d = __builtin_amdgcn_sdot4(w.x, x.x, 0, false);
+    d = __builtin_amdgcn_sdot4(w.y, x.y, d, false);
+    d = __builtin_amdgcn_sdot4(w.z, x.z, d, false);
+    return __builtin_amdgcn_sdot4(w.w, x.w, d, false);
+}
+
+__device__ __forceinline__ float gemv_act(float v, int act) {
+    if (act == 1) {
+        const float q = v * 0.25f;
+        return q / (1.0f + expf(-q));
+    }
+    if (act == 2) return 2.0f / (1.0f + expf(-v * 0.25f));
+    return v;
+}
+
+// X8 of one value per lane over aligned 32-lane groups (qf8_i8_x8's rule)
+__device__ __forceinline__ int x8_code(float v, float &scale) {
+    const float mx = group_max<32>(fabsf(v));
+    scale = mx > 0.0f ? mx * (1.0f / 127.0f) : 1.0f;
+    return min(127, max(-127, (int)rintf(v / scale)));
+}
+
+template <int LPR, int NST>
+__global__ void __launch_bounds__(256)
+k_gemv_i8x8(GemvBatch b, const int8_t *__restrict__ xq, const float *__restrict__ xs, int T, int tpb) {
+    constexpr int K = LPR * 16 * NST, RPB = 256 / LPR;
+    const int mi = blockIdx.y;                                   // select without indexing the argument block
+    const GemvMat d = mi == 0 ? b.d[0] : mi == 1 ? b.d[1] : mi == 2 ? b.d[2] : b.d[3];
+    if ((int)blockIdx.x * RPB >= d.rows) return;                 // block-uniform
+    const int l = threadIdx.x % LPR;
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR;
+    const bool live = row < d.rows;
+    const int8_t *wr = d.w + (size_t)(live ? row : 0) * K + l * 16;
+    i32x4 w[NST];
+#pragma unroll
+    for (int st = 0; st < NST; st++) w[st] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(wr + st * LPR * 16));
+    const float rs = live ? d.s[row] : 0.0f;
+    const int t_end = min(T, (int)(blockIdx.z + 1) * tpb);
+    for (int t = blockIdx.z * tpb; t < t_end; t++) {
+        const int8_t *xr = xq + (size_t)t * K;
+        const float *sr = xs + (size_t)t * (K / 32);
+        float acc = 0.0f;
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            const int e0 = st * LPR * 16 + l * 16;
+            acc = fmaf((float)dot16_i8i8(w[st], *reinterpret_cast<const i32x4 *>(xr + e0)), sr[e0 >> 5], acc);
+        }
+        acc = group_sum<LPR>(acc);
+        if (live && l == 0) d.y[(size_t)t * d.rows + row] = gemv_act(acc * rs, d.act);
+    }
+}
+
+// NV = H / 256 values per thread; grid (4 streams, T rows)
+template <int NV>
+__global__ void __launch_bounds__(256)
+k_hc_norm_x8(float *__restrict__ R, const uint16_t *__restrict__ wn, float *__restrict__ normed, int8_t *__restrict__ q,
+             float *__restrict__ sc, const float *__restrict__ y_prev, const float *__restrict__ inj_prev) {
+    constexpr int H = NV * 256, RS = 4 * H;
+    const int c = blockIdx.x, tid = threadIdx.x;
+    const size_t t = blockIdx.y, base = t * RS + (size_t)c * H;
+    float v[NV];
+    float acc = 0.0f;
+    if (y_prev) {
+        const float sj = inj_prev[t * QF8_HCC + c];
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int e = i * 256 + tid;
+            v[i] = fmaf(sj, y_prev[t * H + e], R[base + e]);
+            R[base + e] = v[i];
+            acc = fmaf(v[i], v[i], acc);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            v[i] = R[base + i * 256 + tid];
+            acc = fmaf(v[i], v[i], acc);
+        }
+    }
+    acc = group_sum<64>(acc);
+    __shared__ float red[4];
+    if ((tid & 63) == 0) red[tid >> 6] = acc;
+    __syncthreads();
+    const float rstd = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int e = i * 256 + tid;                          // 32 consecutive e per half-wave
+        const float nv = v[i] * rstd * (1.0f + bf16_to_f32(wn[(size_t)c * H + e]));
+        normed[base + e] = nv;
+        float s1;
+        q[base + e] = (int8_t)x8_code(nv, s1);
+        if ((tid & 31) == 0) sc[(base + e) >> 5] = s1;
+    }
+}
+
+// grid (H / 32, T), 512 threads: 8 waves x 16 row groups of 4 lanes = 128 up rows
+template <int H>
+__global__ void __launch_bounds__(512)
+k_hc_up_combine(const int8_t *__restrict__ Wu, const float *__restrict__ Su, const float *__restrict__ hc_d,
+                const float *__restrict__ normed, float *__restrict__ hcy, float *__restrict__ mixed,
+                int8_t *__restrict__ xq_out, float *__restrict__ xs_out, int8_t *__restrict__ d8q,
+                float *__restrict__ d8s) {
+    constexpr int L = QF8_HCL, RS = 4 * H;
+    __shared__ __align__(16) int8_t s_q[L];
+    __shared__ float s_s[L / 32];
+    __shared__ float s_h[4][32];
+    const int tid = threadIdx.x;
+    const size_t t = blockIdx.y;
+    const int j0 = blockIdx.x * 32;
+    if (tid < L) {                                            // threads 0..319: five whole waves
+        float s1;
+        const int qi = x8_code(hc_d[t * L + tid], s1);
+        s_q[tid] = (int8_t)qi;
+        if ((tid & 31) == 0) s_s[tid >> 5] = s1;
+        if (blockIdx.x == 0) {
+            d8q[t * L + tid] = (int8_t)qi;
+            if ((tid & 31) == 0) d8s[t * (L / 32) + (tid >> 5)] = s1;
+        }
+    }
+    __syncthreads();
+    const int lane = tid & 63, l = lane & 3;
+    const int li = (tid >> 6) * 16 + (lane >> 2);             // 0..127
+    const int c = li >> 5, jj = li & 31;
+    const size_t row = (size_t)c * H + j0 + jj;
+    const int8_t *wr = Wu + row * L + l * 16;
+    float acc = 0.0f;
+#pragma unroll
+    for (int st = 0; st < L / 64; st++) {
+        const int e0 = st * 64 + l * 16;
+        const i32x4 w = *reinterpret_cast<const i32x4 *>(wr + st * 64);
+        acc = fmaf((float)dot16_i8i8(w, *reinterpret_cast<const i32x4 *>(s_q + e0)), s_s[e0 >> 5], acc);
+    }
+    acc = group_sum<4>(acc);
+    if (l == 0) {
+        const float hv = acc * Su[row];
+        hcy[t * RS + row] = hv;
+        s_h[c][jj] = hv;
+    }
+    __syncthreads();
+    if (tid < 32) {
+        const int j = j0 + tid;
+        float sum = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            const float m = 1.0f / (1.0f + expf(-s_h[cc][tid]));
+            sum = fmaf(m, normed[t * RS + (size_t)cc * H + j], sum);
+        }
+        const float v = sum * 0.25f;
+        mixed[t * H + j] = v;
+        float s1;
+        xq_out[t * H + j] = (int8_t)x8_code(v, s1);
+        if (tid == 0) xs_out[t * (H / 32) + blockIdx.x] = s1;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_stream_inject(float *__restrict__ R, const float *__restrict__ y,
+                                                       const float *__restrict__ inj, int H) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < 4 * H) R[i] = fmaf(inj[i / H], y[i % H], R[i]);
+}
+
+// ---- host side -------------------------------------------------------------------
+static int fill_batch(const Qf8I8Multi *mm, GemvBatch *b, int *maxr, const char *who) {
+    if (!mm || mm->n < 1 || mm->n > 4) { set_error(-1, "%s: 1..4 matrices", who); return -1; }
+    *b = GemvBatch{};
+    b->n = mm->n;
+    *maxr = 0;
+    for (int i = 0; i < mm->n; i++) {
+        const Qf8I8Mat *m = mm->m[i];
+        if (!m || !m->w || !m->s || !mm->y[i] || m->rows < 1 || mm->act[i] < 0 || mm->act[i] > 2) {
+            set_error(-1, "%s: matrix %d: null pointer, no rows or act outside 0..2", who, i);
+            return -1;
+        }
+        if (i == 0) b->K = m->K;
+        if (m->K != b->K) { set_error(-2, "%s: mixed K (%d, %d)", who, b->K, m->K); return -2; }
+        b->d[i] = GemvMat{m->w, m->s, mm->y[i], m->rows, mm->act[i]};
+        *maxr = max(*maxr, m->rows);
+    }
+    return 0;
+}
+
+static int launch_gemv(const GemvBatch &b, int maxr, const int8_t *xq, const float *xs, int T, hipStream_t s,
+                       const char *who) {
+    const int tpb = T == 1 ? 1 : 8;
+    const unsigned gz = (unsigned)((T + tpb - 1) / tpb);
+#define QFM_GEMV(LPR, NST)                                                                                          \
+    hipLaunchKernelGGL((k_gemv_i8x8<LPR, NST>), dim3((unsigned)((maxr + 256 / LPR - 1) / (256 / LPR)), b.n, gz),   \
+                       dim3(256), 0, s, b, xq, xs, T, tpb)
+    switch (b.K) {
+        case 320: QFM_GEMV(4, 5); break;
+        case 512: QFM_GEMV(8, 4); break;
+        case 640: QFM_GEMV(8, 5); break;
+        case 2048: QFM_GEMV(32, 4); break;
+        case 2560: QFM_GEMV(32, 5); break;
+        case 6144: QFM_GEMV(32, 12); break;
+        case 8192: QFM_GEMV(64, 8); break;
+        case 10240: QFM_GEMV(64, 10); break;
+        default: set_error(-2, "%s: unsupported K = %d", who, b.K); return -2;
+    }
+#undef QFM_GEMV
+    return check_launch(who) ? -3 : 0;
+}
+
+static int hc_impl(float *normed, float *hc_d, float *mixed, float *inj, float *R, const uint16_t *wn,
+                   const Qf8I8Mat *down, const Qf8I8Mat *inject, const Qf8I8Mat *up, int8_t *n8q, float *n8s,
+                   int8_t *d8q, float *d8s, float *hcy, const float *y_prev, const float *inj_prev, int8_t *xq_out,
+                   float *xs_out, int T, hipStream_t s, const char *who) {
+    const int H = g_cfg.H, RS = 4 * H;
+    if (!normed || !hc_d || !mixed || !R || !wn || !down || !up || !n8q || !n8s || !d8q || !d8s || !hcy || !xq_out ||
+        !xs_out || (inject && !inj) || (!y_prev) != (!inj_prev) || T < 1) {
+        set_error(-1, "%s: null buffer (inject needs inj; y_prev and inj_prev go together)", who);
+        return -1;
+    }
+    if (H != 2048 && H != 2560) { set_error(-2, "%s: hidden %d unsupported", who, H); return -2; }
+    if (down->rows != QF8_HCL || down->K != RS || up->rows != RS || up->K != QF8_HCL ||
+        (inject && (inject->rows != QF8_HCC || inject->K != RS))) {
+        set_error(-2, "%s: expect down [%d][%d], inject [%d][%d], up [%d][%d]", who, QF8_HCL, RS, QF8_HCC, RS, RS,
+                  QF8_HCL);
+        return -2;
+    }
+    if (H == 2048)
+        hipLaunchKernelGGL(k_hc_norm_x8<8>, dim3(4, T), dim3(256), 0, s, R, wn, normed, n8q, n8s, y_prev, inj_prev);
+    else
+        hipLaunchKernelGGL(k_hc_norm_x8<10>, dim3(4, T), dim3(256), 0, s, R, wn, normed, n8q, n8s, y_prev, inj_prev);
+    if (check_launch(who)) return -3;
+    Qf8I8Multi m{};
+    m.n = inject ? 2 : 1;
+    m.m[0] = down; m.y[0] = hc_d; m.act[0] = 1;
+    if (inject) { m.m[1] = inject; m.y[1] = inj; m.act[1] = 2; }
+    GemvBatch b;
+    int maxr, rc = fill_batch(&m, &b, &maxr, who);
+    if (!rc) rc = launch_gemv(b, maxr, n8q, n8s, T, s, who);
+    if (rc) return rc;
+    const dim3 g((unsigned)(H / 32), (unsigned)T);
+    if (H == 2048)
+        hipLaunchKernelGGL(k_hc_up_combine<2048>, g, dim3(512), 0, s, up->w, up->s, hc_d, normed, hcy, mixed, xq_out,
+                           xs_out, d8q, d8s);
+    else
+        hipLaunchKernelGGL(k_hc_up_combine<2560>, g, dim3(512), 0, s, up->w, up->s, hc_d, normed, hcy, mixed, xq_out,
+                           xs_out, d8q, d8s);
+    return check_launch(who) ? -3 : 0;
+}
+
+}  // namespace qfm
+
+using namespace qfm;
+
+extern "C" {
+
+int qf8_i8_gemv_multi_ex(const Qf8I8Multi *mm, const int8_t *xq, const float *xs, hipStream_t s) {
+    return qf8_i8_gemv_rows(mm, xq, xs, 1, s);
+}
+
+void qf8_i8_gemv_multi(const Qf8I8Multi *mm, const int8_t *xq, const float *xs, hipStream_t s) {
+    (void)qf8_i8_gemv_multi_ex(mm, xq, xs, s);
+}
+
+int qf8_i8_gemv_rows(const Qf8I8Multi *mm, const int8_t *xq, const float *xs, int T, hipStream_t s) {
+    GemvBatch b;
+    int maxr;
+    if (!xq || !xs || T < 1 || T > 65535 * 8) { set_error(-1, "qf8_i8_gemv: null activations or T = %d", T); return -1; }
+    const int rc = fill_batch(mm, &b, &maxr, "qf8_i8_gemv");
+    return rc ? rc : launch_gemv(b, maxr, xq, xs, T, s, "qf8_i8_gemv");
+}
+
+int qf8_i8_hc_m1_ex(float *normed, float *hc_d, float *mixed, float *inj, float *R, const uint16_t *wn,
+                    const Qf8I8Mat *down, const Qf8I8Mat *inject, const Qf8I8Mat *up, int8_t *n8q, float *n8s,
+                    int8_t *d8q, float *d8s, float *hcy, const float *y_prev, const float *inj_prev, int8_t *xq_out,
+                    float *xs_out, hipStream_t s) {
+    return hc_impl(normed, hc_d, mixed, inj, R, wn, down, inject, up, n8q, n8s, d8q, d8s, hcy, y_prev, inj_prev,
+                   xq_out, xs_out, 1, s, "qf8_i8_hc_m1");
+}
+
+void qf8_i8_hc_m1(float *normed, float *hc_d, float *mixed, float *inj, float *R, const uint16_t *wn,
+                  const Qf8I8Mat *down, const Qf8I8Mat *inject, const Qf8I8Mat *up, int8_t *n8q, float *n8s,
+                  int8_t *d8q, float *d8s, float *hcy, const float *y_prev, const float *inj_prev, int8_t *xq_out,
+                  float *xs_out, hipStream_t s) {
+    (void)qf8_i8_hc_m1_ex(normed, hc_d, mixed, inj, R, wn, down, inject, up, n8q, n8s, d8q, d8s, hcy, y_prev,
+                          inj_prev, xq_out, xs_out, s);
+}
+
+int qf8_i8_hc_rows(float *normed, float *hc_d, float *mixed, float *inj, float *R, const uint16_t *wn,
+                   const Qf8I8Mat *down, const Qf8I8Mat *inject, const Qf8I8Mat *up, int8_t *n8q, float *n8s,
+                   int8_t *d8q, float *d8s, float *hcy, const float *y_prev, const float *inj_prev, int8_t *xq_out,
+                   float *xs_out, int T, hipStream_t s) {
+    if (T < 1 || T > 65535) { set_error(-1, "qf8_i8_hc_rows: T = %d", T); return -1; }
+    return hc_impl(normed, hc_d, mixed, inj, R, wn, down, inject, up, n8q, n8s, d8q, d8s, hcy, y_prev, inj_prev,
+                   xq_out, xs_out, T, s, "qf8_i8_hc_rows");
+}
+
+int qf8_stream_inject_ex(float *R, const float *y, const float *inj, hipStream_t s) {
+    if (!R || !y || !inj) { set_error(-1, "qf8_stream_inject: null argument"); return -1; }
+    const int H = g_cfg.H;
+    hipLaunchKernelGGL(k_stream_inject, dim3((unsigned)((4 * H + 255) / 256)), dim3(256), 0, s, R, y, inj, H);
+    return check_launch("qf8_stream_inject") ? -3 : 0;
+}
+
+void qf8_stream_inject(float *R, const float *y, const float *inj, hipStream_t s) {
+    (void)qf8_stream_inject_ex(R, y, inj, s);
+}
+
+}  // extern "C"

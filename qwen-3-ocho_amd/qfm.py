@@ -95,6 +95,11 @@ class QfRouteMailbox(C.Structure):
                 ("miss_slot", C.c_int32 * 16)]
 
 
+class Qf8I8Multi(C.Structure):
+    """Up to 4 INT8 matrices sharing one X8 row (qf8_dense_i8.h:31-32)."""
+    _fields_ = [("m", C.POINTER(Qf8I8Mat) * 4), ("y", vp * 4), ("act", C.c_int * 4), ("n", C.c_int)]
+
+
 class Qf8MoeDesc(C.Structure):
     """FP8 path expert descriptor (qf8_moe_fp8.h:37-44)."""
     _fields_ = [("slot", C.c_int), ("nrow", C.c_int), ("row", C.c_int * 16), ("wt", C.c_float * 16)]
@@ -207,6 +212,14 @@ _SIGS = {
     "qf8_fp8_gateup_ex": (C.c_int, [vp] * 9),
     "qf8_fp8_downacc": (None, [vp] * 7),
     "qf8_fp8_downacc_ex": (C.c_int, [vp] * 7),
+    "qf8_i8_gemv_multi": (None, [C.POINTER(Qf8I8Multi), vp, vp, vp]),
+    "qf8_i8_gemv_multi_ex": (C.c_int, [C.POINTER(Qf8I8Multi), vp, vp, vp]),
+    "qf8_i8_gemv_rows": (C.c_int, [C.POINTER(Qf8I8Multi), vp, vp, C.c_int, vp]),
+    "qf8_i8_hc_m1": (None, [vp] * 6 + [C.POINTER(Qf8I8Mat)] * 3 + [vp] * 9 + [vp]),
+    "qf8_i8_hc_m1_ex": (C.c_int, [vp] * 6 + [C.POINTER(Qf8I8Mat)] * 3 + [vp] * 9 + [vp]),
+    "qf8_i8_hc_rows": (C.c_int, [vp] * 6 + [C.POINTER(Qf8I8Mat)] * 3 + [vp] * 9 + [C.c_int, vp]),
+    "qf8_stream_inject": (None, [vp, vp, vp, vp]),
+    "qf8_stream_inject_ex": (C.c_int, [vp, vp, vp, vp]),
     "qfm_gen_input_rows": (C.c_int, [vp, C.c_int, C.c_uint32, C.c_uint32, C.c_int, vp]),
     "qfm_dev_malloc": (vp, [C.c_size_t]),
     "qfm_dev_free": (C.c_int, [vp]),

@@ -63,6 +63,10 @@ _SIGS = {
     "orc_f8_decode": (C.c_float, [C.c_uint8]),
     "orc_f8_encode": (C.c_uint8, [C.c_float]),
     "orc_fp8_pack_expert": (None, [vp, vp, C.c_float, C.c_int, C.c_int, vp, vp]),
+    "orc_i8_gemv": (None, [vp, vp, C.c_int, C.c_int, vp, vp, C.c_int, vp]),
+    "orc_hc_norm": (None, [vp, vp, C.c_int, vp]),
+    "orc_hc_combine": (None, [vp, vp, C.c_int, vp]),
+    "orc_stream_inject": (None, [vp, vp, vp, C.c_int]),
     "orc_csr_build": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp, vp]),
     "orc_m8_reduce4": (None, [vp, vp, vp, vp, vp, C.c_long]),
     "orc_moe_layer": (C.c_int, [C.POINTER(LayerCfg), C.c_int, vp, vp, vp, vp, vp, vp]),
@@ -219,6 +223,41 @@ def fp8_dequant(w8, sc):
     ch = n_in // 64
     v = f8_decode_table().astype(np.float64)[w8]
     return v * np.repeat(sc.astype(np.float64), ch, axis=1)
+
+
+def i8_gemv(W, s, xq, xs, act=0):
+    """INT8 [rows][K] x one X8 row -> fp64 [rows] (orc_i8_gemv)."""
+    lib = load()
+    W = np.ascontiguousarray(W, np.int8)
+    rows, K = W.shape
+    y = np.empty(rows, np.float64)
+    lib.orc_i8_gemv(ptr(W), ptr(np.ascontiguousarray(s, np.float32)), rows, K, ptr(np.ascontiguousarray(xq, np.int8)),
+                    ptr(np.ascontiguousarray(xs, np.float32)), act, ptr(y))
+    return y
+
+
+def hc_norm(R, w):
+    lib = load()
+    R = np.ascontiguousarray(R, np.float32)
+    out = np.empty(R.shape[0], np.float64)
+    lib.orc_hc_norm(ptr(R), ptr(np.ascontiguousarray(w, np.uint16)), R.shape[0], ptr(out))
+    return out
+
+
+def hc_combine(hcy, normed, H):
+    lib = load()
+    out = np.empty(H, np.float64)
+    lib.orc_hc_combine(ptr(np.ascontiguousarray(hcy, np.float32)), ptr(np.ascontiguousarray(normed, np.float32)), H,
+                       ptr(out))
+    return out
+
+
+def stream_inject(R, y, inj):
+    lib = load()
+    R = np.array(R, np.float32, copy=True)
+    lib.orc_stream_inject(ptr(R), ptr(np.ascontiguousarray(y, np.float32)), ptr(np.ascontiguousarray(inj, np.float32)),
+                          len(y))
+    return R
 
 
 def x8_quant(v):

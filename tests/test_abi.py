@@ -143,6 +143,9 @@ def test_validated_twins_reject_without_launching(built):
         "qf8_fp8_build_desc_ex": (None, None, 1, 10, 0, None, None, None),
         "qf8_fp8_gateup_ex": (None,) * 9,
         "qf8_fp8_downacc_ex": (None,) * 7,
+        "qf8_i8_gemv_multi_ex": (None, None, None, None),
+        "qf8_i8_hc_m1_ex": (None,) * 19,
+        "qf8_stream_inject_ex": (None, None, None, None),
     }
     for name, args in calls.items():
         rc = getattr(lib, name)(*args)
