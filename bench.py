@@ -324,6 +324,191 @@ def run_prefill(lib, st, args, T=8038, nl=4, fmt=0):
                          "traffic": None}}
 
 
+HCL = 320                                   # hyper-connection low rank
+
+
+def run_hc(lib, st, args, nl=48):
+    """The FFN-side hyper-connection pre-mixer (qf8_i8_hc_m1) at M=1 over nl
+    distinct layers of INT8 mixer weights, graph-captured; the fused inject of
+    the previous mixer is on. Algorithmic bytes: the three INT8 matrices and
+    their row scales, the norm weight, and the fp32/int8 vectors each launch
+    reads or writes once."""
+    import qfm
+    RS = 4 * H
+    mats = []
+    for l in range(nl):
+        m = {}
+        for nm, rows, k in (("down", HCL, RS), ("inject", 4, RS), ("up", RS, HCL)):
+            w, sc = qfm.DevBuf(rows * k), qfm.DevBuf(rows * 4)
+            qfm.check(lib.qfm_gen_fill(w.ptr, qfm.GEN_I8, 0, rows * k, 5, 3000 + l, 21 + len(m), 0.0, st.h), "w")
+            qfm.check(lib.qfm_gen_fill(sc.ptr, qfm.GEN_ROWSCALE, 0, rows, 5, 3000 + l, 31 + len(m), 0.0, st.h), "s")
+            m[nm] = (w, sc, qfm.Qf8I8Mat(w.ptr, sc.ptr, rows, k))
+        wn = qfm.DevBuf(RS * 2)
+        qfm.check(lib.qfm_gen_fill(wn.ptr, qfm.GEN_GAUSS_BF16, 0, RS, 5, 3000 + l, 41, 0.0, st.h), "wn")
+        m["wn"] = wn
+        mats.append(m)
+    R, yp = qfm.DevBuf(RS * 4), qfm.DevBuf(H * 4)
+    ip = qfm.DevBuf(16)
+    qfm.check(lib.qfm_gen_fill(R.ptr, qfm.GEN_GAUSS_F32, 0, RS, 5, 1, 1, 1.0, st.h), "R")
+    qfm.check(lib.qfm_gen_fill(yp.ptr, qfm.GEN_GAUSS_F32, 0, H, 5, 1, 2, 0.01, st.h), "y_prev")
+    qfm.check(lib.qfm_fill_f32(ip.ptr, 4, 1.0, st.h), "inj_prev")
+    b = {nm: qfm.DevBuf(n) for nm, n in (("normed", RS * 4), ("hc_d", HCL * 4), ("mixed", H * 4), ("inj", 16),
+                                          ("n8q", RS), ("n8s", RS // 8), ("d8q", HCL), ("d8s", HCL // 8),
+                                          ("hcy", RS * 4), ("xq", H), ("xs", H // 8))}
+    st.sync()
+
+    def enq():
+        for m in mats:
+            qfm.check(lib.qf8_i8_hc_m1_ex(b["normed"].ptr, b["hc_d"].ptr, b["mixed"].ptr, b["inj"].ptr, R.ptr,
+                                          m["wn"].ptr, C.byref(m["down"][2]), C.byref(m["inject"][2]),
+                                          C.byref(m["up"][2]), b["n8q"].ptr, b["n8s"].ptr, b["d8q"].ptr,
+                                          b["d8s"].ptr, b["hcy"].ptr, yp.ptr, ip.ptr, b["xq"].ptr, b["xs"].ptr,
+                                          st.h), "hc")
+    ms = time_graph(lib, st, enq, args.steps, args.warmup)
+    us = ms * 1000.0 / nl
+    wbytes = HCL * RS + 4 * RS + RS * HCL + (HCL + 4 + RS) * 4 + RS * 2
+    vbytes = (RS * 4 * 2 + H * 4 + 16 + RS * 4 + RS + RS // 8              # norm: R in/out, y_prev, inj, normed, X8
+              + RS + RS // 8 + (HCL + 4) * 4                              # down/inject: X8(normed) in, outputs
+              + HCL * 4 + HCL + HCL // 8 + RS * 4 + RS * 4 + H * 4 + H + H // 8)   # up/combine
+    nbytes = wbytes + vbytes
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"hc pre-mixer M=1: {us:.2f} us/layer, {nbytes / 1e6:.2f} MB/layer, {gbs:.0f} GB/s")
+    return {"workload": f"FFN-side hyper-connection pre-mixer qf8_i8_hc_m1, M=1, H={H} (4 streams, low rank {HCL}), "
+                        f"{nl} distinct layers, fused inject on",
+            "us_per_layer": round(us, 3), "algorithmic_bytes_per_layer": nbytes, "launches_per_layer": 3,
+            "roofline": {"bound": "hbm", "level": "layer (all three launches)", "achieved": round(gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+
+
+def run_fp8(lib, st, args, nl=8):
+    """The FP8 lane-chunk MoE (descriptor build, gate/up, down + accumulate)
+    at M=1 and M=8 on fully resident FP8 arenas of nl distinct layers. Timing
+    only: the code bytes are random (the arithmetic is pinned by the GPU
+    tests), the routing is K distinct random experts per row."""
+    import qfm
+    IH = I * H
+    arenas = []
+    for l in range(nl):
+        a = {}
+        for nm, n in (("w8_gate", E * IH), ("w8_up", E * IH), ("w8_down", E * IH)):
+            a[nm] = qfm.DevBuf(n)
+            qfm.check(lib.qfm_gen_fill(a[nm].ptr, qfm.GEN_FP4BYTE, 0, n, 6, 4000 + l, 1 + len(a), 0.0, st.h), "w8")
+        for nm, n in (("sc_gate", E * I * 64), ("sc_up", E * I * 64), ("sc_down", E * H * 64)):
+            a[nm] = qfm.DevBuf(n * 4)
+            qfm.check(lib.qfm_fill_f32(a[nm].ptr, n, 1e-3, st.h), "sc")
+        arenas.append(a)
+    st.sync()
+    rng = np.random.default_rng(11)
+    out = {}
+    for M in (1, 8):
+        sels = [np.stack([rng.choice(E, K, replace=False) for _ in range(M)]).astype(np.int32) for _ in range(nl)]
+        d_sel = [qfm.DevBuf.from_array(s_) for s_ in sels]
+        d_wt = qfm.DevBuf.from_array(np.full((M, K), 0.1, np.float32))
+        d_x = qfm.DevBuf(M * H * 4)
+        qfm.check(lib.qfm_gen_fill(d_x.ptr, qfm.GEN_GAUSS_F32, 0, M * H, 6, 1, 3, 1.0, st.h), "x")
+        nd = min(M * K, E)
+        d_desc = qfm.DevBuf(nd * C.sizeof(qfm.Qf8MoeDesc))
+        d_ctl = qfm.DevBuf(16)
+        d_h = qfm.DevBuf(nd * 16 * I * 4)
+        d_y = qfm.DevBuf(M * H * 4)
+        st.sync()
+
+        def enq():
+            for l, a in enumerate(arenas):
+                qfm.check(lib.qfm_fill_f32(d_y.ptr, M * H, 0.0, st.h), "zero y")
+                qfm.check(lib.qf8_fp8_build_desc_ex(d_sel[l].ptr, d_wt.ptr, M, K, 0, d_desc.ptr, d_ctl.ptr, st.h), "desc")
+                qfm.check(lib.qf8_fp8_gateup_ex(a["w8_gate"].ptr, a["sc_gate"].ptr, a["w8_up"].ptr, a["sc_up"].ptr,
+                                                d_x.ptr, d_h.ptr, d_desc.ptr, d_ctl.ptr, st.h), "gateup")
+                qfm.check(lib.qf8_fp8_downacc_ex(a["w8_down"].ptr, a["sc_down"].ptr, d_h.ptr, d_y.ptr, d_desc.ptr,
+                                                 d_ctl.ptr, st.h), "down")
+        ms = time_graph(lib, st, enq, args.steps, args.warmup)
+        us = ms * 1000.0 / nl
+        U = float(np.mean([len(np.unique(s_)) for s_ in sels]))
+        ebytes = 3 * IH + (2 * I + H) * 64 * 4
+        nbytes = U * ebytes + M * H * 4 * 2                             # experts + x in + y out
+        gbs = nbytes / (us * 1e-6) / 1e9
+        log(f"fp8 lane-chunk M={M}: {us:.2f} us/layer, {U:.1f} experts, {gbs:.0f} GB/s")
+        out[f"M{M}"] = {"us_per_layer": round(us, 3), "mean_distinct_experts": round(U, 2),
+                        "algorithmic_bytes_per_layer": int(nbytes), "launches_per_layer": 4,
+                        "roofline": {"bound": "hbm", "level": "layer (y clear, descriptors, gate/up, down)",
+                                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+    for a in arenas:
+        for b_ in a.values():
+            b_.free()
+    out["workload"] = (f"FP8 lane-chunk routed experts (qf8_fp8_build_desc / gateup / downacc), {nl} distinct "
+                       "layers, random codes (timing only), routed experts only")
+    return out
+
+
+def run_store(lib, st, args):
+    """Ingest and non-resident decode: writes one synthetic layer as a 3-shard
+    safetensors checkpoint (tests/golden/make_store.py), times qfm_layer_load
+    (mmap -> pinned staging -> HBM) for both arena formats, then decodes
+    tokens through a 192-slot LRU arena (dispatch kernel + host mailbox
+    service + NVFP4 experts) with uniform random routing."""
+    import shutil
+    import tempfile
+    import qfm
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import make_store as ms_
+    d = tempfile.mkdtemp(prefix="qfm_store_")
+    try:
+        t0 = time.time()
+        ms_.synthetic_layer(d, H, I, E, 0, 7, shards=3)
+        log(f"store written ({time.time() - t0:.1f}s)")
+        store = qfm.Store(d)
+        xf = qfm.ExpXfer()
+        res = {}
+        nv_bytes = E * 3 * (I * H // 2 + I * H // 16)
+        for fmt, nm in ((qfm.QFM_FMT_NVFP4, "nvfp4"), (qfm.QFM_FMT_INT8, "int8_via_ring")):
+            t0 = time.perf_counter()
+            L = qfm.LoadedLayer(store, 0, fmt, xf, stream=st)
+            dt = time.perf_counter() - t0
+            res[f"layer_load_{nm}_s"] = round(dt, 3)
+            res[f"layer_load_{nm}_GBps"] = round(nv_bytes / dt / 1e9, 2)
+            log(f"qfm_layer_load {nm}: {dt:.2f}s ({nv_bytes / dt / 1e9:.2f} GB/s of checkpoint expert bytes)")
+            L.destroy()
+        c = qfm.Qf4ExpCache()
+        qfm.check(lib.qfm_expcache_init(C.byref(c), C.byref(store.st), 0, 192, qfm.EXPCACHE_NVFP4), "cache")
+        rng = np.random.default_rng(1)
+        d_sel, d_w = qfm.DevBuf(K * 4), qfm.DevBuf.from_array(np.full(K, 0.1, np.float32))
+        d_x, d_h, d_y = qfm.DevBuf(H * 4), qfm.DevBuf(K * I * 4), qfm.DevBuf(H * 4)
+        qfm.check(lib.qfm_gen_fill(d_x.ptr, qfm.GEN_GAUSS_F32, 0, H, 6, 1, 3, 1.0, st.h), "x")
+        ntok, misses = 200, 0
+        c0, m0, b0 = C.c_ulonglong(), C.c_ulonglong(), C.c_ulonglong()
+        lib.qf4_expcache_stats(C.byref(c0), C.byref(m0), C.byref(b0))
+        st.sync()
+        t0 = time.perf_counter()
+        for _ in range(ntok):
+            d_sel.upload(rng.choice(E, K, replace=False).astype(np.int32))
+            c.expected_seq += 1
+            qfm.check(lib.qf_rtr_dispatch_launch_ex(d_sel.ptr, c.slot_for_expert_dev, c.expert_in_slot_dev, c.age_dev,
+                                                    c.clock_dev, c.route_slot_dev, c.mb_dev, c.expected_seq, c.slots,
+                                                    st.h), "dispatch")
+            qfm.check(lib.qf4_expcache_service(C.byref(c), C.byref(store.st), C.byref(xf.x), st.h), "service")
+            lib.qf5_nvfp4_moe_all(c.w_gate, c.s_gate, c.w_up, c.s_up, c.w_down, c.s_down, d_x.ptr, d_h.ptr, d_y.ptr,
+                                  c.s2g_dev, c.s2u_dev, c.s2d_dev, d_w.ptr, d_sel.ptr, c.route_slot_dev, K, st.h)
+        st.sync()
+        dt = time.perf_counter() - t0
+        c1, m1, b1 = C.c_ulonglong(), C.c_ulonglong(), C.c_ulonglong()
+        lib.qf4_expcache_stats(C.byref(c1), C.byref(m1), C.byref(b1))
+        miss = (m1.value - m0.value) / (c1.value - c0.value)
+        res["nonresident_decode"] = {"slots": 192, "tokens": ntok, "us_per_token_layer": round(dt * 1e6 / ntok, 1),
+                                     "miss_rate": round(miss, 4),
+                                     "pcie_bytes_per_token": int((b1.value - b0.value) / ntok),
+                                     "routing": "uniform random, K distinct experts per token (worst case for an LRU)"}
+        log("non-resident decode", res["nonresident_decode"])
+        lib.qf4_expcache_free(C.byref(c))
+        xf.free()
+        store.close()
+        res["workload"] = "one synthetic layer as a 3-shard safetensors checkpoint (~0.9 GB of NVFP4 experts)"
+        return res
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -335,6 +520,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 0 / M=8 INT8 / NVFP4 / prefill lines")
+    ap.add_argument("--store", action="store_true",
+                    help="also time checkpoint ingest and the non-resident (LRU) decode path (writes ~1 GB to a temp dir)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="before the timed region, one device-to-device copy of this many MiB (the "
                          "known-size copy that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -437,6 +624,10 @@ def main():
         extra["config3_nvfp4_m8"] = run_nvfp4(lib, st, nl, args)
         extra["config4_prefill"] = run_prefill(lib, st, args)
         extra["config4_prefill_nvfp4"] = run_prefill(lib, st, args, fmt=1)
+        extra["hc_premixer_m1"] = run_hc(lib, st, args)
+        extra["fp8_lane_chunk"] = run_fp8(lib, st, args)
+    if args.store:
+        extra["store_ingest_and_lru"] = run_store(lib, st, args)
 
     cpu = None
     if not args.no_cpu:

@@ -1,9 +1,10 @@
 // qfm_fp8.hip -- MoE over the FP8 lane-chunk arena (format and contract in
 // include/qf_fp8.h; semantics of ocho/amd_server/qf8_moe_fp8.hip:45-213).
 //
-// k_fp8_build_desc: one wave. The selected experts are marked in an LDS
-// bitmap, enumerated in ascending id, and for each the wave finds its rows
-// (lane t checks token t, a ballot orders them).
+// k_fp8_build_desc: one wave. The routing is staged in LDS, the selected
+// experts are marked in a bitmap (descriptor index = rank of the expert id),
+// and one pass over the tokens in order appends each (row, weight) to its
+// expert's descriptor through per-expert counters.
 // k_fp8_gateup / k_fp8_downacc: a fixed grid of 256-thread workgroups; wave w
 // of workgroup b takes items b*4 + w, then strides by 4 * gridDim.x, until
 // the device-side item count ctl[0] * tiles is exhausted (every wave reaches
@@ -24,51 +25,73 @@ constexpr int kF8MaxExperts = 512;
 constexpr int kF8RowsGu = 4;           // gate/up output rows per item
 constexpr int kF8RowsDn = 8;           // down output rows per item
 
+// Routing of up to kF8LdsPairs (row, k) pairs is staged in LDS; larger
+// batches are read from global memory in the same order.
+constexpr int kF8LdsPairs = 2048;
+
 __global__ void __launch_bounds__(64)
 k_fp8_build_desc(const int *__restrict__ sel, const float *__restrict__ wt, int M, int K, int slot_base,
                  Qf8MoeDesc *__restrict__ desc, int *__restrict__ ctl, int n_experts) {
     __shared__ unsigned bits[kF8MaxExperts / 32];
+    __shared__ int wpre[kF8MaxExperts / 32];            // set bits in the words before
+    __shared__ int cnt[kF8MaxExperts];                  // rows seen per expert so far
+    __shared__ int s_sel[kF8LdsPairs];
+    __shared__ float s_wt[kF8LdsPairs];
     const int lane = threadIdx.x;
-    const int nw = (n_experts + 31) / 32;
+    const int nw = (n_experts + 31) / 32, P = M * K;
+    const bool staged = P <= kF8LdsPairs;
     for (int i = lane; i < nw; i += 64) bits[i] = 0u;
+    for (int i = lane; i < n_experts; i += 64) cnt[i] = 0;
+    if (staged)
+        for (int i = lane; i < P; i += 64) {
+            s_sel[i] = sel[i];
+            s_wt[i] = wt[i];
+        }
     __syncthreads();
-    for (int i = lane; i < M * K; i += 64) {
-        const int e = sel[i];
+    const int *ss = staged ? s_sel : sel;
+    const float *sw = staged ? s_wt : wt;
+    for (int i = lane; i < P; i += 64) {
+        const int e = ss[i];
         if (e >= 0 && e < n_experts) atomicOr(&bits[e >> 5], 1u << (e & 31));
     }
     __syncthreads();
-    int n = 0;
-    for (int w = 0; w < nw; w++) {
-        unsigned b = bits[w];
-        while (b) {
-            const int e = w * 32 + __builtin_ctz(b);
-            b &= b - 1u;
-            int nrow = 0;
-            for (int t0 = 0; t0 < M && nrow < QF8_FP8_MAXROW; t0 += 64) {
-                const int t = t0 + lane;
-                int kf = -1;
-                if (t < M)
-                    for (int k = 0; k < K; k++)
-                        if (sel[t * K + k] == e) { kf = k; break; }
-                const unsigned long long bal = __ballot(kf >= 0);
-                const int rank = __popcll(bal & ((1ull << lane) - 1ull));
-                if (kf >= 0 && nrow + rank < QF8_FP8_MAXROW) {
-                    desc[n].row[nrow + rank] = t;
-                    desc[n].wt[nrow + rank] = wt[t * K + kf];
-                }
-                nrow += __popcll(bal);
-            }
-            if (lane == 0) {
-                desc[n].slot = slot_base + e;
-                desc[n].nrow = min(nrow, QF8_FP8_MAXROW);
-            }
-            n++;
-        }
-    }
     if (lane == 0) {
-        ctl[0] = n;
+        int acc = 0;
+        for (int w = 0; w < nw; w++) {
+            wpre[w] = acc;
+            acc += __popc(bits[w]);
+        }
+        ctl[0] = acc;
         ctl[1] = 0;
         ctl[2] = 0;
+    }
+    __syncthreads();
+    // rows in token order, lane k holding selection k of the token; a repeated
+    // expert within one token keeps only its first k (as the reference's
+    // first-match search does), so the lanes of one step touch distinct counters
+    for (int t = 0; t < M; t++) {
+        const int e = lane < K ? ss[t * K + lane] : -1;
+        bool first = e >= 0 && e < n_experts;
+        for (int j = 0; j < K; j++) {
+            const int ej = __shfl(e, j, 64);
+            if (j < lane && ej == e) first = false;
+        }
+        if (first) {
+            const int di = wpre[e >> 5] + __popc(bits[e >> 5] & ((1u << (e & 31)) - 1u));
+            const int c = cnt[e];
+            cnt[e] = c + 1;
+            if (c < QF8_FP8_MAXROW) {
+                desc[di].row[c] = t;
+                desc[di].wt[c] = sw[t * K + lane];
+            }
+        }
+        __syncthreads();
+    }
+    for (int e = lane; e < n_experts; e += 64) {
+        if (!((bits[e >> 5] >> (e & 31)) & 1u)) continue;
+        const int di = wpre[e >> 5] + __popc(bits[e >> 5] & ((1u << (e & 31)) - 1u));
+        desc[di].slot = slot_base + e;
+        desc[di].nrow = min(cnt[e], QF8_FP8_MAXROW);
     }
 }
 
