@@ -211,6 +211,19 @@ def time_graph(lib, st, enqueue, steps, warmup):
     return e0.elapsed_ms(e1) / steps
 
 
+def profiled_traffic(key):
+    """HBM bytes per layer of a bench line from the committed rocprofv3
+    FETCH_SIZE + WRITE_SIZE runs (copy-calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", "m8_prefill_traffic.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        lay = json.load(f).get("layers", {}).get(key)
+    if not lay:
+        return None, None
+    return lay["traffic_bytes_per_layer"], "profiles/m8_prefill_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
+
+
 def m8_bytes(lib, layers_sel, nl, M, expert_bytes):
     """Algorithmic bytes of an M-row step: distinct experts counted once per layer."""
     tot = 0
@@ -220,7 +233,7 @@ def m8_bytes(lib, layers_sel, nl, M, expert_bytes):
     return tot
 
 
-def run_rows(lib, st, layers, nl, M, args, label, fmt_bytes=EXPERT_BYTES):
+def run_rows(lib, st, layers, nl, M, args, label, fmt_bytes=EXPERT_BYTES, key=None):
     import qfm
     arr = (qfm.QfmLayer * nl)(*[L.s.layer for L in layers])
     x = qfm.DevBuf(nl * M * H * 2)
@@ -248,12 +261,15 @@ def run_rows(lib, st, layers, nl, M, args, label, fmt_bytes=EXPERT_BYTES):
     gbs = nbytes / (ms * 1e-3) / 1e9
     U = float(np.mean([len(np.unique(s)) for s in sels]))
     log(f"{label}: {us_layer:.2f} us/layer ({us_layer / M:.2f} us/token/layer), {gbs:.0f} GB/s, mean distinct experts {U:.1f}")
+    traffic, tsrc = profiled_traffic(key) if key else (None, None)
+    roof = {"bound": "hbm", "level": "layer (every launch of the step)", "achieved": round(gbs, 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "algorithmic_bytes_per_layer": int(nbytes / nl)}
+    if tsrc:
+        roof["traffic_source"] = tsrc
     return {"workload": label, "rows": M, "us_per_layer": round(us_layer, 3), "us_per_token_layer": round(us_layer / M, 3),
             "achieved_GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "mean_distinct_experts": round(U, 2), "algorithmic_bytes_per_step": nbytes,
-            "roofline": {"bound": "hbm", "level": "layer (every launch of the step)", "achieved": round(gbs, 1),
-                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                         "traffic": None}}
+            "mean_distinct_experts": round(U, 2), "algorithmic_bytes_per_step": nbytes, "roofline": roof}
 
 
 NVFP4_EXPERT_BYTES = 3 * (H * I // 2 + H * I // 16) + 3 * 4     # codes + e4m3 block scales + 3 fp32 global scales
@@ -265,7 +281,8 @@ def run_nvfp4(lib, st, nl, args):
     layers = [qfm.SynthLayer(qfm.QFM_FMT_NVFP4, 0, l, stream=st) for l in range(nl)]
     st.sync()
     log(f"generated {nl} NVFP4 layers ({time.time() - t0:.1f}s)")
-    out = run_rows(lib, st, layers, nl, 8, args, "BASELINE config 3: M=8 NVFP4 routed experts", NVFP4_EXPERT_BYTES)
+    out = run_rows(lib, st, layers, nl, 8, args, "BASELINE config 3: M=8 NVFP4 routed experts", NVFP4_EXPERT_BYTES,
+                   key="config3_nvfp4_m8")
     for L in layers:
         L.destroy()
     return out
@@ -311,6 +328,15 @@ def run_prefill(lib, st, args, T=8038, nl=4, fmt=0):
         f"max load {max(max_load)}")
     for L in layers:
         L.destroy()
+    prefill_roof = {"bound": "mfma", "level": "layer (every launch of the step)", "achieved": round(tflops, 1),
+                    "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                    "traffic": None}
+    if fmt == 0:
+        # HBM bytes the layer moves (counters) beside the bytes it must move
+        traffic, tsrc = profiled_traffic("config4_prefill")
+        if traffic:
+            prefill_roof.update(traffic=traffic, traffic_source=tsrc, traffic_unit="bytes per layer",
+                                traffic_over_weight_act_bytes=round(traffic / wbytes, 3))
     wl = ("BASELINE config 4: prefill MoE layer, T=8038 INT8, skewed router bias" if fmt == 0 else
           "config 4 shape (T=8038, skewed router bias) on NVFP4 routed experts, INT8 shared expert")
     return {"workload": wl, "tokens": T,
@@ -319,9 +345,7 @@ def run_prefill(lib, st, args, T=8038, nl=4, fmt=0):
             "mfma_util": round(tflops / MFMA_PEAK_TFLOPS, 4), "weight_act_bytes_per_layer": wbytes,
             "achieved_GBps": round(gbs, 1), "experts_touched": float(np.mean(touched)),
             "max_expert_load": max(max_load),
-            "roofline": {"bound": "mfma", "level": "layer (every launch of the step)", "achieved": round(tflops, 1),
-                         "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
-                         "traffic": None}}
+            "roofline": prefill_roof}
 
 
 HCL = 320                                   # hyper-connection low rank
@@ -520,6 +544,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 0 / M=8 INT8 / NVFP4 / prefill lines")
+    ap.add_argument("--extras", default="all",
+                    help="comma list of extra lines to run: config0,m8_int8,m8_nvfp4,prefill,prefill_nvfp4,hc,fp8 "
+                         "(default all)")
     ap.add_argument("--store", action="store_true",
                     help="also time checkpoint ingest and the non-resident (LRU) decode path (writes ~1 GB to a temp dir)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -615,17 +642,27 @@ def main():
     cpu_info = host_cpu()
     log("host cpu", cpu_info)
     extra = {}
+    want = set(("config0,m8_int8,m8_nvfp4,prefill,prefill_nvfp4,hc,fp8" if args.extras == "all"
+                else args.extras).split(","))
     if not args.no_extra:
-        extra["config0_single_expert"] = run_config0(lib, st, args, cpu_info)
-        extra["config2_int8_m8"] = run_rows(lib, st, layers, nl, 8, args, "BASELINE config 2: M=8 INT8 fork rows")
+        if "config0" in want:
+            extra["config0_single_expert"] = run_config0(lib, st, args, cpu_info)
+        if "m8_int8" in want:
+            extra["config2_int8_m8"] = run_rows(lib, st, layers, nl, 8, args, "BASELINE config 2: M=8 INT8 fork rows",
+                                                key="config2_int8_m8")
         for L in layers:
             L.destroy()
         layers = []
-        extra["config3_nvfp4_m8"] = run_nvfp4(lib, st, nl, args)
-        extra["config4_prefill"] = run_prefill(lib, st, args)
-        extra["config4_prefill_nvfp4"] = run_prefill(lib, st, args, fmt=1)
-        extra["hc_premixer_m1"] = run_hc(lib, st, args)
-        extra["fp8_lane_chunk"] = run_fp8(lib, st, args)
+        if "m8_nvfp4" in want:
+            extra["config3_nvfp4_m8"] = run_nvfp4(lib, st, nl, args)
+        if "prefill" in want:
+            extra["config4_prefill"] = run_prefill(lib, st, args)
+        if "prefill_nvfp4" in want:
+            extra["config4_prefill_nvfp4"] = run_prefill(lib, st, args, fmt=1)
+        if "hc" in want:
+            extra["hc_premixer_m1"] = run_hc(lib, st, args)
+        if "fp8" in want:
+            extra["fp8_lane_chunk"] = run_fp8(lib, st, args)
     if args.store:
         extra["store_ingest_and_lru"] = run_store(lib, st, args)
 
