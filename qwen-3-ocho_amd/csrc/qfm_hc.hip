@@ -7,14 +7,16 @@
 // tile. Block dots are exact int32 (sdot4), scaled by the 32-value block
 // scale and accumulated in fp32, then summed over the LPR lanes with DPP.
 //
-// The pre-mixer runs in three launches:
-//   k_hc_norm_x8    one block per (stream, row): the fused inject of the
-//                   previous mixer, the zero-centered RMS norm and X8(normed);
-//   k_gemv_i8x8     down (silu(v/4)) and inject (2 sigmoid(v/4)) rows;
+// The pre-mixer runs in two launches:
+//   k_hc_norm_down  one wave per down (silu(v/4)) or inject (2 sigmoid(v/4))
+//                   row, 4 rows per block; every block recomputes the fused
+//                   inject of the previous mixer, the zero-centred RMS norm
+//                   and X8(normed) into LDS, block 0 stores them;
 //   k_hc_up_combine one block per 32 outputs j: X8(hc_d) into LDS (every
 //                   block; block 0 also stores it), the 4 x 32 up rows
-//                   {c*H + j} of the up GEMV, then the sigmoid-weighted mean
-//                   over the 4 streams and X8(mixed) of the 32 values.
+//                   {c*H + j} of the up GEMV, the sigmoid-weighted mean over
+//                   the 4 streams and X8(mixed) of the 32 values, and the
+//                   residual's fused inject for those 4 x 32 entries.
 #include "qfm_internal.h"
 #include "qfm_dev.h"
 #include "../../include/qf_dense.h"
@@ -87,45 +89,104 @@ k_gemv_i8x8(GemvBatch b, const int8_t *__restrict__ xq, const float *__restrict_
     }
 }
 
-// NV = H / 256 values per thread; grid (4 streams, T rows)
+// Norm + X8 + down/inject GEMV in one launch. grid (rows / 4, T), 1024
+// threads: block b owns weight rows 4b .. 4b + 3 (down rows first, then the
+// inject rows), the 16-byte steps of each row dealt round-robin to 4 waves;
+// each thread issues its residual loads and then its weight loads.
+// Every block then recomputes the residual's norm and X8 codes for all 4
+// streams into LDS: thread c * 256 + t owns elements i * 256 + t of stream c
+// and sums them in order, then each wave and the four waves of a stream are
+// reduced (the reference's partition and order, so every block gets the same
+// codes); block 0 also stores normed / X8 (the API outputs); then the row's
+// partial dots run against the LDS codes and are summed in wave order. The
+// fused inject's updated residual is not stored here (other blocks still read
+// R): k_hc_up_combine stores it.
 template <int NV>
-__global__ void __launch_bounds__(256)
-k_hc_norm_x8(float *__restrict__ R, const uint16_t *__restrict__ wn, float *__restrict__ normed, int8_t *__restrict__ q,
-             float *__restrict__ sc, const float *__restrict__ y_prev, const float *__restrict__ inj_prev) {
-    constexpr int H = NV * 256, RS = 4 * H;
-    const int c = blockIdx.x, tid = threadIdx.x;
-    const size_t t = blockIdx.y, base = t * RS + (size_t)c * H;
-    float v[NV];
-    float acc = 0.0f;
-    if (y_prev) {
-        const float sj = inj_prev[t * QF8_HCC + c];
-#pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const int e = i * 256 + tid;
-            v[i] = fmaf(sj, y_prev[t * H + e], R[base + e]);
-            R[base + e] = v[i];
-            acc = fmaf(v[i], v[i], acc);
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < NV; i++) {
-            v[i] = R[base + i * 256 + tid];
-            acc = fmaf(v[i], v[i], acc);
-        }
-    }
-    acc = group_sum<64>(acc);
-    __shared__ float red[4];
-    if ((tid & 63) == 0) red[tid >> 6] = acc;
-    __syncthreads();
-    const float rstd = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + 1e-6f);
+__global__ void __launch_bounds__(1024)
+k_hc_norm_down(const float *__restrict__ R, const uint16_t *__restrict__ wn, const float *__restrict__ y_prev,
+               const float *__restrict__ inj_prev, const int8_t *__restrict__ Wd, const float *__restrict__ Sd,
+               const int8_t *__restrict__ Wi, const float *__restrict__ Si, float *__restrict__ hc_d,
+               float *__restrict__ inj, float *__restrict__ normed, int8_t *__restrict__ q, float *__restrict__ sc) {
+    constexpr int H = NV * 256, RS = 4 * H, NST = RS / 1024;
+    __shared__ __align__(16) int8_t s_q[RS];
+    __shared__ float s_s[RS / 32];
+    __shared__ float red[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = tid >> 8, t256 = tid & 255;                  // stream, thread within the stream
+    const size_t t = blockIdx.y;
+    // 4 rows per block, each row's 16-byte steps dealt round-robin to 4 waves
+    constexpr int NSQ = (NST + 3) / 4;                         // steps per wave (the last may be short)
+    const int kq = wave & 3, rloc = wave >> 2;
+    const int row = blockIdx.x * 4 + rloc;
+    const int nrow = QF8_HCL + (Wi ? QF8_HCC : 0);
+    const bool live = row < nrow;
+    const bool is_inj = row >= QF8_HCL;
+    const int8_t *wr = (is_inj ? Wi + (size_t)(live ? row - QF8_HCL : 0) * RS : Wd + (size_t)(live ? row : 0) * RS) +
+                       lane * 16;
+    // this thread's residual values (with the previous mixer's inject) and norm
+    // weights first (memory retires loads in issue order, so the norm then
+    // waits only for these), then the row's weights, which stream meanwhile
+    const size_t base = t * RS + (size_t)c * H;
+    float v[NV], yv[NV];
+    uint16_t wb[NV];
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        const int e = i * 256 + tid;                          // 32 consecutive e per half-wave
-        const float nv = v[i] * rstd * (1.0f + bf16_to_f32(wn[(size_t)c * H + e]));
-        normed[base + e] = nv;
+        v[i] = R[base + i * 256 + t256];
+        wb[i] = wn[(size_t)c * H + i * 256 + t256];
+    }
+    const float sj = y_prev ? inj_prev[t * QF8_HCC + c] : 0.0f;
+    if (y_prev)                                                // uniform
+#pragma unroll
+        for (int i = 0; i < NV; i++) yv[i] = y_prev[t * H + i * 256 + t256];
+    i32x4 w[NSQ];
+#pragma unroll
+    for (int j = 0; j < NSQ; j++) {
+        const int st = kq + 4 * j;
+        if (st < NST) w[j] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(wr + st * 1024));
+    }
+    if (y_prev)
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = fmaf(sj, yv[i], v[i]);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) acc = fmaf(v[i], v[i], acc);
+    acc = group_sum<64>(acc);
+    if (lane == 0) red[wave] = acc;
+    __syncthreads();
+    const float rstd = rsqrtf((red[4 * c] + red[4 * c + 1] + red[4 * c + 2] + red[4 * c + 3]) / (float)H + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int e = c * H + i * 256 + t256;                  // 32 consecutive e per half-wave
+        const float nv = v[i] * rstd * (1.0f + bf16_to_f32(wb[i]));
         float s1;
-        q[base + e] = (int8_t)x8_code(nv, s1);
-        if ((tid & 31) == 0) sc[(base + e) >> 5] = s1;
+        const int qi = x8_code(nv, s1);
+        s_q[e] = (int8_t)qi;
+        if ((tid & 31) == 0) s_s[e >> 5] = s1;
+        if (blockIdx.x == 0) {
+            normed[t * RS + e] = nv;
+            q[t * RS + e] = (int8_t)qi;
+            if ((tid & 31) == 0) sc[(t * RS + e) >> 5] = s1;
+        }
+    }
+    __syncthreads();
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NSQ; j++) {
+        const int st = kq + 4 * j;
+        if (st < NST) {
+            const int e0 = st * 1024 + lane * 16;
+            a = fmaf((float)dot16_i8i8(w[j], *reinterpret_cast<const i32x4 *>(s_q + e0)), s_s[e0 >> 5], a);
+        }
+    }
+    a = group_sum<64>(a);
+    __shared__ float part[4][4];
+    if (lane == 0) part[rloc][kq] = a;
+    __syncthreads();
+    if (tid < 4 && blockIdx.x * 4 + tid < nrow) {              // one lane per row: the four quarters in order
+        const int r = blockIdx.x * 4 + tid;
+        const float sum = ((part[tid][0] + part[tid][1]) + part[tid][2]) + part[tid][3];
+        if (r >= QF8_HCL) inj[t * QF8_HCC + r - QF8_HCL] = gemv_act(sum * Si[r - QF8_HCL], 2);
+        else hc_d[t * QF8_HCL + r] = gemv_act(sum * Sd[r], 1);
     }
 }
 
@@ -135,7 +196,8 @@ __global__ void __launch_bounds__(512)
 k_hc_up_combine(const int8_t *__restrict__ Wu, const float *__restrict__ Su, const float *__restrict__ hc_d,
                 const float *__restrict__ normed, float *__restrict__ hcy, float *__restrict__ mixed,
                 int8_t *__restrict__ xq_out, float *__restrict__ xs_out, int8_t *__restrict__ d8q,
-                float *__restrict__ d8s) {
+                float *__restrict__ d8s, float *__restrict__ R, const float *__restrict__ y_prev,
+                const float *__restrict__ inj_prev) {
     constexpr int L = QF8_HCL, RS = 4 * H;
     __shared__ __align__(16) int8_t s_q[L];
     __shared__ float s_s[L / 32];
@@ -143,6 +205,27 @@ k_hc_up_combine(const int8_t *__restrict__ Wu, const float *__restrict__ Su, con
     const int tid = threadIdx.x;
     const size_t t = blockIdx.y;
     const int j0 = blockIdx.x * 32;
+    // this block's up rows {c*H + j} and, for the combine, the normed values:
+    // issued before the X8 prologue so their latency overlaps it
+    const int lane = tid & 63, l = lane & 3;
+    const int li = (tid >> 6) * 16 + (lane >> 2);             // 0..127
+    const int c = li >> 5, jj = li & 31;
+    const size_t row = (size_t)c * H + j0 + jj;
+    const int8_t *wr = Wu + row * L + l * 16;
+    i32x4 wv[L / 64];
+#pragma unroll
+    for (int st = 0; st < L / 64; st++) wv[st] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(wr + st * 64));
+    const float su = Su[row];
+    float nrm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (tid < 32)
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) nrm[cc] = normed[t * RS + (size_t)cc * H + j0 + tid];
+    // the previous mixer's inject into the residual (k_hc_norm_down read R unchanged)
+    if (y_prev && tid < 128) {
+        const int rc = tid >> 5, rj = j0 + (tid & 31);
+        float *rp = R + t * RS + (size_t)rc * H + rj;
+        *rp = fmaf(inj_prev[t * QF8_HCC + rc], y_prev[t * H + rj], *rp);
+    }
     if (tid < L) {                                            // threads 0..319: five whole waves
         float s1;
         const int qi = x8_code(hc_d[t * L + tid], s1);
@@ -154,21 +237,15 @@ k_hc_up_combine(const int8_t *__restrict__ Wu, const float *__restrict__ Su, con
         }
     }
     __syncthreads();
-    const int lane = tid & 63, l = lane & 3;
-    const int li = (tid >> 6) * 16 + (lane >> 2);             // 0..127
-    const int c = li >> 5, jj = li & 31;
-    const size_t row = (size_t)c * H + j0 + jj;
-    const int8_t *wr = Wu + row * L + l * 16;
     float acc = 0.0f;
 #pragma unroll
     for (int st = 0; st < L / 64; st++) {
         const int e0 = st * 64 + l * 16;
-        const i32x4 w = *reinterpret_cast<const i32x4 *>(wr + st * 64);
-        acc = fmaf((float)dot16_i8i8(w, *reinterpret_cast<const i32x4 *>(s_q + e0)), s_s[e0 >> 5], acc);
+        acc = fmaf((float)dot16_i8i8(wv[st], *reinterpret_cast<const i32x4 *>(s_q + e0)), s_s[e0 >> 5], acc);
     }
     acc = group_sum<4>(acc);
     if (l == 0) {
-        const float hv = acc * Su[row];
+        const float hv = acc * su;
         hcy[t * RS + row] = hv;
         s_h[c][jj] = hv;
     }
@@ -179,7 +256,7 @@ k_hc_up_combine(const int8_t *__restrict__ Wu, const float *__restrict__ Su, con
 #pragma unroll
         for (int cc = 0; cc < 4; cc++) {
             const float m = 1.0f / (1.0f + expf(-s_h[cc][tid]));
-            sum = fmaf(m, normed[t * RS + (size_t)cc * H + j], sum);
+            sum = fmaf(m, nrm[cc], sum);
         }
         const float v = sum * 0.25f;
         mixed[t * H + j] = v;
@@ -254,26 +331,28 @@ static int hc_impl(float *normed, float *hc_d, float *mixed, float *inj, float *
                   QF8_HCL);
         return -2;
     }
+    if (!down->w || !down->s || !up->w || !up->s || (inject && (!inject->w || !inject->s))) {
+        set_error(-1, "%s: matrix without codes or scales", who);
+        return -1;
+    }
+    const int nrow = QF8_HCL + (inject ? QF8_HCC : 0);
+    const dim3 g1((unsigned)((nrow + 3) / 4), (unsigned)T);
+    const int8_t *wi = inject ? inject->w : nullptr;
+    const float *si = inject ? inject->s : nullptr;
     if (H == 2048)
-        hipLaunchKernelGGL(k_hc_norm_x8<8>, dim3(4, T), dim3(256), 0, s, R, wn, normed, n8q, n8s, y_prev, inj_prev);
+        hipLaunchKernelGGL(k_hc_norm_down<8>, g1, dim3(1024), 0, s, R, wn, y_prev, inj_prev, down->w, down->s, wi, si,
+                           hc_d, inj, normed, n8q, n8s);
     else
-        hipLaunchKernelGGL(k_hc_norm_x8<10>, dim3(4, T), dim3(256), 0, s, R, wn, normed, n8q, n8s, y_prev, inj_prev);
+        hipLaunchKernelGGL(k_hc_norm_down<10>, g1, dim3(1024), 0, s, R, wn, y_prev, inj_prev, down->w, down->s, wi, si,
+                           hc_d, inj, normed, n8q, n8s);
     if (check_launch(who)) return -3;
-    Qf8I8Multi m{};
-    m.n = inject ? 2 : 1;
-    m.m[0] = down; m.y[0] = hc_d; m.act[0] = 1;
-    if (inject) { m.m[1] = inject; m.y[1] = inj; m.act[1] = 2; }
-    GemvBatch b;
-    int maxr, rc = fill_batch(&m, &b, &maxr, who);
-    if (!rc) rc = launch_gemv(b, maxr, n8q, n8s, T, s, who);
-    if (rc) return rc;
     const dim3 g((unsigned)(H / 32), (unsigned)T);
     if (H == 2048)
         hipLaunchKernelGGL(k_hc_up_combine<2048>, g, dim3(512), 0, s, up->w, up->s, hc_d, normed, hcy, mixed, xq_out,
-                           xs_out, d8q, d8s);
+                           xs_out, d8q, d8s, R, y_prev, inj_prev);
     else
         hipLaunchKernelGGL(k_hc_up_combine<2560>, g, dim3(512), 0, s, up->w, up->s, hc_d, normed, hcy, mixed, xq_out,
-                           xs_out, d8q, d8s);
+                           xs_out, d8q, d8s, R, y_prev, inj_prev);
     return check_launch(who) ? -3 : 0;
 }
 
