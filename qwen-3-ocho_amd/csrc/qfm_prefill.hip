@@ -29,7 +29,7 @@
 //                      row is independent and partials are owned by (t, k),
 //                      so y does not depend on it) and the GEMM work lists.
 //   k_pf_gemm<GATEUP>  hidden[p][n] = silu(sg (x_p . Wg_n)) * (su (x_p . Wu_n))
-//   k_pf_gemm<DOWN>    part[slot_p][c] = w_p * sd_c * (h_p . Wd_c)
+//   k_pf_gemm<DOWN>    part[slot_p][c] = fp16(w_p * sd_c * (h_p . Wd_c))
 //                      BM=128 rows x BK=64, waves of 64 x 64 on 16x16x32 MFMAs.
 //                      INT8 gate/up (128 x 256 tiles, 8 waves): x rows as fp16
 //                      scaled by 2^k per token, weights kept as int8 in LDS and
@@ -40,7 +40,7 @@
 //                      staged as bf16 u (exact), bf16 MFMA, 128 * sum(h) removed
 //                      (the hidden sums come from the gate/up epilogue). NVFP4:
 //                      e2m1 times its e4m3 block scale staged as bf16 (exact).
-//   k_pf_combine       y[t] = sum over the K+1 slots of t, in slot order.
+//   k_pf_combine_h     y[t] = sum over the K+1 slots of t, in slot order (fp32).
 #include <type_traits>
 
 #include "qfm_dev.h"
@@ -816,7 +816,7 @@ __attribute__((amdgpu_waves_per_eu(GemmEngine<MODE>::WavesPerSimd, GemmEngine<MO
 k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int which, const int *__restrict__ off,
           const int *__restrict__ p_tok, const int *__restrict__ p_slot, const float *__restrict__ p_wt,
           const uint16_t *__restrict__ A, int Kdim, int Nrows, GroupW g0, GroupW g1, int E,
-          uint16_t *__restrict__ hid, float *__restrict__ part, int Hout, int ntiles,
+          uint16_t *__restrict__ hid, uint16_t *__restrict__ part, int Hout, int ntiles,
           const float *__restrict__ xsum, float *__restrict__ hsum, int nt_gu, const float *__restrict__ xisc) {
     static_assert(MODE != kDownI8 || !GATEUP, "the narrow tiles are for the down GEMM");
     using Eng = GemmEngine<MODE>;
@@ -971,9 +971,10 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
                 const int r = wm * RPW + mb * 16 + (lane >> 4) * 4 + i;
                 if (r < rows) {
                     const float cr = f4 ? 0.0f : 128.0f * rsum[r], w = rwt[r];
-                    float *dst = part + (size_t)rslot[r] * Hout + c0;
+                    uint16_t *dst = part + (size_t)rslot[r] * Hout + c0;
 #pragma unroll
-                    for (int nb = 0; nb < 4; nb++) dst[nb * 16] = w * ((acc[mb][nb][i] - cr) * sbv[nb]);
+                    for (int nb = 0; nb < 4; nb++)
+                        dst[nb * 16] = __builtin_bit_cast(uint16_t, (_Float16)(w * ((acc[mb][nb][i] - cr) * sbv[nb])));
                 }
             }
     }
@@ -1001,6 +1002,33 @@ k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__re
     *reinterpret_cast<uint2 *>(y + t * H + c) =
         make_uint2((uint32_t)f32_to_bf16(a.x) | ((uint32_t)f32_to_bf16(a.y) << 16),
                    (uint32_t)f32_to_bf16(a.z) | ((uint32_t)f32_to_bf16(a.w) << 16));
+}
+
+// The prefill form: fp16 partials (the down GEMM's epilogue rounds each to
+// nearest), summed in fp32 in slot order; four columns (8 bytes) per thread.
+__global__ void __launch_bounds__(256)
+k_pf_combine_h(const uint16_t *__restrict__ part, int T, int S, int H, uint16_t *__restrict__ y) {
+    constexpr int kMaxS = 17;
+    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;       // index of 4 outputs
+    if (i4 * 4 >= (size_t)T * H) return;
+    const size_t t = i4 * 4 / H, c = i4 * 4 - t * H;
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 v[kMaxS];
+#pragma unroll
+    for (int k = 0; k < kMaxS; k++)
+        if (k < S) v[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(part + (t * S + k) * H + c));
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < kMaxS; k++)
+        if (k < S) {
+            const uint32_t w[2] = {v[k].x, v[k].y};
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                a[j] += (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j >> 1] >> (16 * (j & 1))));
+        }
+    *reinterpret_cast<uint2 *>(y + t * H + c) =
+        make_uint2((uint32_t)f32_to_bf16(a[0]) | ((uint32_t)f32_to_bf16(a[1]) << 16),
+                   (uint32_t)f32_to_bf16(a[2]) | ((uint32_t)f32_to_bf16(a[3]) << 16));
 }
 
 void launch_pf_combine(const float *part, int T, int S, int H, uint16_t *y, hipStream_t s) {
@@ -1071,7 +1099,7 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     int *p_slot = static_cast<int *>(at(kPfSlot));
     float *p_wt = static_cast<float *>(at(kPfPwt));
     uint16_t *hid = static_cast<uint16_t *>(at(kPfHid));
-    float *part = static_cast<float *>(at(kPfPart));
+    uint16_t *part = static_cast<uint16_t *>(at(kPfPart));
     float *xsum = static_cast<float *>(at(kPfXsum));
     float *hsum = static_cast<float *>(at(kPfHsum));
     uint4 *x16 = static_cast<uint4 *>(at(kPfX16));
@@ -1120,7 +1148,8 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
         hipLaunchKernelGGL((k_pf_gemm<false, kDownI8>), g_dn, nth_dn, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot, p_wt,
                            hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu, nullptr);
     }
-    launch_pf_combine(part, T, S, H, y, s);
+    hipLaunchKernelGGL(k_pf_combine_h, dim3((unsigned)(((size_t)T * H / 4 + 255) / 256)), dim3(256), 0, s, part, T, S,
+                       H, y);
     return check_launch("prefill");
 }
 
