@@ -200,6 +200,16 @@ __device__ __forceinline__ float canon_butterfly(float a) {
     return __fadd_rn(a, __shfl_xor(a, 32, WAVE));
 }
 
+// max over the 16 lanes of a DPP row, all in VALU DPP moves (no LDS round
+// trip): quad permutes xor 1 and xor 2, then the half-row and row mirrors
+// (canon_butterfly's first four steps)
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+}
+
 // v from lane l ^ M (M = 1, 2: DPP quad permutes; 4, 8, 16: ds_swizzle in
 // bitmask mode; 32: bpermute)
 template <int M>

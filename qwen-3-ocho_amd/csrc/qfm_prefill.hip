@@ -29,7 +29,7 @@
 //                      row is independent and partials are owned by (t, k),
 //                      so y does not depend on it) and the GEMM work lists.
 //   k_pf_gemm<GATEUP>  hidden[p][n] = silu(sg (x_p . Wg_n)) * (su (x_p . Wu_n))
-//   k_pf_gemm<DOWN>    part[slot_p][c] = fp16(w_p * sd_c * (h_p . Wd_c))
+//   k_pf_gemm<DOWN>    part[slot_p][c] = fp16(2^k * w_p * sd_c * (h_p . Wd_c)), k per 64 columns
 //                      BM=128 rows x BK=64, waves of 64 x 64 on 16x16x32 MFMAs.
 //                      INT8 gate/up (128 x 256 tiles, 8 waves): x rows as fp16
 //                      scaled by 2^k per token, weights kept as int8 in LDS and
@@ -816,7 +816,7 @@ __attribute__((amdgpu_waves_per_eu(GemmEngine<MODE>::WavesPerSimd, GemmEngine<MO
 k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int which, const int *__restrict__ off,
           const int *__restrict__ p_tok, const int *__restrict__ p_slot, const float *__restrict__ p_wt,
           const uint16_t *__restrict__ A, int Kdim, int Nrows, GroupW g0, GroupW g1, int E,
-          uint16_t *__restrict__ hid, uint16_t *__restrict__ part, int Hout, int ntiles,
+          uint16_t *__restrict__ hid, uint16_t *__restrict__ part, int8_t *__restrict__ partk, int Hout, int ntiles,
           const float *__restrict__ xsum, float *__restrict__ hsum, int nt_gu, const float *__restrict__ xisc) {
     static_assert(MODE != kDownI8 || !GATEUP, "the narrow tiles are for the down GEMM");
     using Eng = GemmEngine<MODE>;
@@ -960,21 +960,67 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
             hsum[(size_t)(pbase + threadIdx.x) * nt_gu + nt] = v;
         }
     } else {
+        // a wave's 64 columns of one row live in the 16 lanes of a row group (4
+        // n-blocks each): that group of the partial row is stored as fp16 scaled
+        // by 2^k, k putting its largest finite magnitude in [2^14, 2^15), and k
+        // goes to partk (no fp16 overflow or underflow at any magnitude; inf and
+        // NaN pass through)
         const int c0 = nt * TBN + wn * 64 + (lane & 15);
+        const int kg = (nt * TBN + wn * 64) >> 6, ngk = Hout >> 6;
         float sbv[4];
 #pragma unroll
         for (int nb = 0; nb < 4; nb++) sbv[nb] = f4 ? s2a : Sb[c0 + nb * 16];
+        // pass 1: the values (in place) and each row group's largest magnitude;
+        // the 16 row chains are independent, so their DPP steps interleave
+        float mr[MWv][4];
 #pragma unroll
         for (int mb = 0; mb < MWv; mb++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int r = wm * RPW + mb * 16 + (lane >> 4) * 4 + i;
+                const bool live = r < rows;
+                const float cr = (f4 || !live) ? 0.0f : 128.0f * rsum[r], w = live ? rwt[r] : 0.0f;
+#pragma unroll
+                for (int nb = 0; nb < 4; nb++) acc[mb][nb][i] = w * ((acc[mb][nb][i] - cr) * sbv[nb]);
+                mr[mb][i] = fmaxf(fmaxf(fabsf(acc[mb][0][i]), fabsf(acc[mb][1][i])),
+                                  fmaxf(fabsf(acc[mb][2][i]), fabsf(acc[mb][3][i])));
+            }
+        bool bad = false;
+#pragma unroll
+        for (int mb = 0; mb < MWv; mb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                mr[mb][i] = row16_max(mr[mb][i]);
+                bad = bad || !(mr[mb][i] <= 3.4028235e38f);
+            }
+        if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+            // rare (a non-finite value in the wave's tile): the finite maxima
+#pragma unroll
+            for (int mb = 0; mb < MWv; mb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    float mf = 0.0f;
+#pragma unroll
+                    for (int nb = 0; nb < 4; nb++)
+                        if ((__float_as_uint(acc[mb][nb][i]) & 0x7F800000u) != 0x7F800000u)
+                            mf = fmaxf(mf, fabsf(acc[mb][nb][i]));
+                    mr[mb][i] = row16_max(mf);
+                }
+        }
+        // pass 2: scale by 2^k, round to fp16, store
+#pragma unroll
+        for (int mb = 0; mb < MWv; mb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = wm * RPW + mb * 16 + (lane >> 4) * 4 + i;
+                const float m = mr[mb][i];
+                const int k = m == 0.0f ? 0 : min(113, max(-113, 141 - (int)(__float_as_uint(m) >> 23)));
                 if (r < rows) {
-                    const float cr = f4 ? 0.0f : 128.0f * rsum[r], w = rwt[r];
                     uint16_t *dst = part + (size_t)rslot[r] * Hout + c0;
 #pragma unroll
                     for (int nb = 0; nb < 4; nb++)
-                        dst[nb * 16] = __builtin_bit_cast(uint16_t, (_Float16)(w * ((acc[mb][nb][i] - cr) * sbv[nb])));
+                        dst[nb * 16] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_ldexpf(acc[mb][nb][i], k));
+                    if ((lane & 15) == 0) partk[(size_t)rslot[r] * ngk + kg] = (int8_t)k;
                 }
             }
     }
@@ -1005,9 +1051,11 @@ k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__re
 }
 
 // The prefill form: fp16 partials (the down GEMM's epilogue rounds each to
-// nearest), summed in fp32 in slot order; four columns (8 bytes) per thread.
+// nearest after scaling its 64-column group by 2^k, k in partk), summed in
+// fp32 in slot order; four columns (8 bytes) per thread.
 __global__ void __launch_bounds__(256)
-k_pf_combine_h(const uint16_t *__restrict__ part, int T, int S, int H, uint16_t *__restrict__ y) {
+k_pf_combine_h(const uint16_t *__restrict__ part, const int8_t *__restrict__ partk, int T, int S, int H,
+               uint16_t *__restrict__ y) {
     constexpr int kMaxS = 17;
     const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;       // index of 4 outputs
     if (i4 * 4 >= (size_t)T * H) return;
@@ -1017,14 +1065,19 @@ k_pf_combine_h(const uint16_t *__restrict__ part, int T, int S, int H, uint16_t 
 #pragma unroll
     for (int k = 0; k < kMaxS; k++)
         if (k < S) v[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(part + (t * S + k) * H + c));
+    int kk[kMaxS];
+#pragma unroll
+    for (int k = 0; k < kMaxS; k++)
+        if (k < S) kk[k] = partk[(t * S + k) * (H >> 6) + (c >> 6)];
     float a[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < kMaxS; k++)
         if (k < S) {
             const uint32_t w[2] = {v[k].x, v[k].y};
+            const float isc = __uint_as_float((uint32_t)(127 - kk[k]) << 23);
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                a[j] += (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j >> 1] >> (16 * (j & 1))));
+                a[j] += (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j >> 1] >> (16 * (j & 1)))) * isc;
         }
     *reinterpret_cast<uint2 *>(y + t * H + c) =
         make_uint2((uint32_t)f32_to_bf16(a[0]) | ((uint32_t)f32_to_bf16(a[1]) << 16),
@@ -1100,6 +1153,7 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
     float *p_wt = static_cast<float *>(at(kPfPwt));
     uint16_t *hid = static_cast<uint16_t *>(at(kPfHid));
     uint16_t *part = static_cast<uint16_t *>(at(kPfPart));
+    int8_t *partk = static_cast<int8_t *>(at(kPfPartK));
     float *xsum = static_cast<float *>(at(kPfXsum));
     float *hsum = static_cast<float *>(at(kPfHsum));
     uint4 *x16 = static_cast<uint4 *>(at(kPfX16));
@@ -1138,18 +1192,18 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
         nth(f4 ? ExpertEngineF4::NT : ExpertEngine::NT), nth_dn(f4 ? ExpertEngineF4::NT : DownEngineI8::NT);
     if (f4) {
         hipLaunchKernelGGL((k_pf_gemm<true, kRoutedF4>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, off, p_tok, p_slot,
-                           p_wt, x, H, I, gg, gu, E, hid, part, H, nt_gu, xsum, hsum, nt_gu, nullptr);
+                           p_wt, x, H, I, gg, gu, E, hid, part, partk, H, nt_gu, xsum, hsum, nt_gu, nullptr);
         hipLaunchKernelGGL((k_pf_gemm<false, kRoutedF4>), g_dn, nth, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot,
-                           p_wt, hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu, nullptr);
+                           p_wt, hid, I, H, gd, gd, E, hid, part, partk, H, nt_dn, xsum, hsum, nt_gu, nullptr);
     } else {
         hipLaunchKernelGGL((k_pf_gemm<true, kAllI8>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, off, p_tok, p_slot, p_wt,
-                           reinterpret_cast<const uint16_t *>(x16), H, I, gg, gu, E, hid, part, H, nt_gu, x16sum, hsum,
+                           reinterpret_cast<const uint16_t *>(x16), H, I, gg, gu, E, hid, part, partk, H, nt_gu, x16sum, hsum,
                            nt_gu, x16isc);
         hipLaunchKernelGGL((k_pf_gemm<false, kDownI8>), g_dn, nth_dn, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot, p_wt,
-                           hid, I, H, gd, gd, E, hid, part, H, nt_dn, xsum, hsum, nt_gu, nullptr);
+                           hid, I, H, gd, gd, E, hid, part, partk, H, nt_dn, xsum, hsum, nt_gu, nullptr);
     }
-    hipLaunchKernelGGL(k_pf_combine_h, dim3((unsigned)(((size_t)T * H / 4 + 255) / 256)), dim3(256), 0, s, part, T, S,
-                       H, y);
+    hipLaunchKernelGGL(k_pf_combine_h, dim3((unsigned)(((size_t)T * H / 4 + 255) / 256)), dim3(256), 0, s, part, partk,
+                       T, S, H, y);
     return check_launch("prefill");
 }
 

@@ -28,7 +28,8 @@ enum PfRegion {
     kPfSlot,      // int [P] pair -> partial slot
     kPfPwt,       // fp32 [P] pair weight
     kPfHid,       // bf16 [P][I] hidden rows
-    kPfPart,      // fp16 [P][H] owned partials
+    kPfPart,      // fp16 [P][H] owned partials, each 64-column group scaled by 2^k
+    kPfPartK,     // int8 [P][H / 64] the k of each partial group
     kPfXsum,      // fp32 [T] sum(x_t)
     kPfHsum,      // fp32 [P][nt_gu] hidden row sums per gate/up n-tile
     kPfX16,       // fp16 [T][H] x rows scaled by 2^k (INT8 gate/up)
@@ -65,7 +66,8 @@ inline PfLayout pf_layout(int T, int H, int I, int E, int K, bool has_sh, int gu
     const size_t want[kPfCount] = {
         (size_t)slices * t * E * 4, t * 4, (size_t)E * 4, (size_t)E * H * 2, t * K * 4, t * K * 4, t * 4, 8 * 4,
         (size_t)(E + 2) * 4, (size_t)L.nblk * E * 4, L.max_mt * L.nt_gu * 16, L.max_mt * L.nt_dn * 16,
-        L.P * 4, L.P * 4, L.P * 4, L.P * I * 2, L.P * H * 2, t * 4, L.P * L.nt_gu * 4, t * H * 2, t * 4, t * 4};
+        L.P * 4, L.P * 4, L.P * 4, L.P * I * 2, L.P * H * 2, L.P * (size_t)(H / 64), t * 4, L.P * L.nt_gu * 4,
+        t * H * 2, t * 4, t * 4};
     size_t o = 0;
     for (int r = 0; r < kPfCount; r++) {
         L.off[r] = o;

@@ -24,9 +24,9 @@ import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-NREG = 22
+NREG = 23
 NAMES = ["lg", "xnorm", "wnorm", "wb16", "sel", "wts", "gam", "ctr", "off", "blk", "items_gu", "items_dn",
-         "p_tok", "p_slot", "p_wt", "hid", "part", "xsum", "hsum", "x16", "x16sum", "x16isc"]
+         "p_tok", "p_slot", "p_wt", "hid", "part", "partk", "xsum", "hsum", "x16", "x16sum", "x16isc"]
 BM, SLICES, PAIRS_PER_BLK = 128, 1, 4096
 GU_I8, GU_F4, DN_I8 = 256, 256, 128           # the tile widths the library is built with
 
@@ -90,7 +90,8 @@ def test_regions_disjoint_and_sized(shim, H, I, has_sh, gu, dn):
         assert m["max_mt"] % 8 == 0                       # the XCD tile maps cover [0, max_mt * nt) exactly
         need = dict(lg=SLICES * T * E * 4, sel=T * K * 4, wts=T * K * 4, ctr=32, off=(E + 2) * 4,
                     blk=m["nblk"] * E * 4, items_gu=m["max_mt"] * nt_gu * 16, items_dn=m["max_mt"] * nt_dn * 16,
-                    p_tok=P * 4, p_slot=P * 4, p_wt=P * 4, hid=P * I * 2, part=P * H * 2, hsum=P * nt_gu * 4,
+                    p_tok=P * 4, p_slot=P * 4, p_wt=P * 4, hid=P * I * 2, part=P * H * 2, partk=P * (H // 64),
+                    hsum=P * nt_gu * 4,
                     x16=T * H * 2, x16sum=T * 4, x16isc=T * 4, wb16=E * H * 2)
         for k, v in need.items():
             assert by[NAMES.index(k)] >= v, (T, k, by[NAMES.index(k)], v)
