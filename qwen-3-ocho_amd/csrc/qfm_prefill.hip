@@ -293,13 +293,17 @@ struct TileEngine {
             ap[j] = A + (long)(ar >= 0 ? ar : a0) * lda + kc * 8;
             a_lds[j] = lds_swz(r, kc);
         }
-        const char *bp[NB], *sp[NB];
+        // the row pointers come from an LDS table of generic pointers: address
+        // them as global memory, or the loads become flat loads, which count
+        // against lgkmcnt and make every LDS wait of the k-step wait for them
+        typedef const __attribute__((address_space(1))) char *gptr_t;
+        gptr_t bp[NB], sp[NB];
         int b_lds[NB];
 #pragma unroll
         for (int j = 0; j < NB; j++) {
             const int c = t + j * NT, r = c / BCPR, kc = c % BCPR;
-            bp[j] = bptr[r] + kc * 16;
-            sp[j] = BMODE == kB_F4 ? sptr[r] + kc * 2 : nullptr;
+            bp[j] = (gptr_t)bptr[r] + kc * 16;
+            sp[j] = BMODE == kB_F4 ? (gptr_t)sptr[r] + kc * 2 : nullptr;
             // first 16-byte chunk of the thread's 1, 2 (int8) or 4 (NVFP4)
             // consecutive chunks; chunk h of them is at b_lds[j] ^ (8 h)
             b_lds[j] = BL8 ? lds_swz8(r, kc * 2) : lds_swz(r, B8 ? kc * 2 : BMODE == kB_F4 ? kc * 4 : kc);
@@ -309,13 +313,15 @@ struct TileEngine {
             for (int j = 0; j < NA; j++) g.a[j] = *reinterpret_cast<const u32x4_t *>(ap[j] + k0);
 #pragma unroll
             for (int j = 0; j < NB; j++) {
+                typedef const __attribute__((address_space(1))) u32x4_t *gv_t;
+                typedef const __attribute__((address_space(1))) uint16_t *gs_t;
                 if constexpr (B8) {
-                    g.b[j] = *reinterpret_cast<const u32x4_t *>(bp[j] + k0);
+                    g.b[j] = *reinterpret_cast<gv_t>(bp[j] + k0);
                 } else if constexpr (BMODE == kB_BF16) {
-                    g.b[j] = *reinterpret_cast<const u32x4_t *>(bp[j] + (size_t)k0 * 2);
+                    g.b[j] = *reinterpret_cast<gv_t>(bp[j] + (size_t)k0 * 2);
                 } else {
-                    g.b[j] = *reinterpret_cast<const u32x4_t *>(bp[j] + k0 / 2);
-                    g.sc[j] = *reinterpret_cast<const uint16_t *>(sp[j] + k0 / 16);
+                    g.b[j] = *reinterpret_cast<gv_t>(bp[j] + k0 / 2);
+                    g.sc[j] = *reinterpret_cast<gs_t>(sp[j] + k0 / 16);
                 }
             }
         };
