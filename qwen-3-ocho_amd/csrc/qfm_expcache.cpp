@@ -346,7 +346,13 @@ int qf4_expcache_init(Qf4ExpCache *c, const QfStore *st, int layer, int slots) {
 namespace {
 
 // Upload `expert` into `slot` (see the file comment for the pipeline).
-int xfer_expert(Qf4ExpCache *c, const QfStore *st, Qf4ExpXfer *xf, int expert, int slot, hipStream_t compute) {
+// after_compute: the slot still holds an expert that kernels already queued on
+// `compute` may read, so the transfer stream first waits for everything queued
+// there (write after read). The mailbox service needs no such wait: its host
+// side runs after the dispatch kernel, and so after every earlier kernel of
+// the stream, has executed.
+int xfer_expert(Qf4ExpCache *c, const QfStore *st, Qf4ExpXfer *xf, int expert, int slot, hipStream_t compute,
+                bool after_compute = false) {
     const Geo g = geo();
     if (!xf || !xf->xfer || !xf->buf[0] || !xf->buf[1]) { set_error(-1, "expert upload: transfer context not initialised"); return -1; }
     if (expert < 0 || expert >= g.E || slot < 0 || slot >= c->slots) {
@@ -360,6 +366,13 @@ int xfer_expert(Qf4ExpCache *c, const QfStore *st, Qf4ExpXfer *xf, int expert, i
     if (hipEventSynchronize(xf->ev[b]) != hipSuccess) { set_error(-3, "expert upload: staging wait failed"); return -1; }
     uint8_t *buf = static_cast<uint8_t *>(xf->buf[b]);
     hipStream_t xs = xf->xfer;
+    // ev[b] is free here (synchronized above) and is recorded again on xs
+    // below; the wait enqueued now keeps the state of this record
+    if (after_compute && (hipEventRecord(xf->ev[b], compute) != hipSuccess ||
+                          hipStreamWaitEvent(xs, xf->ev[b], 0) != hipSuccess)) {
+        set_error(-3, "expert upload: ordering after the compute stream failed L%d E%d", c->layer, expert);
+        return -1;
+    }
     bool ok = true;
     if (c->w8_gate) {
         // FP8 lane-chunk: gate/up are [I][H], down [H][I]
@@ -440,8 +453,8 @@ int qf4_expcache_prepare(Qf4ExpCache *c, const QfStore *st, Qf4ExpXfer *xf, int 
         if (c->expert_in_slot[i] < 0) { slot = i; break; }
         if (c->age[i] < c->age[slot]) slot = i;
     }
-    if (xfer_expert(c, st, xf, expert, slot, compute)) return -1;
     const int evicted = c->expert_in_slot[slot];
+    if (xfer_expert(c, st, xf, expert, slot, compute, evicted >= 0)) return -1;
     if (evicted >= 0) c->slot_for_expert[evicted] = -1;
     c->expert_in_slot[slot] = expert;
     c->slot_for_expert[expert] = slot;

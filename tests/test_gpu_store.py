@@ -313,6 +313,52 @@ def test_host_lru_prepare(lib, gen, store, xfer):
     s.destroy()
 
 
+def test_host_lru_eviction_waits_for_queued_readers(lib, gen, store, xfer):
+    """An evicted slot is refilled only after the kernels already queued on the
+    compute stream (which may still read the old expert) have run: a forward
+    queued behind a long kernel reads the experts it was queued for, although
+    every one of its slots is evicted right after it was enqueued."""
+    _say("host LRU eviction after queued readers")
+    st = _store(store, "safetensors")
+    s = qfm.Stream()
+    c = _cache(lib, st, K, qfm.EXPCACHE_NVFP4)
+    old = np.arange(K, dtype=np.int32)
+    for e in old:     # first empty slot first: expert e lands in slot e
+        assert lib.qf4_expcache_prepare(C.byref(c), C.byref(st.st), C.byref(xfer.x), int(e), s.h) == e
+    s.sync()
+    full = qfm.Qf4ExpCache()
+    qfm.check(lib.qfm_arena_init(C.byref(full), qfm.QFM_FMT_NVFP4, LAYER), "full arena")
+    qfm.check(lib.qfm_arena_generate(C.byref(full), SEED, LAYER, s.h), "full arena generate")
+    rng = np.random.default_rng(21)
+    w = rng.random(K).astype(np.float32)
+    w /= w.sum()
+    d_sel, d_wts = qfm.DevBuf.from_array(old), qfm.DevBuf.from_array(w)
+    d_x = qfm.DevBuf.from_array(rng.standard_normal(H).astype(np.float32))
+    d_h, d_y, d_yref = qfm.DevBuf(K * I * 4), qfm.DevBuf(H * 4), qfm.DevBuf(H * 4)
+    lib.qf5_nvfp4_moe_all(full.w_gate, full.s_gate, full.w_up, full.s_up, full.w_down, full.s_down, d_x.ptr,
+                          d_h.ptr, d_yref.ptr, full.s2g_dev, full.s2u_dev, full.s2d_dev, d_wts.ptr, d_sel.ptr,
+                          d_sel.ptr, K, s.h)
+    s.sync()
+    busy = qfm.DevBuf(1 << 30)     # ~ms of generator work queued ahead of the reader
+    qfm.check(lib.qfm_gen_fill(busy.ptr, qfm.GEN_GAUSS_F32, 0, 1 << 28, 1, 0, 0, C.c_float(1.0), s.h), "busy")
+    lib.qf5_nvfp4_moe_all(c.w_gate, c.s_gate, c.w_up, c.s_up, c.w_down, c.s_down, d_x.ptr, d_h.ptr, d_y.ptr,
+                          c.s2g_dev, c.s2u_dev, c.s2d_dev, d_wts.ptr, d_sel.ptr, d_sel.ptr, K, s.h)
+    for j in range(K):                 # evict every slot the queued forward reads (oldest first)
+        assert lib.qf4_expcache_prepare(C.byref(c), C.byref(st.st), C.byref(xfer.x), 100 + j, s.h) == j
+    s.sync()
+    qfm.status_check("eviction after queued readers")
+    assert np.array_equal(d_y.download(np.float32, (H,)).view(np.uint32),
+                          d_yref.download(np.float32, (H,)).view(np.uint32))
+    arr = _nv_arrays(c, K)             # and the slots now hold the new experts
+    for j in range(K):
+        for nm, _ in NV:
+            assert np.array_equal(arr[nm][j], gen[nm][100 + j]), (j, nm)
+    busy.free()
+    lib.qf4_expcache_free(C.byref(c))
+    lib.qfm_arena_free(C.byref(full))
+    s.destroy()
+
+
 # ------------------------------------------------------------------ device dispatch
 def test_device_dispatch_and_service(lib, gen, store, xfer):
     _say("device dispatch + mailbox service")
