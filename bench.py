@@ -304,7 +304,7 @@ def run_prefill(lib, st, args, T=8038, nl=4, fmt=0):
     wsb = lib.qfm_workspace_bytes(T)
     ws = qfm.DevBuf(wsb)
     view = qfm.QfmWsView()
-    touched, max_load = [], []
+    touched, max_load, fallback = [], [], []
     for l in range(nl):
         qfm.check(lib.qfm_moe_forward(C.byref(arr[l]), x.ptr, T, y.ptr + l * T * H * 2, ws.ptr, wsb, st.h), "fwd")
         st.sync()
@@ -312,6 +312,8 @@ def run_prefill(lib, st, args, T=8038, nl=4, fmt=0):
         cnt = np.bincount(qfm.d2h(view.sel, np.int32, (T, K)).ravel(), minlength=E)
         touched.append(int((cnt > 0).sum()))
         max_load.append(int(cnt.max()))
+        # counters[0]: tokens whose candidate set overflowed (all E logits recomputed exactly)
+        fallback.append(int(qfm.d2h(view.counters, np.int32, (1,))[0]))
 
     def enq():
         qfm.check(lib.qfm_moe_forward_layers(arr, nl, x.ptr, 0, T, y.ptr, T * H, ws.ptr, wsb, st.h), "fwd")
@@ -325,7 +327,7 @@ def run_prefill(lib, st, args, T=8038, nl=4, fmt=0):
     name = "BASELINE config 4" if fmt == 0 else "config 4 on an NVFP4 arena"
     log(f"{name}: prefill T={T}: {us_layer:.1f} us/layer, {T / (us_layer * 1e-6):.0f} tok/s, "
         f"{tflops:.0f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS * 100:.1f}% bf16 MFMA), experts touched {np.mean(touched):.0f}, "
-        f"max load {max(max_load)}")
+        f"max load {max(max_load)}, candidate-overflow tokens {sum(fallback)}")
     for L in layers:
         L.destroy()
     prefill_roof = {"bound": "mfma", "level": "layer (every launch of the step)", "achieved": round(tflops, 1),
@@ -344,7 +346,7 @@ def run_prefill(lib, st, args, T=8038, nl=4, fmt=0):
             "flops_per_layer": flops, "achieved_TFLOPs": round(tflops, 1),
             "mfma_util": round(tflops / MFMA_PEAK_TFLOPS, 4), "weight_act_bytes_per_layer": wbytes,
             "achieved_GBps": round(gbs, 1), "experts_touched": float(np.mean(touched)),
-            "max_expert_load": max(max_load),
+            "max_expert_load": max(max_load), "candidate_overflow_tokens": sum(fallback),
             "roofline": prefill_roof}
 
 
