@@ -342,6 +342,29 @@ def test_moe_layer_reference_shape_ungated(lib, M, fmt):
     _cfg(lib)
 
 
+@pytest.mark.parametrize("M,fmt,renorm,gated,bias", [(1, 0, 0, 1, False), (3, 0, 0, 1, True), (8, 1, 0, 1, False),
+                                                     (1, 0, 1, 0, True), (6, 1, 1, 0, False), (7, 0, 1, 1, True)])
+def test_moe_layer_config_variants(lib, M, fmt, renorm, gated, bias):
+    """The fused decode paths under the other configurations: the full softmax
+    denominator (renorm 0; at M = 1 inside the INT8 gate/up kernel's own
+    selection), an ungated shared expert, a router bias, and 6 and 7 fork rows
+    (a partial eight-row router pass)."""
+    _say("layer variant", M, "int8" if fmt == 0 else "nvfp4", "renorm", renorm, "gated", gated, "bias", bias)
+    _cfg(lib, renorm=renorm, gated=gated)
+    g = _run_layer(lib, M, 6, 11, x_layer=300 + M, fmt=fmt, bias=bias)
+    r = orc.moe_layer(2048, 512, 512, 10, M, 6, 11, 300 + M, fmt=fmt, gated=gated, renorm=renorm,
+                      use_bias=int(bias))
+    _cfg(lib)
+    assert np.array_equal(g["x"], r["x"])
+    assert np.array_equal(g["logits"].view(np.uint32), r["logits"].view(np.uint32))
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    for m in range(M):
+        rel = _rel(g["y"][m], r["y"][m])
+        _say("  row", m, "max rel err", rel)
+        assert rel <= TOL
+
+
 def test_moe_layer_deterministic(lib):
     """Two runs of the same layer give identical bits (no atomics on outputs)."""
     _cfg(lib)
@@ -369,7 +392,7 @@ def _run_prefill(lib, T, seed, layer, x_layer, bias=True, fmt=qfm.QFM_FMT_INT8, 
     return out
 
 
-@pytest.mark.parametrize("T,bias,fmt,renorm", [(37, True, 0, 1), (300, True, 0, 1), (129, False, 0, 1), (37, True, 1, 1),
+@pytest.mark.parametrize("T,bias,fmt,renorm", [(9, True, 0, 1), (37, True, 0, 1), (300, True, 0, 1), (129, False, 0, 1), (37, True, 1, 1),
                                                (300, True, 1, 1), (9, False, 1, 1), (37, True, 0, 0), (129, False, 1, 0)])
 def test_prefill_small(lib, T, bias, fmt, renorm):
     """Prefill path (T > 8): MFMA router + exact candidate selection, grouped GEMMs
