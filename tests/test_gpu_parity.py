@@ -330,16 +330,21 @@ def test_moe_layer(lib, M, seed, layer, fmt):
         assert rel <= TOL
 
 
-@pytest.mark.parametrize("M,fmt", [(1, 0), (4, 0), (4, 1)])
-def test_moe_layer_reference_shape_ungated(lib, M, fmt):
-    _say("layer 2560/640 ungated", M, fmt)
-    _cfg(lib, H=2560, I=640, gated=0)
+@pytest.mark.parametrize("M,fmt,gated", [(1, 0, 0), (4, 0, 0), (4, 1, 0), (8, 0, 0), (8, 1, 0), (8, 0, 1), (1, 0, 1)])
+def test_moe_layer_reference_shape(lib, M, fmt, gated):
+    """The reference's own shape (H=2560, I=640), gated and ungated shared
+    expert, up to 8 fork rows (two four-row router passes)."""
+    _say("layer 2560/640", M, fmt, "gated", gated)
+    _cfg(lib, H=2560, I=640, gated=gated)
     g = _run_layer(lib, M, 2, 4, x_layer=7, fmt=fmt)
-    r = orc.moe_layer(2560, 640, 512, 10, M, 2, 4, 7, gated=0, fmt=fmt)
+    r = orc.moe_layer(2560, 640, 512, 10, M, 2, 4, 7, gated=gated, fmt=fmt)
+    _cfg(lib)
+    assert np.array_equal(g["x"], r["x"])
+    assert np.array_equal(g["logits"].view(np.uint32), r["logits"].view(np.uint32))
     assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
     for m in range(M):
         assert _rel(g["y"][m], r["y"][m]) <= TOL
-    _cfg(lib)
 
 
 @pytest.mark.parametrize("M,fmt,renorm,gated,bias", [(1, 0, 0, 1, False), (3, 0, 0, 1, True), (8, 1, 0, 1, False),
