@@ -339,7 +339,7 @@ def _expert_fp64(seed, layer, e, H, I, fmt):
 
 
 def moe_layer_grouped(H, I, E, K, M, seed, layer, x_layer, x_row0=0, fmt=0, gated=1, renorm=1, use_bias=0, x=None,
-                      router=None, expert_fn=None, shared=None, gate_vec=None):
+                      router=None, expert_fn=None, shared=None, gate_vec=None, bias=None):
     """The whole layer (orc_moe_layer's definition) evaluated expert by expert:
     every distinct expert's weights are dequantized once (the oracle's own
     dequantization, exact in fp64) and applied to all of its tokens with fp64
@@ -347,13 +347,14 @@ def moe_layer_grouped(H, I, E, K, M, seed, layer, x_layer, x_row0=0, fmt=0, gate
     from the oracle's router and top-K. x (bf16 bits [M][H]) overrides the
     generated input rows and router (fp32 [E][H]) the generated router weights;
     expert_fn(e) -> (Wg, Wu, Wd) fp64 overrides the routed experts, shared
-    (Wg, Wu, Wd) the shared expert and gate_vec (fp32 [H]) its gate vector.
+    (Wg, Wu, Wd) the shared expert, gate_vec (fp32 [H]) its gate vector and
+    bias (fp32 [E], with use_bias) the generated router bias.
     Same arithmetic as orc_moe_layer up to the order of fp64 summation (pinned
     against it in tests/test_oracle_path.py)."""
     if x is None:
         x = fill("gauss_bf16", seed, x_layer, T_X, x_row0 * H, M * H).reshape(M, H)
     W = fill("gauss", seed, layer, T_ROUTER, 0, E * H, 0.02).reshape(E, H) if router is None else router
-    b = fill("gauss", seed, layer, T_BIAS, 0, E, 1.5) if use_bias else None
+    b = (fill("gauss", seed, layer, T_BIAS, 0, E, 1.5) if bias is None else bias) if use_bias else None
     logits = router_logits(W, x, b)
     sel, w64, _ = topk(logits, K, renorm)
     X = bf16_to_f32(x).astype(np.float64)

@@ -121,6 +121,37 @@ def test_prefill_zero_rows_fallback(lib, bias):
     st.destroy()
 
 
+# ------------------------------------------------------------------ prefill: tile boundaries
+@pytest.mark.parametrize("T,fmt", [(128, 0), (129, 0), (256, 1), (383, 0)])
+def test_prefill_tile_boundaries(lib, T, fmt):
+    """A router bias of +64 on experts 100..109 (and -64 elsewhere) sends every
+    token to exactly those ten experts: eleven groups (with the shared one) of
+    T rows each, i.e. exactly full 128-row tiles (T = 128, 256), one spare row
+    (129), or 127 rows over (383), and 502 experts with no rows at all. Routing
+    bit-exact and every output row against the grouped fp64 oracle given the
+    same bias."""
+    seed, layer, xl = 4, 23, 91
+    _say("prefill tile boundaries T", T, "fmt", fmt)
+    qfm.init(H, I, E, K, 1, 1)
+    st = qfm.Stream()
+    L = qfm.SynthLayer(fmt, seed, layer, with_bias=True, stream=st)
+    st.sync()                      # the generator writes the layer on st: finish before overwriting the bias
+    bias = np.full(E, -64.0, np.float32)
+    bias[100:110] = 64.0 + np.arange(10, dtype=np.float32) * 0.25
+    qfm.check(lib.qfm_memcpy_h2d(L.s.layer.router_bias, bias.ctypes.data, bias.nbytes), "bias")
+    x = orc.fill("gauss_bf16", seed, xl, orc.T_X, 0, T * H).reshape(T, H)
+    g = _forward(lib, L.s.layer, x, st)
+    r = orc.moe_layer_grouped(H, I, E, K, T, seed, layer, xl, use_bias=1, x=x, fmt=fmt, bias=bias)
+    assert set(np.unique(g["sel"])) == set(range(100, 110))
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    rel = max(_rel(g["y"][t], r["y"][t]) for t in range(T))
+    _say("  max rel err", rel, "counters", g["counters"])
+    assert rel <= TOL
+    L.destroy()
+    st.destroy()
+
+
 # ------------------------------------------------------------------ prefill: near ties
 def test_prefill_near_ties_exact_order(lib):
     """Router rows built so that token 0's 9th..12th experts have identical bf16
@@ -182,6 +213,7 @@ class _F4Layer:
         self.lib, self.seed, self.layer = lib, seed, layer
         self.st = qfm.Stream()
         self.L = qfm.SynthLayer(qfm.QFM_FMT_NVFP4, seed, layer, with_bias=bias, stream=self.st)
+        self.st.sync()             # generated on st; the scales are then overwritten from the host
         lay = qfm.QfmLayer.from_buffer_copy(self.L.s.layer)
         lay.sh_gate, lay.sh_up, lay.sh_down, lay.sh_gate_inp = qfm.Qf8I8Mat(), qfm.Qf8I8Mat(), qfm.Qf8I8Mat(), None
         self.lay = lay
