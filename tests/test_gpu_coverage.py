@@ -406,3 +406,29 @@ def test_e4m3_every_down_byte(lib, f4):
             worst = max(worst, rel)
             assert rel <= TOL, (name, hex(b), rel)
         _say("  ", name, "worst rel err over the 255 finite bytes", worst)
+
+
+# ------------------------------------------------------------------ decode: zero rows
+@pytest.mark.parametrize("M,fmt,bias", [(1, 0, False), (3, 0, False), (1, 1, True), (5, 1, False)])
+def test_decode_zero_rows(lib, M, fmt, bias):
+    """All-zero x rows through the fused decode paths (at M = 1 the INT8 gate/up
+    kernel's own selection): without a bias every logit is 0, the selection is
+    experts 0..9 (ties to the lower index) with weights 0.1; with a bias the
+    logits are the bias and the selection its top 10. Every expert's output is
+    0, so y is 0."""
+    _say("decode zero rows M", M, "fmt", fmt, "bias", bias)
+    qfm.init(H, I, E, K, 1, 1)
+    st = qfm.Stream()
+    L = qfm.SynthLayer(fmt, 5, 61, with_bias=bias, stream=st)
+    st.sync()
+    x = np.zeros((M, H), np.uint16)
+    g = _forward(lib, L.s.layer, x, st)
+    r = orc.moe_layer_grouped(H, I, E, K, M, 5, 61, 0, use_bias=int(bias), x=x, fmt=fmt)
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    if not bias:
+        assert np.array_equal(g["sel"], np.tile(np.arange(K), (M, 1)))
+        assert np.allclose(g["wts"], 0.1, rtol=1e-6)
+    assert not g["y"].any() and not r["y"].any()
+    L.destroy()
+    st.destroy()
