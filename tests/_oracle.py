@@ -363,7 +363,8 @@ def moe_layer_grouped(H, I, E, K, M, seed, layer, x_layer, x_row0=0, fmt=0, gate
     def expert_out(Wg, Wu, Wd, Xe):
         g = Xe @ Wg.T
         u = Xe @ Wu.T
-        return (g / (1.0 + np.exp(-g)) * u) @ Wd.T
+        with np.errstate(over="ignore"):         # silu(g) -> -0 as exp(-g) -> inf for very negative g
+            return (g / (1.0 + np.exp(-g)) * u) @ Wd.T
 
     for e in np.unique(sel):
         rows, ks = np.nonzero(sel == e)

@@ -432,3 +432,32 @@ def test_decode_zero_rows(lib, M, fmt, bias):
     assert not g["y"].any() and not r["y"].any()
     L.destroy()
     st.destroy()
+
+
+# ------------------------------------------------------------------ dynamic range of x
+@pytest.mark.parametrize("M,fmt,shift", [(1, 0, 24), (1, 0, -24), (4, 1, 24), (4, 0, -24), (40, 0, 24), (40, 1, -24)])
+def test_input_dynamic_range(lib, M, fmt, shift):
+    """x rows scaled by 2^shift (exact in bf16) through the fused decode and
+    prefill paths: the activations as fp16 scaled per token or per 16 values,
+    the hidden vectors' fp16 chunks and the prefill's scaled fp16 partials must
+    follow the magnitude. At 2^24 the softmax is one-hot, at 2^-24 nearly
+    uniform; the routing stays bit-exact and y within the usual bound."""
+    _say("dynamic range M", M, "fmt", fmt, "shift", shift)
+    qfm.init(H, I, E, K, 1, 1)
+    st = qfm.Stream()
+    L = qfm.SynthLayer(fmt, 7, 71, with_bias=False, stream=st)
+    st.sync()
+    x0 = orc.fill("gauss_bf16", 7, 600 + M, orc.T_X, 0, M * H).reshape(M, H)
+    xf = orc.bf16_to_f32(x0) * np.float32(2.0 ** shift)
+    x = (xf.view(np.uint32) >> 16).astype(np.uint16)
+    assert np.array_equal(orc.bf16_to_f32(x), xf)                 # the scaling is exact
+    g = _forward(lib, L.s.layer, x, st)
+    r = orc.moe_layer_grouped(H, I, E, K, M, 7, 71, 0, x=x, fmt=fmt)
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    assert np.isfinite(g["y"]).all()
+    rel = max(_rel(g["y"][t], r["y"][t]) for t in range(M))
+    _say("  max rel err", rel)
+    assert rel <= TOL
+    L.destroy()
+    st.destroy()
