@@ -123,7 +123,7 @@ def test_csr_build_bit_exact(lib, T, skew):
     assert np.array_equal(d_pw.download(np.float32, P).view(np.uint32), pw.view(np.uint32))
 
 
-@pytest.mark.parametrize("T", [1, 37])
+@pytest.mark.parametrize("T", [1, 37, 129])
 def test_experts_chunk(lib, T):
     """qf8_i8_experts_chunk: y[t] = sum_k w * expert_k(X8(x_t)), y overwritten."""
     seed, layer = 2, 4
@@ -262,7 +262,7 @@ def test_m8_entry_points(lib, card, epc, il):
 
 
 # ------------------------------------------------------------------ shared expert
-@pytest.mark.parametrize("T", [1, 5])
+@pytest.mark.parametrize("T", [1, 5, 37])
 def test_shexp_rows(lib, T):
     seed, layer = 6, 8
     _say("shexp", T)
