@@ -375,6 +375,7 @@ def moe_layer_grouped(H, I, E, K, M, seed, layer, x_layer, x_row0=0, fmt=0, gate
     ys = expert_out(Wg, Wu, Wd, X)
     if gated:
         g = (fill("gauss", seed, layer, T_SHGATE, 0, H, 0.02) if gate_vec is None else gate_vec).astype(np.float64)
-        ys *= (1.0 / (1.0 + np.exp(-(X @ g))))[:, None]
+        with np.errstate(over="ignore"):          # sigma -> 0 as exp(-v) -> inf
+            ys *= (1.0 / (1.0 + np.exp(-(X @ g))))[:, None]
     y += ys
     return dict(x=x, logits=logits, sel=sel, w=w64, y=y)
