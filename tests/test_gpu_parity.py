@@ -418,7 +418,7 @@ def test_prefill_small(lib, T, bias, fmt, renorm):
 
 
 def test_prefill_config4_routing_and_sample(lib):
-    """BASELINE config 4 shape: T=8038, skewed router bias. Routing is checked for
+    """The benchmark prefill shape: T=8038, skewed router bias. Routing is checked for
     every token (bit-exact) and the outputs of every token against the fp64
     oracle, so all tokens of the hottest (7741 of them) and coldest experts are
     covered."""
@@ -456,7 +456,7 @@ def test_prefill_reference_shape(lib, T, fmt, gated):
 
 
 def test_prefill_config4_nvfp4_all_rows(lib):
-    """Config 4's prefill (T=8038, skewed router bias) on an NVFP4 arena: routing
+    """The benchmark prefill (T=8038, skewed router bias) on an NVFP4 arena: routing
     of every token bit-exact, and the outputs of every token (all tokens of the
     hottest and the coldest expert among them) against the fp64 layer, evaluated
     expert by expert on the oracle's dequantized weights (moe_layer_grouped)."""
