@@ -56,6 +56,23 @@ int  qf8_i8_hc_rows(float *normed, float *hc_d, float *mixed, float *inj, float 
  * qf8_hc.hip:99-103, :148-150). */
 void qf8_stream_inject(float *R, const float *y, const float *inj, hipStream_t s);
 
+/* bf16 shared expert of the NVFP4 stage (ocho/amd_server/qf8_dense.h:275-286):
+ * gate, up [I][H], gate_inp [H], down [H][I], all bf16. */
+typedef struct { const uint16_t *gate, *up, *down, *gate_inp; } Qf8ShexpW;
+/* One row: y2560[H] += sigmoid(g1) * ed, with x = mixed fp32 [H] and, written
+ * as in the reference, eu [I] = up . x, g1 [1] = gate_inp . x,
+ * eg [I] = silu(gate . x) * eu, ed [H] = down . eg (fp32 accumulate).
+ * Replaces qf8_shexp (qf8_dense.h:280-282, qf8_layer.hip:42-54). */
+void qf8_shexp(const Qf8ShexpW *w, const float *mixed, float *eg, float *eu, float *g1, float *ed,
+               float *y2560, hipStream_t s);
+/* 1 <= M <= 8 rows (the reference's QF8_M_MAX): mixed [M][H], eg / eu [M][I],
+ * g1 [M], ed [M][H], y2560 row m at m * y_stride (>= H); eg_stride is accepted
+ * and not used (eg rows are I apart, as in the reference). Each weight byte is
+ * read once for all rows. Replaces qf8_shexp_M (qf8_dense.h:284-286,
+ * qf8_layer.hip:23-40). */
+void qf8_shexp_M(const Qf8ShexpW *w, const float *mixed, int M, float *eg, float *eu, float *g1, float *ed,
+                 float *y2560, int eg_stride, int y_stride, hipStream_t s);
+
 /* Validated twins: 0, or -1 / -2 on a rejected argument (nothing launched),
  * -3 on a launch error. */
 int  qf8_i8_gemv_multi_ex(const Qf8I8Multi *mm, const int8_t *xq, const float *xs, hipStream_t s);
@@ -64,6 +81,10 @@ int  qf8_i8_hc_m1_ex(float *normed, float *hc_d, float *mixed, float *inj, float
                      int8_t *d8q, float *d8s, float *hcy, const float *y_prev, const float *inj_prev, int8_t *xq_out,
                      float *xs_out, hipStream_t s);
 int  qf8_stream_inject_ex(float *R, const float *y, const float *inj, hipStream_t s);
+int  qf8_shexp_ex(const Qf8ShexpW *w, const float *mixed, float *eg, float *eu, float *g1, float *ed,
+                  float *y2560, hipStream_t s);
+int  qf8_shexp_M_ex(const Qf8ShexpW *w, const float *mixed, int M, float *eg, float *eu, float *g1, float *ed,
+                    float *y2560, int eg_stride, int y_stride, hipStream_t s);
 
 #pragma GCC visibility pop
 #ifdef __cplusplus

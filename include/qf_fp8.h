@@ -6,9 +6,11 @@
  * as E4M3 codes of value / sc[row][l], with one fp32 scale per (row, chunk).
  *   weights [slot][rows][in] bytes, scales [slot][rows][64] fp32;
  *   gate/up: rows = I, in = H; down: rows = H, in = I.
- * Codes come from qf8_fp8_pack_expert (qf_store.h), which never emits 0x7F
- * or 0xFF, so every stored code decodes to the same value under the
- * reference's integer decode and the gfx950 E4M3 convert used here.
+ * Every code byte decodes as the reference's integer decode does
+ * (qf8_moe_fp8.hip:19-26): sign, 4-bit exponent (bias 7, subnormal step
+ * 2^-9), 3-bit mantissa and no NaN, so 0x7F / 0xFF read +-480. (The packer,
+ * qf8_fp8_pack_expert in qf_store.h, saturates at 0x7E and never emits them;
+ * an arena filled another way may hold them.)
  *
  * Execution: a descriptor per distinct selected expert (ascending expert id,
  * its rows in token order, at most 16), then a fused gate/up and a fused

@@ -472,6 +472,36 @@ void orc_stream_inject(float *R, const float *y, const float *inj, int H) {
         for (int i = 0; i < H; i++) R[c * H + i] = fmaf(inj[c], y[i], R[c * H + i]);
 }
 
+/* The bf16 shared expert of the NVFP4 stage (qf8_layer.hip:23-54, weights
+   Qf8ShexpW qf8_dense.h:275-277), fp64: eu = up . x, g1 = gate_inp . x,
+   eg = silu(gate . x) * eu (k8_silu_mul, :8-12), ed = down . eg,
+   y += sigmoid(g1) * ed (k8_shexp_add, :14-18), per row m < M. */
+void orc_shexp_bf16(const uint16_t *gate, const uint16_t *up, const uint16_t *down, const uint16_t *gate_inp,
+                    const float *x, int M, int H, int I, double *eg, double *eu, double *g1, double *ed, double *y) {
+    for (int m = 0; m < M; m++) {
+        const float *xm = x + (size_t)m * H;
+        double gi = 0.0;
+        for (int k = 0; k < H; k++) gi += (double)orc_bf16_to_f32(gate_inp[k]) * (double)xm[k];
+        g1[m] = gi;
+        for (int r = 0; r < I; r++) {
+            double g = 0.0, u = 0.0;
+            for (int k = 0; k < H; k++) {
+                g += (double)orc_bf16_to_f32(gate[(size_t)r * H + k]) * (double)xm[k];
+                u += (double)orc_bf16_to_f32(up[(size_t)r * H + k]) * (double)xm[k];
+            }
+            eu[(size_t)m * I + r] = u;
+            eg[(size_t)m * I + r] = g / (1.0 + exp(-g)) * u;
+        }
+        const double sg = 1.0 / (1.0 + exp(-gi));
+        for (int o = 0; o < H; o++) {
+            double d = 0.0;
+            for (int r = 0; r < I; r++) d += (double)orc_bf16_to_f32(down[(size_t)o * I + r]) * eg[(size_t)m * I + r];
+            ed[(size_t)m * H + o] = d;
+            y[(size_t)m * H + o] += sg * d;
+        }
+    }
+}
+
 /* Four-card combine: y[i] = ((y0[i] + y1[i]) + y2[i]) + y3[i], fp32, the
    left-to-right order of k_m8_reduce4 (qf_moe_m8_wave64.hip:216-221). */
 void orc_m8_reduce4(float *y, const float *y0, const float *y1, const float *y2, const float *y3, long n) {

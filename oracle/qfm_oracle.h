@@ -57,6 +57,9 @@
  *   orc_hc_norm            numpy restatement; unit-RMS rows give normed = R * (1 + w)
  *   orc_hc_combine         numpy restatement; equal streams reduce to sigmoid * normed
  *   orc_stream_inject      numpy float32 fma restatement (np.float32 products rounded once)
+ *   orc_shexp_bf16         numpy fp64 matmuls of the bf16 weights; closed forms: one-hot gate /
+ *                          up / down rows pick single activations, zero x leaves y unchanged,
+ *                          a zero gate_inp row gives the factor sigmoid(0) = 1/2
  *   orc_moe_layer          recomposition from the pieces with numpy fp64 experts
  */
 #ifndef QFM_ORACLE_H
@@ -133,6 +136,10 @@ void orc_i8_gemv(const int8_t *W, const float *s, int rows, int K, const int8_t 
 void orc_hc_norm(const float *R, const uint16_t *w, int H, double *normed);
 void orc_hc_combine(const float *hcy, const float *normed, int H, double *mixed);
 void orc_stream_inject(float *R, const float *y, const float *inj, int H);
+/* bf16 shared expert, M rows of fp32 x [M][H]: eg/eu [M][I], g1 [M], ed [M][H] (fp64) and
+   y [M][H] (fp64, in/out: y += sigmoid(g1) * ed) */
+void orc_shexp_bf16(const uint16_t *gate, const uint16_t *up, const uint16_t *down, const uint16_t *gate_inp,
+                    const float *x, int M, int H, int I, double *eg, double *eu, double *g1, double *ed, double *y);
 
 /* ---- X8 activation quantizer (reference's lossy activation mode) ---- */
 void orc_x8_quant(const float *v, int n, int8_t *q, float *s);

@@ -36,8 +36,11 @@ const char *const kProj[3] = {"gate_proj", "up_proj", "down_proj"};
 
 // One staging buffer holds one expert in the largest form at the largest
 // supported shape (H 2560, I 640): FP8 lane-chunk 3*I*H bytes + (2I + H) * 64
-// fp32 scales = 6,062,080 bytes (NVFP4 needs 2,764,800).
+// fp32 scales = 5,898,240 bytes (NVFP4 needs 2,764,800).
 constexpr size_t kStageBytes = (size_t)3 * 2560 * 640 + (size_t)(2 * 640 + 2560) * 64 * 4;
+static_assert(kStageBytes == 5898240, "staging size");
+static_assert(kStageBytes >= (size_t)3 * 2560 * 640 / 2 + (size_t)3 * 2560 * 640 / 16, "NVFP4 expert fits the staging buffer");
+static_assert(kStageBytes >= (size_t)3 * 2048 * 512 + (size_t)(2 * 512 + 2048) * 64 * 4, "FP8 expert at 2048/512 fits");
 constexpr int kLanes = 64;
 
 std::atomic<unsigned long long> g_calls{0}, g_miss{0}, g_bytes{0};

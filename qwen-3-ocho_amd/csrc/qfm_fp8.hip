@@ -95,12 +95,27 @@ k_fp8_build_desc(const int *__restrict__ sel, const float *__restrict__ wt, int 
     }
 }
 
-// decode 8 E4M3 codes (one uint2) into out[0..7]
+// a byte of w whose low seven bits are all set (0x7F or 0xFF)
+__device__ __forceinline__ bool has_f8_top_code(uint32_t w) {
+    const uint32_t v = ~(w | 0x80808080u);             // that byte of v is zero, every other byte nonzero
+    return ((v - 0x01010101u) & ~v & 0x80808080u) != 0u;
+}
+// decode 8 E4M3 codes (one uint2) into out[0..7]: the gfx950 OCP convert, which
+// matches the reference's integer decode (qf8_moe_fp8.hip:19-26) on every code
+// but 0x7F / 0xFF; those read +-480 there (exponent 15, mantissa 7, no NaN) and
+// NaN here, so a lane holding one takes the integer value instead
 __device__ __forceinline__ void f8x8(uint2 q, float *out) {
     const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8(q.x, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(q.x, true);
     const f32x2_t c = __builtin_amdgcn_cvt_pk_f32_fp8(q.y, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(q.y, true);
     out[0] = a.x; out[1] = a.y; out[2] = b.x; out[3] = b.y;
     out[4] = c.x; out[5] = c.y; out[6] = d.x; out[7] = d.y;
+    if (__builtin_expect(has_f8_top_code(q.x) || has_f8_top_code(q.y), 0)) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t byte = ((i < 4 ? q.x : q.y) >> (8 * (i & 3))) & 0xFFu;
+            if ((byte & 0x7Fu) == 0x7Fu) out[i] = (byte & 0x80u) ? -480.0f : 480.0f;
+        }
+    }
 }
 
 // CH = H / 64 code bytes per lane and row (32 at H 2048, 40 at H 2560)

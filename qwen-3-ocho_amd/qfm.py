@@ -100,6 +100,11 @@ class Qf8I8Multi(C.Structure):
     _fields_ = [("m", C.POINTER(Qf8I8Mat) * 4), ("y", vp * 4), ("act", C.c_int * 4), ("n", C.c_int)]
 
 
+class Qf8ShexpW(C.Structure):
+    """bf16 shared-expert weights (qf8_dense.h:275-277)."""
+    _fields_ = [("gate", vp), ("up", vp), ("down", vp), ("gate_inp", vp)]
+
+
 class Qf8MoeDesc(C.Structure):
     """FP8 path expert descriptor (qf8_moe_fp8.h:37-44)."""
     _fields_ = [("slot", C.c_int), ("nrow", C.c_int), ("row", C.c_int * 16), ("wt", C.c_float * 16)]
@@ -220,6 +225,10 @@ _SIGS = {
     "qf8_i8_hc_rows": (C.c_int, [vp] * 6 + [C.POINTER(Qf8I8Mat)] * 3 + [vp] * 9 + [C.c_int, vp]),
     "qf8_stream_inject": (None, [vp, vp, vp, vp]),
     "qf8_stream_inject_ex": (C.c_int, [vp, vp, vp, vp]),
+    "qf8_shexp": (None, [C.POINTER(Qf8ShexpW), vp, vp, vp, vp, vp, vp, vp]),
+    "qf8_shexp_ex": (C.c_int, [C.POINTER(Qf8ShexpW), vp, vp, vp, vp, vp, vp, vp]),
+    "qf8_shexp_M": (None, [C.POINTER(Qf8ShexpW), vp, C.c_int, vp, vp, vp, vp, vp, C.c_int, C.c_int, vp]),
+    "qf8_shexp_M_ex": (C.c_int, [C.POINTER(Qf8ShexpW), vp, C.c_int, vp, vp, vp, vp, vp, C.c_int, C.c_int, vp]),
     "qfm_gen_input_rows": (C.c_int, [vp, C.c_int, C.c_uint32, C.c_uint32, C.c_int, vp]),
     "qfm_dev_malloc": (vp, [C.c_size_t]),
     "qfm_dev_free": (C.c_int, [vp]),

@@ -67,6 +67,7 @@ _SIGS = {
     "orc_hc_norm": (None, [vp, vp, C.c_int, vp]),
     "orc_hc_combine": (None, [vp, vp, C.c_int, vp]),
     "orc_stream_inject": (None, [vp, vp, vp, C.c_int]),
+    "orc_shexp_bf16": (None, [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp]),
     "orc_csr_build": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp, vp]),
     "orc_m8_reduce4": (None, [vp, vp, vp, vp, vp, C.c_long]),
     "orc_moe_layer": (C.c_int, [C.POINTER(LayerCfg), C.c_int, vp, vp, vp, vp, vp, vp]),
@@ -258,6 +259,21 @@ def stream_inject(R, y, inj):
     lib.orc_stream_inject(ptr(R), ptr(np.ascontiguousarray(y, np.float32)), ptr(np.ascontiguousarray(inj, np.float32)),
                           len(y))
     return R
+
+
+def shexp_bf16(gate, up, down, gate_inp, x, y):
+    """bf16 shared expert over the rows of x [M][H] (orc_shexp_bf16): (eg, eu, g1, ed, y + sigmoid(g1) * ed), fp64."""
+    lib = load()
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    M, H = x.shape
+    I = gate.shape[0]
+    eg, eu, ed = np.empty((M, I)), np.empty((M, I)), np.empty((M, H))
+    g1 = np.empty(M)
+    yo = np.array(np.atleast_2d(y), np.float64, copy=True)
+    lib.orc_shexp_bf16(ptr(np.ascontiguousarray(gate, np.uint16)), ptr(np.ascontiguousarray(up, np.uint16)),
+                       ptr(np.ascontiguousarray(down, np.uint16)), ptr(np.ascontiguousarray(gate_inp, np.uint16)),
+                       ptr(x), M, H, I, ptr(eg), ptr(eu), ptr(g1), ptr(ed), ptr(yo))
+    return eg, eu, g1, ed, yo
 
 
 def x8_quant(v):

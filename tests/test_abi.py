@@ -18,7 +18,7 @@ def _declared_functions():
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     src = re.sub(r"//[^\n]*", "", src)
     names = set()
-    for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b([a-z_][a-z0-9_]*)\s*\(", src, flags=re.M):
+    for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b([a-z_][A-Za-z0-9_]*)\s*\(", src, flags=re.M):
         name = m.group(1)
         if name not in ("if", "while", "for", "sizeof", "typedef"):
             names.add(name)

@@ -235,6 +235,38 @@ def test_dense_quant_and_gemv(libs):
             assert _rel(outs[1][i], outs[0][i]) <= 2e-5, (Kd, i)
 
 
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_bf16_shared_expert(libs, M):
+    """qf8_shexp (M = 1) / qf8_shexp_M against the reference's own
+    (qf8_layer.hip:23-54): eg, eu, g1, ed and the gated add into y."""
+    lib, ref = libs
+    rng = np.random.default_rng(40 + M)
+    bf = lambda a: ((np.asarray(a, np.float32).view(np.uint32) + 0x8000) >> 16).astype(np.uint16)
+    ws = [qfm.DevBuf.from_array(bf(rng.standard_normal(sh) * sc))
+          for sh, sc in (((I, H), 0.03), ((I, H), 0.03), ((H, I), 0.03), ((H,), 0.05))]
+    w = qfm.Qf8ShexpW(*[b.ptr for b in ws])
+    x = qfm.DevBuf.from_array(rng.standard_normal((M, H)).astype(np.float32))
+    ys = H + 32
+    y0 = rng.standard_normal((M, ys)).astype(np.float32)
+    outs = []
+    for L in (ref, lib):
+        eg, eu, g1, ed = qfm.DevBuf(M * I * 4), qfm.DevBuf(M * I * 4), qfm.DevBuf(M * 4), qfm.DevBuf(M * H * 4)
+        y = qfm.DevBuf.from_array(y0)
+        if M == 1:
+            _fn(L, "qf8_shexp", None, [C.POINTER(qfm.Qf8ShexpW)] + [vp] * 7)(C.byref(w), x.ptr, eg.ptr, eu.ptr,
+                                                                            g1.ptr, ed.ptr, y.ptr, None)
+        else:
+            _fn(L, "qf8_shexp_M", None, [C.POINTER(qfm.Qf8ShexpW), vp, C.c_int] + [vp] * 5 + [C.c_int, C.c_int, vp])(
+                C.byref(w), x.ptr, M, eg.ptr, eu.ptr, g1.ptr, ed.ptr, y.ptr, I, ys, None)
+        qfm.check(lib.qfm_device_sync(), "sync")
+        outs.append({"eg": eg.download(np.float32, (M, I)), "eu": eu.download(np.float32, (M, I)),
+                     "g1": g1.download(np.float32, (M,)), "ed": ed.download(np.float32, (M, H)),
+                     "y": y.download(np.float32, (M, ys))})
+    errs = {k: _rel(outs[1][k], outs[0][k]) for k in outs[0]}
+    _say("bf16 shared expert M", M, {k: f"{v:.1e}" for k, v in errs.items()})
+    assert max(errs.values()) <= 2e-5, errs
+
+
 def test_hc_premixer(libs):
     lib, ref = libs
     rng = np.random.default_rng(6)

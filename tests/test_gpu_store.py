@@ -448,9 +448,12 @@ def _desc_model(sel, wt):
     return out
 
 
-@pytest.mark.parametrize("M", [1, 3, 8])
-def test_fp8_arena_and_kernels(lib, gen, store, xfer, M):
-    _say("fp8 lane-chunk M", M)
+@pytest.mark.parametrize("M,plant", [(1, False), (3, False), (8, False), (3, True)])
+def test_fp8_arena_and_kernels(lib, gen, store, xfer, M, plant):
+    """plant: codes 0x7F / 0xFF written into every slot (the packer never emits
+    them; the reference's integer decode reads them as +-480, the hardware
+    E4M3 convert as NaN, and the kernels must follow the reference)."""
+    _say("fp8 lane-chunk M", M, "planted 0x7F/0xFF" if plant else "")
     st = _store(store, "safetensors")
     s = qfm.Stream()
     slots = 16
@@ -467,6 +470,12 @@ def test_fp8_arena_and_kernels(lib, gen, store, xfer, M):
         for e in range(slots):
             rw, rs = orc.fp8_pack_expert(gen[wsrc][e], gen[ssrc][e], 0.01, rows, cols)
             assert np.array_equal(w8[e], rw) and np.array_equal(sc[e].view(np.uint32), rs.view(np.uint32)), (nm, e)
+        if plant:
+            flat = w8.reshape(slots, -1)
+            idx = np.arange(5, flat.shape[1], 61)
+            flat[:, idx[0::2]] = 0x7F
+            flat[:, idx[1::2]] = 0xFF
+            qfm.check(lib.qfm_memcpy_h2d(getattr(c, nm), flat.ctypes.data, flat.nbytes), "plant codes")
         dq[nm] = [orc.fp8_dequant(w8[e], sc[e]) for e in range(slots)]
     rng = np.random.default_rng(M)
     sel = np.stack([rng.choice(slots, K, replace=False) for _ in range(M)]).astype(np.int32)

@@ -1,6 +1,6 @@
-"""The dense INT8 x X8 GEMV, hyper-connection norm / combine and stream
-inject of the oracle (ocho/amd_server/qf8_dense_i8.hip:78-175,
-qf8_hc.hip:99-103) pinned by numpy restatements and closed forms."""
+"""The dense INT8 x X8 GEMV, hyper-connection norm / combine, stream
+inject and bf16 shared expert of the oracle (ocho/amd_server/qf8_dense_i8.hip:78-175,
+qf8_hc.hip:99-103, qf8_layer.hip:23-54) pinned by numpy restatements and closed forms."""
 import numpy as np
 
 import _oracle as orc
@@ -67,3 +67,43 @@ def test_stream_inject_is_one_fma():
     assert np.array_equal(got, exact.astype(np.float32))
     two = (np.repeat(inj, H) * np.tile(y, 4)).astype(np.float32) + R       # two roundings differ somewhere
     assert not np.array_equal(got, two)
+
+
+def _bf16(a):
+    """fp32 -> bf16 bits (round to nearest even), and the values they hold."""
+    u = np.asarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    b = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return b, (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def test_shexp_bf16_numpy_and_closed_forms():
+    rng = np.random.default_rng(4)
+    M, H, I = 3, 256, 64
+    gb, g = _bf16(rng.standard_normal((I, H)) * 0.05)
+    ub, u = _bf16(rng.standard_normal((I, H)) * 0.05)
+    db, d = _bf16(rng.standard_normal((H, I)) * 0.05)
+    ib, gi = _bf16(rng.standard_normal(H) * 0.05)
+    x = rng.standard_normal((M, H)).astype(np.float32)
+    y0 = rng.standard_normal((M, H)).astype(np.float32)
+    eg, eu, g1, ed, y = orc.shexp_bf16(gb, ub, db, ib, x, y0)
+    x64 = x.astype(np.float64)
+    gg, uu, g1r = x64 @ g.T, x64 @ u.T, x64 @ gi
+    egr = gg / (1 + np.exp(-gg)) * uu
+    edr = egr @ d.T
+    assert np.allclose(eu, uu, rtol=1e-12, atol=1e-14) and np.allclose(g1, g1r, rtol=1e-12, atol=1e-14)
+    assert np.allclose(eg, egr, rtol=1e-12, atol=1e-14) and np.allclose(ed, edr, rtol=1e-12, atol=1e-14)
+    assert np.allclose(y, y0 + edr / (1 + np.exp(-g1r))[:, None], rtol=1e-12, atol=1e-14)
+    # one-hot rows: gate row r picks x[r], up row r picks x[r + 1], down row o picks eg[o mod I]
+    G = np.zeros((I, H), np.float32); U = np.zeros((I, H), np.float32); D = np.zeros((H, I), np.float32)
+    G[np.arange(I), np.arange(I)] = 1.0
+    U[np.arange(I), np.arange(I) + 1] = 1.0
+    D[np.arange(H), np.arange(H) % I] = 2.0
+    zi = np.zeros(H, np.uint16)                                   # gate_inp 0: factor sigmoid(0) = 1/2
+    eg1, eu1, g11, ed1, y1 = orc.shexp_bf16(_bf16(G)[0], _bf16(U)[0], _bf16(D)[0], zi, x, np.zeros((M, H)))
+    xa, xb = x64[:, :I], x64[:, 1:I + 1]
+    assert np.array_equal(eu1, xb) and np.array_equal(g11, np.zeros(M))
+    assert np.allclose(eg1, xa / (1 + np.exp(-xa)) * xb, rtol=1e-15)
+    assert np.allclose(y1, 0.5 * 2.0 * eg1[:, np.arange(H) % I], rtol=1e-15)
+    # zero x: eg, ed = 0 and y unchanged
+    _, _, _, edz, yz = orc.shexp_bf16(gb, ub, db, ib, np.zeros((M, H), np.float32), y0)
+    assert not edz.any() and np.array_equal(yz, y0.astype(np.float64))
