@@ -53,6 +53,16 @@ int         qfm_get_config(qfm_config *cfg);
 const char *qfm_last_error(void);   /* "" when no error is latched; reading clears it */
 int         qfm_status(void);       /* 0, or the latched error code; also polls hipGetLastError */
 const char *qfm_version(void);
+/* Memory preflight, the reference's budget guard (qf_hip4_stage.hip:792-813):
+ * every entry that allocates arena-sized memory (qfm_arena_init,
+ * qfm_synth_layer_create, qfm_expcache_init / qf4_expcache_init,
+ * qfm_layer_load) prices all of its device bytes first and refuses, with -4
+ * and nothing allocated, a plan larger than the device's free memory or one
+ * that would take the device's memory in use above the budget. budget 0: no
+ * limit beyond the device. Default: QFM_HBM_BUDGET_MIB from the environment
+ * (MiB), else 0. Process-wide, not thread-safe. */
+int         qfm_set_hbm_budget(size_t bytes);
+size_t      qfm_get_hbm_budget(void);
 /* sizeof of the ABI structs (0 Qf4ExpCache, 1 qfm_layer, 2 qfm_synth_layer,
    3 Qf8I8Mat, 4 Qf5M8Route, 5 qfm_config, 6 qfm_ws_view, 7 QfEntry, 8 QfStore,
    9 Qf4ExpXfer, 10 QfRouteMailbox) for FFI layout checks. */
@@ -387,6 +397,8 @@ int qfm_fill_f32(float *out, uint64_t cnt, float value, hipStream_t s);
  * qfm_arena_init allocates the INT8 (i8_*) or NVFP4 (w_*, s_*, s2*_dev)
  * blobs; qfm_arena_generate fills whatever is allocated from the generator. */
 int  qfm_arena_init(Qf4ExpCache *c, int fmt, int layer);
+/* Device bytes qfm_arena_init allocates for fmt at the current shape (0 for an unknown fmt). */
+size_t qfm_arena_bytes(int fmt);
 int  qfm_arena_generate(Qf4ExpCache *c, uint32_t seed, uint32_t layer, hipStream_t s);
 void qfm_arena_free(Qf4ExpCache *c);
 /* A complete synthetic layer: arena + fp32 router (+ optional skew bias) +

@@ -129,6 +129,10 @@ int  qf4_expcache_init(Qf4ExpCache *c, const QfStore *st, int layer, int slots);
 /* The same with the modes given explicitly (QFM_EXPCACHE_*; the environment is
  * not read). FP8 excludes NVFP4 and INT8; INT8_ONLY needs INT8 and NVFP4. */
 int  qfm_expcache_init(Qf4ExpCache *c, const QfStore *st, int layer, int slots, int modes);
+/* Device bytes qfm_expcache_init(.., slots, modes) allocates at the current
+ * shape (slot arrays, scales, device routing state); 0 for invalid modes or
+ * slots. The init prices this before allocating (qfm_set_hbm_budget). */
+size_t qfm_expcache_bytes(int slots, int modes);
 /* Releases every device, host and pinned allocation of the cache (also those
  * of a synthetic arena from qfm_arena_init). Replaces qf4_expcache_free (:206-228). */
 void qf4_expcache_free(Qf4ExpCache *c);

@@ -9,6 +9,7 @@
 #include <vector>
 #include <cstdio>
 #include <cstddef>
+#include <cstdlib>
 #include <cstring>
 
 namespace qfm {
@@ -73,6 +74,33 @@ static size_t prof_event(hipStream_t s) {
 }
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// ---- memory preflight ------------------------------------------------------
+static size_t g_hbm_budget = 0;        // bytes; 0: the device's own memory
+static bool g_hbm_budget_set = false;  // set by qfm_set_hbm_budget (else QFM_HBM_BUDGET_MIB)
+static size_t hbm_budget() {
+    if (!g_hbm_budget_set) {
+        const char *v = std::getenv("QFM_HBM_BUDGET_MIB");
+        g_hbm_budget = v ? (size_t)std::strtoull(v, nullptr, 10) << 20 : 0;
+        g_hbm_budget_set = true;
+    }
+    return g_hbm_budget;
+}
+int preflight_device_bytes(size_t bytes, const char *who) {
+    size_t fr = 0, tot = 0;
+    if (hipMemGetInfo(&fr, &tot) != hipSuccess) { set_error(-5, "%s: hipMemGetInfo failed", who); return -5; }
+    const size_t budget = hbm_budget(), used = tot - fr;
+    if (bytes > fr) {
+        set_error(-4, "%s: needs %zu device bytes, %zu free (nothing allocated)", who, bytes, fr);
+        return -4;
+    }
+    if (budget && used + bytes > budget) {
+        set_error(-4, "%s: needs %zu device bytes; %zu in use, budget %zu (nothing allocated)", who, bytes, used,
+                  budget);
+        return -4;
+    }
+    return 0;
+}
 
 struct WsLayout {
     size_t logits, sel, wts, hidden, csr, xh16, part, total;
@@ -161,6 +189,13 @@ int qfm_status(void) {
 }
 
 const char *qfm_version(void) { return "qfm 0.1 gfx950"; }
+
+int qfm_set_hbm_budget(size_t bytes) {
+    g_hbm_budget = bytes;
+    g_hbm_budget_set = true;
+    return 0;
+}
+size_t qfm_get_hbm_budget(void) { return hbm_budget(); }
 
 size_t qfm_sizeof(int which) {
     switch (which) {

@@ -42,9 +42,17 @@ using namespace qfm;
 
 extern "C" {
 
+size_t qfm_arena_bytes(int fmt) {
+    const size_t E = (size_t)g_cfg.E, I = (size_t)g_cfg.I, H = (size_t)g_cfg.H;
+    if (fmt == QFM_FMT_INT8) return 3 * E * I * H + E * (2 * I + H) * 4;
+    if (fmt == QFM_FMT_NVFP4) return 3 * (E * I * H / 2 + E * I * H / 16) + 3 * E * 4;
+    return 0;
+}
+
 int qfm_arena_init(Qf4ExpCache *c, int fmt, int layer) {
     if (!c || (fmt != QFM_FMT_INT8 && fmt != QFM_FMT_NVFP4)) { set_error(-1, "qfm_arena_init: bad arguments"); return -1; }
     std::memset(c, 0, sizeof *c);
+    if (const int rc = preflight_device_bytes(qfm_arena_bytes(fmt), "qfm_arena_init")) return rc;
     const size_t E = (size_t)g_cfg.E, I = (size_t)g_cfg.I, H = (size_t)g_cfg.H;
     c->layer = layer;
     c->slots = (int)E;
@@ -102,9 +110,14 @@ int qfm_synth_layer_create(qfm_synth_layer *out, int fmt, uint32_t seed, uint32_
                            hipStream_t s) {
     if (!out) { set_error(-1, "qfm_synth_layer_create: null output"); return -1; }
     std::memset(out, 0, sizeof *out);
+    const size_t E = (size_t)g_cfg.E, I = (size_t)g_cfg.I, H = (size_t)g_cfg.H;
+    // the whole layer is priced before anything is allocated
+    const size_t plan = qfm_arena_bytes(fmt) + E * H * 4 + (with_bias ? E * 4 : 0) + H * 4 + 3 * I * H +
+                        (2 * I + H) * 4;
+    if (fmt != QFM_FMT_INT8 && fmt != QFM_FMT_NVFP4) { set_error(-1, "qfm_synth_layer_create: bad format"); return -1; }
+    if (int rc = preflight_device_bytes(plan, "qfm_synth_layer_create")) return rc;
     int rc = qfm_arena_init(&out->arena, fmt, (int)layer);
     if (rc) return rc;
-    const size_t E = (size_t)g_cfg.E, I = (size_t)g_cfg.I, H = (size_t)g_cfg.H;
     qfm_layer &L = out->layer;
     L.arena = &out->arena;
     L.fmt = fmt;

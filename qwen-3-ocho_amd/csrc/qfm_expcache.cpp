@@ -245,13 +245,34 @@ void qf4_expcache_free(Qf4ExpCache *c) {
     std::memset(c, 0, sizeof *c);
 }
 
+static bool modes_ok(int modes) {
+    const bool fp8 = modes & QFM_EXPCACHE_FP8, nv = modes & QFM_EXPCACHE_NVFP4, i8 = modes & QFM_EXPCACHE_INT8,
+               ring = modes & QFM_EXPCACHE_INT8_ONLY;
+    return !((modes & ~15) || (fp8 && (nv || i8 || ring)) || (!fp8 && !nv) || (ring && !i8));
+}
+
+size_t qfm_expcache_bytes(int slots, int modes) {
+    const Geo g = geo();
+    if (!modes_ok(modes) || slots < 1 || slots > g.E) return 0;
+    const size_t S = (size_t)slots, n = (size_t)g.I * g.H;
+    size_t b = 0;
+    if (modes & QFM_EXPCACHE_FP8) {
+        b += 3 * S * n + S * ((size_t)2 * g.I + g.H) * kLanes * 4;
+    } else {
+        const size_t nvs = (modes & QFM_EXPCACHE_INT8_ONLY) ? 2 : S;
+        b += 3 * nvs * (g.wb + g.sb);
+        if (modes & QFM_EXPCACHE_INT8) b += 3 * S * n + S * ((size_t)2 * g.I + g.H) * 4;
+    }
+    // device routing state: slot maps, ages, clock, route slots, global scales
+    return b + (size_t)g.E * 4 + S * 4 + S * 8 + 8 + QF_ROUTE_MB_CAP * 4 + 3 * (size_t)g.E * 4;
+}
+
 int qfm_expcache_init(Qf4ExpCache *c, const QfStore *st, int layer, int slots, int modes) {
     if (!c || !st || layer < 0) { set_error(-1, "qfm_expcache_init: bad arguments"); return -1; }
     std::memset(c, 0, sizeof *c);
     const Geo g = geo();
-    const bool fp8 = modes & QFM_EXPCACHE_FP8, nv = modes & QFM_EXPCACHE_NVFP4, i8 = modes & QFM_EXPCACHE_INT8,
-               ring = modes & QFM_EXPCACHE_INT8_ONLY;
-    if ((modes & ~15) || (fp8 && (nv || i8 || ring)) || (!fp8 && !nv) || (ring && !i8)) {
+    const bool fp8 = modes & QFM_EXPCACHE_FP8, i8 = modes & QFM_EXPCACHE_INT8, ring = modes & QFM_EXPCACHE_INT8_ONLY;
+    if (!modes_ok(modes)) {
         set_error(-1, "qfm_expcache_init: invalid modes 0x%x (FP8 alone, or NVFP4 [+ INT8 [+ INT8_ONLY]])", modes);
         return -1;
     }
@@ -259,6 +280,7 @@ int qfm_expcache_init(Qf4ExpCache *c, const QfStore *st, int layer, int slots, i
         set_error(-1, "qfm_expcache_init: slots = %d outside [top_k %d, %d]", slots, g.K, g.E);
         return -1;
     }
+    if (const int rc = preflight_device_bytes(qfm_expcache_bytes(slots, modes), "qfm_expcache_init")) return rc;
     if (g.K > QF_ROUTE_MB_CAP) {
         set_error(-1, "qfm_expcache_init: top_k %d exceeds the mailbox capacity %d", g.K, QF_ROUTE_MB_CAP);
         return -1;
@@ -598,6 +620,14 @@ int qfm_layer_load(qfm_synth_layer *out, const QfStore *st, int layer, int fmt, 
     std::memset(out, 0, sizeof *out);
     if (qfm_store_check_layer(st, layer)) return -1;
     const Geo g = geo();
+    {   // the whole layer is priced before anything is allocated: router, gate
+        // vector, the INT8 shared expert and the expert arena
+        const int modes = fmt == QFM_FMT_INT8 ? (QFM_EXPCACHE_NVFP4 | QFM_EXPCACHE_INT8 | QFM_EXPCACHE_INT8_ONLY)
+                                              : QFM_EXPCACHE_NVFP4;
+        const size_t plan = (size_t)g.E * g.H * 4 + (size_t)g.H * 4 + (size_t)3 * g.I * g.H +
+                            ((size_t)2 * g.I + g.H) * 4 + qfm_expcache_bytes(g.E, modes);
+        if (const int rc = preflight_device_bytes(plan, "qfm_layer_load")) return rc;
+    }
     qfm_layer &L = out->layer;
     L.fmt = fmt;
     L.arena = &out->arena;

@@ -15,6 +15,12 @@ extern Cfg g_cfg;
 void set_error(int code, const char *fmt, ...);
 int  check_launch(const char *what);   // polls hipGetLastError after a launch
 
+// Memory preflight (the reference's budget guard, qf_hip4_stage.hip:792-813):
+// 0 when `bytes` more device memory fit both the device's free memory and the
+// budget (qfm_set_hbm_budget / QFM_HBM_BUDGET_MIB) on the memory already in
+// use; otherwise -4 latched with `who` and the figures. Allocates nothing.
+int preflight_device_bytes(size_t bytes, const char *who);
+
 // shape dispatch helpers
 inline bool shape_2048() { return g_cfg.H == 2048 && g_cfg.I == 512; }
 inline bool shape_2560() { return g_cfg.H == 2560 && g_cfg.I == 640; }

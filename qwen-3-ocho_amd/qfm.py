@@ -126,6 +126,10 @@ _SIGS = {
     "qfm_last_error": (C.c_char_p, []),
     "qfm_status": (C.c_int, []),
     "qfm_version": (C.c_char_p, []),
+    "qfm_set_hbm_budget": (C.c_int, [C.c_size_t]),
+    "qfm_get_hbm_budget": (C.c_size_t, []),
+    "qfm_arena_bytes": (C.c_size_t, [C.c_int]),
+    "qfm_expcache_bytes": (C.c_size_t, [C.c_int, C.c_int]),
     "qfm_sizeof": (C.c_size_t, [C.c_int]),
     "qf_rtr_gemv_launch": (None, [vp, vp, vp, vp]),
     "qf_rtr_topk10_launch": (None, [vp, vp, vp, vp]),

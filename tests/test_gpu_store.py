@@ -113,6 +113,53 @@ def _cache(lib, st, slots, modes):
     return c
 
 
+# ------------------------------------------------------------------ memory preflight
+def _free_bytes(lib):
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    fr, tot = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(fr), ctypes.byref(tot)) == 0
+    return fr.value, tot.value
+
+
+def test_preflight_refuses_before_allocating(lib, store):
+    """A plan above the budget is refused with -4 and nothing allocated
+    (device free memory unchanged); within it, the cache allocates what
+    qfm_expcache_bytes priced (the reference's guard, qf_hip4_stage.hip:792-813)."""
+    st = _store(store, "safetensors")
+    s = qfm.Stream()
+    old = lib.qfm_get_hbm_budget()
+    try:
+        for modes, slots in ((qfm.EXPCACHE_NVFP4, 192), (qfm.EXPCACHE_NVFP4 | qfm.EXPCACHE_INT8, 64),
+                             (qfm.EXPCACHE_FP8, 32)):
+            plan = lib.qfm_expcache_bytes(slots, modes)
+            fr0, tot = _free_bytes(lib)
+            used = tot - fr0
+            lib.qfm_set_hbm_budget(used + plan - (1 << 20))          # 1 MiB short
+            c = qfm.Qf4ExpCache()
+            assert lib.qfm_expcache_init(C.byref(c), C.byref(st.st), LAYER, slots, modes) == -4
+            msg = lib.qfm_last_error().decode()
+            assert "nothing allocated" in msg and str(plan) in msg, msg
+            assert abs(_free_bytes(lib)[0] - fr0) <= (8 << 20)        # nothing allocated
+            assert not c.w_gate and not c.i8_gate and not c.w8_gate
+            lib.qfm_set_hbm_budget(used + plan + (256 << 20))
+            qfm.check(lib.qfm_expcache_init(C.byref(c), C.byref(st.st), LAYER, slots, modes), "init within budget")
+            took = fr0 - _free_bytes(lib)[0]
+            _say("  preflight modes", modes, "slots", slots, "priced", plan, "allocated", took)
+            assert plan * 0.99 <= took <= plan + (64 << 20), (plan, took)
+            lib.qf4_expcache_free(C.byref(c))
+        # a whole synthetic layer is priced first as well
+        fr0, tot = _free_bytes(lib)
+        lib.qfm_set_hbm_budget(tot - fr0 + (64 << 20))
+        sl = qfm.QfmSynthLayer()
+        assert lib.qfm_synth_layer_create(C.byref(sl), qfm.QFM_FMT_INT8, SEED, LAYER, 0, s.h) == -4
+        assert "nothing allocated" in lib.qfm_last_error().decode()
+        assert abs(_free_bytes(lib)[0] - fr0) <= (8 << 20)
+    finally:
+        lib.qfm_set_hbm_budget(old)
+        s.destroy()
+
+
 # ------------------------------------------------------------------ dense quantizer
 @pytest.mark.parametrize("rows,Kd", [(512, 2048), (2048, 512), (640, 2560)])
 def test_quant_bf16_bit_exact(lib, rows, Kd):

@@ -261,3 +261,37 @@ def test_layer_preflight_names_the_bad_expert_tensor(tmp_path):
     assert lib.qfm_store_check_layer(C.byref(s.st), L) == -1
     msg = lib.qfm_last_error().decode()
     assert "L0 E311 down_proj" in msg, msg
+
+
+# ------------------------------------------------------------------ memory preflight pricing
+def test_preflight_pricing_matches_the_reference_slot_sizes():
+    """qfm_expcache_bytes / qfm_arena_bytes (priced before any allocation, the
+    reference's budget guard qf_hip4_stage.hip:792-813) against the reference's
+    own per-expert constants at 2560/640: QF5_EXP_SLOT_BYTES = 2,764,800
+    (qf_nvfp4_wave64.h:67-69), QF8_FP8_SLOT_BYTES = 3*640*2560 + 2*640*64*4
+    + 2560*64*4 (qf8_moe_fp8.h:38-39) and the INT8 slot 3*640*2560 +
+    (2*640 + 2560)*4 = 4,930,560 (qf_hip4_stage.hip:808)."""
+    lib = qfm.load()
+    qfm.init(2560, 640, 512, 10, 1, 1)
+    E, slots = 512, 192
+    nv, fp8, i8 = 2764800, 3 * 640 * 2560 + 2 * 640 * 64 * 4 + 2560 * 64 * 4, 4930560
+    routing = lambda S: E * 4 + S * 4 + S * 8 + 8 + 16 * 4 + 3 * E * 4
+    NV, I8, RING, F8 = 1, 2, 4, 8
+    assert lib.qfm_expcache_bytes(slots, NV) == slots * nv + routing(slots)
+    assert lib.qfm_expcache_bytes(slots, NV | I8) == slots * (nv + i8) + routing(slots)
+    assert lib.qfm_expcache_bytes(E, NV | I8 | RING) == 2 * nv + E * i8 + routing(E)
+    assert lib.qfm_expcache_bytes(slots, F8) == slots * fp8 + routing(slots)
+    for bad in ((slots, 0), (slots, F8 | NV), (slots, RING | NV), (0, NV), (E + 1, NV), (slots, 16)):
+        assert lib.qfm_expcache_bytes(*bad) == 0, bad
+    assert lib.qfm_arena_bytes(qfm.QFM_FMT_NVFP4) == E * nv + 3 * E * 4
+    assert lib.qfm_arena_bytes(qfm.QFM_FMT_INT8) == E * i8
+    assert lib.qfm_arena_bytes(7) == 0
+    qfm.init(2048, 512, 512, 10, 1, 1)
+    # one config-1 layer: 512 routed INT8 experts of 3,158,016 bytes; with the shared expert
+    # and the fp32 router the layer is the 1,624,256,512 bytes of the benchmark's workload
+    assert lib.qfm_arena_bytes(qfm.QFM_FMT_INT8) == 512 * 3158016
+    assert lib.qfm_arena_bytes(qfm.QFM_FMT_INT8) + 3158016 + 512 * 2048 * 4 == 1624256512
+    # the budget setter: 0 means no limit beyond the device
+    old = lib.qfm_get_hbm_budget()
+    assert lib.qfm_set_hbm_budget(123 << 20) == 0 and lib.qfm_get_hbm_budget() == 123 << 20
+    lib.qfm_set_hbm_budget(old)
