@@ -51,6 +51,16 @@ int  qf8_i8_hc_rows(float *normed, float *hc_d, float *mixed, float *inj, float 
                     const Qf8I8Mat *down, const Qf8I8Mat *inject, const Qf8I8Mat *up, int8_t *n8q, float *n8s,
                     int8_t *d8q, float *d8s, float *hcy, const float *y_prev, const float *inj_prev, int8_t *xq_out,
                     float *xs_out, int T, hipStream_t s);
+/* qf8_i8_hc_m1 (T = 1) / qf8_i8_hc_rows that also writes x_bf16 [T][H] =
+ * bf16(mixed) (round to nearest even): the input row of qfm_moe_forward /
+ * qfm_moe_forward_f32, so the fused MoE path follows the mixer with no
+ * conversion launch (the reference's experts read X8(mixed) instead,
+ * qf_hip4_stage.hip:1508-1515). Every other output as in qf8_i8_hc_m1. No
+ * counterpart in the reference. 0 or -1 / -2 / -3. */
+int  qfm_hc_premix(float *normed, float *hc_d, float *mixed, float *inj, float *R, const uint16_t *wn,
+                   const Qf8I8Mat *down, const Qf8I8Mat *inject, const Qf8I8Mat *up, int8_t *n8q, float *n8s,
+                   int8_t *d8q, float *d8s, float *hcy, const float *y_prev, const float *inj_prev, int8_t *xq_out,
+                   float *xs_out, uint16_t *x_bf16, int T, hipStream_t s);
 /* R[c][i] = fma(inj[c], y[i], R[c][i]) for the 4 streams: the MoE output
  * written back into the residual. Replaces qf8_stream_inject (qf8_dense.h:158,
  * qf8_hc.hip:99-103, :148-150). */

@@ -336,6 +336,15 @@ int qfm_workspace_view(void *ws, int M, qfm_ws_view *v);
 int qfm_moe_forward(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y,
                     void *ws, size_t ws_bytes, hipStream_t s);
 
+/* qfm_moe_forward with the engine's y contract: y[M][H] fp32, seeded (the
+ * routed experts plus the gated shared expert, as qf8_i8_down_m1 seeds y2560
+ * and qf8_i8_shexp_m1 adds to it, qf_hip4_stage.hip:1563-1571, :1626-1640),
+ * ready for qf8_stream_inject. Same kernels and routing as qfm_moe_forward;
+ * only the final store differs (fp32 instead of bf16). No counterpart in the
+ * reference (its whole layer is a sequence of the launchers above). */
+int qfm_moe_forward_f32(const qfm_layer *L, const uint16_t *x, int M, float *y,
+                        void *ws, size_t ws_bytes, hipStream_t s);
+
 /* qfm_moe_forward for callers that cannot allocate or pass a workspace (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). No counterpart in the reference. The workspace is a 2 MiB

@@ -302,24 +302,32 @@ int qfm_workspace_view(void *ws, int M, qfm_ws_view *v) {
     return 0;
 }
 
-static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
-                        int mask, hipStream_t s, bool prof = true);
+static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, float *y32, void *ws,
+                        size_t ws_bytes, int mask, hipStream_t s, bool prof = true);
 
 
 int qfm_moe_forward(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
                     hipStream_t s) {
-    return forward_impl(L, x, M, y, ws, ws_bytes, 7, s);
+    if (!y) { set_error(-1, "qfm_moe_forward: bad arguments (null y)"); return -1; }
+    return forward_impl(L, x, M, y, nullptr, ws, ws_bytes, 7, s);
+}
+
+int qfm_moe_forward_f32(const qfm_layer *L, const uint16_t *x, int M, float *y, void *ws, size_t ws_bytes,
+                        hipStream_t s) {
+    if (!y) { set_error(-1, "qfm_moe_forward_f32: bad arguments (null y)"); return -1; }
+    return forward_impl(L, x, M, nullptr, y, ws, ws_bytes, 7, s);
 }
 
 int qfm_moe_forward_sections(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
                              int mask, hipStream_t s) {
     if (M != 1 || mask < 1 || mask > 7) { set_error(-1, "qfm_moe_forward_sections: M=1 and mask 1..7 only"); return -1; }
-    return forward_impl(L, x, M, y, ws, ws_bytes, mask, s);
+    if (!y) { set_error(-1, "qfm_moe_forward_sections: bad arguments (null y)"); return -1; }
+    return forward_impl(L, x, M, y, nullptr, ws, ws_bytes, mask, s);
 }
 
-static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
-                        int mask, hipStream_t s, bool prof) {
-    if (!layer_ok(L) || !x || !y || !ws || M < 1) { set_error(-1, "qfm_moe_forward: bad arguments"); return -1; }
+static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, float *y32, void *ws,
+                        size_t ws_bytes, int mask, hipStream_t s, bool prof) {
+    if (!layer_ok(L) || !x || (!y && !y32) || !ws || M < 1) { set_error(-1, "qfm_moe_forward: bad arguments"); return -1; }
     if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) { set_error(-1, "qfm_moe_forward: workspace not 256-byte aligned"); return -1; }
     if (ws_bytes < qfm_workspace_bytes(M)) {
         set_error(-1, "qfm_moe_forward: workspace too small (%zu < %zu)", ws_bytes, qfm_workspace_bytes(M)); return -1;
@@ -328,7 +336,7 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
     if (L->sh_gate.w && g_cfg.gated && !L->sh_gate_inp) {
         set_error(-1, "qfm_moe_forward: gated shared expert needs sh_gate_inp"); return -1;
     }
-    if (M > 8) return launch_prefill(L, x, M, y, ws, g_cfg.gated, s);
+    if (M > 8) return launch_prefill(L, x, M, y, y32, ws, g_cfg.gated, s);
     const WsLayout w = ws_layout(M);
     const Cfg &c = g_cfg;
     char *b = static_cast<char *>(ws);
@@ -363,7 +371,7 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
         if (!rc && (mask & 2)) rc = launch_i8_gateup_m1(L->arena, x, nullptr, logits, sel, wts, c.K, hidden, s, sp, x16);
         if (marks) pm[2] = prof_event(s);
         if (!rc && (mask & 4))
-            rc = launch_i8_down_m1(L->arena, hidden, wts, sel, c.K, sp, g ? logits + c.E : nullptr, nullptr, y, s);
+            rc = launch_i8_down_m1(L->arena, hidden, wts, sel, c.K, sp, g ? logits + c.E : nullptr, y32, y, s);
         if (marks) { pm[3] = prof_event(s); g_prof.marks.push_back(pm); }
         return rc;
     }
@@ -371,10 +379,10 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
         float *hsh = hidden + (size_t)M * c.K * c.I;
         int rc = launch_router_shared(L->router, L->router_bias, g, sp, x, M, logits, ld, hsh, c.I, s);
         if (!rc) rc = launch_csr_forward(L->arena, L->fmt, sp, x, logits, ld, g ? 1 : 0, M, hidden, hsh, sel, wts, csr,
-                                         b + w.xh16, part, y, s);
+                                         b + w.xh16, part, y, y32, s);
         return rc;
     }
-    return launch_prefill(L, x, M, y, ws, c.gated, s);
+    return launch_prefill(L, x, M, y, y32, ws, c.gated, s);
 }
 
 int qfm_moe_forward_layers(const qfm_layer *layers, int nl, const uint16_t *x, long x_stride, int M, uint16_t *y,
@@ -500,5 +508,5 @@ int qfm_device_info(char *name, int name_len, int *n_cu, size_t *mem_bytes, int 
 // section profiler (whose event pool may create events): the no-allocation entry
 int qfm::forward_on_workspace(const qfm_layer *L, const uint16_t *x, int M, uint16_t *y, void *ws, size_t ws_bytes,
                               hipStream_t s) {
-    return forward_impl(L, x, M, y, ws, ws_bytes, 7, s, false);
+    return forward_impl(L, x, M, y, nullptr, ws, ws_bytes, 7, s, false);
 }

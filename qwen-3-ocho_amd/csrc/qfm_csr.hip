@@ -455,7 +455,7 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
 // ---- launchers -------------------------------------------------------------------
 int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,
                        int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
-                       void *xh16, float *part, uint16_t *y, hipStream_t s) {
+                       void *xh16, float *part, uint16_t *y, float *y32, hipStream_t s) {
     const int K = g_cfg.K, E = g_cfg.E, P = M * K;
     if (M < 1 || M > kMaxRows || P > kMaxPairs || E != 512) {
         set_error(-2, "csr path: needs 1 <= M <= %d, M*top_k <= %d, 512 experts", kMaxRows, kMaxPairs); return -2;
@@ -485,7 +485,7 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
                        hpair);                                                                                   \
     hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / down_rows<F, II>(), umax + (sh ? (M + 1) / 2 : 0)), b256, 0, s, wd,   \
                        a->i8s_down, bd, a->s2d_dev, hpair, wts, csr, P, part, K, sp, hsh, logits, ld, gated, M);   \
-    launch_pf_combine(part, M, K + (sh ? 1 : 0), HH, y, s)
+    launch_pf_combine(part, M, K + (sh ? 1 : 0), HH, y, y32, s)
     if (shape_2048()) {
         if (fmt == QFM_FMT_INT8) { QFM_CSR_LAUNCH(FmtI8, 2048, 512); } else { QFM_CSR_LAUNCH(FmtF4, 2048, 512); }
     } else if (shape_2560()) {

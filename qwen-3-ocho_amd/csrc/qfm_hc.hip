@@ -201,7 +201,7 @@ k_hc_up_combine(const int8_t *__restrict__ Wu, const float *__restrict__ Su, con
                 const float *__restrict__ normed, float *__restrict__ hcy, float *__restrict__ mixed,
                 int8_t *__restrict__ xq_out, float *__restrict__ xs_out, int8_t *__restrict__ d8q,
                 float *__restrict__ d8s, float *__restrict__ R, const float *__restrict__ y_prev,
-                const float *__restrict__ inj_prev) {
+                const float *__restrict__ inj_prev, uint16_t *__restrict__ xb_out) {
     constexpr int L = QF8_HCL, RS = 4 * H;
     __shared__ __align__(16) int8_t s_q[L];
     __shared__ float s_s[L / 32];
@@ -264,6 +264,7 @@ k_hc_up_combine(const int8_t *__restrict__ Wu, const float *__restrict__ Su, con
         }
         const float v = sum * 0.25f;
         mixed[t * H + j] = v;
+        if (xb_out) xb_out[t * H + j] = f32_to_bf16(v);   // the fused MoE forward's input row
         float s1;
         xq_out[t * H + j] = (int8_t)x8_code(v, s1);
         if (tid == 0) xs_out[t * (H / 32) + blockIdx.x] = s1;
@@ -321,7 +322,7 @@ static int launch_gemv(const GemvBatch &b, int maxr, const int8_t *xq, const flo
 static int hc_impl(float *normed, float *hc_d, float *mixed, float *inj, float *R, const uint16_t *wn,
                    const Qf8I8Mat *down, const Qf8I8Mat *inject, const Qf8I8Mat *up, int8_t *n8q, float *n8s,
                    int8_t *d8q, float *d8s, float *hcy, const float *y_prev, const float *inj_prev, int8_t *xq_out,
-                   float *xs_out, int T, hipStream_t s, const char *who) {
+                   float *xs_out, int T, hipStream_t s, const char *who, uint16_t *xb_out = nullptr) {
     const int H = g_cfg.H, RS = 4 * H;
     if (!normed || !hc_d || !mixed || !R || !wn || !down || !up || !n8q || !n8s || !d8q || !d8s || !hcy || !xq_out ||
         !xs_out || (inject && !inj) || (!y_prev) != (!inj_prev) || T < 1) {
@@ -356,10 +357,10 @@ static int hc_impl(float *normed, float *hc_d, float *mixed, float *inj, float *
     const dim3 g((unsigned)(H / 32), (unsigned)T);
     if (H == 2048)
         hipLaunchKernelGGL(k_hc_up_combine<2048>, g, dim3(512), 0, s, up->w, up->s, hc_d, normed, hcy, mixed, xq_out,
-                           xs_out, d8q, d8s, R, y_prev, inj_prev);
+                           xs_out, d8q, d8s, R, y_prev, inj_prev, xb_out);
     else
         hipLaunchKernelGGL(k_hc_up_combine<2560>, g, dim3(512), 0, s, up->w, up->s, hc_d, normed, hcy, mixed, xq_out,
-                           xs_out, d8q, d8s, R, y_prev, inj_prev);
+                           xs_out, d8q, d8s, R, y_prev, inj_prev, xb_out);
     return check_launch(who) ? -3 : 0;
 }
 
@@ -408,6 +409,15 @@ int qf8_i8_hc_rows(float *normed, float *hc_d, float *mixed, float *inj, float *
     if (T < 1 || T > 65535) { set_error(-1, "qf8_i8_hc_rows: T = %d", T); return -1; }
     return hc_impl(normed, hc_d, mixed, inj, R, wn, down, inject, up, n8q, n8s, d8q, d8s, hcy, y_prev, inj_prev,
                    xq_out, xs_out, T, s, "qf8_i8_hc_rows");
+}
+
+int qfm_hc_premix(float *normed, float *hc_d, float *mixed, float *inj, float *R, const uint16_t *wn,
+                  const Qf8I8Mat *down, const Qf8I8Mat *inject, const Qf8I8Mat *up, int8_t *n8q, float *n8s,
+                  int8_t *d8q, float *d8s, float *hcy, const float *y_prev, const float *inj_prev, int8_t *xq_out,
+                  float *xs_out, uint16_t *x_bf16, int T, hipStream_t s) {
+    if (T < 1 || T > 65535 || !x_bf16) { set_error(-1, "qfm_hc_premix: T = %d or no bf16 output", T); return -1; }
+    return hc_impl(normed, hc_d, mixed, inj, R, wn, down, inject, up, n8q, n8s, d8q, d8s, hcy, y_prev, inj_prev,
+                   xq_out, xs_out, T, s, "qfm_hc_premix", x_bf16);
 }
 
 int qf8_stream_inject_ex(float *R, const float *y, const float *inj, hipStream_t s) {

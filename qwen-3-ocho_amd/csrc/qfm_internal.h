@@ -73,7 +73,7 @@ int launch_i8_down_m1(const Qf4ExpCache *c, const float *hidden, const float *wt
 // [M][K+1][H] fp32; xh16 (INT8): M*H*2 + M*(H/16)*8 bytes, 16-byte aligned.
 int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,
                        int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
-                       void *xh16, float *part, uint16_t *y, hipStream_t s);
+                       void *xh16, float *part, uint16_t *y, float *y32, hipStream_t s);
 
 // The fused forward on a caller-vouched workspace, without the section
 // profiler (qfm_moe_forward minus its event marks): the no-allocation entry.
@@ -86,10 +86,13 @@ void noalloc_prepare_current_device();
 // Prefill (T > 8 rows): MFMA router + exact candidate selection, grouped
 // MFMA gate/up and down over the routing inversion, owned-partial combine.
 size_t prefill_ws_bytes(int T);
-// y[t] = sum of the S owned partial slots part[t*S + k][H] in slot order (bf16 out)
-void launch_pf_combine(const float *part, int T, int S, int H, uint16_t *y, hipStream_t s);
+// y[t] = sum of the S owned partial slots part[t*S + k][H] in slot order (bf16 out,
+// or fp32 into y32 when y32 != nullptr)
+void launch_pf_combine(const float *part, int T, int S, int H, uint16_t *y, float *y32, hipStream_t s);
 // ctr: {candidate overflows (tokens whose logits were all recomputed), gate/up items, down items}
 void prefill_ws_view(void *ws, int T, float **lg_approx, int **sel, float **wts, int **ctr);
-int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, void *ws, int gated, hipStream_t s);
+// y32 != nullptr: y is written as fp32 there instead of bf16 into y
+int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, float *y32, void *ws, int gated,
+                   hipStream_t s);
 
 }  // namespace qfm

@@ -1039,8 +1039,17 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
 
 // y[t] = sum over the K (+ shared) owned partial slots of token t, in slot
 // order; four columns per thread (16-byte loads, all S in flight together).
+// y32 != nullptr: the sums are stored as fp32 there (y is not written).
+__device__ __forceinline__ void store4(uint16_t *y, float *y32, size_t i, float a0, float a1, float a2, float a3) {
+    if (y32) {
+        *reinterpret_cast<float4 *>(y32 + i) = make_float4(a0, a1, a2, a3);
+    } else {
+        *reinterpret_cast<uint2 *>(y + i) = make_uint2((uint32_t)f32_to_bf16(a0) | ((uint32_t)f32_to_bf16(a1) << 16),
+                                                       (uint32_t)f32_to_bf16(a2) | ((uint32_t)f32_to_bf16(a3) << 16));
+    }
+}
 __global__ void __launch_bounds__(256)
-k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__restrict__ y) {
+k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__restrict__ y, float *__restrict__ y32) {
     constexpr int kMaxS = 17;
     const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;       // index of 4 outputs
     if (i4 * 4 >= (size_t)T * H) return;
@@ -1056,9 +1065,7 @@ k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__re
 #pragma unroll
     for (int k = 0; k < kMaxS; k++)
         if (k < S) { a.x += v[k].x; a.y += v[k].y; a.z += v[k].z; a.w += v[k].w; }
-    *reinterpret_cast<uint2 *>(y + t * H + c) =
-        make_uint2((uint32_t)f32_to_bf16(a.x) | ((uint32_t)f32_to_bf16(a.y) << 16),
-                   (uint32_t)f32_to_bf16(a.z) | ((uint32_t)f32_to_bf16(a.w) << 16));
+    store4(y, y32, t * H + c, a.x, a.y, a.z, a.w);
 }
 
 // The prefill form: fp16 partials (the down GEMM's epilogue rounds each to
@@ -1066,7 +1073,7 @@ k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__re
 // fp32 in slot order; four columns (8 bytes) per thread.
 __global__ void __launch_bounds__(256)
 k_pf_combine_h(const uint16_t *__restrict__ part, const int8_t *__restrict__ partk, int T, int S, int H,
-               uint16_t *__restrict__ y) {
+               uint16_t *__restrict__ y, float *__restrict__ y32) {
     constexpr int kMaxS = 17;
     const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;       // index of 4 outputs
     if (i4 * 4 >= (size_t)T * H) return;
@@ -1090,14 +1097,12 @@ k_pf_combine_h(const uint16_t *__restrict__ part, const int8_t *__restrict__ par
             for (int j = 0; j < 4; j++)
                 a[j] += (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j >> 1] >> (16 * (j & 1)))) * isc;
         }
-    *reinterpret_cast<uint2 *>(y + t * H + c) =
-        make_uint2((uint32_t)f32_to_bf16(a[0]) | ((uint32_t)f32_to_bf16(a[1]) << 16),
-                   (uint32_t)f32_to_bf16(a[2]) | ((uint32_t)f32_to_bf16(a[3]) << 16));
+    store4(y, y32, t * H + c, a[0], a[1], a[2], a[3]);
 }
 
-void launch_pf_combine(const float *part, int T, int S, int H, uint16_t *y, hipStream_t s) {
+void launch_pf_combine(const float *part, int T, int S, int H, uint16_t *y, float *y32, hipStream_t s) {
     hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)(((size_t)T * H / 4 + 255) / 256)), dim3(256), 0, s, part, T, S,
-                       H, y);
+                       H, y, y32);
 }
 
 // ---- launcher -------------------------------------------------------------------------
@@ -1125,7 +1130,8 @@ void prefill_ws_view(void *ws, int T, float **lg, int **sel, float **wts, int **
     *ctr = reinterpret_cast<int *>(b + Lw.off[kPfCtr]);   // {candidate overflows, gate/up items, down items}
 }
 
-int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, void *ws, int gated, hipStream_t s) {
+int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, float *y32, void *ws, int gated,
+                   hipStream_t s) {
     const Cfg &c = g_cfg;
     if (c.E != 512 || !(shape_2048() || shape_2560())) { set_error(-2, "prefill: unsupported shape"); return -2; }
     static_assert(kZeroRowElems >= 2560, "the zero A row must cover every K of the supported shapes");
@@ -1215,7 +1221,7 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, vo
                            hid, I, H, gd, gd, E, hid, part, partk, H, nt_dn, xsum, hsum, nt_gu, nullptr);
     }
     hipLaunchKernelGGL(k_pf_combine_h, dim3((unsigned)(((size_t)T * H / 4 + 255) / 256)), dim3(256), 0, s, part, partk,
-                       T, S, H, y);
+                       T, S, H, y, y32);
     return check_launch("prefill");
 }
 

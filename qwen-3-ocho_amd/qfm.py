@@ -173,6 +173,7 @@ _SIGS = {
     "qfm_workspace_bytes": (C.c_size_t, [C.c_int]),
     "qfm_workspace_view": (C.c_int, [vp, C.c_int, C.POINTER(QfmWsView)]),
     "qfm_moe_forward": (C.c_int, [C.POINTER(QfmLayer), vp, C.c_int, vp, vp, C.c_size_t, vp]),
+    "qfm_moe_forward_f32": (C.c_int, [C.POINTER(QfmLayer), vp, C.c_int, vp, vp, C.c_size_t, vp]),
     "qfm_moe_forward_noalloc": (C.c_int, [C.POINTER(QfmLayer), vp, C.c_int, vp, vp]),
     "qfm_moe_forward_sections": (C.c_int, [C.POINTER(QfmLayer), vp, C.c_int, vp, vp, C.c_size_t, C.c_int, vp]),
     "qfm_moe_forward_layers": (C.c_int, [C.POINTER(QfmLayer), C.c_int, vp, C.c_long, C.c_int, vp, C.c_long,
@@ -227,6 +228,7 @@ _SIGS = {
     "qf8_i8_hc_m1": (None, [vp] * 6 + [C.POINTER(Qf8I8Mat)] * 3 + [vp] * 9 + [vp]),
     "qf8_i8_hc_m1_ex": (C.c_int, [vp] * 6 + [C.POINTER(Qf8I8Mat)] * 3 + [vp] * 9 + [vp]),
     "qf8_i8_hc_rows": (C.c_int, [vp] * 6 + [C.POINTER(Qf8I8Mat)] * 3 + [vp] * 9 + [C.c_int, vp]),
+    "qfm_hc_premix": (C.c_int, [vp] * 6 + [C.POINTER(Qf8I8Mat)] * 3 + [vp] * 10 + [C.c_int, vp]),
     "qf8_stream_inject": (None, [vp, vp, vp, vp]),
     "qf8_stream_inject_ex": (C.c_int, [vp, vp, vp, vp]),
     "qf8_shexp": (None, [C.POINTER(Qf8ShexpW), vp, vp, vp, vp, vp, vp, vp]),
