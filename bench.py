@@ -406,6 +406,43 @@ def run_hc(lib, st, args, nl=48):
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
 
 
+def run_shard(lib, st, args, nl=48):
+    """One GPU's share of config 1 under the tensor-parallel decode layout:
+    every expert's intermediate dimension split 8 ways (I = 512 / 8 = 64 per
+    GPU), the router and the shared gate vector replicated; M = 1 INT8, 48
+    distinct layers, graph-replayed. The partial y of each GPU would then be
+    summed across the eight (not run: one GPU)."""
+    import qfm
+    IS = I // 8
+    qfm.init(H, IS, E, K, 1, 1)
+    try:
+        layers = [qfm.SynthLayer(qfm.QFM_FMT_INT8, 0, l, stream=st) for l in range(nl)]
+        arr = (qfm.QfmLayer * nl)(*[L.s.layer for L in layers])
+        x, y = qfm.DevBuf(nl * H * 2), qfm.DevBuf(nl * H * 2)
+        for l in range(nl):
+            qfm.check(lib.qfm_gen_input_rows(x.ptr + l * H * 2, 1, 0, 1000 + l, 0, st.h), "x")
+        wsb = lib.qfm_workspace_bytes(1)
+        ws = qfm.DevBuf(wsb)
+        st.sync()
+
+        def enq():
+            qfm.check(lib.qfm_moe_forward_layers(arr, nl, x.ptr, H, 1, y.ptr, H, ws.ptr, wsb, st.h), "shard fwd")
+        ms = time_graph(lib, st, enq, args.steps, args.warmup)
+        us = ms * 1000.0 / nl
+        nbytes = (K + 1) * (3 * H * IS + (2 * IS + H) * 4) + ROUTER_BYTES + ACT_BYTES + GATE_VEC_BYTES
+        gbs = nbytes / (us * 1e-6) / 1e9
+        log(f"tensor-parallel shard (I = {IS}) M=1: {us:.2f} us/layer, {nbytes / 1e6:.2f} MB/layer, {gbs:.0f} GB/s")
+        for L in layers:
+            L.destroy()
+    finally:
+        qfm.init(H, I, E, K, 1, 1)
+    return {"workload": f"one GPU's shard of BASELINE config 1 (expert intermediate split 8 ways: I = {IS}; "
+                        f"router replicated), M=1 INT8, {nl} distinct layers, graph", "inter": IS,
+            "us_per_layer": round(us, 3), "algorithmic_bytes_per_layer": nbytes, "launches_per_layer": 3,
+            "roofline": {"bound": "hbm", "level": "layer (router, gate/up, down)", "achieved": round(gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+
+
 def run_fp8(lib, st, args, nl=8):
     """The FP8 lane-chunk MoE (descriptor build, gate/up, down + accumulate)
     at M=1 and M=8 on fully resident FP8 arenas of nl distinct layers. Timing
@@ -547,7 +584,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 0 / M=8 INT8 / NVFP4 / prefill lines")
     ap.add_argument("--extras", default="all",
-                    help="comma list of extra lines to run: config0,m8_int8,m8_nvfp4,prefill,prefill_nvfp4,hc,fp8 "
+                    help="comma list of extra lines to run: config0,m8_int8,m8_nvfp4,prefill,prefill_nvfp4,hc,fp8,shard "
                          "(default all)")
     ap.add_argument("--store", action="store_true",
                     help="also time checkpoint ingest and the non-resident (LRU) decode path (writes ~1 GB to a temp dir)")
@@ -644,7 +681,7 @@ def main():
     cpu_info = host_cpu()
     log("host cpu", cpu_info)
     extra = {}
-    want = set(("config0,m8_int8,m8_nvfp4,prefill,prefill_nvfp4,hc,fp8" if args.extras == "all"
+    want = set(("config0,m8_int8,m8_nvfp4,prefill,prefill_nvfp4,hc,fp8,shard" if args.extras == "all"
                 else args.extras).split(","))
     if not args.no_extra:
         if "config0" in want:
@@ -665,6 +702,8 @@ def main():
             extra["hc_premixer_m1"] = run_hc(lib, st, args)
         if "fp8" in want:
             extra["fp8_lane_chunk"] = run_fp8(lib, st, args)
+        if "shard" in want:
+            extra["tp_shard_m1_int8"] = run_shard(lib, st, args)
     if args.store:
         extra["store_ingest_and_lru"] = run_store(lib, st, args)
 

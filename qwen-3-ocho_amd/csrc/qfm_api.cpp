@@ -155,7 +155,8 @@ extern "C" {
 
 int qfm_init(const qfm_config *cfg) {
     if (!cfg) { set_error(-1, "qfm_init: null config"); return -1; }
-    const bool shape = (cfg->hidden == 2048 && cfg->inter == 512) || (cfg->hidden == 2560 && cfg->inter == 640);
+    const bool shape = (cfg->hidden == 2048 && cfg->inter == 512) || (cfg->hidden == 2560 && cfg->inter == 640) ||
+                       (cfg->hidden == 2048 && cfg->inter == 64);   // the tensor-parallel shard
     const int E = cfg->n_experts;
     const bool e_ok = E == 512;   // the reference's expert count; every path is built for it
     if (!shape || !e_ok || cfg->top_k < 1 || cfg->top_k > 16 || cfg->top_k > E) {

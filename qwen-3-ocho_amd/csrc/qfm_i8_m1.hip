@@ -305,6 +305,8 @@ int launch_i8_gateup_m1(const Qf4ExpCache *c, const uint16_t *xb, const float *x
         if (xh) QFM_GU_M1(2048, 512, true); else QFM_GU_M1(2048, 512, false);
     } else if (shape_2560()) {
         if (xh) QFM_GU_M1(2560, 640, true); else QFM_GU_M1(2560, 640, false);
+    } else if (shape_shard()) {
+        if (xh) QFM_GU_M1(2048, 64, true); else QFM_GU_M1(2048, 64, false);
     } else {
         set_error(-2, "i8_gateup_m1: unsupported shape"); return -2;
     }
@@ -330,6 +332,8 @@ int launch_i8_down_m1(const Qf4ExpCache *c, const float *hidden, const float *wt
         ok = down_dispatch_nj<2048, 512, 32, kMaxJobs, 1>(nj, sh != nullptr, c, hidden, wts, sel, sp, gdot, y32, ybf, s);
     } else if (shape_2560()) {
         ok = down_dispatch_nj<2560, 640, 8, 3, 1>(nj, sh != nullptr, c, hidden, wts, sel, sp, gdot, y32, ybf, s);
+    } else if (shape_shard()) {   // 64-byte down rows: 4 lanes each
+        ok = down_dispatch_nj<2048, 64, 4, kMaxJobs, 1>(nj, sh != nullptr, c, hidden, wts, sel, sp, gdot, y32, ybf, s);
     } else {
         set_error(-2, "i8_down_m1: unsupported shape"); return -2;
     }

@@ -24,6 +24,9 @@ int preflight_device_bytes(size_t bytes, const char *who);
 // shape dispatch helpers
 inline bool shape_2048() { return g_cfg.H == 2048 && g_cfg.I == 512; }
 inline bool shape_2560() { return g_cfg.H == 2560 && g_cfg.I == 640; }
+// one GPU's share of the 8-way split of every expert's intermediate dimension
+// (2048, 512 / 8): only the M = 1 INT8 forward, the router and top-K run at it
+inline bool shape_shard() { return g_cfg.H == 2048 && g_cfg.I == 64; }
 
 // ---- launchers (defined in the .hip files) ----------------------------------
 // generator

@@ -208,6 +208,8 @@ int launch_router_shared(const float *W, const float *bias, const float *g, cons
             hipLaunchKernelGGL((k_router_shared<8, 512, 4>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
         else
             hipLaunchKernelGGL((k_router_shared<8, 512, 8>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
+    } else if (shape_shard() && M == 1 && !sh) {
+        hipLaunchKernelGGL((k_router_shared<8, 64, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
     } else if (shape_2560()) {
         if (M == 1)
             hipLaunchKernelGGL((k_router_shared<10, 640, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
