@@ -443,6 +443,52 @@ def run_shard(lib, st, args, nl=48):
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
 
 
+def run_shexp(lib, st, args, nl=48):
+    """The bf16 shared expert (qf8_shexp at one row, qf8_shexp_M at eight)
+    over nl distinct bf16 weight sets, graph-captured. Algorithmic bytes: the
+    gate, up and down matrices and the gate vector once per launch pair, plus
+    the fp32 x, eg, eu, g1, ed and y rows each launch reads or writes."""
+    import qfm
+    wb = []
+    for l in range(nl):
+        t = {}
+        for j, (nm, n) in enumerate((("g", I * H), ("u", I * H), ("d", H * I), ("i", H))):
+            t[nm] = qfm.DevBuf(n * 2)
+            qfm.check(lib.qfm_gen_fill(t[nm].ptr, qfm.GEN_GAUSS_BF16, 0, n, 5, 4000 + l, 51 + j, 0.03, st.h), nm)
+        t["w"] = qfm.Qf8ShexpW(t["g"].ptr, t["u"].ptr, t["d"].ptr, t["i"].ptr)
+        wb.append(t)
+    out = {}
+    for M in (1, 8):
+        x, y = qfm.DevBuf(M * H * 4), qfm.DevBuf(M * H * 4)
+        qfm.check(lib.qfm_gen_fill(x.ptr, qfm.GEN_GAUSS_F32, 0, M * H, 5, 2, 3, 1.0, st.h), "x")
+        qfm.check(lib.qfm_fill_f32(y.ptr, M * H, 0.0, st.h), "y")
+        eg, eu, g1, ed = qfm.DevBuf(M * I * 4), qfm.DevBuf(M * I * 4), qfm.DevBuf(M * 4), qfm.DevBuf(M * H * 4)
+        st.sync()
+
+        def enq():
+            for t in wb:
+                if M == 1:
+                    qfm.check(lib.qf8_shexp_ex(C.byref(t["w"]), x.ptr, eg.ptr, eu.ptr, g1.ptr, ed.ptr, y.ptr,
+                                               st.h), "shexp")
+                else:
+                    qfm.check(lib.qf8_shexp_M_ex(C.byref(t["w"]), x.ptr, M, eg.ptr, eu.ptr, g1.ptr, ed.ptr, y.ptr,
+                                                 I, H, st.h), "shexp_M")
+        ms = time_graph(lib, st, enq, args.steps, args.warmup)
+        us = ms * 1000.0 / nl
+        nbytes = (3 * I * H * 2 + H * 2                      # gate, up, down, gate vector (bf16)
+                  + M * (H * 4 + 2 * I * 4 + 4)              # launch 1: x in; eg, eu, g1 out
+                  + M * (I * 4 + 4 + H * 4 + H * 8))         # launch 2: eg, g1 in; ed out; y read + written
+        gbs = nbytes / (us * 1e-6) / 1e9
+        log(f"bf16 shared expert M={M}: {us:.2f} us/layer, {nbytes / 1e6:.2f} MB/layer, {gbs:.0f} GB/s")
+        out[f"M{M}"] = {"us_per_layer": round(us, 3), "algorithmic_bytes_per_layer": nbytes, "launches_per_layer": 2,
+                        "roofline": {"bound": "hbm", "level": "layer (k_shexp_gu, k_shexp_down)",
+                                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+    out["workload"] = (f"bf16 shared expert qf8_shexp / qf8_shexp_M (H={H}, I={I}), fp32 x and y, "
+                       f"{nl} distinct weight sets, graph")
+    return out
+
+
 def run_fp8(lib, st, args, nl=8):
     """The FP8 lane-chunk MoE (descriptor build, gate/up, down + accumulate)
     at M=1 and M=8 on fully resident FP8 arenas of nl distinct layers. Timing
@@ -584,7 +630,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 0 / M=8 INT8 / NVFP4 / prefill lines")
     ap.add_argument("--extras", default="all",
-                    help="comma list of extra lines to run: config0,m8_int8,m8_nvfp4,prefill,prefill_nvfp4,hc,fp8,shard "
+                    help="comma list of extra lines to run: config0,m8_int8,m8_nvfp4,prefill,prefill_nvfp4,hc,fp8,shard,shexp "
                          "(default all)")
     ap.add_argument("--store", action="store_true",
                     help="also time checkpoint ingest and the non-resident (LRU) decode path (writes ~1 GB to a temp dir)")
@@ -681,7 +727,7 @@ def main():
     cpu_info = host_cpu()
     log("host cpu", cpu_info)
     extra = {}
-    want = set(("config0,m8_int8,m8_nvfp4,prefill,prefill_nvfp4,hc,fp8,shard" if args.extras == "all"
+    want = set(("config0,m8_int8,m8_nvfp4,prefill,prefill_nvfp4,hc,fp8,shard,shexp" if args.extras == "all"
                 else args.extras).split(","))
     if not args.no_extra:
         if "config0" in want:
@@ -704,6 +750,8 @@ def main():
             extra["fp8_lane_chunk"] = run_fp8(lib, st, args)
         if "shard" in want:
             extra["tp_shard_m1_int8"] = run_shard(lib, st, args)
+        if "shexp" in want:
+            extra["shexp_bf16"] = run_shexp(lib, st, args)
     if args.store:
         extra["store_ingest_and_lru"] = run_store(lib, st, args)
 
