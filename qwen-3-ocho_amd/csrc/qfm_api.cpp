@@ -113,7 +113,7 @@ static WsLayout ws_layout(int M) {
     w.sel = off;    off += align256((size_t)M * c.K * sizeof(int));
     w.wts = off;    off += align256((size_t)M * c.K * sizeof(float));
     w.hidden = off; off += align256((size_t)M * (c.K + 1) * c.I * sizeof(float));
-    w.csr = off;    off += align256((size_t)(3 * M * c.K + 2) * sizeof(int));
+    w.csr = off;    off += align256((size_t)csr_ints(M * c.K) * sizeof(int));
     w.xh16 = off;   off += align256((size_t)M * c.H * 2 + (size_t)M * (c.H / 16) * 8);   // fp16 activations + chunk scales
     w.part = off;   off += align256((size_t)M * (c.K + 1) * c.H * sizeof(float));   // K routed + shared slots
     w.total = off;

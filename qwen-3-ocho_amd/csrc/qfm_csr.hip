@@ -144,7 +144,8 @@ __device__ __forceinline__ void csr_build_lds(CsrLds &c, int M, int K) {
 }
 
 // ---- top-K of all rows + routing inversion: one block, one wave per row ---------
-// Published: sel/wts [M][K]; csr = {n_exp, exp_id[P], exp_ptr[P+1], pair[P]}.
+// Published: sel/wts [M][K]; csr = {n_exp, exp_id[P], exp_ptr[P+1], pair[P]}
+// and the per-slot descriptors at csr_desc_off(P).
 // With xh != nullptr, threads [kTopkThreads, blockDim.x) meanwhile write the
 // activations x [M][H] (bf16) as scaled fp16 chunks for the INT8 dot:
 // xh [M][H] fp16, xci [M][H/16] = (seed, 2^-k) of each 16-value chunk.
@@ -186,6 +187,14 @@ k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, i
     }
     for (int i = threadIdx.x; i <= P; i += blockDim.x) g_csr[1 + P + i] = c.exp_ptr[i];
     if (threadIdx.x == 0) g_csr[0] = c.n_exp;
+    for (int u = threadIdx.x; u < P; u += blockDim.x) {
+        int4 d = make_int4(-1, P, 0, 0);
+        if (u < c.n_exp) {
+            const int p0 = c.exp_ptr[u], np = c.exp_ptr[u + 1] - p0;
+            d = make_int4(c.exp_id[u], p0 | (np << 16), c.pair[p0], np > 1 ? c.pair[p0 + 1] : 0);
+        }
+        reinterpret_cast<int4 *>(g_csr + csr_desc_off(P))[u] = d;
+    }
 }
 
 // ---- gate/up: one distinct expert per blockIdx.y ---------------------------------
@@ -222,10 +231,15 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
     __shared__ uint4 s_x[PG * XQ];
     __shared__ float2 s_ci[I8 ? PG * NCH : 1];
     const int u = blockIdx.y;
-    const int n_exp = g_csr[0];
-    if (u >= n_exp) return;
-    const int *exp_ptr = g_csr + 1 + P, *pair = g_csr + 1 + P + P + 1;
-    const int e = g_csr[1 + u], p0 = exp_ptr[u], np = exp_ptr[u + 1] - p0;
+    const int4 dsc = reinterpret_cast<const int4 *>(g_csr + csr_desc_off(P))[u];   // one load before any weight
+    // keep the descriptor one 16-byte load and the weight bases loaded before the
+    // branch (the compiler otherwise sinks each field, and each kernel argument,
+    // below the branch that first needs it: a dependent round trip apiece)
+    asm volatile("" ::"s"(dsc.x), "s"(dsc.y), "s"(dsc.z), "s"(dsc.w), "s"(Wg), "s"(Wu));
+    const int e = dsc.x;
+    if (e < 0) return;                           // past the last distinct expert
+    const int p0 = dsc.y & 0xFFFF, np = dsc.y >> 16;
+    const int *pair = g_csr + 1 + P + P + 1;
     const int l = threadIdx.x % LPR;
     const int row = blockIdx.x * RPB + threadIdx.x / LPR;
     const size_t roff = ((size_t)e * I + row) * ROWB;
@@ -256,7 +270,8 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
         // straight into LDS (global_load_lds: lane i of a wave load writes base + 16 i / 4 i)
         for (int k = wave; k < ng * (XQ / 64); k += 4) {
             const int j = k / (XQ / 64), c = k - j * (XQ / 64);
-            __builtin_amdgcn_global_load_lds(src + (size_t)(pair[p0 + j0 + j] / K) * XQ + c * 64 + lane,
+            const int pr = j0 + j == 0 ? dsc.z : j0 + j == 1 ? dsc.w : pair[p0 + j0 + j];
+            __builtin_amdgcn_global_load_lds(src + (size_t)(pr / K) * XQ + c * 64 + lane,
                                              (__attribute__((address_space(3))) void *)(s_x + j * XQ + c * 64), 16, 0, 0);
         }
         if constexpr (I8) {
@@ -264,7 +279,8 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
             const uint32_t *cs = reinterpret_cast<const uint32_t *>(xci);
             for (int k = wave; k < ng * CW; k += 4) {
                 const int j = k / CW, c = k - j * CW;
-                __builtin_amdgcn_global_load_lds(cs + (size_t)(pair[p0 + j0 + j] / K) * NCH * 2 + c * 64 + lane,
+                const int pr = j0 + j == 0 ? dsc.z : j0 + j == 1 ? dsc.w : pair[p0 + j0 + j];
+                __builtin_amdgcn_global_load_lds(cs + (size_t)(pr / K) * NCH * 2 + c * 64 + lane,
                                                  (__attribute__((address_space(3))) void *)(reinterpret_cast<uint32_t *>(s_ci) + j * NCH * 2 + c * 64), 4, 0, 0);
             }
         }
@@ -401,10 +417,12 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
         return;
     }
     const int u = blockIdx.y - nsh;
-    const int n_exp = g_csr[0];
-    if (u >= n_exp) return;
-    const int *exp_id = g_csr + 1, *exp_ptr = g_csr + 1 + P, *pair = g_csr + 1 + P + P + 1;
-    const int e = exp_id[u], p0 = exp_ptr[u], np = exp_ptr[u + 1] - p0;
+    const int4 dsc = reinterpret_cast<const int4 *>(g_csr + csr_desc_off(P))[u];   // one load before any weight
+    asm volatile("" ::"s"(dsc.x), "s"(dsc.y), "s"(Wd));   // as in k_csr_gateup
+    const int e = dsc.x;
+    if (e < 0) return;                           // past the last distinct expert
+    const int p0 = dsc.y & 0xFFFF, np = dsc.y >> 16;
+    const int *pair = g_csr + 1 + P + P + 1;
     const int l = threadIdx.x % LPR, grp = threadIdx.x / LPR;
     // weights for this thread's rows first (ROWS/GROUPS rows per group)
     constexpr int RPG = ROWS / GROUPS;

@@ -72,8 +72,15 @@ int launch_i8_down_m1(const Qf4ExpCache *c, const float *hidden, const float *wt
 // partials per (expert, row block) with the shared expert's down in the first
 // grid rows (k_csr_down), combine (k_pf_combine). fmt: QFM_FMT_INT8 or
 // QFM_FMT_NVFP4 for the routed experts. hsh: shared hidden [M][I] (from
-// launch_router_shared); csr: 3*M*K+2 ints; hpair: [M*K][I] fp32; part:
+// launch_router_shared); csr: csr_ints(M*K) ints, 16-byte aligned; hpair: [M*K][I] fp32; part:
 // [M][K+1][H] fp32; xh16 (INT8): M*H*2 + M*(H/16)*8 bytes, 16-byte aligned.
+// The csr buffer of P = M*K pairs: {n_exp, exp_id[P], exp_ptr[P+1], pair[P]}
+// followed, at the next multiple of 4 ints, by one 4-int descriptor per
+// distinct-expert slot u < P: {expert id or -1 past the last, p0 | np << 16,
+// first pair, second pair}, so a gate/up or down block finds everything it
+// needs to start its loads with one 16-byte load.
+__host__ __device__ constexpr int csr_desc_off(int P) { return (3 * P + 2 + 3) & ~3; }
+__host__ __device__ constexpr int csr_ints(int P) { return csr_desc_off(P) + 4 * P; }
 int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,
                        int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
                        void *xh16, float *part, uint16_t *y, float *y32, hipStream_t s);
