@@ -235,7 +235,7 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
     // keep the descriptor one 16-byte load and the weight bases loaded before the
     // branch (the compiler otherwise sinks each field, and each kernel argument,
     // below the branch that first needs it: a dependent round trip apiece)
-    asm volatile("" ::"s"(dsc.x), "s"(dsc.y), "s"(dsc.z), "s"(dsc.w), "s"(Wg), "s"(Wu));
+    args_now(dsc.x, dsc.y, dsc.z, dsc.w, Wg, Wu);
     const int e = dsc.x;
     if (e < 0) return;                           // past the last distinct expert
     const int p0 = dsc.y & 0xFFFF, np = dsc.y >> 16;
@@ -418,7 +418,7 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
     }
     const int u = blockIdx.y - nsh;
     const int4 dsc = reinterpret_cast<const int4 *>(g_csr + csr_desc_off(P))[u];   // one load before any weight
-    asm volatile("" ::"s"(dsc.x), "s"(dsc.y), "s"(Wd));   // as in k_csr_gateup
+    args_now(dsc.x, dsc.y, Wd);                  // as in k_csr_gateup
     const int e = dsc.x;
     if (e < 0) return;                           // past the last distinct expert
     const int p0 = dsc.y & 0xFFFF, np = dsc.y >> 16;

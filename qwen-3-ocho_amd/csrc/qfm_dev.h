@@ -154,6 +154,17 @@ __device__ __forceinline__ void wave_row_to_f16(const uint16_t *__restrict__ x, 
     if (lane == 0) *info = make_float2(hs, __uint_as_float((uint32_t)(127 - k) << 23));
 }
 
+// Kernel arguments are read through the scalar cache on first use, and the
+// compiler places each argument's load below the first branch that needs it:
+// a kernel whose arguments span several 64-byte lines can then take one
+// dependent scalar-cache miss per line before its first memory load.
+// args_now(...) makes every value given live in SGPRs at that point, so all
+// the lines are requested together (one miss).
+template <typename T>
+__device__ __forceinline__ void arg_now(const T &v) { asm volatile("" ::"s"(v)); }
+template <typename... T>
+__device__ __forceinline__ void args_now(const T &...v) { (arg_now(v), ...); }
+
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_nt16(const void *p) {
     const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));

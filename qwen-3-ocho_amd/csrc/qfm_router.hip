@@ -56,6 +56,7 @@ k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, con
                 float *__restrict__ hsh, int ldh, uint4 *__restrict__ x16, float2 *__restrict__ x16i) {
     constexpr int H = NJ * 256;
     const int lane = threadIdx.x;
+    args_now(W, bias, g, sh.qg, sh.qu, sh.sg, sh.su, x, M, E, logits, ld, hsh, ldh, x16, x16i);
     if (x16 && blockIdx.x == 0) {                   // the first block: x row 0 as scaled fp16
         wave_row_to_f16<H>(x, x16, x16i, lane);
         return;
