@@ -203,6 +203,13 @@ k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, i
 template <class F, int H>
 constexpr int gateup_lpr() { return lpr_of(H / F::VPB / 16); }
 constexpr int kGateupPG = 2;   // routed activation rows staged in LDS at a time
+// threads per gate/up block (M = 8 over 48 layers, INT8 / NVFP4: 256 threads
+// 58.0 / 47.0 us per layer; 64: 66.5 / 51.1; 128: 59.8 / 48.5; 512: 58.7 / 48.1;
+// 1024: 62.0 / 52.5)
+#ifndef QFM_GU_THREADS
+#define QFM_GU_THREADS 256
+#endif
+constexpr int kGuThreads = QFM_GU_THREADS;
 // One block per (distinct expert, RPB rows), one LPR-lane group per gate/up
 // row. The row pair's weights are loaded first (the HBM stream starts at
 // once); the activation rows of the expert's pairs are staged in LDS straight
@@ -212,7 +219,7 @@ constexpr int kGateupPG = 2;   // routed activation rows staged in LDS at a time
 // slower: its registers allowed two waves per SIMD instead of four, and the
 // dot and reduction latencies then went unhidden.)
 template <class F, int H, int I>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kGuThreads)
 k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
              const float *__restrict__ Sg, const float *__restrict__ Su,          // INT8 row scales
              const uint8_t *__restrict__ Bg, const uint8_t *__restrict__ Bu,      // NVFP4 block scales
@@ -223,7 +230,8 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
     constexpr int ROWB = H / F::VPB;             // bytes per gate/up row
     constexpr int LPR = gateup_lpr<F, H>();      // lanes per row
     constexpr int NST = ROWB / (LPR * 16);
-    constexpr int RPB = 256 / LPR;               // rows per block
+    constexpr int RPB = kGuThreads / LPR;        // rows per block
+    constexpr int NW = kGuThreads / 64;          // waves per block
     constexpr int XQ = H / 8;                    // 16-byte words per staged activation row
     constexpr int NCH = H / 16;                  // 16-value chunks per row
     constexpr int PG = kGateupPG;
@@ -268,7 +276,7 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
         const int ng = min(PG, np - j0);
         if (j0 > 0) __syncthreads();             // the previous group's rows are consumed
         // straight into LDS (global_load_lds: lane i of a wave load writes base + 16 i / 4 i)
-        for (int k = wave; k < ng * (XQ / 64); k += 4) {
+        for (int k = wave; k < ng * (XQ / 64); k += NW) {
             const int j = k / (XQ / 64), c = k - j * (XQ / 64);
             const int pr = j0 + j == 0 ? dsc.z : j0 + j == 1 ? dsc.w : pair[p0 + j0 + j];
             __builtin_amdgcn_global_load_lds(src + (size_t)(pr / K) * XQ + c * 64 + lane,
@@ -277,7 +285,7 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
         if constexpr (I8) {
             constexpr int CW = NCH * 2 / 64;
             const uint32_t *cs = reinterpret_cast<const uint32_t *>(xci);
-            for (int k = wave; k < ng * CW; k += 4) {
+            for (int k = wave; k < ng * CW; k += NW) {
                 const int j = k / CW, c = k - j * CW;
                 const int pr = j0 + j == 0 ? dsc.z : j0 + j == 1 ? dsc.w : pair[p0 + j0 + j];
                 __builtin_amdgcn_global_load_lds(cs + (size_t)(pr / K) * NCH * 2 + c * 64 + lane,
@@ -498,7 +506,8 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
 #define QFM_CSR_LAUNCH(F, HH, II)                                                                                   \
     hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), dim3(xh ? 1024 : kTopkThreads), 0, s, logits, ld, M, K,          \
                        g_cfg.renorm, sel, wts, csr, x, HH, xh, xci);                                             \
-    hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(II / (256 / gateup_lpr<F, HH>()), umax), b256, 0, s,  \
+    hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(II / (kGuThreads / gateup_lpr<F, HH>()), umax),       \
+                       dim3(kGuThreads), 0, s,                                                                   \
                        wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, xh, xci, K, csr, P,  \
                        hpair);                                                                                   \
     hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / down_rows<F, II>(), umax + (sh ? (M + 1) / 2 : 0)), b256, 0, s, wd,   \

@@ -4,6 +4,9 @@
 * prefill tokens whose x row is zero: every expert is a candidate (the
   candidate-overflow fallback), ties go to the lowest expert index, and the
   workspace counter reports those tokens;
+* fork rows (M <= 8) whose experts coincide, all rows on the same ten experts
+  or a mix of shared and private ones (each distinct expert's pair range
+  staged past its first two rows);
 * prefill selection on constructed near-ties: router rows whose bf16 roundings
   coincide, so the MFMA logits cannot order them and only the exact
   recomputation does;
@@ -147,6 +150,41 @@ def test_prefill_tile_boundaries(lib, T, fmt):
     assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
     rel = max(_rel(g["y"][t], r["y"][t]) for t in range(T))
     _say("  max rel err", rel, "counters", g["counters"])
+    assert rel <= TOL
+    L.destroy()
+    st.destroy()
+
+
+# ------------------------------------------------------------------ fork rows sharing experts
+@pytest.mark.parametrize("M,fmt,boost", [(2, 0, 64.0), (8, 0, 64.0), (8, 1, 64.0), (8, 0, 1.5), (5, 1, 1.5)])
+def test_fork_rows_sharing_experts(lib, M, fmt, boost):
+    """Fork rows (M <= 8) whose experts coincide: a router bias of +boost on
+    experts 100..109 sends every row to exactly those ten (boost 64: each
+    distinct expert carries all M rows, so the gate/up blocks stage rows past
+    the first two of their pair range) or makes them likely without forcing
+    them (boost 1.5 against logits of spread ~0.9: a mix of shared and
+    private experts). Routing bit-exact,
+    every row's y against the grouped fp64 oracle with the same bias."""
+    seed, layer, xl = 6, 27, 93
+    _say("fork rows sharing experts M", M, "fmt", fmt, "boost", boost)
+    qfm.init(H, I, E, K, 1, 1)
+    st = qfm.Stream()
+    L = qfm.SynthLayer(fmt, seed, layer, with_bias=True, stream=st)
+    st.sync()
+    forced = boost >= 32
+    bias = np.full(E, -64.0, np.float32) if forced else np.zeros(E, np.float32)
+    bias[100:110] = boost + np.arange(10, dtype=np.float32) * (0.25 if forced else 0.0)
+    qfm.check(lib.qfm_memcpy_h2d(L.s.layer.router_bias, bias.ctypes.data, bias.nbytes), "bias")
+    x = orc.fill("gauss_bf16", seed, xl, orc.T_X, 0, M * H).reshape(M, H)
+    g = _forward(lib, L.s.layer, x, st)
+    r = orc.moe_layer_grouped(H, I, E, K, M, seed, layer, xl, use_bias=1, x=x, fmt=fmt, bias=bias)
+    assert np.array_equal(g["sel"], r["sel"])
+    if forced:
+        assert (np.sort(g["sel"], axis=1) == np.arange(100, 110)).all()
+    shared = len(np.unique(g["sel"]))
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    rel = max(_rel(g["y"][t], r["y"][t]) for t in range(M))
+    _say("  distinct experts", shared, "of", M * K, "max rel err", rel)
     assert rel <= TOL
     L.destroy()
     st.destroy()
