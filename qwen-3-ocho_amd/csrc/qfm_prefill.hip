@@ -723,7 +723,7 @@ __global__ void __launch_bounds__(1024)
 k_pf_plan(int *__restrict__ blk, int nblk, int E, int has_sh, int T, int nt_gu, int nt_dn, int *__restrict__ off,
           int4 *__restrict__ items_gu, int4 *__restrict__ items_dn, int *__restrict__ n_items, int max_gu,
           int max_dn) {
-    __shared__ int s_cnt[1024], s_mt[1024], sa[1024], sb[1024];
+    __shared__ int s_cnt[1024], s_mt[1024], s_off[1024], sa[1024], sb[1024];
     const int G = E + (has_sh ? 1 : 0);
     const int g = threadIdx.x;
     int c = 0;
@@ -756,22 +756,32 @@ k_pf_plan(int *__restrict__ blk, int nblk, int E, int has_sh, int T, int nt_gu, 
     }
     s_cnt[g] = c;
     s_mt[g] = sb[g] - mt;                        // exclusive: first m-tile of group g
+    s_off[g] = sa[g] - c;                        // exclusive: first pair of group g
     if (g <= G) off[g] = sa[g] - c;              // groups >= G are empty: off[G] = all pairs
     __syncthreads();
     const int mtot = s_mt[G];
     if (g == 0) { n_items[0] = mtot * nt_gu; n_items[1] = mtot * nt_dn; }
-    // one thread per m-tile: its group (one search), then its n-tiles' items of both lists
+    // one thread per m-tile: its group (one search), then its n-tiles' items of
+    // both lists, each stored at the index of the GEMM block that runs it (the
+    // inverses of xcd_tile_contig and xcd_tile), as {group, first pair, rows,
+    // n-tile}: a GEMM block then needs one load to know its tile
+    const int cgu = (mtot + 7) >> 3;             // gate/up: m-tiles per XCD
     for (int m = g; m < mtot; m += 1024) {
         int lo = 0, hi = G - 1;                      // last group whose first m-tile is <= m
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
             if (s_mt[mid] <= m) lo = mid; else hi = mid - 1;
         }
-        const int row0 = (m - s_mt[lo]) * BM, rows = min(BM, s_cnt[lo] - row0);
-        for (int n = 0; n < nt_gu; n++)
-            if (m * nt_gu + n < max_gu) items_gu[m * nt_gu + n] = make_int4(lo, row0, rows, n);
-        for (int n = 0; n < nt_dn; n++)
-            if (m * nt_dn + n < max_dn) items_dn[m * nt_dn + n] = make_int4(lo, row0, rows, n);
+        const int row0 = (m - s_mt[lo]) * BM, rows = min(BM, s_cnt[lo] - row0), pb = s_off[lo] + row0;
+        const int xg = m / cgu, mlg = m - xg * cgu;
+        for (int n = 0; n < nt_gu; n++) {
+            const int b = ((mlg * nt_gu + n) << 3) | xg;
+            if (b < max_gu) items_gu[b] = make_int4(lo, pb, rows, n);
+        }
+        for (int n = 0; n < nt_dn; n++) {
+            const int b = (((m >> 3) * nt_dn + n) << 3) | (m & 7);
+            if (b < max_dn) items_dn[b] = make_int4(lo, pb, rows, n);
+        }
     }
 }
 
@@ -824,8 +834,7 @@ using GemmEngine = std::conditional_t<MODE == kDownI8, DownEngineI8,
 template <bool GATEUP, int MODE>
 __global__ void __launch_bounds__(GemmEngine<MODE>::NT)
 __attribute__((amdgpu_waves_per_eu(GemmEngine<MODE>::WavesPerSimd, GemmEngine<MODE>::WavesPerSimd)))
-k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int which, const int *__restrict__ off,
-          const int *__restrict__ p_tok, const int *__restrict__ p_slot, const float *__restrict__ p_wt,
+k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int which, const int *__restrict__ p_tok, const int *__restrict__ p_slot, const float *__restrict__ p_wt,
           const uint16_t *__restrict__ A, int Kdim, int Nrows, GroupW g0, GroupW g1, int E,
           uint16_t *__restrict__ hid, uint16_t *__restrict__ part, int8_t *__restrict__ partk, int Hout, int ntiles,
           const float *__restrict__ xsum, float *__restrict__ hsum, int nt_gu, const float *__restrict__ xisc) {
@@ -842,16 +851,19 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     __shared__ float rsum[BM], rscl[H16 ? BM : 1], hpart[WN][BM];
     __shared__ int rslot[GATEUP ? 1 : BM];          // down: the owned partial slot of each row
     __shared__ float rwt[GATEUP ? 1 : BM];          // down: the routing weight of each row
+    // the tile count and this block's item (stored at the block's index by
+    // k_pf_plan) as two independent loads ahead of the first branch
+    const int nit = n_items[which];
+    const int4 it = items[blockIdx.x];
+    args_now(nit, it.x, it.y, it.z, it.w);
     int mi, ni;
     if constexpr (GATEUP) {
-        if (!xcd_tile_contig(blockIdx.x, ntiles, n_items[which] / ntiles, mi, ni)) return;
+        if (!xcd_tile_contig(blockIdx.x, ntiles, nit / ntiles, mi, ni)) return;
     } else {
         xcd_tile(blockIdx.x, ntiles, mi, ni);
-        if (mi * ntiles >= n_items[which]) return;
+        if (mi * ntiles >= nit) return;
     }
-    const int4 it = items[mi * ntiles + ni];
-    const int grp = it.x, r0 = it.y, rows = it.z, nt = it.w;
-    const int pbase = off[grp] + r0;
+    const int grp = it.x, pbase = it.y, rows = it.z, nt = it.w;
     const bool f4 = F4 && grp < E;
     const size_t rowb = f4 ? (size_t)Kdim / 2 : (size_t)Kdim;       // weight row bytes
     const int8_t *Wb, *Wb2 = nullptr;
@@ -1209,15 +1221,15 @@ int launch_prefill(const qfm_layer *L, const uint16_t *x, int T, uint16_t *y, fl
     const dim3 g_gu((unsigned)(max_mt * nt_gu)), g_dn((unsigned)(max_mt * nt_dn)),
         nth(f4 ? ExpertEngineF4::NT : ExpertEngine::NT), nth_dn(f4 ? ExpertEngineF4::NT : DownEngineI8::NT);
     if (f4) {
-        hipLaunchKernelGGL((k_pf_gemm<true, kRoutedF4>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, off, p_tok, p_slot,
+        hipLaunchKernelGGL((k_pf_gemm<true, kRoutedF4>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, p_tok, p_slot,
                            p_wt, x, H, I, gg, gu, E, hid, part, partk, H, nt_gu, xsum, hsum, nt_gu, nullptr);
-        hipLaunchKernelGGL((k_pf_gemm<false, kRoutedF4>), g_dn, nth, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot,
+        hipLaunchKernelGGL((k_pf_gemm<false, kRoutedF4>), g_dn, nth, 0, s, items_dn, ctr + 1, 1, p_tok, p_slot,
                            p_wt, hid, I, H, gd, gd, E, hid, part, partk, H, nt_dn, xsum, hsum, nt_gu, nullptr);
     } else {
-        hipLaunchKernelGGL((k_pf_gemm<true, kAllI8>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, off, p_tok, p_slot, p_wt,
+        hipLaunchKernelGGL((k_pf_gemm<true, kAllI8>), g_gu, nth, 0, s, items_gu, ctr + 1, 0, p_tok, p_slot, p_wt,
                            reinterpret_cast<const uint16_t *>(x16), H, I, gg, gu, E, hid, part, partk, H, nt_gu, x16sum, hsum,
                            nt_gu, x16isc);
-        hipLaunchKernelGGL((k_pf_gemm<false, kDownI8>), g_dn, nth_dn, 0, s, items_dn, ctr + 1, 1, off, p_tok, p_slot, p_wt,
+        hipLaunchKernelGGL((k_pf_gemm<false, kDownI8>), g_dn, nth_dn, 0, s, items_dn, ctr + 1, 1, p_tok, p_slot, p_wt,
                            hid, I, H, gd, gd, E, hid, part, partk, H, nt_dn, xsum, hsum, nt_gu, nullptr);
     }
     hipLaunchKernelGGL(k_pf_combine_h, dim3((unsigned)(((size_t)T * H / 4 + 255) / 256)), dim3(256), 0, s, part, partk,

@@ -22,8 +22,8 @@ enum PfRegion {
     kPfCtr,       // int [8] {candidate overflows, gate/up items, down items, ...}
     kPfOff,       // int [E + 2] group offsets
     kPfBlk,       // int [nblk][E] per counting block histograms
-    kPfItemsGu,   // int4 [max_mt * nt_gu] gate/up work items
-    kPfItemsDn,   // int4 [max_mt * nt_dn] down work items
+    kPfItemsGu,   // int4 [max_mt * nt_gu] gate/up work items, each at the index of the block that runs it
+    kPfItemsDn,   // int4 [max_mt * nt_dn] down work items, likewise
     kPfTok,       // int [P] pair -> token
     kPfSlot,      // int [P] pair -> partial slot
     kPfPwt,       // fp32 [P] pair weight
