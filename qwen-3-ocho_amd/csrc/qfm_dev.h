@@ -94,25 +94,42 @@ __device__ __forceinline__ float2 chunk16_to_f16(const float *v, uint4 &ha, uint
 }
 
 // ---- hidden rows staged in LDS as scaled fp16 chunks ---------------------------
-// rows h[0..n) of I fp32 values (contiguous), one 16-value chunk per thread and
-// pass of an NT-thread block: s_h16 two 16-byte words per chunk, s_hci its
-// (seed, 2^-k) (chunk16_to_f16)
-template <int I, int NT = 256>
-__device__ __forceinline__ void stage_h16(const float *__restrict__ h, int n, uint4 *s_h16, float2 *s_hci) {
-    for (int c = threadIdx.x; c < n * (I / 16); c += NT) {
-        const float4 *hp = reinterpret_cast<const float4 *>(h) + 4 * c;
-        float v[16];
+// Rows h[0..n) (n <= RMAX) of I fp32 values (contiguous), one 16-value chunk
+// per thread and pass of an NT-thread block: s_h16 two 16-byte words per
+// chunk, s_hci its (seed, 2^-k) (chunk16_to_f16). In two halves, so the loads
+// can be issued ahead of others whose data arrives later (loads retire in
+// issue order): load() into registers, then store() converts and writes LDS.
+template <int I, int RMAX, int NT = 256>
+struct H16Stage {
+    static constexpr int CPT = (RMAX * (I / 16) + NT - 1) / NT;   // chunks per thread
+    float v[CPT][16];
+    __device__ __forceinline__ void load(const float *__restrict__ h, int n) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 f = hp[q];
-            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+        for (int q = 0; q < CPT; q++) {
+            const int c = (int)threadIdx.x + q * NT;
+            if (c < n * (I / 16)) {
+                const float4 *hp = reinterpret_cast<const float4 *>(h) + 4 * c;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float4 f = hp[j];
+                    v[q][4 * j] = f.x; v[q][4 * j + 1] = f.y; v[q][4 * j + 2] = f.z; v[q][4 * j + 3] = f.w;
+                }
+            }
         }
-        uint4 ha, hb;
-        s_hci[c] = chunk16_to_f16(v, ha, hb);
-        s_h16[2 * c] = ha;
-        s_h16[2 * c + 1] = hb;
     }
-}
+    __device__ __forceinline__ void store(int n, uint4 *s_h16, float2 *s_hci) {
+#pragma unroll
+        for (int q = 0; q < CPT; q++) {
+            const int c = (int)threadIdx.x + q * NT;
+            if (c < n * (I / 16)) {
+                uint4 ha, hb;
+                s_hci[c] = chunk16_to_f16(v[q], ha, hb);
+                s_h16[2 * c] = ha;
+                s_h16[2 * c + 1] = hb;
+            }
+        }
+    }
+};
 // One wave converts a bf16 row of H values to fp16 scaled by 2^k (largest
 // magnitude in [2^14, 2^15): exact for bf16 values, no overflow); writes the
 // row (H / 8 16-byte words, same value order) and info = (sum of the scaled
