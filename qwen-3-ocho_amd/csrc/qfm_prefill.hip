@@ -972,27 +972,27 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
                 }
             }
         __syncthreads();
-        // TPR threads per row, each 16-byte chunks of CPT columns; the row's bf16
-        // sum (the down GEMM's offset correction) in chunk order, then over the
-        // row's threads (consecutive lanes) in a fixed order: deterministic
-        constexpr int TPR = Eng::NT / BM, CPT = HC / TPR;
-        static_assert(TPR == 4 && CPT % 8 == 0, "four threads per hidden row");
-        const int r = threadIdx.x / TPR, q = threadIdx.x % TPR;
-        float hs = 0.0f;
-        if (r < rows) {
-            uint16_t *dst = hid + (size_t)(pbase + r) * Nrows + nt * HC + q * CPT;
+        // a row's HC / 8 16-byte chunks go to consecutive lanes (one contiguous
+        // row segment per store), RPP rows per pass; the row's bf16 sum (the down
+        // GEMM's offset correction): each lane's 8 values in order, then the
+        // 16-lane reduction in its fixed order (deterministic)
+        constexpr int CPR = HC / 8, RPP = Eng::NT / CPR;
+        static_assert(CPR == 16 && BM % RPP == 0, "16 chunks per hidden row");
+        const int cch = threadIdx.x % CPR, rr = threadIdx.x / CPR;
 #pragma unroll
-            for (int c8 = 0; c8 < CPT / 8; c8++) {
-                const uint4 v = *reinterpret_cast<const uint4 *>(&ep[r * HSR + q * CPT + c8 * 8]);
-                *reinterpret_cast<uint4 *>(dst + c8 * 8) = v;
+        for (int p = 0; p < BM / RPP; p++) {
+            const int r = p * RPP + rr;
+            float hs = 0.0f;
+            if (r < rows) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(&ep[r * HSR + cch * 8]);
+                *reinterpret_cast<uint4 *>(hid + (size_t)(pbase + r) * Nrows + nt * HC + cch * 8) = v;
                 const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int j = 0; j < 4; j++) hs += bf16_lo(w[j]) + bf16_hi(w[j]);
             }
+            hs = group_sum<CPR>(hs);
+            if (cch == 0 && r < rows) hsum[(size_t)(pbase + r) * nt_gu + nt] = hs;
         }
-        hs += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, hs), 0xB1, 0xF, 0xF, false));
-        hs += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, hs), 0x4E, 0xF, 0xF, false));
-        if (q == 0 && r < rows) hsum[(size_t)(pbase + r) * nt_gu + nt] = hs;
     } else {
         // a wave's 64 columns of one row live in the 16 lanes of a row group (4
         // n-blocks each): that group of the partial row is stored as fp16 scaled
@@ -1037,10 +1037,11 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
                     mr[mb][i] = row16_max(mf);
                 }
         }
-        // pass 2: scale by 2^k, round to fp16, store (straight from the
-        // accumulators: staging the tile in LDS for 16-byte stores measured
-        // slower here, 453 -> 502 us for the INT8 down GEMM, since the stores
-        // then wait for an LDS round trip and a barrier)
+        // pass 2: scale by 2^k, round to fp16, store straight from the
+        // accumulators (the tile staged in LDS for coalesced 16-byte row stores
+        // measured 6-15 us slower per layer: the stores then wait for an LDS
+        // round trip and a barrier, and the 2-byte stores already fill 32-byte
+        // row segments)
 #pragma unroll
         for (int mb = 0; mb < MWv; mb++)
 #pragma unroll
