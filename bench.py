@@ -492,8 +492,9 @@ def run_shexp(lib, st, args, nl=48):
 def run_fp8(lib, st, args, nl=8):
     """The FP8 lane-chunk MoE (descriptor build, gate/up, down + accumulate)
     at M=1 and M=8 on fully resident FP8 arenas of nl distinct layers. Timing
-    only: the code bytes are random (the arithmetic is pinned by the GPU
-    tests), the routing is K distinct random experts per row."""
+    only: the code bytes are the generator's E4M3 bytes of U(0.25, 2) (valid
+    codes without 0x7F / 0xFF, which the packer never emits; the arithmetic is
+    pinned by the GPU tests), the routing is K distinct random experts per row."""
     import qfm
     IH = I * H
     arenas = []
@@ -501,7 +502,7 @@ def run_fp8(lib, st, args, nl=8):
         a = {}
         for nm, n in (("w8_gate", E * IH), ("w8_up", E * IH), ("w8_down", E * IH)):
             a[nm] = qfm.DevBuf(n)
-            qfm.check(lib.qfm_gen_fill(a[nm].ptr, qfm.GEN_FP4BYTE, 0, n, 6, 4000 + l, 1 + len(a), 0.0, st.h), "w8")
+            qfm.check(lib.qfm_gen_fill(a[nm].ptr, qfm.GEN_E4M3SCALE, 0, n, 6, 4000 + l, 1 + len(a), 0.0, st.h), "w8")
         for nm, n in (("sc_gate", E * I * 64), ("sc_up", E * I * 64), ("sc_down", E * H * 64)):
             a[nm] = qfm.DevBuf(n * 4)
             qfm.check(lib.qfm_fill_f32(a[nm].ptr, n, 1e-3, st.h), "sc")
@@ -546,7 +547,7 @@ def run_fp8(lib, st, args, nl=8):
         for b_ in a.values():
             b_.free()
     out["workload"] = (f"FP8 lane-chunk routed experts (qf8_fp8_build_desc / gateup / downacc), {nl} distinct "
-                       "layers, random codes (timing only), routed experts only")
+                       "layers, generated E4M3 codes (timing only), routed experts only")
     return out
 
 

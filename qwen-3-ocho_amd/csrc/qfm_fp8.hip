@@ -10,10 +10,11 @@
 // the device-side item count ctl[0] * tiles is exhausted (every wave reaches
 // that bound). An item is (descriptor, tile of output rows); the wave loads
 // all of the tile's weight chunks first (lane l owns chunk l of every row),
-// decodes them with the gfx950 E4M3 convert, then for each of the
-// descriptor's rows forms the chunk dot products, scales by the chunk scale
-// and sums across the wave (DPP). Gate/up writes silu(g) * u; down adds
-// wt * a into y with one atomic per (row, output).
+// then for each of the descriptor's rows decodes them with the gfx950 E4M3
+// convert, forms the chunk dot products, scales by the chunk scale and sums
+// the tile's outputs across the wave together (one reduce-scatter). Gate/up
+// writes silu(g) * u; down adds wt * a into y, the tile's outputs in one
+// atomic instruction (one lane per output).
 #include "qfm_internal.h"
 #include "qfm_dev.h"
 #include "../../include/qf_fp8.h"
@@ -22,8 +23,18 @@ namespace qfm {
 
 constexpr int kF8Grid = 1024;          // workgroups of the item walks (4 per CU)
 constexpr int kF8MaxExperts = 512;
-constexpr int kF8RowsGu = 4;           // gate/up output rows per item
-constexpr int kF8RowsDn = 8;           // down output rows per item
+// output rows per item, measured over 8 layers at H 2048 (M = 1 / M = 8 us per
+// layer): gate/up 2 rows and down 8 rows 25.6-25.9 / 102.5-102.7; gate/up 1
+// row 26.3-26.8 / 129-134; gate/up 4 rows 30.6-34.4 / 124-142; down 4 or 16
+// rows 26.2-29.6 / 107-118 with 2 gate/up rows
+#ifndef QFM_F8_GU_ROWS
+#define QFM_F8_GU_ROWS 2
+#endif
+#ifndef QFM_F8_DN_ROWS
+#define QFM_F8_DN_ROWS 8
+#endif
+constexpr int kF8RowsGu = QFM_F8_GU_ROWS;   // gate/up output rows per item
+constexpr int kF8RowsDn = QFM_F8_DN_ROWS;   // down output rows per item
 
 // Routing of up to kF8LdsPairs (row, k) pairs is staged in LDS; larger
 // batches are read from global memory in the same order.
@@ -118,71 +129,127 @@ __device__ __forceinline__ void f8x8(uint2 q, float *out) {
     }
 }
 
-// CH = H / 64 code bytes per lane and row (32 at H 2048, 40 at H 2560)
+// CH = H / 64 code bytes per lane and row (32 at H 2048, 40 at H 2560), loaded
+// as 16-byte words when CH allows (8-byte words otherwise)
+template <int CH>
+struct F8Row {
+    static constexpr bool W16 = CH % 16 == 0;
+    static constexpr int NQ = W16 ? CH / 16 : CH / 8;
+    uint4 q[W16 ? NQ : 1];
+    uint2 d[W16 ? 1 : NQ];
+    __device__ __forceinline__ void load(const uint8_t *p) {
+        if constexpr (W16) {
+#pragma unroll
+            for (int j = 0; j < NQ; j++) q[j] = reinterpret_cast<const uint4 *>(p)[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < NQ; j++) d[j] = reinterpret_cast<const uint2 *>(p)[j];
+        }
+    }
+    // the codes as opaque to the compiler: a decode inside a loop is then not
+    // hoisted out of it (R rows decoded at once would not fit the registers)
+    __device__ __forceinline__ void opaque() {
+        if constexpr (W16) {
+#pragma unroll
+            for (int j = 0; j < NQ; j++) asm volatile("" : "+v"(q[j].x), "+v"(q[j].y), "+v"(q[j].z), "+v"(q[j].w));
+        } else {
+#pragma unroll
+            for (int j = 0; j < NQ; j++) asm volatile("" : "+v"(d[j].x), "+v"(d[j].y));
+        }
+    }
+    __device__ __forceinline__ void decode(float *out) const {
+        if constexpr (W16) {
+#pragma unroll
+            for (int j = 0; j < NQ; j++) {
+                f8x8(make_uint2(q[j].x, q[j].y), out + 16 * j);
+                f8x8(make_uint2(q[j].z, q[j].w), out + 16 * j + 8);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NQ; j++) f8x8(d[j], out + 8 * j);
+        }
+    }
+};
+
+// gate/up: item = (descriptor, R output rows); the wave loads the R gate and
+// up rows' chunks (lane l owns bytes [l CH, l CH + CH) of each row) and their
+// chunk scales, and for each descriptor row decodes and dots them with the
+// lane's slice of x (loaded once per row, not per output row), the 2R
+// sums reduced across the wave together (reduce-scatter: lane 2 r + m holds
+// output r's gate (m = 0) or up (m = 1) sum)
 template <int CH>
 __global__ void __launch_bounds__(256)
 k_fp8_gateup(const uint8_t *__restrict__ Wg, const float *__restrict__ Sg, const uint8_t *__restrict__ Wu,
              const float *__restrict__ Su, const float *__restrict__ x, float *__restrict__ hidden,
              const Qf8MoeDesc *__restrict__ desc, const int *__restrict__ ctl, int I) {
-    constexpr int H = CH * 64, NW = CH / 8, R = kF8RowsGu;
+    constexpr int H = CH * 64, R = kF8RowsGu;
+    static_assert(2 * R <= 32 && (R & (R - 1)) == 0, "2R sums per lane, a power of two");
     const int lane = threadIdx.x & 63;
     const int tiles = I / R;
     const int total = ctl[0] * tiles;
     for (int item = blockIdx.x * 4 + (threadIdx.x >> 6); item < total; item += gridDim.x * 4) {
         const int di = item / tiles, o0 = (item % tiles) * R;
-        const int slot = desc[di].slot, nrow = desc[di].nrow;
+        const Qf8MoeDesc &D = desc[di];
+        const int slot = D.slot, nrow = D.nrow;
         const size_t wb = (size_t)slot * I * H + (size_t)o0 * H + (size_t)lane * CH;
         const size_t sb = ((size_t)slot * I + o0) * 64 + lane;
-        uint2 gq[R][NW], uq[R][NW];
+        F8Row<CH> gq[R], uq[R];
         float sg[R], su[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const uint2 *pg = reinterpret_cast<const uint2 *>(Wg + wb + (size_t)r * H);
-            const uint2 *pu = reinterpret_cast<const uint2 *>(Wu + wb + (size_t)r * H);
-#pragma unroll
-            for (int j = 0; j < NW; j++) {
-                gq[r][j] = pg[j];
-                uq[r][j] = pu[j];
-            }
+            gq[r].load(Wg + wb + (size_t)r * H);
+            uq[r].load(Wu + wb + (size_t)r * H);
             sg[r] = Sg[sb + r * 64];
             su[r] = Su[sb + r * 64];
         }
+        for (int t = 0; t < nrow; t++) {
+            const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)D.row[t] * H + (size_t)lane * CH);
+            float xv[CH];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            float gv[CH], uv[CH];
-#pragma unroll
-            for (int j = 0; j < NW; j++) {
-                f8x8(gq[r][j], gv + 8 * j);
-                f8x8(uq[r][j], uv + 8 * j);
+            for (int j = 0; j < CH / 4; j++) {
+                const float4 v = xr[j];
+                xv[4 * j] = v.x; xv[4 * j + 1] = v.y; xv[4 * j + 2] = v.z; xv[4 * j + 3] = v.w;
             }
-            for (int t = 0; t < nrow; t++) {
-                const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)desc[di].row[t] * H + (size_t)lane * CH);
-                float ag = 0.0f, au = 0.0f;
+            float s[2 * R];
 #pragma unroll
-                for (int j = 0; j < CH / 4; j++) {
-                    const float4 xv = xr[j];
-                    ag = fmaf(gv[4 * j + 3], xv.w, fmaf(gv[4 * j + 2], xv.z, fmaf(gv[4 * j + 1], xv.y, fmaf(gv[4 * j], xv.x, ag))));
-                    au = fmaf(uv[4 * j + 3], xv.w, fmaf(uv[4 * j + 2], xv.z, fmaf(uv[4 * j + 1], xv.y, fmaf(uv[4 * j], xv.x, au))));
-                }
-                const float g = group_sum<64>(ag * sg[r]), u = group_sum<64>(au * su[r]);
-                if (lane == 0) hidden[((size_t)di * QF8_FP8_MAXROW + t) * I + o0 + r] = silu(g) * u;
+            for (int r = 0; r < R; r++) {          // codes decoded per row of x (one row on average)
+                float wv[CH], ag = 0.0f, au = 0.0f;
+                gq[r].opaque();
+                uq[r].opaque();
+                gq[r].decode(wv);
+#pragma unroll
+                for (int j = 0; j < CH; j++) ag = fmaf(wv[j], xv[j], ag);
+                uq[r].decode(wv);
+#pragma unroll
+                for (int j = 0; j < CH; j++) au = fmaf(wv[j], xv[j], au);
+                s[2 * r] = ag * sg[r];
+                s[2 * r + 1] = au * su[r];
+                __builtin_amdgcn_sched_barrier(0);   // one row's decode at a time (registers)
             }
+            const float v = canon_scatter_level<2 * R, 1>(s, lane);     // lane l: sum l & (2R - 1)
+            const float u = lane_xor<1>(v);                             // the partner's (up, at odd lanes)
+            if (lane < 2 * R && (lane & 1) == 0)
+                hidden[((size_t)di * QF8_FP8_MAXROW + t) * I + o0 + (lane >> 1)] = silu(v) * u;
         }
     }
 }
 
-// CHD = I / 64 code bytes per lane and row (8 at I 512, 10 at I 640)
+// CHD = I / 64 code bytes per lane and row (8 at I 512, 10 at I 640); item =
+// (descriptor, R output rows), the R sums of a descriptor row reduced together
+// (lane r holds output r) and added into y by R lanes of one atomic instruction
 template <int CHD>
 __global__ void __launch_bounds__(256)
 k_fp8_downacc(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const float *__restrict__ hidden,
               float *__restrict__ y, const Qf8MoeDesc *__restrict__ desc, const int *__restrict__ ctl, int H) {
     constexpr int I = CHD * 64, R = kF8RowsDn;
+    static_assert(R <= 32 && (R & (R - 1)) == 0, "R sums per lane, a power of two");
     const int lane = threadIdx.x & 63;
     const int tiles = H / R;
     const int total = ctl[0] * tiles;
     for (int item = blockIdx.x * 4 + (threadIdx.x >> 6); item < total; item += gridDim.x * 4) {
         const int di = item / tiles, o0 = (item % tiles) * R;
-        const int slot = desc[di].slot, nrow = desc[di].nrow;
+        const Qf8MoeDesc &D = desc[di];
+        const int slot = D.slot, nrow = D.nrow;
         const size_t wb = (size_t)slot * H * I + (size_t)o0 * I + (size_t)lane * CHD;
         const size_t sb = ((size_t)slot * H + o0) * 64 + lane;
         float w[R][CHD], sd[R];
@@ -197,6 +264,9 @@ k_fp8_downacc(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, cons
                     const f32x2_t v = __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)p[j], false);
                     w[r][2 * j] = v.x;
                     w[r][2 * j + 1] = v.y;
+                    const uint32_t b0 = p[j] & 0xFFu, b1 = p[j] >> 8;
+                    if (__builtin_expect((b0 & 0x7Fu) == 0x7Fu, 0)) w[r][2 * j] = (b0 & 0x80u) ? -480.0f : 480.0f;
+                    if (__builtin_expect((b1 & 0x7Fu) == 0x7Fu, 0)) w[r][2 * j + 1] = (b1 & 0x80u) ? -480.0f : 480.0f;
                 }
             }
             sd[r] = Sd[sb + r * 64];
@@ -210,16 +280,18 @@ k_fp8_downacc(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, cons
                 h[2 * j] = v.x;
                 h[2 * j + 1] = v.y;
             }
-            const int yrow = desc[di].row[t];
-            const float wt = desc[di].wt[t];
+            const int yrow = D.row[t];
+            const float wt = D.wt[t];
+            float s[R];
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 float a = 0.0f;
 #pragma unroll
                 for (int j = 0; j < CHD; j++) a = fmaf(w[r][j], h[j], a);
-                a = group_sum<64>(a * sd[r]);
-                if (lane == 0) atomicAdd(&y[(size_t)yrow * H + o0 + r], wt * a);
+                s[r] = a * sd[r];
             }
+            const float a = canon_scatter_level<R, 1>(s, lane);          // lane l: output l & (R - 1)
+            if (lane < R) atomicAdd(&y[(size_t)yrow * H + o0 + lane], wt * a);
         }
     }
 }

@@ -497,6 +497,66 @@ def _desc_model(sel, wt):
     return out
 
 
+@pytest.mark.parametrize("M", [1, 5])
+def test_fp8_kernels_reference_shape_planted(lib, M):
+    """The FP8 lane-chunk kernels at the reference's own shape (H 2560, I 640:
+    40 code bytes per lane and row for gate/up, 10 for down, the down decode's
+    2-byte path) on an arena packed from random NVFP4 experts with 0x7F / 0xFF
+    codes planted (+-480 as the reference decodes them), against the fp64
+    dequantization of the same codes and scales."""
+    Hr, Ir, slots = 2560, 640, 12
+    _say("fp8 lane-chunk reference shape M", M)
+    qfm.init(Hr, Ir, E, K, 1, 1)
+    try:
+        rng = np.random.default_rng(40 + M)
+        dev, dq = {}, {}
+        for nm, snm, rows, cols in (("g", "sg", Ir, Hr), ("u", "su", Ir, Hr), ("d", "sd", Hr, Ir)):
+            w8 = np.empty((slots, rows, cols), np.uint8)
+            sc = np.empty((slots, rows, 64), np.float32)
+            for e in range(slots):
+                W = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)           # e2m1 pairs
+                S = rng.integers(0x30, 0x40, (rows, cols // 16), dtype=np.uint8)      # e4m3 block scales
+                w8[e], sc[e] = orc.fp8_pack_expert(W, S, 0.01, rows, cols)
+            flat = w8.reshape(slots, -1)
+            idx = np.arange(7, flat.shape[1], 53)
+            flat[:, idx[0::2]] = 0x7F
+            flat[:, idx[1::2]] = 0xFF
+            dev[nm], dev[snm] = qfm.DevBuf.from_array(w8), qfm.DevBuf.from_array(sc)
+            dq[nm] = [orc.fp8_dequant(w8[e], sc[e]) for e in range(slots)]
+        sel = np.stack([rng.choice(slots, K, replace=False) for _ in range(M)]).astype(np.int32)
+        wt = rng.random((M, K)).astype(np.float32)
+        x = rng.standard_normal((M, Hr)).astype(np.float32)
+        nd = min(M * K, E)
+        d_sel, d_wt, d_x = qfm.DevBuf.from_array(sel), qfm.DevBuf.from_array(wt), qfm.DevBuf.from_array(x)
+        d_desc, d_ctl = qfm.DevBuf(nd * C.sizeof(qfm.Qf8MoeDesc)), qfm.DevBuf(16)
+        d_h, d_y = qfm.DevBuf(nd * 16 * Ir * 4), qfm.DevBuf(M * Hr * 4)
+        d_y.zero()
+        s = qfm.Stream()
+        assert lib.qf8_fp8_build_desc_ex(d_sel.ptr, d_wt.ptr, M, K, 0, d_desc.ptr, d_ctl.ptr, s.h) == 0
+        assert lib.qf8_fp8_gateup_ex(dev["g"].ptr, dev["sg"].ptr, dev["u"].ptr, dev["su"].ptr, d_x.ptr, d_h.ptr,
+                                     d_desc.ptr, d_ctl.ptr, s.h) == 0
+        assert lib.qf8_fp8_downacc_ex(dev["d"].ptr, dev["sd"].ptr, d_h.ptr, d_y.ptr, d_desc.ptr, d_ctl.ptr, s.h) == 0
+        s.sync()
+        model = _desc_model(sel, wt)
+        hidden = d_h.download(np.float32, (nd, 16, Ir))
+        x64 = x.astype(np.float64)
+        y_ref = np.zeros((M, Hr))
+        for di, (e, rows, wts) in enumerate(model):
+            g = x64[rows] @ dq["g"][e].T
+            u = x64[rows] @ dq["u"][e].T
+            h = g / (1.0 + np.exp(-g)) * u
+            assert np.isfinite(hidden[di, :len(rows)]).all()
+            assert _rel(hidden[di, :len(rows)], h) <= 1e-4, (di, e)
+            y_ref[rows] += np.array(wts)[:, None] * (h @ dq["d"][e].T)
+        y = d_y.download(np.float32, (M, Hr))
+        worst = _rel(y, y_ref)
+        _say("  fp8 reference-shape y rel err", worst)
+        assert np.isfinite(y).all() and worst <= 1e-4
+        s.destroy()
+    finally:
+        qfm.init(H, I, E, K, 1, 1)
+
+
 @pytest.mark.parametrize("M,plant", [(1, False), (3, False), (8, False), (3, True)])
 def test_fp8_arena_and_kernels(lib, gen, store, xfer, M, plant):
     """plant: codes 0x7F / 0xFF written into every slot (the packer never emits
