@@ -316,7 +316,11 @@ typedef struct {
     const float       *sh_gate_inp;              /* [H] fp32 sigmoid-gate vector */
 } qfm_layer;
 
-/* Workspace for M rows (device memory, caller-owned, >= 256-byte aligned). */
+/* Workspace for M rows (device memory, caller-owned, >= 256-byte aligned).
+ * Zero it once after allocating it (qfm_dev_malloc returns zeroed memory):
+ * its first bytes hold per-row sequence tags that the M <= 8 forward keeps
+ * across calls (the same offsets for every M, so one workspace of the largest
+ * size serves calls of any M); calls that share a workspace must not overlap. */
 size_t qfm_workspace_bytes(int M);
 /* For M > 8 (prefill) logits is [M][E] of the MFMA router GEMM (the exact
  * canonical logits are computed only for the selection candidates), hidden is
@@ -424,7 +428,7 @@ int  qfm_gen_input_rows(uint16_t *x, int M, uint32_t seed, uint32_t x_layer, int
 
 /* ------------------------------------------------------------------------ */
 /* Harness utilities (thin wrappers over the HIP runtime). */
-void  *qfm_dev_malloc(size_t bytes);
+void  *qfm_dev_malloc(size_t bytes);   /* zeroed */
 int    qfm_dev_free(void *p);
 int    qfm_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int    qfm_memcpy_d2h(void *dst, const void *src, size_t bytes);

@@ -102,18 +102,28 @@ int preflight_device_bytes(size_t bytes, const char *who) {
     return 0;
 }
 
+// Every workspace starts with the M <= 8 selection tail's state, at the same
+// offsets for every M (prefill included, whose own layout follows it): ctl =
+// per-row tags (+ the timeout count), lw = [kTailRows][E] tagged logit words.
+// Zero is a valid start (tag 1 is then expected, and no word carries it); each
+// call leaves ctl[m] equal to every tag of row m's words, so a workspace that is
+// zeroed once stays valid across calls of any M.
+static size_t ws_tag_bytes() { return 256 + align256((size_t)kTailRows * g_cfg.E * 8); }
+
 struct WsLayout {
-    size_t logits, sel, wts, hidden, csr, xh16, part, total;
+    size_t ctl, lw, logits, sel, wts, hidden, csr, xh16, part, total;
 };
 static WsLayout ws_layout(int M) {
     const Cfg &c = g_cfg;
     WsLayout w{};
-    size_t off = 0;
+    w.ctl = 0;
+    w.lw = 256;
+    size_t off = ws_tag_bytes();
     w.logits = off; off += align256((size_t)M * (c.E + 1) * sizeof(float));
     w.sel = off;    off += align256((size_t)M * c.K * sizeof(int));
     w.wts = off;    off += align256((size_t)M * c.K * sizeof(float));
     w.hidden = off; off += align256((size_t)M * (c.K + 1) * c.I * sizeof(float));
-    w.csr = off;    off += align256((size_t)csr_ints(M * c.K) * sizeof(int));
+    w.csr = off;    off += align256((size_t)csr_ints(M * c.K) * sizeof(int));   // the routing launch's (NVFP4, M >= 7)
     w.xh16 = off;   off += align256((size_t)M * c.H * 2 + (size_t)M * (c.H / 16) * 8);   // fp16 activations + chunk scales
     w.part = off;   off += align256((size_t)M * (c.K + 1) * c.H * sizeof(float));   // K routed + shared slots
     w.total = off;
@@ -283,13 +293,13 @@ void qf8_i8_down_m1(const Qf4ExpCache *c, const float *hidden, int8_t *h8q, floa
 // ---- fused layer ---------------------------------------------------------------
 size_t qfm_workspace_bytes(int M) {
     if (M < 1) return 0;
-    return M <= 8 ? ws_layout(M).total : prefill_ws_bytes(M);
+    return M <= 8 ? ws_layout(M).total : ws_tag_bytes() + prefill_ws_bytes(M);
 }
 
 int qfm_workspace_view(void *ws, int M, qfm_ws_view *v) {
     if (!ws || !v || M < 1) return -1;
     if (M > 8) {
-        prefill_ws_view(ws, M, &v->logits, &v->sel, &v->wts, &v->counters);
+        prefill_ws_view(static_cast<char *>(ws) + ws_tag_bytes(), M, &v->logits, &v->sel, &v->wts, &v->counters);
         v->hidden = nullptr;
         return 0;
     }
@@ -337,7 +347,7 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
     if (L->sh_gate.w && g_cfg.gated && !L->sh_gate_inp) {
         set_error(-1, "qfm_moe_forward: gated shared expert needs sh_gate_inp"); return -1;
     }
-    if (M > 8) return launch_prefill(L, x, M, y, y32, ws, g_cfg.gated, s);
+    if (M > 8) return launch_prefill(L, x, M, y, y32, static_cast<char *>(ws) + ws_tag_bytes(), g_cfg.gated, s);
     const WsLayout w = ws_layout(M);
     const Cfg &c = g_cfg;
     char *b = static_cast<char *>(ws);
@@ -345,7 +355,6 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
     int *sel = reinterpret_cast<int *>(b + w.sel);
     float *wts = reinterpret_cast<float *>(b + w.wts);
     float *hidden = reinterpret_cast<float *>(b + w.hidden);
-    int *csr = reinterpret_cast<int *>(b + w.csr);
     float *part = reinterpret_cast<float *>(b + w.part);
     const bool has_sh = L->sh_gate.w != nullptr;
     const float *g = (has_sh && c.gated) ? L->sh_gate_inp : nullptr;
@@ -378,12 +387,28 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
     }
     if (M <= 8) {
         float *hsh = hidden + (size_t)M * c.K * c.I;
-        int rc = launch_router_shared(L->router, L->router_bias, g, sp, x, M, logits, ld, hsh, c.I, s);
+        // the router launch also ranks every row (its selection tail) and, for
+        // INT8, writes the rows as fp16 chunks for the fork-row dots
+        RouteTail tail{};
+        tail.lw = reinterpret_cast<unsigned long long *>(b + w.lw);
+        tail.ctl = reinterpret_cast<uint32_t *>(b + w.ctl);
+        tail.sel = sel;
+        tail.wts = wts;
+        if (L->fmt == QFM_FMT_INT8) {
+            tail.xh = reinterpret_cast<uint4 *>(b + w.xh16);
+            tail.xci = reinterpret_cast<float2 *>(tail.xh + (size_t)M * c.H / 8);
+        }
+        tail.K = c.K;
+        tail.renorm = c.renorm;
+        int *csr = reinterpret_cast<int *>(b + w.csr);
+        const bool routing_launch = csr_routing_for(L->fmt, M);     // (NVFP4, M >= 7: faster with it)
+        int rc = launch_router_shared(L->router, L->router_bias, g, sp, x, M, logits, ld, hsh, c.I, s, nullptr,
+                                      routing_launch ? nullptr : &tail);
         if (!rc) rc = launch_csr_forward(L->arena, L->fmt, sp, x, logits, ld, g ? 1 : 0, M, hidden, hsh, sel, wts, csr,
                                          b + w.xh16, part, y, y32, s);
         return rc;
     }
-    return launch_prefill(L, x, M, y, y32, ws, c.gated, s);
+    return launch_prefill(L, x, M, y, y32, b + ws_tag_bytes(), c.gated, s);
 }
 
 int qfm_moe_forward_layers(const qfm_layer *layers, int nl, const uint16_t *x, long x_stride, int M, uint16_t *y,
@@ -453,8 +478,10 @@ int qfm_fill_f32(float *out, uint64_t cnt, float value, hipStream_t s) { return 
 // ---- harness utilities -------------------------------------------------------------
 void *qfm_dev_malloc(size_t bytes) {
     void *p = nullptr;
-    const hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
     if (e != hipSuccess) { set_error(-4, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e)); return nullptr; }
+    e = hipMemset(p, 0, bytes ? bytes : 1);             // zeroed (a workspace must start zeroed)
+    if (e != hipSuccess) { (void)hipFree(p); set_error(-4, "hipMemset(%zu): %s", bytes, hipGetErrorString(e)); return nullptr; }
     return p;
 }
 int qfm_dev_free(void *p) { return hipFree(p) == hipSuccess ? 0 : -1; }

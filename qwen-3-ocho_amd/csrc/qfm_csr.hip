@@ -10,26 +10,36 @@
 // read once per distinct expert and dotted against all rows routed to it,
 // owned partials part[t][k][H] summed in k order (no atomics, deterministic).
 //
-// Launch sequence (all stream-ordered):
+// Launch sequence (all stream-ordered), after the router launch:
+//   pair-keyed form (INT8 at every M, NVFP4 at M <= 6): the router launch's
+//                  selection tail has written sel/wts (and, INT8, the fp16
+//                  activation chunks);
+//   CSR form (NVFP4 at M >= 7, measured faster there):
 //   k_topk_csr     one block: the top-K of all M rows (one wave per row), then
 //                  the routing inversion in LDS (per-row expert bitmaps and
 //                  their word prefix counts, P = M*K <= 128 pairs); publishes
-//                  sel/wts/CSR. For INT8 a
-//                  second set of waves meanwhile writes the activations as
-//                  scaled fp16 chunks (chunk16_to_f16).
-//   k_csr_gateup   grid (I/rows, min(M*K, E)), 256 threads: distinct expert
-//                  blockIdx.y. One lane group per gate/up row: the row pair is
-//                  loaded once, then dotted with the LDS-staged activation row
-//                  of each routed token. hidden is written per pair, in CSR
-//                  order.
-//   k_csr_down     grid (H/ROWS, min(M*K, E) + shared), 256 threads: expert
-//                  u's down rows [ROWS b, ROWS b + ROWS), pairs' hidden vectors
+//                  sel/wts/CSR. For INT8 a second set of waves meanwhile
+//                  writes the activations as scaled fp16 chunks
+//                  (chunk16_to_f16).
+//   k_csr_gateup   grid (I/rows, M*K), 256 threads. Pair-keyed: grid row y is
+//                  pair y; it works only if y is its expert's first pair, for
+//                  all of the expert's pairs (ballots over sel, pairs_of);
+//                  CSR: grid row y is the y-th distinct expert (a descriptor).
+//                  One lane group per gate/up row: the row pair is loaded
+//                  once, then dotted with the LDS-staged activation row of each
+//                  routed token. hidden is written per pair (row = pair id /
+//                  CSR position).
+//   k_csr_down     grid (H/ROWS, M*K + shared), 256 threads: the expert's down
+//                  rows [ROWS b, ROWS b + ROWS), its pairs' hidden vectors
 //                  staged in LDS as scaled fp16 chunks; writes
 //                  part[t*S + k][c] = w * <Wd_e[c], h_pair> * scale, S = K + 1
 //                  with a shared expert. Grid rows [0, ceil(M/2)) are then the
 //                  shared expert (INT8), two tokens each:
 //                  part[t*S + K][c] = gamma_t * <Wd_sh[c], hsh_t> * sd_sh[c].
 //   k_pf_combine   y[t][c] = sum over the S slots of t in slot order, bf16 out.
+// The pair set of an expert is the same in both forms (ascending pair id =
+// (token, k) order) and every sum runs in the same order: the two forms give
+// identical bits.
 // INT8 dots widen the codes to fp16 (dot16_i8h); NVFP4 gate/up converts e2m1
 // to bf16 pairs against the bf16 activations, NVFP4 down to fp16 pairs.
 #include "qfm_dev.h"
@@ -197,6 +207,54 @@ k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, i
     }
 }
 
+// ---- the pairs of an expert, from sel -------------------------------------------
+// Pair q = t K + k of the P = M K pairs has expert sel[q] (written by the router
+// launch's selection tail). The workgroups of pair p run the expert's work only
+// if p is its first pair (the owner); the K experts of a row are distinct, so an
+// expert has at most M <= kMaxRows pairs. Ballots over the P ids give the owner
+// test and the pair list (ascending pair id, i.e. (row, k) order) in scalar
+// registers: no routing-inversion pass. Grid row y is pair y.
+struct PairSet {
+    int e, np;                 // e < 0: this workgroup's pair is not the owner
+    unsigned long long a, c;   // the expert's pairs: bit q of a (q < 64), bit q - 64 of c
+    int pl;                    // in lane j < np: the j-th pair id (ascending)
+};
+// the lowest pair of (a, c), removed from them (0 when none is left)
+__device__ __forceinline__ int next_pair(unsigned long long &a, unsigned long long &c) {
+    int q = 0;
+    if (a) { q = (int)__builtin_ctzll(a); a &= a - 1ull; }
+    else if (c) { q = 64 + (int)__builtin_ctzll(c); c &= c - 1ull; }
+    return __builtin_amdgcn_readfirstlane(q);
+}
+__device__ __forceinline__ PairSet pairs_of(const int *__restrict__ sel, int P, int p) {
+    const int lane = threadIdx.x & 63;
+    PairSet r;
+    r.e = __builtin_amdgcn_readfirstlane(sel[p]);
+    const int s0 = lane < P ? sel[lane] : -1, s1 = lane + 64 < P ? sel[lane + 64] : -1;
+    unsigned long long a = __ballot(s0 == r.e), c = __ballot(s1 == r.e);
+    r.a = a;
+    r.c = c;
+    const int first = a ? (int)__builtin_ctzll(a) : 64 + (int)__builtin_ctzll(c);
+    r.np = __builtin_amdgcn_readfirstlane(__popcll(a) + __popcll(c));
+    if (__builtin_amdgcn_readfirstlane(first) != p) r.e = -1;
+    // lane j: the j-th set bit of (a, c), by clearing the j lowest (an expert
+    // with one pair, the common case at M = 8, has pair p alone: no walk)
+    r.pl = p;
+    if (r.np > 1) {
+        const int na = __popcll(a);
+        unsigned long long m = lane < na ? a : c;
+        const int skip = lane < na ? lane : lane - na;
+#pragma unroll
+        for (int i = 0; i < kMaxRows - 1; i++)
+            if (i < skip) m &= m - 1ull;
+        r.pl = (lane < na ? 0 : 64) + (m ? (int)__builtin_ctzll(m) : 0);
+    }
+    return r;
+}
+// pair j of the set: j wave-uniform (readlane) or per thread (shuffle)
+__device__ __forceinline__ int pair_at(const PairSet &ps, int j) { return __builtin_amdgcn_readlane(ps.pl, j); }
+__device__ __forceinline__ int pair_of_lane(const PairSet &ps, int j) { return ps.np > 1 ? __shfl(ps.pl, j) : ps.pl; }
+
 // ---- gate/up: one distinct expert per blockIdx.y ---------------------------------
 // lanes per gate/up row (32 measured best for both formats at M = 8; 16 and 8
 // were slower)
@@ -218,14 +276,14 @@ constexpr int kGuThreads = QFM_GU_THREADS;
 // (A persistent form over tile ranges with two tiles of weights in flight was
 // slower: its registers allowed two waves per SIMD instead of four, and the
 // dot and reduction latencies then went unhidden.)
-template <class F, int H, int I>
+template <class F, int H, int I, bool PAIRS>
 __global__ void __launch_bounds__(kGuThreads)
 k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
              const float *__restrict__ Sg, const float *__restrict__ Su,          // INT8 row scales
              const uint8_t *__restrict__ Bg, const uint8_t *__restrict__ Bu,      // NVFP4 block scales
              const float *__restrict__ s2g, const float *__restrict__ s2u,        // NVFP4 per-expert scale
              const uint16_t *__restrict__ x, const uint4 *__restrict__ xh, const float2 *__restrict__ xci,
-             int K, const int *__restrict__ g_csr, int P, float *__restrict__ hpair) {
+             int K, const int *__restrict__ rt, int P, float *__restrict__ hpair) {
     constexpr bool I8 = F::VPB == 1;
     constexpr int ROWB = H / F::VPB;             // bytes per gate/up row
     constexpr int LPR = gateup_lpr<F, H>();      // lanes per row
@@ -238,16 +296,26 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
     static_assert(XQ % 64 == 0 && (NCH * 2) % 64 == 0, "rows are staged in 64-lane wave loads");
     __shared__ uint4 s_x[PG * XQ];
     __shared__ float2 s_ci[I8 ? PG * NCH : 1];
-    const int u = blockIdx.y;
-    const int4 dsc = reinterpret_cast<const int4 *>(g_csr + csr_desc_off(P))[u];   // one load before any weight
-    // keep the descriptor one 16-byte load and the weight bases loaded before the
-    // branch (the compiler otherwise sinks each field, and each kernel argument,
-    // below the branch that first needs it: a dependent round trip apiece)
-    args_now(dsc.x, dsc.y, dsc.z, dsc.w, Wg, Wu);
-    const int e = dsc.x;
-    if (e < 0) return;                           // past the last distinct expert
-    const int p0 = dsc.y & 0xFFFF, np = dsc.y >> 16;
-    const int *pair = g_csr + 1 + P + P + 1;
+    // PAIRS (rt = sel): grid row y is pair y, run by its expert's first pair
+    // (pairs_of); otherwise (rt = the routing launch's csr buffer) grid row y is
+    // the y-th distinct expert, found with one 16-byte descriptor load
+    int e, np, p0 = 0;
+    int4 dsc = make_int4(0, 0, 0, 0);
+    unsigned long long pa = 0ull, pc = 0ull;     // PAIRS: pairs not staged yet, ascending
+    if constexpr (PAIRS) {
+        const PairSet ps = pairs_of(rt, P, blockIdx.y);
+        args_now(ps.e, Wg, Wu);                  // (the weight bases requested with sel, before the branch)
+        e = ps.e; np = ps.np; pa = ps.a; pc = ps.c;
+    } else {
+        dsc = reinterpret_cast<const int4 *>(rt + csr_desc_off(P))[blockIdx.y];   // one load before any weight
+        // keep the descriptor one 16-byte load and the weight bases loaded before
+        // the branch (the compiler otherwise sinks each field, and each kernel
+        // argument, below the branch that first needs it: a round trip apiece)
+        args_now(dsc.x, dsc.y, dsc.z, dsc.w, Wg, Wu);
+        e = dsc.x; p0 = dsc.y & 0xFFFF; np = dsc.y >> 16;
+    }
+    if (e < 0) return;                           // not an expert's first pair / past the last expert
+    const int *pair = rt + 1 + P + P + 1;        // csr: CSR position -> pair id
     const int l = threadIdx.x % LPR;
     const int row = blockIdx.x * RPB + threadIdx.x / LPR;
     const size_t roff = ((size_t)e * I + row) * ROWB;
@@ -272,13 +340,29 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
     }
     const uint4 *src = I8 ? xh : reinterpret_cast<const uint4 *>(x);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    static_assert(PG == 2, "two staged rows per group (pq0, pq1)");
     for (int j0 = 0; j0 < np; j0 += PG) {
         const int ng = min(PG, np - j0);
+        // staged row j's pair id and hidden row (PAIRS: row = pair id; csr: row =
+        // CSR position, pair id from the descriptor for the first two)
+        int pq0 = 0, pq1 = 0;
+        if constexpr (PAIRS) {
+            pq0 = next_pair(pa, pc);
+            pq1 = next_pair(pa, pc);
+        }
+        auto pair_id = [&](int j) -> int {
+            if constexpr (PAIRS) return j == 0 ? pq0 : pq1;
+            else return j0 + j == 0 ? dsc.z : j0 + j == 1 ? dsc.w : pair[p0 + j0 + j];
+        };
+        auto hid_row = [&](int j) -> int {
+            if constexpr (PAIRS) return j == 0 ? pq0 : pq1;
+            else return p0 + j0 + j;
+        };
         if (j0 > 0) __syncthreads();             // the previous group's rows are consumed
         // straight into LDS (global_load_lds: lane i of a wave load writes base + 16 i / 4 i)
         for (int k = wave; k < ng * (XQ / 64); k += NW) {
             const int j = k / (XQ / 64), c = k - j * (XQ / 64);
-            const int pr = j0 + j == 0 ? dsc.z : j0 + j == 1 ? dsc.w : pair[p0 + j0 + j];
+            const int pr = pair_id(j);
             __builtin_amdgcn_global_load_lds(src + (size_t)(pr / K) * XQ + c * 64 + lane,
                                              (__attribute__((address_space(3))) void *)(s_x + j * XQ + c * 64), 16, 0, 0);
         }
@@ -287,7 +371,7 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
             const uint32_t *cs = reinterpret_cast<const uint32_t *>(xci);
             for (int k = wave; k < ng * CW; k += NW) {
                 const int j = k / CW, c = k - j * CW;
-                const int pr = j0 + j == 0 ? dsc.z : j0 + j == 1 ? dsc.w : pair[p0 + j0 + j];
+                const int pr = pair_id(j);
                 __builtin_amdgcn_global_load_lds(cs + (size_t)(pr / K) * NCH * 2 + c * 64 + lane,
                                                  (__attribute__((address_space(3))) void *)(reinterpret_cast<uint32_t *>(s_ci) + j * NCH * 2 + c * 64), 4, 0, 0);
             }
@@ -318,7 +402,7 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
             }
             ag = group_sum<LPR>(ag);
             au = group_sum<LPR>(au);
-            if (l == 0) hpair[(size_t)(p0 + j0 + j) * I + row] = silu(ag * rsg) * (au * rsu);
+            if (l == 0) hpair[(size_t)hid_row(j) * I + row] = silu(ag * rsg) * (au * rsu);
         }
     }
 }
@@ -403,11 +487,11 @@ constexpr int down_rows() {
     constexpr int want = F::VPB == 1 ? QFM_DOWN_ROWS_I8 : QFM_DOWN_ROWS_F4;
     return want > 256 / lpr_of(I / F::VPB / 16) ? want : 256 / lpr_of(I / F::VPB / 16);
 }
-template <class F, int H, int I>
+template <class F, int H, int I, bool PAIRS>
 __global__ void __launch_bounds__(256)
 k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const uint8_t *__restrict__ Bd,
            const float *__restrict__ s2d, const float *__restrict__ hpair, const float *__restrict__ g_wts,
-           const int *__restrict__ g_csr, int P, float *__restrict__ part, int K, ShPtrs sh,
+           const int *__restrict__ rt, int P, float *__restrict__ part, int K, ShPtrs sh,
            const float *__restrict__ hsh, const float *__restrict__ logits, int ld, int gated, int M) {
     constexpr int ROWB = I / F::VPB;                   // bytes per down row
     constexpr int CPR = ROWB / 16;                     // 16-byte chunks per row
@@ -426,19 +510,34 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
                                     s_hci, part);
         return;
     }
-    const int u = blockIdx.y - nsh;
-    const int4 dsc = reinterpret_cast<const int4 *>(g_csr + csr_desc_off(P))[u];   // one load before any weight
-    args_now(dsc.x, dsc.y, Wd);                  // as in k_csr_gateup
-    const int e = dsc.x;
-    if (e < 0) return;                           // past the last distinct expert
-    const int p0 = dsc.y & 0xFFFF, np = dsc.y >> 16;
-    const int *pair = g_csr + 1 + P + P + 1;
+    // as in k_csr_gateup: PAIRS, grid row y - nsh is a pair; csr, a distinct expert
+    PairSet ps{};
+    int e, np, p0 = 0;
+    if constexpr (PAIRS) {
+        ps = pairs_of(rt, P, (int)blockIdx.y - nsh);
+        args_now(ps.e, Wd);
+        e = ps.e; np = ps.np;
+    } else {
+        const int4 dsc = reinterpret_cast<const int4 *>(rt + csr_desc_off(P))[blockIdx.y - nsh];
+        args_now(dsc.x, dsc.y, Wd);
+        e = dsc.x; p0 = dsc.y & 0xFFFF; np = dsc.y >> 16;
+    }
+    if (e < 0) return;                           // not an expert's first pair / past the last expert
+    const int *pair = rt + 1 + P + P + 1;        // csr: CSR position -> pair id
     const int l = threadIdx.x % LPR, grp = threadIdx.x / LPR;
     // the pairs' hidden rows first (in L2 or the memory-side cache: they arrive
     // before the weights, and loads retire in issue order, so their conversion
     // runs while the weights stream; M = 8 NVFP4 layer 47.1 -> 46.1 us)
     H16Stage<I, kMaxRows> hst;
-    hst.load(hpair + (size_t)p0 * I, np);
+    if constexpr (PAIRS) {
+        hst.load_rows(hpair, ps, np);
+        // (their addresses wait for the pair list, the weights' only for e:
+        // without this barrier the scheduler issues the weights first and the
+        // conversion then waits for them)
+        __builtin_amdgcn_sched_barrier(0);
+    } else {
+        hst.load(hpair + (size_t)p0 * I, np);    // the expert's rows are contiguous in CSR order
+    }
     // then the weights for this thread's rows (ROWS/GROUPS rows per group)
     constexpr int RPG = ROWS / GROUPS;
     uint4 w[RPG][NST];
@@ -473,7 +572,7 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
             for (int st = 0; st < NST; st++) bs[q][st] = dec[q * NST + st];
     }
     for (int j = 0; j < np; j++) {
-        const int pr = pair[p0 + j];
+        const int pr = PAIRS ? pair_at(ps, j) : pair[p0 + j];
         const float wp = g_wts[pr];
 #pragma unroll
         for (int q = 0; q < RPG; q++) {
@@ -486,6 +585,12 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
 }
 
 // ---- launchers -------------------------------------------------------------------
+// NVFP4 at M >= 7 keeps the routing launch: measured per layer (48 layers,
+// graph, A/B on one box) the pair-keyed form is 1.2-1.9 / 0.4 us slower at M
+// = 8 / 7 and 0 / 0.5 / 2 us faster at M = 6 / 5 / 1-3; INT8 is faster at every
+// M (1.9 us at M = 8, 2.2-2.8 us at M = 2-4).
+bool csr_routing_for(int fmt, int M) { return fmt == QFM_FMT_NVFP4 && M >= 7; }
+
 int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,
                        int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
                        void *xh16, float *part, uint16_t *y, float *y32, hipStream_t s) {
@@ -493,7 +598,8 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
     if (M < 1 || M > kMaxRows || P > kMaxPairs || E != 512) {
         set_error(-2, "csr path: needs 1 <= M <= %d, M*top_k <= %d, 512 experts", kMaxRows, kMaxPairs); return -2;
     }
-    const int umax = P < E ? P : E;
+    const bool use_csr = csr_routing_for(fmt, M);
+    if (use_csr && !csr) { set_error(-1, "csr path: the routing launch needs the csr buffer"); return -1; }
     ShPtrs sp{};
     if (sh) sp = *sh;
     const dim3 b256(256);
@@ -510,15 +616,21 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
         if (!a->w_gate || !a->s_gate || !a->s2g_dev) { set_error(-1, "csr path: arena has no NVFP4 blobs"); return -1; }
         wg = a->w_gate; wu = a->w_up; wd = a->w_down; bg = a->s_gate; bu = a->s_up; bd = a->s_down;
     }
-#define QFM_CSR_LAUNCH(F, HH, II)                                                                                   \
-    hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), dim3(xh ? 1024 : kTopkThreads), 0, s, logits, ld, M, K,          \
-                       g_cfg.renorm, sel, wts, csr, x, HH, xh, xci);                                             \
-    hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(II / (kGuThreads / gateup_lpr<F, HH>()), umax),       \
+#define QFM_CSR_KERNELS(F, HH, II, PAIRS, RT)                                                                       \
+    hipLaunchKernelGGL((k_csr_gateup<F, HH, II, PAIRS>), dim3(II / (kGuThreads / gateup_lpr<F, HH>()), P),   \
                        dim3(kGuThreads), 0, s,                                                                   \
-                       wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, xh, xci, K, csr, P,  \
+                       wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, xh, xci, K, RT, P,   \
                        hpair);                                                                                   \
-    hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / down_rows<F, II>(), umax + (sh ? (M + 1) / 2 : 0)), b256, 0, s, wd,   \
-                       a->i8s_down, bd, a->s2d_dev, hpair, wts, csr, P, part, K, sp, hsh, logits, ld, gated, M);   \
+    hipLaunchKernelGGL((k_csr_down<F, HH, II, PAIRS>), dim3(HH / down_rows<F, II>(), P + (sh ? (M + 1) / 2 : 0)), b256, 0, s, wd, \
+                       a->i8s_down, bd, a->s2d_dev, hpair, wts, RT, P, part, K, sp, hsh, logits, ld, gated, M)
+#define QFM_CSR_LAUNCH(F, HH, II)                                                                                   \
+    if (use_csr) {                                                                                                \
+        hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), dim3(xh ? 1024 : kTopkThreads), 0, s, logits, ld, M, K,      \
+                           g_cfg.renorm, sel, wts, csr, x, HH, xh, xci);                                         \
+        QFM_CSR_KERNELS(F, HH, II, false, csr);                                                                   \
+    } else {                                                                                                      \
+        QFM_CSR_KERNELS(F, HH, II, true, sel);                                                                    \
+    }                                                                                                             \
     launch_pf_combine(part, M, K + (sh ? 1 : 0), HH, y, y32, s)
     if (shape_2048()) {
         if (fmt == QFM_FMT_INT8) { QFM_CSR_LAUNCH(FmtI8, 2048, 512); } else { QFM_CSR_LAUNCH(FmtF4, 2048, 512); }
@@ -528,6 +640,7 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
         set_error(-2, "csr path: unsupported shape"); return -2;
     }
 #undef QFM_CSR_LAUNCH
+#undef QFM_CSR_KERNELS
     return check_launch("csr_forward");
 }
 

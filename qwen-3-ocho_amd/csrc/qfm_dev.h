@@ -117,6 +117,25 @@ struct H16Stage {
             }
         }
     }
+    // rows h + ids.pair_of(j) * I for j < n (ids: a pair set whose j-th id a
+    // thread gets with a shuffle)
+    template <class IDS>
+    __device__ __forceinline__ void load_rows(const float *__restrict__ h, const IDS &ids, int n) {
+#pragma unroll
+        for (int q = 0; q < CPT; q++) {
+            const int c = (int)threadIdx.x + q * NT;
+            const int j = c / (I / 16), o = c - j * (I / 16);
+            const int r = pair_of_lane(ids, j < RMAX ? j : 0);     // (every lane takes part in the shuffle)
+            if (c < n * (I / 16)) {
+                const float4 *hp = reinterpret_cast<const float4 *>(h + (size_t)r * I) + 4 * o;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float4 f = hp[k];
+                    v[q][4 * k] = f.x; v[q][4 * k + 1] = f.y; v[q][4 * k + 2] = f.z; v[q][4 * k + 3] = f.w;
+                }
+            }
+        }
+    }
     __device__ __forceinline__ void store(int n, uint4 *s_h16, float2 *s_hci) {
 #pragma unroll
         for (int q = 0; q < CPT; q++) {
@@ -181,6 +200,15 @@ template <typename T>
 __device__ __forceinline__ void arg_now(const T &v) { asm volatile("" ::"s"(v)); }
 template <typename... T>
 __device__ __forceinline__ void args_now(const T &...v) { (arg_now(v), ...); }
+
+// 64-bit loads and stores at agent scope (coherent across the XCDs' L2s
+// without a fence: written through, read from the memory side)
+__device__ __forceinline__ unsigned long long ld_agent_u64(const unsigned long long *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent_u64(unsigned long long *p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_nt16(const void *p) {
@@ -339,7 +367,8 @@ __device__ __forceinline__ float topk_key_value(unsigned long long key) {
 // compacted to LDS with ballots and mbcnt and each candidate's exact rank
 // within C is its rank among all E.
 constexpr int kTopkLds = 16 + 256 + 64 + 64;   // results, candidates, junk slots, lane maxima
-template <int EPL>
+// (LOAD false: v[] already holds the logits, v[i] = logit i * 64 + lane; lr unused)
+template <int EPL, bool LOAD = true>
 __device__ __forceinline__ int topk_candidates(const float *lr, int K, int lane, unsigned long long *lds,
                                                float (&v)[EPL]) {
     static_assert(EPL >= 1 && EPL <= 16, "E = 64 * EPL, EPL <= 16");
@@ -350,7 +379,7 @@ __device__ __forceinline__ int topk_candidates(const float *lr, int K, int lane,
     uint32_t k31[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
-        v[i] = lr[i * 64 + lane];
+        if constexpr (LOAD) v[i] = lr[i * 64 + lane];
         key[i] = topk_key(v[i], i * 64 + lane);
         k31[i] = ((uint32_t)(key[i] >> (64 - PB)) << IB) | (uint32_t)(E - 1 - (i * 64 + lane));
     }
@@ -435,11 +464,10 @@ __device__ __forceinline__ int topk_cand_rank(const unsigned long long *cand, in
 }
 // Lane k < K receives the k-th expert id and its weight exp(l_k - l_max) /
 // denom, denom = sum over the K selected (renorm) or over all E (plain softmax).
-template <int EPL>
-__device__ __forceinline__ void wave_topk(const float *lr, int K, int renorm, int lane,
-                                          unsigned long long *lds, int &my_i, float &my_w) {
-    float v[EPL];
-    const int n = topk_candidates<EPL>(lr, K, lane, lds, v);
+template <int EPL, bool LOAD>
+__device__ __forceinline__ void wave_topk_v(float (&v)[EPL], const float *lr, int K, int renorm, int lane,
+                                            unsigned long long *lds, int &my_i, float &my_w) {
+    const int n = topk_candidates<EPL, LOAD>(lr, K, lane, lds, v);
     const unsigned long long *cand = lds + 16;
     for (int j = lane; j < n; j += 64) {
         const unsigned long long cj = cand[j];
@@ -462,6 +490,18 @@ __device__ __forceinline__ void wave_topk(const float *lr, int K, int renorm, in
     }
     my_i = lane < K ? topk_key_index(mine) : -1;
     my_w = ek / denom;
+}
+template <int EPL>
+__device__ __forceinline__ void wave_topk(const float *lr, int K, int renorm, int lane,
+                                          unsigned long long *lds, int &my_i, float &my_w) {
+    float v[EPL];
+    wave_topk_v<EPL, true>(v, lr, K, renorm, lane, lds, my_i, my_w);
+}
+// The same from logits held in registers (v[i] = logit i * 64 + lane)
+template <int EPL>
+__device__ __forceinline__ void wave_topk_regs(float (&v)[EPL], int K, int renorm, int lane,
+                                               unsigned long long *lds, int &my_i, float &my_w) {
+    wave_topk_v<EPL, false>(v, nullptr, K, renorm, lane, lds, my_i, my_w);
 }
 // The expert id of rank `job` (< K) only (wave-uniform result): same candidate
 // set and ranks as wave_topk, no permutation through LDS and no softmax.

@@ -41,9 +41,25 @@ struct ShPtrs { const int8_t *qg, *qu, *qd; const float *sg, *su, *sd; };
 // and, when sh != nullptr, the shared-expert hidden hsh[m * ld_hsh + r], in one launch.
 // With x16 != nullptr (M = 1) the launch also writes x as scaled fp16 (H / 8
 // 16-byte words) followed by a float2 (sum of the scaled values, 2^-k).
+// With tail != nullptr (1 <= M <= kTailRows, E = 512, no x16) the launch also
+// ranks every row (k_router_shared's selection tail): sel/wts [M][K], and for
+// INT8 fork rows x as scaled fp16 chunks (xh [M][H] fp16, xci [M][H/16]).
+// lw: [M][E] 64-bit words; ctl: kTailRows + 1 words (per-row tags, then the
+// count of bounded waits that ran out).
+constexpr int kTailRows = 8;
+constexpr int kTailSpinMax = 1 << 16;
+struct RouteTail {
+    unsigned long long *lw;
+    uint32_t *ctl;
+    int *sel;
+    float *wts;
+    uint4 *xh;
+    float2 *xci;
+    int K, renorm;
+};
 int launch_router_shared(const float *W, const float *bias, const float *g, const ShPtrs *sh,
                          const uint16_t *x, int M, float *logits, int ld_logits, float *hsh, int ld_hsh,
-                         hipStream_t s, void *x16 = nullptr);
+                         hipStream_t s, void *x16 = nullptr, const RouteTail *tail = nullptr);
 int launch_router_bf16w(const uint16_t *W, const float *x, float *logits, hipStream_t s);
 int launch_topk(const float *logits, int ld_logits, int M, int *sel, float *wts, hipStream_t s);
 
@@ -67,18 +83,27 @@ int launch_x8(const float *x, int8_t *q, float *sc, int n, hipStream_t s);
 int launch_i8_down_m1(const Qf4ExpCache *c, const float *hidden, const float *wts, const int *sel,
                       int nexp, const ShPtrs *sh, const float *gdot, float *y32, uint16_t *ybf, hipStream_t s);
 
-// Multi-row decode (1 <= M <= 8): top-K of all rows + routing inversion
-// (k_topk_csr), weight-once-per-distinct-expert gate/up (k_csr_gateup), down
-// partials per (expert, row block) with the shared expert's down in the first
-// grid rows (k_csr_down), combine (k_pf_combine). fmt: QFM_FMT_INT8 or
-// QFM_FMT_NVFP4 for the routed experts. hsh: shared hidden [M][I] (from
-// launch_router_shared); csr: csr_ints(M*K) ints, 16-byte aligned; hpair: [M*K][I] fp32; part:
-// [M][K+1][H] fp32; xh16 (INT8): M*H*2 + M*(H/16)*8 bytes, 16-byte aligned.
-// The csr buffer of P = M*K pairs: {n_exp, exp_id[P], exp_ptr[P+1], pair[P]}
-// followed, at the next multiple of 4 ints, by one 4-int descriptor per
-// distinct-expert slot u < P: {expert id or -1 past the last, p0 | np << 16,
-// first pair, second pair}, so a gate/up or down block finds everything it
-// needs to start its loads with one 16-byte load.
+// Multi-row decode (1 <= M <= 8). Two routing forms:
+//  * csr_routing_for(fmt, M) false: launch_router_shared has run with its
+//    selection tail (sel/wts [M][K], INT8: the fp16 activation chunks in xh16);
+//    gate/up keyed by pair (k_csr_gateup<PAIRS>: the first pair of each distinct
+//    expert reads the expert's rows once for all its pairs), down partials per
+//    (pair, row block) (k_csr_down<PAIRS>); hidden row = pair id;
+//  * true (NVFP4 at M >= 7): the router ran without the tail; a routing launch
+//    (k_topk_csr: top-K of all rows, routing inversion into csr, INT8: the fp16
+//    chunks) runs first and the kernels take one distinct expert per grid row;
+//    hidden row = CSR position.
+// Then the combine (k_pf_combine); the shared expert's down rows are the down
+// launch's first grid rows. fmt: QFM_FMT_INT8 or QFM_FMT_NVFP4 for the routed
+// experts. hsh: shared hidden [M][I] (from launch_router_shared); hpair: [M*K][I]
+// fp32; part: [M][K+1][H] fp32; xh16 (INT8): M*H*2 + M*(H/16)*8 bytes, 16-byte
+// aligned; csr: csr_ints(M*K) ints, 16-byte aligned (used by the routing
+// launch only): {n_exp, exp_id[P], exp_ptr[P+1], pair[P]} followed, at the next
+// multiple of 4 ints, by one 4-int descriptor per distinct-expert slot u < P:
+// {expert id or -1 past the last, p0 | np << 16, first pair, second pair}, so
+// a gate/up or down block finds everything it needs to start its loads with
+// one 16-byte load.
+bool csr_routing_for(int fmt, int M);
 __host__ __device__ constexpr int csr_desc_off(int P) { return (3 * P + 2 + 3) & ~3; }
 __host__ __device__ constexpr int csr_ints(int P) { return csr_desc_off(P) + 4 * P; }
 int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,

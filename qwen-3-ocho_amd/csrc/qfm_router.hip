@@ -49,11 +49,26 @@ __device__ __forceinline__ float canon_reduce_row(const float4 (&w)[NJ], const f
 // per pair, laid out so that one pair's blocks share an XCD (and its L2).
 // With x16 != nullptr one more block (the first) writes x row 0 as scaled
 // fp16 with its (sum, 2^-k) for the M = 1 gate/up kernel.
-template <int NJ, int I, int MR>
+//
+// With TAIL (the M <= 8 forward; tail.lw != nullptr) the launch also selects: each
+// router row's logits go out a second time as 64-bit words (fp32 bits | tag <<
+// 32, stored at agent scope), tag = ctl[m] + 1 for row m; the grid's last
+// blocks are then (INT8) x as scaled fp16 chunks (chunk16_to_f16, the fork
+// rows' dot16_i8h input) and one selector wave per row, which reads its row's
+// words until every tag is ctl[m] + 1 (bounded: a timeout is counted in
+// ctl[kTailRows] and the words are used as found), ranks them from registers
+// (wave_topk_regs: the same selection as wave_topk), writes sel/wts and then
+// ctl[m] = the tag. Every router wave has read ctl before it writes a word, so
+// no wave of this launch reads the updated ctl[m]; the next call tags with
+// ctl[m] + 1 again, so words left by this call are never taken for the next
+// call's. A selector waits only on router waves dispatched before it, which
+// never wait, so the waits end.
+template <int NJ, int I, int MR, bool TAIL>
 __global__ void __launch_bounds__(64)
 k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, const float *__restrict__ g,
                 ShPtrs sh, const uint16_t *__restrict__ x, int M, int E, float *__restrict__ logits, int ld,
-                float *__restrict__ hsh, int ldh, uint4 *__restrict__ x16, float2 *__restrict__ x16i) {
+                float *__restrict__ hsh, int ldh, uint4 *__restrict__ x16, float2 *__restrict__ x16i,
+                RouteTail tail, int tail0) {
     constexpr int H = NJ * 256;
     const int lane = threadIdx.x;
     args_now(W, bias, g, sh.qg, sh.qu, sh.sg, sh.su, x, M, E, logits, ld, hsh, ldh, x16, x16i);
@@ -63,6 +78,66 @@ k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, con
     }
     const int b = (int)blockIdx.x - (x16 ? 1 : 0);
     const int ng = g ? 1 : 0;
+    if (TAIL && b >= tail0) {                       // the selection tail (block-uniform)
+        const int nxb = tail.xh ? (M * (H / 16) + 63) / 64 : 0;
+        if (b < tail0 + nxb) {                      // x as scaled fp16 chunks
+            const int ch = (b - tail0) * 64 + lane;
+            if (ch < M * (H / 16)) {
+                const uint4 a = reinterpret_cast<const uint4 *>(x)[2 * ch], c = reinterpret_cast<const uint4 *>(x)[2 * ch + 1];
+                const uint32_t d[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+                float v[16];
+#pragma unroll
+                for (int i = 0; i < 8; i++) { v[2 * i] = bf16_lo(d[i]); v[2 * i + 1] = bf16_hi(d[i]); }
+                uint4 ha, hb;
+                tail.xci[ch] = chunk16_to_f16(v, ha, hb);
+                tail.xh[2 * ch] = ha;
+                tail.xh[2 * ch + 1] = hb;
+            }
+            return;
+        }
+        const int m = b - tail0 - nxb;              // selector of row m
+        constexpr int EPL = 8;                      // E == 512 (checked by the host)
+        __shared__ __align__(16) unsigned long long s_tk[kTopkLds];
+        const uint32_t tg = tail.ctl[m] + 1u;
+        const unsigned long long *row = tail.lw + (size_t)m * E;
+        float v[EPL];
+        uint32_t pend = 0u;
+        {
+            unsigned long long w[EPL];
+#pragma unroll
+            for (int i = 0; i < EPL; i++) w[i] = ld_agent_u64(row + i * 64 + lane);
+#pragma unroll
+            for (int i = 0; i < EPL; i++) {
+                v[i] = __uint_as_float((uint32_t)w[i]);
+                if ((uint32_t)(w[i] >> 32) != tg) pend |= 1u << i;
+            }
+        }
+        for (int it = 0; __builtin_amdgcn_ballot_w64(pend != 0u) != 0; it++) {
+            if (it == kTailSpinMax) {               // bounded: count it, rank what is there
+                if (lane == 0) __hip_atomic_fetch_add(tail.ctl + kTailRows, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            unsigned long long w[EPL];
+#pragma unroll
+            for (int i = 0; i < EPL; i++) w[i] = ld_agent_u64(row + i * 64 + lane);
+#pragma unroll
+            for (int i = 0; i < EPL; i++)
+                if ((pend & (1u << i)) && (uint32_t)(w[i] >> 32) == tg) {
+                    v[i] = __uint_as_float((uint32_t)w[i]);
+                    pend &= ~(1u << i);
+                }
+        }
+        int my_i;
+        float my_w;
+        wave_topk_regs<EPL>(v, tail.K, tail.renorm, lane, s_tk, my_i, my_w);
+        if (lane < tail.K) {
+            tail.sel[m * tail.K + lane] = my_i;
+            tail.wts[m * tail.K + lane] = my_w;
+        }
+        if (lane == 0) tail.ctl[m] = tg;
+        return;
+    }
     if (b < E + ng) {
         const bool is_g = b == E;
         const float *wr = is_g ? g : W + (size_t)b * H;
@@ -71,6 +146,9 @@ k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, con
         for (int j = 0; j < NJ; j++) w[j] = *reinterpret_cast<const float4 *>(wr + j * 256 + lane * 4);
         const float bb = (!is_g && bias) ? bias[b] : 0.0f;
         for (int m0 = 0; m0 < M; m0 += MR) {
+            // the tag of the row this lane ends with (lane r < MR: row m0 + r),
+            // requested with the pass's x rows
+            const uint32_t tgl = (TAIL && lane < MR && m0 + lane < M) ? tail.ctl[m0 + lane] + 1u : 0u;
             uint2 xp[MR][NJ];
 #pragma unroll
             for (int r = 0; r < MR; r++)
@@ -93,12 +171,19 @@ k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, con
             if constexpr (MR == 1) {
                 float v = canon_butterfly(a[0]);
                 if (bias && !is_g) v = __fadd_rn(v, bb);
-                if (lane == 0 && m0 < M) logits[(size_t)m0 * ld + b] = v;
+                if (lane == 0 && m0 < M) {
+                    logits[(size_t)m0 * ld + b] = v;
+                    if (TAIL && !is_g) st_agent_u64(tail.lw + (size_t)m0 * E + b, __float_as_uint(v) | ((unsigned long long)tgl << 32));
+                }
             } else {
                 // lane r < MR ends with row m0 + r (the same addition tree per row)
                 float v = canon_reduce_rows<MR>(a, lane);
                 if (bias && !is_g) v = __fadd_rn(v, bb);
-                if (lane < MR && m0 + lane < M) logits[(size_t)(m0 + lane) * ld + b] = v;
+                if (lane < MR && m0 + lane < M) {
+                    logits[(size_t)(m0 + lane) * ld + b] = v;
+                    if (TAIL && !is_g)
+                        st_agent_u64(tail.lw + (size_t)(m0 + lane) * E + b, __float_as_uint(v) | ((unsigned long long)tgl << 32));
+                }
             }
         }
         return;
@@ -193,32 +278,46 @@ k_topk(const float *__restrict__ logits, int ld, int M, int K, int renorm,
 
 int launch_router_shared(const float *W, const float *bias, const float *g, const ShPtrs *sh,
                          const uint16_t *x, int M, float *logits, int ld, float *hsh, int ldh, hipStream_t s,
-                         void *x16) {
+                         void *x16, const RouteTail *tail) {
     const int E = g_cfg.E, I = g_cfg.I;
     if (sh && !hsh) { set_error(-1, "router: shared rows need an output"); return -1; }
     if (x16 && M != 1) { set_error(-1, "router: the fp16 x row is for M = 1"); return -1; }
+    if (tail && (x16 || E != 512 || M > kTailRows || !tail->lw || !tail->ctl || !tail->sel || !tail->wts ||
+                 tail->K < 1 || tail->K > 16 || (!tail->xh) != (!tail->xci))) {
+        set_error(-1, "router: bad selection tail"); return -1;
+    }
     ShPtrs sp{};
     if (sh) sp = *sh;
     uint4 *xh = static_cast<uint4 *>(x16);
     float2 *xi = xh ? reinterpret_cast<float2 *>(xh + g_cfg.H / 8) : nullptr;
-    const int nblk = E + (g ? 1 : 0) + (sh ? (I / 2) * (M == 1 ? 1 : (M + 1) / 2) : 0) + (xh ? 1 : 0);
+    int nblk = E + (g ? 1 : 0) + (sh ? (I / 2) * (M == 1 ? 1 : (M + 1) / 2) : 0) + (xh ? 1 : 0);
+    RouteTail tl{};
+    const int tail0 = nblk - (xh ? 1 : 0);           // first tail block (counted without the fp16-row block)
+    if (tail) {
+        tl = *tail;
+        nblk += (tl.xh ? (M * (g_cfg.H / 16) + 63) / 64 : 0) + M;
+    }
+#define QFM_ROUTER(NJ, II, MR)                                                                                 \
+    if (tail)                                                                                                  \
+        hipLaunchKernelGGL((k_router_shared<NJ, II, MR, true>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, \
+                           logits, ld, hsh, ldh, xh, xi, tl, tail0);                                          \
+    else                                                                                                       \
+        hipLaunchKernelGGL((k_router_shared<NJ, II, MR, false>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, \
+                           logits, ld, hsh, ldh, xh, xi, tl, tail0)
     if (shape_2048()) {
-        if (M == 1)
-            hipLaunchKernelGGL((k_router_shared<8, 512, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
-        else if (M <= 4)
-            hipLaunchKernelGGL((k_router_shared<8, 512, 4>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
-        else
-            hipLaunchKernelGGL((k_router_shared<8, 512, 8>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
-    } else if (shape_shard() && M == 1 && !sh) {
-        hipLaunchKernelGGL((k_router_shared<8, 64, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
+        if (M == 1) { QFM_ROUTER(8, 512, 1); }
+        else if (M <= 4) { QFM_ROUTER(8, 512, 4); }
+        else { QFM_ROUTER(8, 512, 8); }
+    } else if (shape_shard() && M == 1 && !sh && !tail) {
+        hipLaunchKernelGGL((k_router_shared<8, 64, 1, false>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E,
+                           logits, ld, hsh, ldh, xh, xi, tl, tail0);
     } else if (shape_2560()) {
-        if (M == 1)
-            hipLaunchKernelGGL((k_router_shared<10, 640, 1>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
-        else
-            hipLaunchKernelGGL((k_router_shared<10, 640, 4>), dim3(nblk), dim3(64), 0, s, W, bias, g, sp, x, M, E, logits, ld, hsh, ldh, xh, xi);
+        if (M == 1) { QFM_ROUTER(10, 640, 1); }
+        else { QFM_ROUTER(10, 640, 4); }
     } else {
         set_error(-2, "router: unsupported shape"); return -2;
     }
+#undef QFM_ROUTER
     return check_launch("router_shared");
 }
 

@@ -378,6 +378,53 @@ def test_moe_layer_deterministic(lib):
     assert np.array_equal(a["y"].view(np.uint32), b["y"].view(np.uint32))
 
 
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_moe_layer_workspace_reuse(lib, fmt):
+    """One zeroed workspace serves a run of calls of different M, prefill
+    included: every call's y, sel and wts equal a fresh workspace's bits. The
+    M <= 8 forward ranks each row in the router launch's tail from tagged logit
+    words whose tags live at the workspace's start; its first 36 bytes are then
+    {per-row tag = number of tail calls that had that row, timeout count = 0}
+    (NVFP4 at M >= 7 runs the separate routing launch and leaves them alone)."""
+    _cfg(lib)
+    H, K = 2048, 10
+    seq = [8, 3, 37, 8, 5, 1, 6, 7]
+    st = qfm.Stream()
+    L = qfm.SynthLayer(fmt, 3, 8, stream=st)
+    wsb = max(lib.qfm_workspace_bytes(M) for M in seq)
+    ws = qfm.DevBuf(wsb)
+    tags = np.zeros(8, np.int64)
+    for i, M in enumerate(seq):
+        _say("workspace reuse", "int8" if fmt == 0 else "nvfp4", "call", i, "M", M)
+        dx, dy = qfm.DevBuf(M * H * 2), qfm.DevBuf(M * H * 2)
+        qfm.check(lib.qfm_gen_input_rows(dx.ptr, M, 3, 40 + i, 0, st.h), "x")
+        qfm.check(lib.qfm_moe_forward(C.byref(L.s.layer), dx.ptr, M, dy.ptr, ws.ptr, wsb, st.h), "forward")
+        st.sync()
+        view = qfm.QfmWsView()
+        lib.qfm_workspace_view(ws.ptr, M, C.byref(view))
+        got = (dy.download(np.uint16, (M, H)), qfm.d2h(view.sel, np.int32, (M, K)),
+               qfm.d2h(view.wts, np.float32, (M, K)))
+        w1b = lib.qfm_workspace_bytes(M)
+        w1, y1 = qfm.DevBuf(w1b), qfm.DevBuf(M * H * 2)
+        qfm.check(lib.qfm_moe_forward(C.byref(L.s.layer), dx.ptr, M, y1.ptr, w1.ptr, w1b, st.h), "forward")
+        st.sync()
+        lib.qfm_workspace_view(w1.ptr, M, C.byref(view))
+        ref = (y1.download(np.uint16, (M, H)), qfm.d2h(view.sel, np.int32, (M, K)),
+               qfm.d2h(view.wts, np.float32, (M, K)))
+        for a, b in zip(got, ref):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (i, M)
+        if M <= 8 and not (fmt == 0 and M == 1) and not (fmt == 1 and M >= 7):
+            tags[:M] += 1
+        hdr = ws.download(np.uint32, (9,))
+        assert np.array_equal(hdr[:8], tags), (i, M, hdr)
+        assert hdr[8] == 0, hdr
+        for b in (dx, dy, w1, y1):
+            b.free()
+    ws.free()
+    L.destroy()
+    st.destroy()
+
+
 # ------------------------------------------------------------------ prefill
 def _run_prefill(lib, T, seed, layer, x_layer, bias=True, fmt=qfm.QFM_FMT_INT8, H=2048):
     st = qfm.Stream()
