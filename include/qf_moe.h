@@ -317,7 +317,8 @@ typedef struct {
 } qfm_layer;
 
 /* Workspace for M rows (device memory, caller-owned, >= 256-byte aligned).
- * Zero it once after allocating it (qfm_dev_malloc returns zeroed memory):
+ * Zero it once after allocating it, ordered before the first call (on that
+ * call's stream, or finished; qfm_dev_malloc returns zeroed memory):
  * its first bytes hold per-row sequence tags that the M <= 8 forward keeps
  * across calls (the same offsets for every M, so one workspace of the largest
  * size serves calls of any M); calls that share a workspace must not overlap. */
@@ -351,7 +352,7 @@ int qfm_moe_forward_f32(const qfm_layer *L, const uint16_t *x, int M, float *y,
 
 /* qfm_moe_forward for callers that cannot allocate or pass a workspace (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). No counterpart in the reference. The workspace is a 2 MiB
+ * hipMalloc). No counterpart in the reference. The workspace is a 3 MiB
  * device array inside the library (one per GPU, held until the process ends),
  * which serves 1 <= M <= 8 rows at either supported shape; larger M is
  * rejected with -1 and a message (prefill needs qfm_moe_forward and a caller
@@ -428,7 +429,7 @@ int  qfm_gen_input_rows(uint16_t *x, int M, uint32_t seed, uint32_t x_layer, int
 
 /* ------------------------------------------------------------------------ */
 /* Harness utilities (thin wrappers over the HIP runtime). */
-void  *qfm_dev_malloc(size_t bytes);   /* zeroed */
+void  *qfm_dev_malloc(size_t bytes);   /* zeroed (the fill has finished at return) */
 int    qfm_dev_free(void *p);
 int    qfm_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int    qfm_memcpy_d2h(void *dst, const void *src, size_t bytes);

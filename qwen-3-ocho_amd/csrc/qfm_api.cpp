@@ -102,30 +102,35 @@ int preflight_device_bytes(size_t bytes, const char *who) {
     return 0;
 }
 
-// Every workspace starts with the M <= 8 selection tail's state, at the same
+// Every workspace starts with the M <= 8 forward's tagged state, at the same
 // offsets for every M (prefill included, whose own layout follows it): ctl =
-// per-row tags (+ the timeout count), lw = [kTailRows][E] tagged logit words.
-// Zero is a valid start (tag 1 is then expected, and no word carries it); each
-// call leaves ctl[m] equal to every tag of row m's words, so a workspace that is
-// zeroed once stays valid across calls of any M.
-static size_t ws_tag_bytes() { return 256 + align256((size_t)kTailRows * g_cfg.E * 8); }
+// per-row tags (+ the count of bounded waits that ran out), lw =
+// [kTailRows][E] tagged logit words (the router launch's selection tail), pw =
+// [kTailRows][K+1][H] tagged partial words (the down launch's combine row).
+// Zero is a valid start (the first tag is 1, and no zero word carries it);
+// every later tag is larger than any tag a word already holds, so a workspace
+// that is zeroed once stays valid across calls of any M.
+static size_t ws_lw_bytes() { return align256((size_t)kTailRows * g_cfg.E * 8); }
+static size_t ws_tag_bytes() {
+    return 256 + ws_lw_bytes() + align256((size_t)kTailRows * (g_cfg.K + 1) * g_cfg.H * 8);
+}
 
 struct WsLayout {
-    size_t ctl, lw, logits, sel, wts, hidden, csr, xh16, part, total;
+    size_t ctl, lw, pw, logits, sel, wts, hidden, csr, xh16, total;
 };
 static WsLayout ws_layout(int M) {
     const Cfg &c = g_cfg;
     WsLayout w{};
     w.ctl = 0;
     w.lw = 256;
+    w.pw = 256 + ws_lw_bytes();
     size_t off = ws_tag_bytes();
     w.logits = off; off += align256((size_t)M * (c.E + 1) * sizeof(float));
     w.sel = off;    off += align256((size_t)M * c.K * sizeof(int));
     w.wts = off;    off += align256((size_t)M * c.K * sizeof(float));
     w.hidden = off; off += align256((size_t)M * (c.K + 1) * c.I * sizeof(float));
-    w.csr = off;    off += align256((size_t)csr_ints(M * c.K) * sizeof(int));   // the routing launch's (NVFP4, M >= 7)
+    w.csr = off;    off += align256((size_t)csr_ints(M * c.K) * sizeof(int));   // the routing launch's (NVFP4, M = 8)
     w.xh16 = off;   off += align256((size_t)M * c.H * 2 + (size_t)M * (c.H / 16) * 8);   // fp16 activations + chunk scales
-    w.part = off;   off += align256((size_t)M * (c.K + 1) * c.H * sizeof(float));   // K routed + shared slots
     w.total = off;
     return w;
 }
@@ -355,7 +360,6 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
     int *sel = reinterpret_cast<int *>(b + w.sel);
     float *wts = reinterpret_cast<float *>(b + w.wts);
     float *hidden = reinterpret_cast<float *>(b + w.hidden);
-    float *part = reinterpret_cast<float *>(b + w.part);
     const bool has_sh = L->sh_gate.w != nullptr;
     const float *g = (has_sh && c.gated) ? L->sh_gate_inp : nullptr;
     ShPtrs shp{};
@@ -401,11 +405,12 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
         tail.K = c.K;
         tail.renorm = c.renorm;
         int *csr = reinterpret_cast<int *>(b + w.csr);
-        const bool routing_launch = csr_routing_for(L->fmt, M);     // (NVFP4, M >= 7: faster with it)
+        const bool routing_launch = csr_routing_for(L->fmt, M);     // (NVFP4, M = 8: faster with it)
         int rc = launch_router_shared(L->router, L->router_bias, g, sp, x, M, logits, ld, hsh, c.I, s, nullptr,
                                       routing_launch ? nullptr : &tail);
         if (!rc) rc = launch_csr_forward(L->arena, L->fmt, sp, x, logits, ld, g ? 1 : 0, M, hidden, hsh, sel, wts, csr,
-                                         b + w.xh16, part, y, y32, s);
+                                         b + w.xh16, reinterpret_cast<unsigned long long *>(b + w.pw),
+                                         reinterpret_cast<uint32_t *>(b + w.ctl), y, y32, s);
         return rc;
     }
     return launch_prefill(L, x, M, y, y32, b + ws_tag_bytes(), c.gated, s);
@@ -480,7 +485,11 @@ void *qfm_dev_malloc(size_t bytes) {
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
     if (e != hipSuccess) { set_error(-4, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e)); return nullptr; }
-    e = hipMemset(p, 0, bytes ? bytes : 1);             // zeroed (a workspace must start zeroed)
+    // zeroed (a workspace must start zeroed), and finished before the return:
+    // the fill runs on the null stream, which a non-blocking stream does not
+    // wait for, so work the caller then queues there could run first
+    e = hipMemsetAsync(p, 0, bytes ? bytes : 1, nullptr);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
     if (e != hipSuccess) { (void)hipFree(p); set_error(-4, "hipMemset(%zu): %s", bytes, hipGetErrorString(e)); return nullptr; }
     return p;
 }
@@ -488,7 +497,9 @@ int qfm_dev_free(void *p) { return hipFree(p) == hipSuccess ? 0 : -1; }
 int qfm_memcpy_h2d(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1; }
 int qfm_memcpy_d2h(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1; }
 int qfm_memcpy_d2d(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyDeviceToDevice) == hipSuccess ? 0 : -1; }
-int qfm_memset(void *dst, int v, size_t n) { return hipMemset(dst, v, n) == hipSuccess ? 0 : -1; }
+int qfm_memset(void *dst, int v, size_t n) {   // finished before the return (as qfm_dev_malloc's fill)
+    return hipMemsetAsync(dst, v, n, nullptr) == hipSuccess && hipStreamSynchronize(nullptr) == hipSuccess ? 0 : -1;
+}
 void *qfm_stream_create(void) {
     hipStream_t s = nullptr;
     if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;

@@ -11,10 +11,10 @@
 // owned partials part[t][k][H] summed in k order (no atomics, deterministic).
 //
 // Launch sequence (all stream-ordered), after the router launch:
-//   pair-keyed form (INT8 at every M, NVFP4 at M <= 6): the router launch's
+//   pair-keyed form (INT8 at every M, NVFP4 at M <= 7): the router launch's
 //                  selection tail has written sel/wts (and, INT8, the fp16
 //                  activation chunks);
-//   CSR form (NVFP4 at M >= 7, measured faster there):
+//   CSR form (NVFP4 at M = 8, measured faster there):
 //   k_topk_csr     one block: the top-K of all M rows (one wave per row), then
 //                  the routing inversion in LDS (per-row expert bitmaps and
 //                  their word prefix counts, P = M*K <= 128 pairs); publishes
@@ -29,14 +29,16 @@
 //                  once, then dotted with the LDS-staged activation row of each
 //                  routed token. hidden is written per pair (row = pair id /
 //                  CSR position).
-//   k_csr_down     grid (H/ROWS, M*K + shared), 256 threads: the expert's down
-//                  rows [ROWS b, ROWS b + ROWS), its pairs' hidden vectors
-//                  staged in LDS as scaled fp16 chunks; writes
-//                  part[t*S + k][c] = w * <Wd_e[c], h_pair> * scale, S = K + 1
-//                  with a shared expert. Grid rows [0, ceil(M/2)) are then the
-//                  shared expert (INT8), two tokens each:
-//                  part[t*S + K][c] = gamma_t * <Wd_sh[c], hsh_t> * sd_sh[c].
-//   k_pf_combine   y[t][c] = sum over the S slots of t in slot order, bf16 out.
+//   k_csr_down     grid (H/ROWS, M*K + shared + M), 256 threads: the
+//                  expert's down rows [ROWS b, ROWS b + ROWS), its pairs'
+//                  hidden vectors staged in LDS as scaled fp16 chunks; writes
+//                  the partial w * <Wd_e[c], h_pair> * scale of (t, k) as a
+//                  tagged word pw[t][k][c] (slots S = K + 1 with a shared
+//                  expert). Grid rows [0, ceil(M/2)) are the shared expert
+//                  (INT8), two tokens each, slot K:
+//                  gamma_t * <Wd_sh[c], hsh_t> * sd_sh[c]. The last M grid
+//                  rows are the combine: y[t][c] = the sum of the S slots of
+//                  t in slot order, once every word carries the call's tag.
 // The pair set of an expert is the same in both forms (ascending pair id =
 // (token, k) order) and every sum runs in the same order: the two forms give
 // identical bits.
@@ -155,7 +157,7 @@ __device__ __forceinline__ void csr_build_lds(CsrLds &c, int M, int K) {
 
 // ---- top-K of all rows + routing inversion: one block, one wave per row ---------
 // Published: sel/wts [M][K]; csr = {n_exp, exp_id[P], exp_ptr[P+1], pair[P]}
-// and the per-slot descriptors at csr_desc_off(P).
+// and the per-slot descriptors at csr_desc_off(P); ctl[0] = the call's tag.
 // With xh != nullptr, threads [kTopkThreads, blockDim.x) meanwhile write the
 // activations x [M][H] (bf16) as scaled fp16 chunks for the INT8 dot:
 // xh [M][H] fp16, xci [M][H/16] = (seed, 2^-k) of each 16-value chunk.
@@ -164,7 +166,7 @@ template <int EPL>
 __global__ void __launch_bounds__(1024)
 k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, int *__restrict__ g_sel,
            float *__restrict__ g_wts, int *__restrict__ g_csr, const uint16_t *__restrict__ x, int H,
-           uint4 *__restrict__ xh, float2 *__restrict__ xci) {
+           uint4 *__restrict__ xh, float2 *__restrict__ xci, uint32_t *__restrict__ ctl) {
     __shared__ CsrLds c;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int P = M * K;
@@ -196,7 +198,10 @@ k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, i
         g_csr[1 + P + (P + 1) + i] = c.pair[i];
     }
     for (int i = threadIdx.x; i <= P; i += blockDim.x) g_csr[1 + P + i] = c.exp_ptr[i];
-    if (threadIdx.x == 0) g_csr[0] = c.n_exp;
+    if (threadIdx.x == 0) {
+        g_csr[0] = c.n_exp;
+        ctl[0] = next_tag(ctl[0]);                // this call's partial-word tag (k_csr_down)
+    }
     for (int u = threadIdx.x; u < P; u += blockDim.x) {
         int4 d = make_int4(-1, P, 0, 0);
         if (u < c.n_exp) {
@@ -432,13 +437,89 @@ __device__ __forceinline__ float down_dot(const uint4 (&w)[NST], const f32x2_t (
     return d;
 }
 
+// ---- partial words and the combine -------------------------------------------------
+// A partial is stored as a 64-bit word (fp32 bits | tag << 32) at agent scope:
+// written through to memory, readable from every XCD without a fence.
+__device__ __forceinline__ void st_part(unsigned long long *p, float v, uint32_t tag) {
+    st_agent_u64(p, (unsigned long long)__float_as_uint(v) | ((unsigned long long)tag << 32));
+}
+// The down launch's last M grid rows: workgroup (b, M - 1 - ...) owns output
+// columns [c0, c0 + ROWS) of one row t. SL = 256 / ROWS adjacent lanes (one
+// wave) share a column, lane j reading slots j, j + SL, ...: each wave first
+// waits for one word, then each lane (bounded: 2^16 polls, a timeout counted
+// in *tmo and the words used as found) until its words carry this call's tag,
+// only pending words being read again; the column's values then go through LDS to its first lane, which sums
+// them in slot order from 0 (k_pf_combine's order) and stores y (bf16, round
+// to nearest even) or y32. The words come from workgroups of earlier grid
+// rows, dispatched before this one, which never wait: the waits end.
+template <int H, int ROWS>
+__device__ __forceinline__ void csr_combine(const unsigned long long *__restrict__ pw, uint32_t tag, int t, int S,
+                                            int c0, float *s_v, uint16_t *__restrict__ y, float *__restrict__ y32,
+                                            uint32_t *__restrict__ tmo) {
+    constexpr int SL = 256 / ROWS;                 // lanes per column
+    constexpr int kMaxS = 17;                      // K <= 16 routed + the shared slot
+    constexpr int NW = (kMaxS + SL - 1) / SL;      // words per lane
+    constexpr int SP = kMaxS;                      // LDS floats per column
+    static_assert(SL >= 1 && 64 % SL == 0, "a column's lanes must share a wave");
+    const int c = threadIdx.x / SL, j = threadIdx.x - c * SL;
+    const unsigned long long *w = pw + (size_t)t * S * H + c0 + c;
+    {   // first one word per wave (its first column's slot 0): almost no traffic
+        // while the producers still stream their weights
+        const unsigned long long *w0 = pw + (size_t)t * S * H + c0 + (int)(threadIdx.x & ~63u) / SL;
+        for (int it = 0; it < kTailSpinMax; it++) {
+            const unsigned long long x = ld_agent_u64(w0);
+            if (__builtin_amdgcn_readfirstlane((int)((uint32_t)(x >> 32) == tag))) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    float v[NW];
+    uint32_t pend = 0u;
+#pragma unroll
+    for (int q = 0; q < NW; q++) {
+        const int sl = j + q * SL;
+        v[q] = 0.0f;
+        if (sl < S) {
+            const unsigned long long x = ld_agent_u64(w + (size_t)sl * H);
+            if ((uint32_t)(x >> 32) == tag) v[q] = __uint_as_float((uint32_t)x);
+            else pend |= 1u << q;
+        }
+    }
+    for (int it = 0; __builtin_amdgcn_ballot_w64(pend != 0u) != 0; it++) {
+        if (it == kTailSpinMax) {
+            if (pend) __hip_atomic_fetch_add(tmo, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int q = 0; q < NW; q++) {
+            if (pend & (1u << q)) {
+                const unsigned long long x = ld_agent_u64(w + (size_t)(j + q * SL) * H);
+                if ((uint32_t)(x >> 32) == tag) {
+                    v[q] = __uint_as_float((uint32_t)x);
+                    pend &= ~(1u << q);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < NW; q++)
+        if (j + q * SL < S) s_v[c * SP + j + q * SL] = v[q];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // the column's lanes are in this wave
+    if (j == 0) {
+        float a = 0.0f;
+        for (int sl = 0; sl < S; sl++) a += s_v[c * SP + sl];
+        if (y32) y32[(size_t)t * H + c0 + c] = a;
+        else y[(size_t)t * H + c0 + c] = f32_to_bf16(a);
+    }
+}
+
 // ---- shared expert's down rows (INT8) for tokens [t0, t1): one k_csr_down block ----
 // rows [c0, c0 + ROWS)
 template <int H, int I, int ROWS>
 __device__ __forceinline__ void csr_down_shared(const ShPtrs &sh, const float *__restrict__ hsh,
                                                 const float *__restrict__ logits, int ld, int gated, int t0,
                                                 int t1, int S, int K, int c0, uint4 *s_h16, float2 *s_hci,
-                                                float *__restrict__ part) {
+                                                float *s_out, unsigned long long *__restrict__ pw, uint32_t tag) {
     constexpr int CPR = I / 16, LPR = lpr_of(CPR), NST = CPR / LPR, GROUPS = 256 / LPR, RPG = ROWS / GROUPS;
     static_assert(RPG >= 1 && RPG * GROUPS == ROWS, "shared rows must tile the block");
     const int l = threadIdx.x % LPR, grp = threadIdx.x / LPR;
@@ -467,11 +548,15 @@ __device__ __forceinline__ void csr_down_shared(const ShPtrs &sh, const float *_
         const float g = gated ? sigmoid(gam[t]) : 1.0f;
 #pragma unroll
         for (int q = 0; q < RPG; q++) {
-            const int c = c0 + q * GROUPS + grp;
             float d = down_dot<FmtI8, I, LPR, NST>(w[q], bs, s_h16, s_hci, t, l);
             d = group_sum<LPR>(d);
-            if (l == 0) part[((size_t)(t0 + t) * S + K) * H + c] = g * (d * rs[q]);
+            if (l == 0) s_out[t * ROWS + q * GROUPS + grp] = g * (d * rs[q]);
         }
+    }
+    __syncthreads();                              // contiguous runs of words, as in k_csr_down
+    for (int i = threadIdx.x; i < nt * ROWS; i += 256) {
+        const int t = i / ROWS, r = i - t * ROWS;
+        st_part(pw + ((size_t)(t0 + t) * S + K) * H + c0 + r, s_out[i], tag);
     }
 }
 
@@ -491,8 +576,9 @@ template <class F, int H, int I, bool PAIRS>
 __global__ void __launch_bounds__(256)
 k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const uint8_t *__restrict__ Bd,
            const float *__restrict__ s2d, const float *__restrict__ hpair, const float *__restrict__ g_wts,
-           const int *__restrict__ rt, int P, float *__restrict__ part, int K, ShPtrs sh,
-           const float *__restrict__ hsh, const float *__restrict__ logits, int ld, int gated, int M) {
+           const int *__restrict__ rt, int P, unsigned long long *__restrict__ pw, int K, ShPtrs sh,
+           const float *__restrict__ hsh, const float *__restrict__ logits, int ld, int gated, int M,
+           uint32_t *__restrict__ ctl, uint16_t *__restrict__ y, float *__restrict__ y32) {
     constexpr int ROWB = I / F::VPB;                   // bytes per down row
     constexpr int CPR = ROWB / 16;                     // 16-byte chunks per row
     constexpr int LPR = lpr_of(CPR);                   // lanes per row
@@ -501,13 +587,21 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
     constexpr int ROWS = down_rows<F, I>();
     __shared__ uint4 s_h16[kMaxRows * I / 8];
     __shared__ float2 s_hci[kMaxRows * I / 16];
+    __shared__ float s_out[kMaxRows * ROWS];      // the block's partials, [pair j or token][row]
     const bool has_sh = sh.qd != nullptr;
     const int S = K + (has_sh ? 1 : 0);
     const int nsh = has_sh ? (M + 1) / 2 : 0;      // grid rows of shared blocks, two tokens each
+    const uint32_t tag = ctl[0];                   // this call's partial-word tag
+    if ((int)blockIdx.y >= (int)gridDim.y - M) {   // the combine rows, one per token row (dispatched last)
+        static_assert(sizeof(s_h16) >= ROWS * 17 * sizeof(float), "combine values fit the staging buffer");
+        csr_combine<H, ROWS>(pw, tag, (int)blockIdx.y - ((int)gridDim.y - M), S, blockIdx.x * ROWS,
+                             reinterpret_cast<float *>(s_h16), y, y32, ctl + kTailRows);
+        return;
+    }
     if ((int)blockIdx.y < nsh) {                  // dispatched first
         const int t0 = blockIdx.y * 2;
         csr_down_shared<H, I, ROWS>(sh, hsh, logits, ld, gated, t0, min(M, t0 + 2), S, K, blockIdx.x * ROWS, s_h16,
-                                    s_hci, part);
+                                    s_hci, s_out, pw, tag);
         return;
     }
     // as in k_csr_gateup: PAIRS, grid row y - nsh is a pair; csr, a distinct expert
@@ -571,35 +665,45 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
 #pragma unroll
             for (int st = 0; st < NST; st++) bs[q][st] = dec[q * NST + st];
     }
+    __shared__ int s_pr[kMaxRows];
     for (int j = 0; j < np; j++) {
         const int pr = PAIRS ? pair_at(ps, j) : pair[p0 + j];
         const float wp = g_wts[pr];
+        if (threadIdx.x == 0) s_pr[j] = pr;
 #pragma unroll
         for (int q = 0; q < RPG; q++) {
-            const int c = blockIdx.x * ROWS + q * GROUPS + grp;
             float d = down_dot<F, I, LPR, NST>(w[q], bs[q], s_h16, s_hci, j, l);
             d = group_sum<LPR>(d);
-            if (l == 0) part[((size_t)(pr / K) * S + pr % K) * H + c] = wp * (d * rs[q]);
+            if (l == 0) s_out[j * ROWS + q * GROUPS + grp] = wp * (d * rs[q]);
         }
+    }
+    // each pair's ROWS partials leave as one contiguous run of words (the
+    // write-through stores then fill whole memory segments)
+    __syncthreads();
+    for (int i = threadIdx.x; i < np * ROWS; i += 256) {
+        const int j = i / ROWS, r = i - j * ROWS;
+        const int pr = s_pr[j];
+        st_part(pw + ((size_t)(pr / K) * S + pr % K) * H + blockIdx.x * ROWS + r, s_out[i], tag);
     }
 }
 
 // ---- launchers -------------------------------------------------------------------
-// NVFP4 at M >= 7 keeps the routing launch: measured per layer (48 layers,
-// graph, A/B on one box) the pair-keyed form is 1.2-1.9 / 0.4 us slower at M
-// = 8 / 7 and 0 / 0.5 / 2 us faster at M = 6 / 5 / 1-3; INT8 is faster at every
-// M (1.9 us at M = 8, 2.2-2.8 us at M = 2-4).
-bool csr_routing_for(int fmt, int M) { return fmt == QFM_FMT_NVFP4 && M >= 7; }
+// NVFP4 at M = 8 keeps the routing launch: measured per layer (48 layers,
+// graph, A/B on one box, combine in the down launch) the pair-keyed form is
+// 0.9 us slower there and 0.4 us faster at M = 7 (and faster at every smaller
+// M); INT8 is faster pair-keyed at every M.
+bool csr_routing_for(int fmt, int M) { return fmt == QFM_FMT_NVFP4 && M >= 8; }
 
 int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,
                        int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
-                       void *xh16, float *part, uint16_t *y, float *y32, hipStream_t s) {
+                       void *xh16, unsigned long long *pw, uint32_t *ctl, uint16_t *y, float *y32, hipStream_t s) {
     const int K = g_cfg.K, E = g_cfg.E, P = M * K;
     if (M < 1 || M > kMaxRows || P > kMaxPairs || E != 512) {
         set_error(-2, "csr path: needs 1 <= M <= %d, M*top_k <= %d, 512 experts", kMaxRows, kMaxPairs); return -2;
     }
     const bool use_csr = csr_routing_for(fmt, M);
     if (use_csr && !csr) { set_error(-1, "csr path: the routing launch needs the csr buffer"); return -1; }
+    if (!pw || !ctl || K > 16) { set_error(-1, "csr path: needs the partial words and tags, top_k <= 16"); return -1; }
     ShPtrs sp{};
     if (sh) sp = *sh;
     const dim3 b256(256);
@@ -621,17 +725,17 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
                        dim3(kGuThreads), 0, s,                                                                   \
                        wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, xh, xci, K, RT, P,   \
                        hpair);                                                                                   \
-    hipLaunchKernelGGL((k_csr_down<F, HH, II, PAIRS>), dim3(HH / down_rows<F, II>(), P + (sh ? (M + 1) / 2 : 0)), b256, 0, s, wd, \
-                       a->i8s_down, bd, a->s2d_dev, hpair, wts, RT, P, part, K, sp, hsh, logits, ld, gated, M)
+    hipLaunchKernelGGL((k_csr_down<F, HH, II, PAIRS>), dim3(HH / down_rows<F, II>(), P + (sh ? (M + 1) / 2 : 0) + M), \
+                       b256, 0, s, wd, a->i8s_down, bd, a->s2d_dev, hpair, wts, RT, P, pw, K, sp, hsh, logits, ld,      \
+                       gated, M, ctl, y, y32)
 #define QFM_CSR_LAUNCH(F, HH, II)                                                                                   \
     if (use_csr) {                                                                                                \
         hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), dim3(xh ? 1024 : kTopkThreads), 0, s, logits, ld, M, K,      \
-                           g_cfg.renorm, sel, wts, csr, x, HH, xh, xci);                                         \
+                           g_cfg.renorm, sel, wts, csr, x, HH, xh, xci, ctl);                                    \
         QFM_CSR_KERNELS(F, HH, II, false, csr);                                                                   \
     } else {                                                                                                      \
         QFM_CSR_KERNELS(F, HH, II, true, sel);                                                                    \
-    }                                                                                                             \
-    launch_pf_combine(part, M, K + (sh ? 1 : 0), HH, y, y32, s)
+    }
     if (shape_2048()) {
         if (fmt == QFM_FMT_INT8) { QFM_CSR_LAUNCH(FmtI8, 2048, 512); } else { QFM_CSR_LAUNCH(FmtF4, 2048, 512); }
     } else if (shape_2560()) {

@@ -48,6 +48,8 @@ struct ShPtrs { const int8_t *qg, *qu, *qd; const float *sg, *su, *sd; };
 // count of bounded waits that ran out).
 constexpr int kTailRows = 8;
 constexpr int kTailSpinMax = 1 << 16;
+// The tag after c: c + 1, skipping 0 (zeroed words never carry a live tag).
+__host__ __device__ constexpr uint32_t next_tag(uint32_t c) { return c + 1u ? c + 1u : 1u; }
 struct RouteTail {
     unsigned long long *lw;
     uint32_t *ctl;
@@ -89,14 +91,19 @@ int launch_i8_down_m1(const Qf4ExpCache *c, const float *hidden, const float *wt
 //    gate/up keyed by pair (k_csr_gateup<PAIRS>: the first pair of each distinct
 //    expert reads the expert's rows once for all its pairs), down partials per
 //    (pair, row block) (k_csr_down<PAIRS>); hidden row = pair id;
-//  * true (NVFP4 at M >= 7): the router ran without the tail; a routing launch
+//  * true (NVFP4 at M = 8): the router ran without the tail; a routing launch
 //    (k_topk_csr: top-K of all rows, routing inversion into csr, INT8: the fp16
 //    chunks) runs first and the kernels take one distinct expert per grid row;
 //    hidden row = CSR position.
-// Then the combine (k_pf_combine); the shared expert's down rows are the down
-// launch's first grid rows. fmt: QFM_FMT_INT8 or QFM_FMT_NVFP4 for the routed
+// The down launch's last grid row then sums each output's partials (the
+// combine); the shared expert's down rows are its first grid rows. Partials
+// travel as 64-bit words (fp32 bits | tag << 32, agent-scope stores) in pw
+// [kTailRows][K+1][H], tag = ctl[0] after the routing step (the row-0 tag the
+// selection tail wrote, or bumped by the routing launch): one tag per call,
+// larger than any tag a word left by an earlier call carries.
+// fmt: QFM_FMT_INT8 or QFM_FMT_NVFP4 for the routed
 // experts. hsh: shared hidden [M][I] (from launch_router_shared); hpair: [M*K][I]
-// fp32; part: [M][K+1][H] fp32; xh16 (INT8): M*H*2 + M*(H/16)*8 bytes, 16-byte
+// fp32; xh16 (INT8): M*H*2 + M*(H/16)*8 bytes, 16-byte
 // aligned; csr: csr_ints(M*K) ints, 16-byte aligned (used by the routing
 // launch only): {n_exp, exp_id[P], exp_ptr[P+1], pair[P]} followed, at the next
 // multiple of 4 ints, by one 4-int descriptor per distinct-expert slot u < P:
@@ -108,7 +115,7 @@ __host__ __device__ constexpr int csr_desc_off(int P) { return (3 * P + 2 + 3) &
 __host__ __device__ constexpr int csr_ints(int P) { return csr_desc_off(P) + 4 * P; }
 int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,
                        int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
-                       void *xh16, float *part, uint16_t *y, float *y32, hipStream_t s);
+                       void *xh16, unsigned long long *pw, uint32_t *ctl, uint16_t *y, float *y32, hipStream_t s);
 
 // The fused forward on a caller-vouched workspace, without the section
 // profiler (qfm_moe_forward minus its event marks): the no-allocation entry.
@@ -123,7 +130,6 @@ void noalloc_prepare_current_device();
 size_t prefill_ws_bytes(int T);
 // y[t] = sum of the S owned partial slots part[t*S + k][H] in slot order (bf16 out,
 // or fp32 into y32 when y32 != nullptr)
-void launch_pf_combine(const float *part, int T, int S, int H, uint16_t *y, float *y32, hipStream_t s);
 // ctr: {candidate overflows (tokens whose logits were all recomputed), gate/up items, down items}
 void prefill_ws_view(void *ws, int T, float **lg_approx, int **sel, float **wts, int **ctr);
 // y32 != nullptr: y is written as fp32 there instead of bf16 into y

@@ -11,8 +11,8 @@
 // stand-in, not a device address): qfm_init (for the device current then) and
 // otherwise the first call on a device, with that device current, take the
 // array's device address with hipGetSymbolAddress and keep it per device
-// (each GPU holds its own copy). The M <= 8 path
-// writes every workspace word it later reads, so nothing has to start at zero.
+// (each GPU holds its own copy). The array starts zeroed, as the workspace's
+// tags require, and every call leaves them valid for the next.
 // Every call on one GPU uses that GPU's array: calls that overlap on one GPU
 // (two streams, two host threads) race and must be serialized by the caller.
 #include <mutex>
@@ -21,7 +21,7 @@
 
 namespace qfm {
 
-constexpr size_t kScratchBytes = size_t(2) << 20;   // the M <= 8 workspace at H = 2560 is ~1.3 MiB
+constexpr size_t kScratchBytes = size_t(3) << 20;   // the M <= 8 workspace at H = 2560, K = 10 is ~2.1 MiB
 constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];

@@ -1060,9 +1060,8 @@ k_pf_gemm(const int4 *__restrict__ items, const int *__restrict__ n_items, int w
     }
 }
 
-// y[t] = sum over the K (+ shared) owned partial slots of token t, in slot
-// order; four columns per thread (16-byte loads, all S in flight together).
-// y32 != nullptr: the sums are stored as fp32 there (y is not written).
+// Four sums to y as bf16 (round to nearest even), or to y32 as fp32 when
+// y32 != nullptr (y is then not written).
 __device__ __forceinline__ void store4(uint16_t *y, float *y32, size_t i, float a0, float a1, float a2, float a3) {
     if (y32) {
         *reinterpret_cast<float4 *>(y32 + i) = make_float4(a0, a1, a2, a3);
@@ -1071,26 +1070,6 @@ __device__ __forceinline__ void store4(uint16_t *y, float *y32, size_t i, float 
                                                        (uint32_t)f32_to_bf16(a2) | ((uint32_t)f32_to_bf16(a3) << 16));
     }
 }
-__global__ void __launch_bounds__(256)
-k_pf_combine(const float *__restrict__ part, int T, int S, int H, uint16_t *__restrict__ y, float *__restrict__ y32) {
-    constexpr int kMaxS = 17;
-    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;       // index of 4 outputs
-    if (i4 * 4 >= (size_t)T * H) return;
-    const size_t t = i4 * 4 / H, c = i4 * 4 - t * H;
-    float4 v[kMaxS];
-#pragma unroll
-    for (int k = 0; k < kMaxS; k++)
-        if (k < S) {
-            const f32x4_t q = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t *>(part + (t * S + k) * H + c));
-            v[k] = make_float4(q.x, q.y, q.z, q.w);
-        }
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int k = 0; k < kMaxS; k++)
-        if (k < S) { a.x += v[k].x; a.y += v[k].y; a.z += v[k].z; a.w += v[k].w; }
-    store4(y, y32, t * H + c, a.x, a.y, a.z, a.w);
-}
-
 // The prefill form: fp16 partials (the down GEMM's epilogue rounds each to
 // nearest after scaling its 64-column group by 2^k, k in partk), summed in
 // fp32 in slot order; four columns (8 bytes) per thread.
@@ -1123,10 +1102,6 @@ k_pf_combine_h(const uint16_t *__restrict__ part, const int8_t *__restrict__ par
     store4(y, y32, t * H + c, a[0], a[1], a[2], a[3]);
 }
 
-void launch_pf_combine(const float *part, int T, int S, int H, uint16_t *y, float *y32, hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)(((size_t)T * H / 4 + 255) / 256)), dim3(256), 0, s, part, T, S,
-                       H, y, y32);
-}
 
 // ---- launcher -------------------------------------------------------------------------
 // The carve-up of one configuration (qfm_prefill_layout.h): gate/up tiles of

@@ -52,15 +52,15 @@ __device__ __forceinline__ float canon_reduce_row(const float4 (&w)[NJ], const f
 //
 // With TAIL (the M <= 8 forward; tail.lw != nullptr) the launch also selects: each
 // router row's logits go out a second time as 64-bit words (fp32 bits | tag <<
-// 32, stored at agent scope), tag = ctl[m] + 1 for row m; the grid's last
+// 32, stored at agent scope), tag = next_tag(ctl[m]) for row m; the grid's last
 // blocks are then (INT8) x as scaled fp16 chunks (chunk16_to_f16, the fork
 // rows' dot16_i8h input) and one selector wave per row, which reads its row's
-// words until every tag is ctl[m] + 1 (bounded: a timeout is counted in
+// words until every tag is that tag (bounded: a timeout is counted in
 // ctl[kTailRows] and the words are used as found), ranks them from registers
 // (wave_topk_regs: the same selection as wave_topk), writes sel/wts and then
 // ctl[m] = the tag. Every router wave has read ctl before it writes a word, so
 // no wave of this launch reads the updated ctl[m]; the next call tags with
-// ctl[m] + 1 again, so words left by this call are never taken for the next
+// the tag after it, so words left by this call are never taken for the next
 // call's. A selector waits only on router waves dispatched before it, which
 // never wait, so the waits end.
 template <int NJ, int I, int MR, bool TAIL>
@@ -98,7 +98,7 @@ k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, con
         const int m = b - tail0 - nxb;              // selector of row m
         constexpr int EPL = 8;                      // E == 512 (checked by the host)
         __shared__ __align__(16) unsigned long long s_tk[kTopkLds];
-        const uint32_t tg = tail.ctl[m] + 1u;
+        const uint32_t tg = next_tag(tail.ctl[m]);
         const unsigned long long *row = tail.lw + (size_t)m * E;
         float v[EPL];
         uint32_t pend = 0u;
@@ -148,7 +148,7 @@ k_router_shared(const float *__restrict__ W, const float *__restrict__ bias, con
         for (int m0 = 0; m0 < M; m0 += MR) {
             // the tag of the row this lane ends with (lane r < MR: row m0 + r),
             // requested with the pass's x rows
-            const uint32_t tgl = (TAIL && lane < MR && m0 + lane < M) ? tail.ctl[m0 + lane] + 1u : 0u;
+            const uint32_t tgl = (TAIL && lane < MR && m0 + lane < M) ? next_tag(tail.ctl[m0 + lane]) : 0u;
             uint2 xp[MR][NJ];
 #pragma unroll
             for (int r = 0; r < MR; r++)

@@ -148,13 +148,14 @@ def test_plan_fits_the_bounds(shim, H, I, gu, dn):
 
 def test_library_sizes_match_the_layout(shim):
     """qfm_workspace_bytes (M > 8) = the workspace's tag header (256 bytes of row
-    tags + 8 rows x E 8-byte logit words, shared with the M <= 8 forward) + the
-    larger of the INT8 and NVFP4 layouts with the shared expert, at the tile
-    widths the library is built with."""
+    tags, 8 rows x E 8-byte logit words and 8 rows x (K + 1) slots x H 8-byte
+    partial words, kept by the M <= 8 forward) + the larger of the INT8 and
+    NVFP4 layouts with the shared expert, at the tile widths the library is
+    built with."""
     import qfm
     lib = qfm.load()
-    hdr = 256 + 8 * 512 * 8
     for H, I in SHAPES:
+        hdr = 256 + 8 * 512 * 8 + 8 * 11 * H * 8
         qfm.init(H, I, 512, 10, 1, 1)
         for T in TS:
             a = layout(shim, T, H, I, 512, 10, True, GU_I8, DN_I8)[2]["total"]
