@@ -6,8 +6,10 @@ eager work and synchronizations between the replays, and every replay must
 give the bits of the eager run of the same chain (the kernels write each
 output once, in a fixed order, so eager and replayed results are identical).
 The chain covers M = 1 (the single-row INT8 kernels), M = 8 (the fork-row
-kernels, INT8 and NVFP4) and a prefill (T = 37: the counters cleared by a fill
-kernel, never by a memset node).
+kernels, INT8 pair-keyed and NVFP4 with the routing launch), M = 4 NVFP4
+(pair-keyed: the selection in the router launch and the combine in the down
+launch, whose tags advance on every replay) and a prefill (T = 37: the
+counters cleared by a fill kernel, never by a memset node).
 """
 import ctypes as C
 import sys
@@ -36,7 +38,7 @@ def lib():
     return L
 
 
-@pytest.mark.parametrize("M,fmt,nl", [(1, 0, 4), (8, 0, 3), (8, 1, 3), (37, 0, 2)])
+@pytest.mark.parametrize("M,fmt,nl", [(1, 0, 4), (8, 0, 3), (8, 1, 3), (4, 1, 3), (37, 0, 2)])
 def test_graph_replays_match_eager(lib, M, fmt, nl):
     _say("graph chain M", M, "fmt", fmt, "layers", nl)
     qfm.init(H, 512, 512, 10, 1, 1)
