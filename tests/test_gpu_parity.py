@@ -370,6 +370,25 @@ def test_moe_layer_config_variants(lib, M, fmt, renorm, gated, bias):
         assert rel <= TOL
 
 
+@pytest.mark.parametrize("M,K,fmt", [(8, 16, 0), (8, 16, 1), (3, 1, 0), (5, 4, 1)])
+def test_moe_layer_top_k_edges(lib, M, K, fmt):
+    """Other top-K widths through the fork-row path: K = 16 at M = 8 fills all
+    128 pairs (both 64-pair ballot words, 17 combine slots per output), K = 1
+    and 4 leave rows sharing experts more often (several pairs per expert)."""
+    _say("layer top_k", K, "M", M, "int8" if fmt == 0 else "nvfp4")
+    _cfg(lib, K=K)
+    g = _run_layer(lib, M, 4, 13, x_layer=600 + K, fmt=fmt)
+    r = orc.moe_layer(2048, 512, 512, K, M, 4, 13, 600 + K, fmt=fmt)
+    _cfg(lib)
+    assert np.array_equal(g["logits"].view(np.uint32), r["logits"].view(np.uint32))
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    for m in range(M):
+        rel = _rel(g["y"][m], r["y"][m])
+        _say("  row", m, "max rel err", rel)
+        assert rel <= TOL
+
+
 def test_moe_layer_deterministic(lib):
     """Two runs of the same layer give identical bits (no atomics on outputs)."""
     _cfg(lib)
