@@ -116,7 +116,7 @@ static size_t ws_tag_bytes() {
 }
 
 struct WsLayout {
-    size_t ctl, lw, pw, logits, sel, wts, hidden, csr, xh16, total;
+    size_t ctl, lw, pw, logits, sel, wts, hidden, pdsc, xh16, total;
 };
 static WsLayout ws_layout(int M) {
     const Cfg &c = g_cfg;
@@ -129,7 +129,7 @@ static WsLayout ws_layout(int M) {
     w.sel = off;    off += align256((size_t)M * c.K * sizeof(int));
     w.wts = off;    off += align256((size_t)M * c.K * sizeof(float));
     w.hidden = off; off += align256((size_t)M * (c.K + 1) * c.I * sizeof(float));
-    w.csr = off;    off += align256((size_t)csr_ints(M * c.K) * sizeof(int));   // the routing launch's (NVFP4, M = 8)
+    w.pdsc = off;   off += align256((size_t)M * c.K * 16);                      // per-pair descriptors (NVFP4)
     w.xh16 = off;   off += align256((size_t)M * c.H * 2 + (size_t)M * (c.H / 16) * 8);   // fp16 activations + chunk scales
     w.total = off;
     return w;
@@ -404,12 +404,10 @@ static int forward_impl(const qfm_layer *L, const uint16_t *x, int M, uint16_t *
         }
         tail.K = c.K;
         tail.renorm = c.renorm;
-        int *csr = reinterpret_cast<int *>(b + w.csr);
-        const bool routing_launch = csr_routing_for(L->fmt, M);     // (NVFP4, M = 8: faster with it)
-        int rc = launch_router_shared(L->router, L->router_bias, g, sp, x, M, logits, ld, hsh, c.I, s, nullptr,
-                                      routing_launch ? nullptr : &tail);
-        if (!rc) rc = launch_csr_forward(L->arena, L->fmt, sp, x, logits, ld, g ? 1 : 0, M, hidden, hsh, sel, wts, csr,
-                                         b + w.xh16, reinterpret_cast<unsigned long long *>(b + w.pw),
+        int rc = launch_router_shared(L->router, L->router_bias, g, sp, x, M, logits, ld, hsh, c.I, s, nullptr, &tail);
+        if (!rc) rc = launch_csr_forward(L->arena, L->fmt, sp, x, logits, ld, g ? 1 : 0, M, hidden, hsh, sel, wts,
+                                         reinterpret_cast<int4 *>(b + w.pdsc), b + w.xh16,
+                                         reinterpret_cast<unsigned long long *>(b + w.pw),
                                          reinterpret_cast<uint32_t *>(b + w.ctl), y, y32, s);
         return rc;
     }

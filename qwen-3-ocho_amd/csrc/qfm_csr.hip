@@ -1,6 +1,5 @@
-// qfm_csr.hip -- multi-row decode (M <= 8 "Ocho" fork rows): routing
-// inversion + weight-once-per-distinct-expert gate/up and down, INT8 and
-// NVFP4 arenas.
+// qfm_csr.hip -- multi-row decode (M <= 8 "Ocho" fork rows): weight-once-per-
+// distinct-expert gate/up and down keyed by pair, INT8 and NVFP4 arenas.
 //
 // Reference behaviour: the M=8 CSR tier k_m8_build_csr / k_m8_gateup /
 // k_m8_downacc (ocho/amd_server/qf_moe_m8_wave64.hip:72-211, :261-299) and the
@@ -10,25 +9,17 @@
 // read once per distinct expert and dotted against all rows routed to it,
 // owned partials part[t][k][H] summed in k order (no atomics, deterministic).
 //
-// Launch sequence (all stream-ordered), after the router launch:
-//   pair-keyed form (INT8 at every M, NVFP4 at M <= 7): the router launch's
-//                  selection tail has written sel/wts (and, INT8, the fp16
-//                  activation chunks);
-//   CSR form (NVFP4 at M = 8, measured faster there):
-//   k_topk_csr     one block: the top-K of all M rows (one wave per row), then
-//                  the routing inversion in LDS (per-row expert bitmaps and
-//                  their word prefix counts, P = M*K <= 128 pairs); publishes
-//                  sel/wts/CSR. For INT8 a second set of waves meanwhile
-//                  writes the activations as scaled fp16 chunks
-//                  (chunk16_to_f16).
-//   k_csr_gateup   grid (I/rows, M*K), 256 threads. Pair-keyed: grid row y is
-//                  pair y; it works only if y is its expert's first pair, for
-//                  all of the expert's pairs (ballots over sel, pairs_of);
-//                  CSR: grid row y is the y-th distinct expert (a descriptor).
+// Launch sequence (all stream-ordered), after the router launch, whose
+// selection tail has written sel/wts (and, INT8, the activations as scaled
+// fp16 chunks):
+//   k_csr_gateup   grid (I/rows, M*K), 256 threads: grid row y is pair y; it
+//                  stores only if y is its expert's first pair, for all of the
+//                  expert's pairs (ballots over sel, pairs_of / pairs_from).
 //                  One lane group per gate/up row: the row pair is loaded
 //                  once, then dotted with the LDS-staged activation row of each
-//                  routed token. hidden is written per pair (row = pair id /
-//                  CSR position).
+//                  routed token. hidden is written per pair (row = pair id).
+//                  NVFP4: workgroup (0, y) also writes pair y's descriptor for
+//                  the down launch (pair_desc).
 //   k_csr_down     grid (H/ROWS, M*K + shared + M), 256 threads: the
 //                  expert's down rows [ROWS b, ROWS b + ROWS), its pairs'
 //                  hidden vectors staged in LDS as scaled fp16 chunks; writes
@@ -39,9 +30,8 @@
 //                  gamma_t * <Wd_sh[c], hsh_t> * sd_sh[c]. The last M grid
 //                  rows are the combine: y[t][c] = the sum of the S slots of
 //                  t in slot order, once every word carries the call's tag.
-// The pair set of an expert is the same in both forms (ascending pair id =
-// (token, k) order) and every sum runs in the same order: the two forms give
-// identical bits.
+// An expert's pairs are visited in ascending pair id, i.e. (token, k) order,
+// the order of the reference's CSR within one expert.
 // INT8 dots widen the codes to fp16 (dot16_i8h); NVFP4 gate/up converts e2m1
 // to bf16 pairs against the bf16 activations, NVFP4 down to fp16 pairs.
 #include "qfm_dev.h"
@@ -60,157 +50,6 @@ struct FmtI8 {
 struct FmtF4 {
     static constexpr int VPB = 2, VPC = 32;
 };
-
-// x slice for a chunk-strided lane layout: chunk q of a row covers values
-// [q*VPC, q*VPC + VPC); lane l of an LPR group owns chunks st*LPR + l.
-template <int K, int LPR, int VPC>
-__device__ __forceinline__ void load_slice_bf16(const uint16_t *x, int l, float (&xs)[K / (LPR * VPC)][VPC]) {
-    constexpr int NST = K / (LPR * VPC);
-#pragma unroll
-    for (int st = 0; st < NST; st++) {
-        const uint16_t *p = x + (st * LPR + l) * VPC;
-#pragma unroll
-        for (int q = 0; q < VPC / 8; q++) {
-            const uint4 a = *reinterpret_cast<const uint4 *>(p + q * 8);
-            const uint32_t d[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-            for (int b = 0; b < 4; b++) { xs[st][q * 8 + 2 * b] = bf16_lo(d[b]); xs[st][q * 8 + 2 * b + 1] = bf16_hi(d[b]); }
-        }
-    }
-}
-
-// ---- routing inversion in LDS ---------------------------------------------------
-struct CsrLds {
-    int sel[kMaxPairs];
-    float wts[kMaxPairs];
-    int pair[kMaxPairs];      // CSR position -> original pair index t*K + k
-    int exp_id[kMaxPairs];
-    int exp_ptr[kMaxPairs + 1];
-    uint32_t tbits[kMaxRows][512 / 32];   // per row: bitmap of its selected experts (E == 512)
-    int tpre[kMaxRows][512 / 32];         // per row: its selected experts in bitmap words [0, w)
-    uint32_t bits[512 / 32];              // union of the rows' bitmaps
-    int gpre[512 / 32 + 1];               // distinct experts in words [0, w); [16] = all
-    int n_exp;
-    alignas(16) unsigned long long tk[8][kTopkLds];
-};
-
-// Called by all threads of the block after sel of the P = M K pairs is in LDS
-// and tbits is zero; the K experts of a row are distinct (top-K). Position of
-// pair p = (t, k) with expert e in (expert, token, k) order
-//   #{q: e_q < e} + #{q < p: e_q == e}
-//   = sum over rows u of #{experts of u below e} + #{rows u < t selecting e},
-// and e's distinct index = #{distinct experts below e}: both read from the
-// per-row bitmaps and their word prefix counts (no scan over the pairs).
-__device__ __forceinline__ void csr_build_lds(CsrLds &c, int M, int K) {
-    const int P = M * K, i = threadIdx.x, wave = i >> 6, lane = i & 63;
-    if (i < P) {
-        const int e = c.sel[i];
-        atomicOr(&c.tbits[i / K][e >> 5], 1u << (e & 31));
-    }
-    __syncthreads();
-    if (wave < M && lane < 32) {
-        // lanes 0-15: row `wave`'s word w; lanes 16-31: the union's word w;
-        // exclusive prefix sums of the popcounts over the 16 words
-        const int w = lane & 15;
-        uint32_t b = 0u;
-        if (lane < 16) {
-            b = c.tbits[wave][w];
-        } else {
-            for (int u = 0; u < M; u++) b |= c.tbits[u][w];
-        }
-        const int pc = __popc(b);
-        int inc = pc;
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) {
-            const int o = __shfl_up(inc, d, 16);
-            if (w >= d) inc += o;
-        }
-        if (lane < 16) {
-            c.tpre[wave][w] = inc - pc;
-        } else if (wave == 0) {
-            c.bits[w] = b;
-            c.gpre[w] = inc - pc;
-            if (w == 15) c.gpre[16] = inc;
-        }
-    }
-    __syncthreads();
-    if (i < P) {
-        const int e = c.sel[i], t = i / K, w = e >> 5, sh = e & 31;
-        const uint32_t below = (1u << sh) - 1u;
-        int less = 0, before = 0;
-        for (int u = 0; u < M; u++) {
-            const uint32_t b = c.tbits[u][w];
-            less += c.tpre[u][w] + __popc(b & below);
-            before += u < t ? (int)((b >> sh) & 1u) : 0;
-        }
-        const int first_less = c.gpre[w] + __popc(c.bits[w] & below);
-        c.pair[less + before] = i;
-        if (before == 0) { c.exp_id[first_less] = e; c.exp_ptr[first_less] = less; }
-    }
-    if (i == 0) {
-        const int n = c.gpre[16];
-        c.n_exp = n;
-        c.exp_ptr[n] = P;
-    }
-    __syncthreads();
-}
-
-// ---- top-K of all rows + routing inversion: one block, one wave per row ---------
-// Published: sel/wts [M][K]; csr = {n_exp, exp_id[P], exp_ptr[P+1], pair[P]}
-// and the per-slot descriptors at csr_desc_off(P); ctl[0] = the call's tag.
-// With xh != nullptr, threads [kTopkThreads, blockDim.x) meanwhile write the
-// activations x [M][H] (bf16) as scaled fp16 chunks for the INT8 dot:
-// xh [M][H] fp16, xci [M][H/16] = (seed, 2^-k) of each 16-value chunk.
-constexpr int kTopkThreads = 512;
-template <int EPL>
-__global__ void __launch_bounds__(1024)
-k_topk_csr(const float *__restrict__ logits, int ld, int M, int K, int renorm, int *__restrict__ g_sel,
-           float *__restrict__ g_wts, int *__restrict__ g_csr, const uint16_t *__restrict__ x, int H,
-           uint4 *__restrict__ xh, float2 *__restrict__ xci, uint32_t *__restrict__ ctl) {
-    __shared__ CsrLds c;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int P = M * K;
-    if (threadIdx.x < kMaxRows * 16) (&c.tbits[0][0])[threadIdx.x] = 0u;
-    if (wave < M) {
-        int my_i;
-        float my_w;
-        wave_topk<EPL>(logits + (size_t)wave * ld, K, renorm, lane, c.tk[wave], my_i, my_w);
-        if (lane < K) { c.sel[wave * K + lane] = my_i; c.wts[wave * K + lane] = my_w; }
-    } else if (xh && (int)threadIdx.x >= kTopkThreads) {
-        const int nch = M * (H / 16);
-        for (int ch = threadIdx.x - kTopkThreads; ch < nch; ch += blockDim.x - kTopkThreads) {
-            const uint4 a = reinterpret_cast<const uint4 *>(x)[2 * ch], b = reinterpret_cast<const uint4 *>(x)[2 * ch + 1];
-            const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            float v[16];
-#pragma unroll
-            for (int i = 0; i < 8; i++) { v[2 * i] = bf16_lo(d[i]); v[2 * i + 1] = bf16_hi(d[i]); }
-            uint4 ha, hb;
-            xci[ch] = chunk16_to_f16(v, ha, hb);
-            xh[2 * ch] = ha;
-            xh[2 * ch + 1] = hb;
-        }
-    }
-    __syncthreads();
-    csr_build_lds(c, M, K);
-    for (int i = threadIdx.x; i < P; i += blockDim.x) {
-        g_sel[i] = c.sel[i]; g_wts[i] = c.wts[i];
-        g_csr[1 + i] = c.exp_id[i];
-        g_csr[1 + P + (P + 1) + i] = c.pair[i];
-    }
-    for (int i = threadIdx.x; i <= P; i += blockDim.x) g_csr[1 + P + i] = c.exp_ptr[i];
-    if (threadIdx.x == 0) {
-        g_csr[0] = c.n_exp;
-        ctl[0] = next_tag(ctl[0]);                // this call's partial-word tag (k_csr_down)
-    }
-    for (int u = threadIdx.x; u < P; u += blockDim.x) {
-        int4 d = make_int4(-1, P, 0, 0);
-        if (u < c.n_exp) {
-            const int p0 = c.exp_ptr[u], np = c.exp_ptr[u + 1] - p0;
-            d = make_int4(c.exp_id[u], p0 | (np << 16), c.pair[p0], np > 1 ? c.pair[p0 + 1] : 0);
-        }
-        reinterpret_cast<int4 *>(g_csr + csr_desc_off(P))[u] = d;
-    }
-}
 
 // ---- the pairs of an expert, from sel -------------------------------------------
 // Pair q = t K + k of the P = M K pairs has expert sel[q] (written by the router
@@ -231,11 +70,12 @@ __device__ __forceinline__ int next_pair(unsigned long long &a, unsigned long lo
     else if (c) { q = 64 + (int)__builtin_ctzll(c); c &= c - 1ull; }
     return __builtin_amdgcn_readfirstlane(q);
 }
-__device__ __forceinline__ PairSet pairs_of(const int *__restrict__ sel, int P, int p) {
+// the pair set of pair p with expert e, from s0 = sel[lane] and s1 = sel[lane +
+// 64] (-1 past P) already loaded
+__device__ __forceinline__ PairSet pairs_from(int s0, int s1, int e, int p) {
     const int lane = threadIdx.x & 63;
     PairSet r;
-    r.e = __builtin_amdgcn_readfirstlane(sel[p]);
-    const int s0 = lane < P ? sel[lane] : -1, s1 = lane + 64 < P ? sel[lane + 64] : -1;
+    r.e = e;
     unsigned long long a = __ballot(s0 == r.e), c = __ballot(s1 == r.e);
     r.a = a;
     r.c = c;
@@ -255,6 +95,35 @@ __device__ __forceinline__ PairSet pairs_of(const int *__restrict__ sel, int P, 
         r.pl = (lane < na ? 0 : 64) + (m ? (int)__builtin_ctzll(m) : 0);
     }
     return r;
+}
+__device__ __forceinline__ PairSet pairs_of(const int *__restrict__ sel, int P, int p) {
+    const int lane = threadIdx.x & 63;
+    const int e = __builtin_amdgcn_readfirstlane(sel[p]);
+    return pairs_from(lane < P ? sel[lane] : -1, lane + 64 < P ? sel[lane + 64] : -1, e, p);
+}
+// NVFP4: the down launch's view of grid row y, written by the gate/up launch's
+// workgroup (0, y): {expert or -1 (not an owner), np, pair ids 0-3 and 4-7 as
+// bytes (P <= 128)}: one 16-byte scalar load gives a down workgroup its expert
+// and every pair (the ballots over sel cost a vector round trip more).
+struct PairBytes {
+    uint32_t lo, hi;
+};
+__device__ __forceinline__ int4 pair_desc(const PairSet &ps) {
+    unsigned long long a = ps.a, c = ps.c;
+    uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+    for (int j = 0; j < kMaxRows; j++) {
+        if (j < ps.np) {
+            const uint32_t q = (uint32_t)next_pair(a, c);
+            if (j < 4) lo |= q << (8 * j);
+            else hi |= q << (8 * (j - 4));
+        }
+    }
+    return make_int4(ps.e, ps.e < 0 ? 0 : ps.np, (int)lo, (int)hi);
+}
+// pair j of the list (j < kMaxRows; per thread or wave-uniform)
+__device__ __forceinline__ int pair_of_lane(const PairBytes &pb, int j) {
+    return (int)(((j < 4 ? pb.lo : pb.hi) >> (8 * (j & 3))) & 0xFFu);
 }
 // pair j of the set: j wave-uniform (readlane) or per thread (shuffle)
 __device__ __forceinline__ int pair_at(const PairSet &ps, int j) { return __builtin_amdgcn_readlane(ps.pl, j); }
@@ -281,14 +150,14 @@ constexpr int kGuThreads = QFM_GU_THREADS;
 // (A persistent form over tile ranges with two tiles of weights in flight was
 // slower: its registers allowed two waves per SIMD instead of four, and the
 // dot and reduction latencies then went unhidden.)
-template <class F, int H, int I, bool PAIRS>
+template <class F, int H, int I>
 __global__ void __launch_bounds__(kGuThreads)
 k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
              const float *__restrict__ Sg, const float *__restrict__ Su,          // INT8 row scales
              const uint8_t *__restrict__ Bg, const uint8_t *__restrict__ Bu,      // NVFP4 block scales
              const float *__restrict__ s2g, const float *__restrict__ s2u,        // NVFP4 per-expert scale
              const uint16_t *__restrict__ x, const uint4 *__restrict__ xh, const float2 *__restrict__ xci,
-             int K, const int *__restrict__ rt, int P, float *__restrict__ hpair) {
+             int K, const int *__restrict__ sel, int P, float *__restrict__ hpair, int4 *__restrict__ pdsc) {
     constexpr bool I8 = F::VPB == 1;
     constexpr int ROWB = H / F::VPB;             // bytes per gate/up row
     constexpr int LPR = gateup_lpr<F, H>();      // lanes per row
@@ -301,26 +170,31 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
     static_assert(XQ % 64 == 0 && (NCH * 2) % 64 == 0, "rows are staged in 64-lane wave loads");
     __shared__ uint4 s_x[PG * XQ];
     __shared__ float2 s_ci[I8 ? PG * NCH : 1];
-    // PAIRS (rt = sel): grid row y is pair y, run by its expert's first pair
-    // (pairs_of); otherwise (rt = the routing launch's csr buffer) grid row y is
-    // the y-th distinct expert, found with one 16-byte descriptor load
-    int e, np, p0 = 0;
-    int4 dsc = make_int4(0, 0, 0, 0);
-    unsigned long long pa = 0ull, pc = 0ull;     // PAIRS: pairs not staged yet, ascending
-    if constexpr (PAIRS) {
-        const PairSet ps = pairs_of(rt, P, blockIdx.y);
+    // grid row y is pair y; its expert's first pair (the owner) stores
+    int e, np;
+    unsigned long long pa = 0ull, pc = 0ull;     // pairs not staged yet, ascending
+    // NVFP4 (SPEC): the pair's expert is known after one scalar load and the
+    // owner test needs the ballots over sel (vector loads, ~0.35 us more per
+    // block, wall-clock stamps): sel is requested, then the weights, and only
+    // then are the ballots taken; a block that is not its expert's owner runs
+    // without storing. INT8, bound by the weight stream, keeps the owner test
+    // first (the non-owners' loads cost it more than the wait).
+    constexpr bool SPEC = !I8;
+    bool owner = true;
+    int s0 = -1, s1 = -1;                        // SPEC: sel[lane], sel[lane + 64]
+    if constexpr (SPEC) {
+        const int lane = threadIdx.x & 63;
+        e = __builtin_amdgcn_readfirstlane(sel[blockIdx.y]);
+        s0 = lane < P ? sel[lane] : -1;
+        s1 = lane + 64 < P ? sel[lane + 64] : -1;
+        args_now(e, Wg, Wu);
+        np = 0;
+    } else {
+        const PairSet ps = pairs_of(sel, P, blockIdx.y);
         args_now(ps.e, Wg, Wu);                  // (the weight bases requested with sel, before the branch)
         e = ps.e; np = ps.np; pa = ps.a; pc = ps.c;
-    } else {
-        dsc = reinterpret_cast<const int4 *>(rt + csr_desc_off(P))[blockIdx.y];   // one load before any weight
-        // keep the descriptor one 16-byte load and the weight bases loaded before
-        // the branch (the compiler otherwise sinks each field, and each kernel
-        // argument, below the branch that first needs it: a round trip apiece)
-        args_now(dsc.x, dsc.y, dsc.z, dsc.w, Wg, Wu);
-        e = dsc.x; p0 = dsc.y & 0xFFFF; np = dsc.y >> 16;
     }
-    if (e < 0) return;                           // not an expert's first pair / past the last expert
-    const int *pair = rt + 1 + P + P + 1;        // csr: CSR position -> pair id
+    if (e < 0) return;                           // not its expert's first pair (INT8)
     const int l = threadIdx.x % LPR;
     const int row = blockIdx.x * RPB + threadIdx.x / LPR;
     const size_t roff = ((size_t)e * I + row) * ROWB;
@@ -343,26 +217,22 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
     } else {
         rsg = Sg[(size_t)e * I + row]; rsu = Su[(size_t)e * I + row];
     }
+    if constexpr (SPEC) {
+        __builtin_amdgcn_sched_barrier(0);       // (the weights stay requested before the ballots wait on sel)
+        const PairSet ps = pairs_from(s0, s1, e, blockIdx.y);
+        owner = ps.e >= 0;
+        np = ps.np; pa = ps.a; pc = ps.c;
+        __builtin_assume(np >= 1);               // (pair y itself: no loop guard to sink the scale loads under)
+        if (blockIdx.x == 0 && threadIdx.x == 0) pdsc[blockIdx.y] = pair_desc(ps);   // for the down launch
+    }
     const uint4 *src = I8 ? xh : reinterpret_cast<const uint4 *>(x);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     static_assert(PG == 2, "two staged rows per group (pq0, pq1)");
     for (int j0 = 0; j0 < np; j0 += PG) {
         const int ng = min(PG, np - j0);
-        // staged row j's pair id and hidden row (PAIRS: row = pair id; csr: row =
-        // CSR position, pair id from the descriptor for the first two)
-        int pq0 = 0, pq1 = 0;
-        if constexpr (PAIRS) {
-            pq0 = next_pair(pa, pc);
-            pq1 = next_pair(pa, pc);
-        }
-        auto pair_id = [&](int j) -> int {
-            if constexpr (PAIRS) return j == 0 ? pq0 : pq1;
-            else return j0 + j == 0 ? dsc.z : j0 + j == 1 ? dsc.w : pair[p0 + j0 + j];
-        };
-        auto hid_row = [&](int j) -> int {
-            if constexpr (PAIRS) return j == 0 ? pq0 : pq1;
-            else return p0 + j0 + j;
-        };
+        // the group's pair ids (= their hidden rows)
+        const int pq0 = next_pair(pa, pc), pq1 = next_pair(pa, pc);
+        auto pair_id = [&](int j) -> int { return j == 0 ? pq0 : pq1; };
         if (j0 > 0) __syncthreads();             // the previous group's rows are consumed
         // straight into LDS (global_load_lds: lane i of a wave load writes base + 16 i / 4 i)
         for (int k = wave; k < ng * (XQ / 64); k += NW) {
@@ -407,7 +277,7 @@ k_csr_gateup(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
             }
             ag = group_sum<LPR>(ag);
             au = group_sum<LPR>(au);
-            if (l == 0) hpair[(size_t)hid_row(j) * I + row] = silu(ag * rsg) * (au * rsu);
+            if (owner && l == 0) hpair[(size_t)pair_id(j) * I + row] = silu(ag * rsg) * (au * rsu);
         }
     }
 }
@@ -572,7 +442,7 @@ constexpr int down_rows() {
     constexpr int want = F::VPB == 1 ? QFM_DOWN_ROWS_I8 : QFM_DOWN_ROWS_F4;
     return want > 256 / lpr_of(I / F::VPB / 16) ? want : 256 / lpr_of(I / F::VPB / 16);
 }
-template <class F, int H, int I, bool PAIRS>
+template <class F, int H, int I>
 __global__ void __launch_bounds__(256)
 k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const uint8_t *__restrict__ Bd,
            const float *__restrict__ s2d, const float *__restrict__ hpair, const float *__restrict__ g_wts,
@@ -604,34 +474,34 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
                                     s_hci, s_out, pw, tag);
         return;
     }
-    // as in k_csr_gateup: PAIRS, grid row y - nsh is a pair; csr, a distinct expert
+    // as in k_csr_gateup, grid row y - nsh is a pair, run by its expert's first
+    // pair: INT8 from the ballots over sel (rt = sel), NVFP4 from the gate/up
+    // launch's pair descriptor (rt = the descriptors; one scalar load; one
+    // pointer for both keeps the kernel arguments in three 64-byte lines)
+    constexpr bool DSC = F::VPB == 2;
     PairSet ps{};
-    int e, np, p0 = 0;
-    if constexpr (PAIRS) {
+    PairBytes pb{0u, 0u};
+    int e, np;
+    if constexpr (DSC) {
+        const int4 dsc = reinterpret_cast<const int4 *>(rt)[blockIdx.y - nsh];   // one load before any weight
+        args_now(dsc.x, dsc.y, dsc.z, dsc.w, Wd);
+        e = dsc.x; np = dsc.y; pb.lo = (uint32_t)dsc.z; pb.hi = (uint32_t)dsc.w;
+    } else {
         ps = pairs_of(rt, P, (int)blockIdx.y - nsh);
         args_now(ps.e, Wd);
         e = ps.e; np = ps.np;
-    } else {
-        const int4 dsc = reinterpret_cast<const int4 *>(rt + csr_desc_off(P))[blockIdx.y - nsh];
-        args_now(dsc.x, dsc.y, Wd);
-        e = dsc.x; p0 = dsc.y & 0xFFFF; np = dsc.y >> 16;
     }
-    if (e < 0) return;                           // not an expert's first pair / past the last expert
-    const int *pair = rt + 1 + P + P + 1;        // csr: CSR position -> pair id
+    if (e < 0) return;                           // not its expert's first pair
     const int l = threadIdx.x % LPR, grp = threadIdx.x / LPR;
     // the pairs' hidden rows first (in L2 or the memory-side cache: they arrive
     // before the weights, and loads retire in issue order, so their conversion
     // runs while the weights stream; M = 8 NVFP4 layer 47.1 -> 46.1 us)
     H16Stage<I, kMaxRows> hst;
-    if constexpr (PAIRS) {
-        hst.load_rows(hpair, ps, np);
-        // (their addresses wait for the pair list, the weights' only for e:
-        // without this barrier the scheduler issues the weights first and the
-        // conversion then waits for them)
-        __builtin_amdgcn_sched_barrier(0);
-    } else {
-        hst.load(hpair + (size_t)p0 * I, np);    // the expert's rows are contiguous in CSR order
-    }
+    if constexpr (DSC) hst.load_rows(hpair, pb, np);
+    else hst.load_rows(hpair, ps, np);
+    // (without this barrier the scheduler issues the weights first, whose
+    // addresses are ready earlier, and the conversion then waits for them)
+    __builtin_amdgcn_sched_barrier(0);
     // then the weights for this thread's rows (ROWS/GROUPS rows per group)
     constexpr int RPG = ROWS / GROUPS;
     uint4 w[RPG][NST];
@@ -667,7 +537,9 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
     }
     __shared__ int s_pr[kMaxRows];
     for (int j = 0; j < np; j++) {
-        const int pr = PAIRS ? pair_at(ps, j) : pair[p0 + j];
+        int pr;
+        if constexpr (DSC) pr = pair_of_lane(pb, j);
+        else pr = pair_at(ps, j);
         const float wp = g_wts[pr];
         if (threadIdx.x == 0) s_pr[j] = pr;
 #pragma unroll
@@ -687,23 +559,18 @@ k_csr_down(const uint8_t *__restrict__ Wd, const float *__restrict__ Sd, const u
     }
 }
 
-// ---- launchers -------------------------------------------------------------------
-// NVFP4 at M = 8 keeps the routing launch: measured per layer (48 layers,
-// graph, A/B on one box, combine in the down launch) the pair-keyed form is
-// 0.9 us slower there and 0.4 us faster at M = 7 (and faster at every smaller
-// M); INT8 is faster pair-keyed at every M.
-bool csr_routing_for(int fmt, int M) { return fmt == QFM_FMT_NVFP4 && M >= 8; }
-
+// ---- launcher ---------------------------------------------------------------------
 int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,
-                       int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
-                       void *xh16, unsigned long long *pw, uint32_t *ctl, uint16_t *y, float *y32, hipStream_t s) {
+                       int ld, int gated, int M, float *hpair, const float *hsh, const int *sel, const float *wts,
+                       int4 *pdsc, void *xh16, unsigned long long *pw, uint32_t *ctl, uint16_t *y, float *y32,
+                       hipStream_t s) {
     const int K = g_cfg.K, E = g_cfg.E, P = M * K;
     if (M < 1 || M > kMaxRows || P > kMaxPairs || E != 512) {
         set_error(-2, "csr path: needs 1 <= M <= %d, M*top_k <= %d, 512 experts", kMaxRows, kMaxPairs); return -2;
     }
-    const bool use_csr = csr_routing_for(fmt, M);
-    if (use_csr && !csr) { set_error(-1, "csr path: the routing launch needs the csr buffer"); return -1; }
-    if (!pw || !ctl || K > 16) { set_error(-1, "csr path: needs the partial words and tags, top_k <= 16"); return -1; }
+    if (!pdsc || !pw || !ctl || K > 16) {
+        set_error(-1, "csr path: needs the pair descriptors, partial words and tags, top_k <= 16"); return -1;
+    }
     ShPtrs sp{};
     if (sh) sp = *sh;
     const dim3 b256(256);
@@ -720,22 +587,15 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
         if (!a->w_gate || !a->s_gate || !a->s2g_dev) { set_error(-1, "csr path: arena has no NVFP4 blobs"); return -1; }
         wg = a->w_gate; wu = a->w_up; wd = a->w_down; bg = a->s_gate; bu = a->s_up; bd = a->s_down;
     }
-#define QFM_CSR_KERNELS(F, HH, II, PAIRS, RT)                                                                       \
-    hipLaunchKernelGGL((k_csr_gateup<F, HH, II, PAIRS>), dim3(II / (kGuThreads / gateup_lpr<F, HH>()), P),   \
-                       dim3(kGuThreads), 0, s,                                                                   \
-                       wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, xh, xci, K, RT, P,   \
-                       hpair);                                                                                   \
-    hipLaunchKernelGGL((k_csr_down<F, HH, II, PAIRS>), dim3(HH / down_rows<F, II>(), P + (sh ? (M + 1) / 2 : 0) + M), \
-                       b256, 0, s, wd, a->i8s_down, bd, a->s2d_dev, hpair, wts, RT, P, pw, K, sp, hsh, logits, ld,      \
-                       gated, M, ctl, y, y32)
 #define QFM_CSR_LAUNCH(F, HH, II)                                                                                   \
-    if (use_csr) {                                                                                                \
-        hipLaunchKernelGGL((k_topk_csr<8>), dim3(1), dim3(xh ? 1024 : kTopkThreads), 0, s, logits, ld, M, K,      \
-                           g_cfg.renorm, sel, wts, csr, x, HH, xh, xci, ctl);                                    \
-        QFM_CSR_KERNELS(F, HH, II, false, csr);                                                                   \
-    } else {                                                                                                      \
-        QFM_CSR_KERNELS(F, HH, II, true, sel);                                                                    \
-    }
+    hipLaunchKernelGGL((k_csr_gateup<F, HH, II>), dim3(II / (kGuThreads / gateup_lpr<F, HH>()), P),          \
+                       dim3(kGuThreads), 0, s,                                                                   \
+                       wg, wu, a->i8s_gate, a->i8s_up, bg, bu, a->s2g_dev, a->s2u_dev, x, xh, xci, K, sel, P,  \
+                       hpair, pdsc);                                                                             \
+    hipLaunchKernelGGL((k_csr_down<F, HH, II>), dim3(HH / down_rows<F, II>(), P + (sh ? (M + 1) / 2 : 0) + M),      \
+                       b256, 0, s, wd, a->i8s_down, bd, a->s2d_dev, hpair, wts,                                 \
+                       fmt == QFM_FMT_INT8 ? sel : reinterpret_cast<const int *>(pdsc), P, pw, K, sp, hsh,          \
+                       logits, ld, gated, M, ctl, y, y32)
     if (shape_2048()) {
         if (fmt == QFM_FMT_INT8) { QFM_CSR_LAUNCH(FmtI8, 2048, 512); } else { QFM_CSR_LAUNCH(FmtF4, 2048, 512); }
     } else if (shape_2560()) {
@@ -744,7 +604,6 @@ int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const ui
         set_error(-2, "csr path: unsupported shape"); return -2;
     }
 #undef QFM_CSR_LAUNCH
-#undef QFM_CSR_KERNELS
     return check_launch("csr_forward");
 }
 

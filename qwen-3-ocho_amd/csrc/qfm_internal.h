@@ -85,37 +85,24 @@ int launch_x8(const float *x, int8_t *q, float *sc, int n, hipStream_t s);
 int launch_i8_down_m1(const Qf4ExpCache *c, const float *hidden, const float *wts, const int *sel,
                       int nexp, const ShPtrs *sh, const float *gdot, float *y32, uint16_t *ybf, hipStream_t s);
 
-// Multi-row decode (1 <= M <= 8). Two routing forms:
-//  * csr_routing_for(fmt, M) false: launch_router_shared has run with its
-//    selection tail (sel/wts [M][K], INT8: the fp16 activation chunks in xh16);
-//    gate/up keyed by pair (k_csr_gateup<PAIRS>: the first pair of each distinct
-//    expert reads the expert's rows once for all its pairs), down partials per
-//    (pair, row block) (k_csr_down<PAIRS>); hidden row = pair id;
-//  * true (NVFP4 at M = 8): the router ran without the tail; a routing launch
-//    (k_topk_csr: top-K of all rows, routing inversion into csr, INT8: the fp16
-//    chunks) runs first and the kernels take one distinct expert per grid row;
-//    hidden row = CSR position.
-// The down launch's last grid row then sums each output's partials (the
-// combine); the shared expert's down rows are its first grid rows. Partials
-// travel as 64-bit words (fp32 bits | tag << 32, agent-scope stores) in pw
-// [kTailRows][K+1][H], tag = ctl[0] after the routing step (the row-0 tag the
-// selection tail wrote, or bumped by the routing launch): one tag per call,
-// larger than any tag a word left by an earlier call carries.
-// fmt: QFM_FMT_INT8 or QFM_FMT_NVFP4 for the routed
-// experts. hsh: shared hidden [M][I] (from launch_router_shared); hpair: [M*K][I]
-// fp32; xh16 (INT8): M*H*2 + M*(H/16)*8 bytes, 16-byte
-// aligned; csr: csr_ints(M*K) ints, 16-byte aligned (used by the routing
-// launch only): {n_exp, exp_id[P], exp_ptr[P+1], pair[P]} followed, at the next
-// multiple of 4 ints, by one 4-int descriptor per distinct-expert slot u < P:
-// {expert id or -1 past the last, p0 | np << 16, first pair, second pair}, so
-// a gate/up or down block finds everything it needs to start its loads with
-// one 16-byte load.
-bool csr_routing_for(int fmt, int M);
-__host__ __device__ constexpr int csr_desc_off(int P) { return (3 * P + 2 + 3) & ~3; }
-__host__ __device__ constexpr int csr_ints(int P) { return csr_desc_off(P) + 4 * P; }
+// Multi-row decode (1 <= M <= 8), after launch_router_shared with its selection
+// tail (sel/wts [M][K], INT8: the fp16 activation chunks in xh16): gate/up
+// keyed by pair (k_csr_gateup: the first pair of each distinct expert reads
+// the expert's rows once for all its pairs; hidden row = pair id), down
+// partials per (pair, row block) (k_csr_down), whose last M grid rows sum each
+// output's partials (the combine) and whose first grid rows are the shared
+// expert's down rows. Partials travel as 64-bit words (fp32 bits | tag << 32,
+// agent-scope stores) in pw [kTailRows][K+1][H], tag = ctl[0] as the selection
+// tail left it (row 0's tag): one tag per call, larger than any tag a word left
+// by an earlier call carries. fmt: QFM_FMT_INT8 or QFM_FMT_NVFP4 for the routed
+// experts. hsh: shared hidden [M][I] (from launch_router_shared); hpair:
+// [M*K][I] fp32; xh16 (INT8): M*H*2 + M*(H/16)*8 bytes, 16-byte aligned; pdsc:
+// M*K 16-byte pair descriptors (NVFP4: written by the gate/up launch, read by
+// the down launch).
 int launch_csr_forward(const Qf4ExpCache *a, int fmt, const ShPtrs *sh, const uint16_t *x, const float *logits,
-                       int ld, int gated, int M, float *hpair, const float *hsh, int *sel, float *wts, int *csr,
-                       void *xh16, unsigned long long *pw, uint32_t *ctl, uint16_t *y, float *y32, hipStream_t s);
+                       int ld, int gated, int M, float *hpair, const float *hsh, const int *sel, const float *wts,
+                       int4 *pdsc, void *xh16, unsigned long long *pw, uint32_t *ctl, uint16_t *y, float *y32,
+                       hipStream_t s);
 
 // The fused forward on a caller-vouched workspace, without the section
 // profiler (qfm_moe_forward minus its event marks): the no-allocation entry.

@@ -404,9 +404,7 @@ def test_moe_layer_workspace_reuse(lib, fmt):
     M <= 8 forward ranks each row in the router launch's tail from tagged logit
     words and combines tagged partial words in the down launch, with the tags
     at the workspace's start; its first 36 bytes are then {per-row tag =
-    number of tail calls that had that row (row 0: also the routing launches
-    of NVFP4 at M = 8, which bump it for the partial words), count of waits
-    that ran out = 0}."""
+    number of tail calls that had that row, count of waits that ran out = 0}."""
     _cfg(lib)
     H, K = 2048, 10
     seq = [8, 3, 37, 8, 5, 1, 6, 7]
@@ -435,10 +433,7 @@ def test_moe_layer_workspace_reuse(lib, fmt):
         for a, b in zip(got, ref):
             assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (i, M)
         if M <= 8 and not (fmt == 0 and M == 1):
-            if fmt == 1 and M == 8:
-                tags[0] += 1
-            else:
-                tags[:M] += 1
+            tags[:M] += 1
         hdr = ws.download(np.uint32, (9,))
         assert np.array_equal(hdr[:8], tags), (i, M, hdr)
         assert hdr[8] == 0, hdr
