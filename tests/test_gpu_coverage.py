@@ -317,7 +317,7 @@ def _paths(lib, F, x_rows, x_pf, rng):
     """Run every NVFP4 decode path on the current scale bytes. Returns a list of
     (name, y, x, sel, wts)."""
     out = []
-    g = _forward(lib, F.lay, x_rows, F.st)                       # fused fork-row CSR kernels (M = 2)
+    g = _forward(lib, F.lay, x_rows, F.st)                       # fused fork-row kernels (M = 2)
     out.append(("fused M=2", g["y"], x_rows, g["sel"], g["wts"]))
     p = _forward(lib, F.lay, x_pf, F.st)                         # prefill grouped GEMMs (T = 9)
     out.append(("prefill T=9", p["y"], x_pf, p["sel"], p["wts"]))

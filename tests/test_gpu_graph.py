@@ -6,10 +6,10 @@ eager work and synchronizations between the replays, and every replay must
 give the bits of the eager run of the same chain (the kernels write each
 output once, in a fixed order, so eager and replayed results are identical).
 The chain covers M = 1 (the single-row INT8 kernels), M = 8 (the fork-row
-kernels, INT8 pair-keyed and NVFP4 with the routing launch), M = 4 NVFP4
-(pair-keyed: the selection in the router launch and the combine in the down
-launch, whose tags advance on every replay) and a prefill (T = 37: the
-counters cleared by a fill kernel, never by a memset node).
+kernels, INT8 and NVFP4) and M = 4 NVFP4 (the selection in the router launch
+and the combine in the down launch, whose tags advance on every replay), and
+a prefill (T = 37: the counters cleared by a fill kernel, never by a memset
+node).
 """
 import ctypes as C
 import sys

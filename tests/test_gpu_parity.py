@@ -315,7 +315,7 @@ def _run_layer(lib, M, seed, layer, x_layer, fmt=qfm.QFM_FMT_INT8, bias=False):
                                                (1, 0, 5, 1), (8, 1, 6, 1), (3, 3, 7, 1)])
 def test_moe_layer(lib, M, seed, layer, fmt):
     """INT8 (fmt 0) and NVFP4 (fmt 1) routed experts; M=1 uses the single-row
-    kernels (INT8) or the CSR kernels (NVFP4); M>1 always the CSR kernels."""
+    kernels (INT8) or the fork-row kernels (NVFP4); M>1 always the fork-row kernels."""
     _say("layer", "int8" if fmt == 0 else "nvfp4", M, seed, layer)
     _cfg(lib)
     g = _run_layer(lib, M, seed, layer, x_layer=100 + layer, fmt=fmt)
