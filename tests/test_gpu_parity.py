@@ -389,6 +389,34 @@ def test_moe_layer_top_k_edges(lib, M, K, fmt):
         assert rel <= TOL
 
 
+def _sweep_cases():
+    rng = np.random.default_rng(2026)
+    out = []
+    for i in range(16):
+        out.append((int(rng.integers(1, 9)), int(rng.choice([2, 6, 10, 16])), int(rng.integers(0, 2)),
+                    int(rng.integers(0, 2)), int(rng.integers(0, 2)), bool(rng.integers(0, 2)), 700 + i))
+    return out
+
+
+@pytest.mark.parametrize("M,K,fmt,gated,renorm,bias,seed", _sweep_cases())
+def test_moe_layer_random_sweep(lib, M, K, fmt, gated, renorm, bias, seed):
+    """Seeded random configurations of the fused decode forward (rows, top-K,
+    format, gate, renorm, bias) against the oracle: the selection in the router
+    launch, pair-keyed gate/up and down and the combine in the down launch
+    across their combinations."""
+    _say("sweep", M, K, "int8" if fmt == 0 else "nvfp4", "gated", gated, "renorm", renorm, "bias", bias, "seed", seed)
+    _cfg(lib, K=K, renorm=renorm, gated=gated)
+    g = _run_layer(lib, M, seed, seed % 48, x_layer=seed, fmt=fmt, bias=bias)
+    r = orc.moe_layer(2048, 512, 512, K, M, seed, seed % 48, seed, fmt=fmt, gated=gated, renorm=renorm,
+                      use_bias=int(bias))
+    _cfg(lib)
+    assert np.array_equal(g["logits"].view(np.uint32), r["logits"].view(np.uint32))
+    assert np.array_equal(g["sel"], r["sel"])
+    assert np.allclose(g["wts"], r["w"], rtol=2e-6, atol=1e-7)
+    for m in range(M):
+        assert _rel(g["y"][m], r["y"][m]) <= TOL, m
+
+
 def test_moe_layer_deterministic(lib):
     """Two runs of the same layer give identical bits (no atomics on outputs)."""
     _cfg(lib)
