@@ -117,15 +117,15 @@ struct H16Stage {
             }
         }
     }
-    // rows h + ids.pair_of(j) * I for j < n (ids: a pair set whose j-th id a
-    // thread gets with a shuffle)
+    // rows h + pair_of_lane(ids, j) * I for j < n (ids: a pair set, whose j-th
+    // id a lane gets with a shuffle, or a pair descriptor's packed id bytes)
     template <class IDS>
     __device__ __forceinline__ void load_rows(const float *__restrict__ h, const IDS &ids, int n) {
 #pragma unroll
         for (int q = 0; q < CPT; q++) {
             const int c = (int)threadIdx.x + q * NT;
             const int j = c / (I / 16), o = c - j * (I / 16);
-            const int r = pair_of_lane(ids, j < RMAX ? j : 0);     // (every lane takes part in the shuffle)
+            const int r = pair_of_lane(ids, j < RMAX ? j : 0);     // (every lane calls it: a shuffle needs all)
             if (c < n * (I / 16)) {
                 const float4 *hp = reinterpret_cast<const float4 *>(h + (size_t)r * I) + 4 * o;
 #pragma unroll
