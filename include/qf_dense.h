@@ -40,7 +40,11 @@ int  qf8_i8_gemv_rows(const Qf8I8Multi *mm, const int8_t *xq, const float *xs, i
  *   hc_d = silu(down . normed / 4) [320];  inj = 2 sigmoid(inject . normed / 4) [4] (inject may be NULL)
  *   d8q/d8s = X8(hc_d);  hcy = up . hc_d [4H]
  *   mixed[j] = 1/4 sum_c sigmoid(hcy[c][j]) * normed[c][j] [H];  xq_out/xs_out = X8(mixed)
- * down [320][4H], inject [4][4H], up [4H][320] INT8 matrices. Replaces qf8_i8_hc_m1. */
+ * down [320][4H], inject [4][4H], up [4H][320] INT8 matrices. Replaces qf8_i8_hc_m1.
+ * One row (T = 1) runs as one launch whose up blocks take hc_d and normed from
+ * the down blocks through a hand-off area that the library keeps in device
+ * memory, one per GPU: one-row calls (here, qf8_i8_hc_rows and qfm_hc_premix
+ * at T = 1) that overlap in time on one GPU must be serialized by the caller. */
 void qf8_i8_hc_m1(float *normed, float *hc_d, float *mixed, float *inj, float *R, const uint16_t *wn,
                   const Qf8I8Mat *down, const Qf8I8Mat *inject, const Qf8I8Mat *up, int8_t *n8q, float *n8s,
                   int8_t *d8q, float *d8s, float *hcy, const float *y_prev, const float *inj_prev, int8_t *xq_out,
@@ -61,6 +65,11 @@ int  qfm_hc_premix(float *normed, float *hc_d, float *mixed, float *inj, float *
                    const Qf8I8Mat *down, const Qf8I8Mat *inject, const Qf8I8Mat *up, int8_t *n8q, float *n8s,
                    int8_t *d8q, float *d8s, float *hcy, const float *y_prev, const float *inj_prev, int8_t *xq_out,
                    float *xs_out, uint16_t *x_bf16, int T, hipStream_t s);
+/* The count of hand-off words whose bounded wait ran out in one-row pre-mixer
+ * calls on the current GPU since the library was loaded (0 unless a launch
+ * could not run its blocks together). Synchronous copy. No counterpart in the
+ * reference. 0, or -1 / -3 / -5. */
+int  qfm_hc_wait_timeouts(uint32_t *count);
 /* R[c][i] = fma(inj[c], y[i], R[c][i]) for the 4 streams: the MoE output
  * written back into the residual. Replaces qf8_stream_inject (qf8_dense.h:158,
  * qf8_hc.hip:99-103, :148-150). */

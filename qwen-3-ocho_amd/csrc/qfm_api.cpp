@@ -181,6 +181,7 @@ int qfm_init(const qfm_config *cfg) {
     g_cfg.H = cfg->hidden; g_cfg.I = cfg->inter; g_cfg.E = E; g_cfg.K = cfg->top_k;
     g_cfg.renorm = cfg->renorm ? 1 : 0; g_cfg.gated = cfg->shared_gated ? 1 : 0;
     noalloc_prepare_current_device();
+    hc_prepare_current_device();
     return 0;
 }
 

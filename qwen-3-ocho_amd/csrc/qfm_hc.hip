@@ -7,7 +7,10 @@
 // tile. Block dots are exact int32 (sdot4), scaled by the 32-value block
 // scale and accumulated in fp32, then summed over the LPR lanes with DPP.
 //
-// The pre-mixer runs in two launches:
+// One row (T = 1) runs in one launch, k_hc_one: k_hc_norm_down's blocks, which
+// also publish hc_d, the inject values and normed as tagged words, followed by
+// up blocks of 64 outputs that wait for those words (hc_up_body). T rows run
+// in two launches:
 //   k_hc_norm_down  one wave per down (silu(v/4)) or inject (2 sigmoid(v/4))
 //                   row, 2 rows per block; every block recomputes the fused
 //                   inject of the previous mixer, the zero-centred RMS norm
@@ -17,6 +20,8 @@
 //                   {c*H + j} of the up GEMV, the sigmoid-weighted mean over
 //                   the 4 streams and X8(mixed) of the 32 values, and the
 //                   residual's fused inject for those 4 x 32 entries.
+#include <mutex>
+
 #include "qfm_internal.h"
 #include "qfm_dev.h"
 #include "../../include/qf_dense.h"
@@ -89,6 +94,26 @@ k_gemv_i8x8(GemvBatch b, const int8_t *__restrict__ xq, const float *__restrict_
     }
 }
 
+// ---- hand-off area of the one-launch pre-mixer (T = 1) -----------------------------
+// 64-bit words (fp32 bits | tag << 32, agent-scope stores): [0, 320) hc_d,
+// [320, 324) the inject values, [324, 324 + 4H) normed. The call's tag is
+// next_tag(epoch): every block reads epoch at its start and the last up block
+// to finish reading its words advances it (arrivals counts them), so the next
+// call, stream-ordered after this one, uses the next tag and no word needs
+// clearing. The array starts zeroed (epoch 0, no live tag); timeouts counts
+// the words whose bounded wait ran out (0 unless something is badly wrong).
+constexpr int kHcNormed = QF8_HCL + QF8_HCC;
+constexpr int kHcWordsMax = kHcNormed + 4 * 2560;
+struct HcArea {
+    uint32_t epoch, arrivals, timeouts, pad[61];
+    unsigned long long w[kHcWordsMax];
+};
+static __device__ __align__(256) HcArea hc_area;
+
+__device__ __forceinline__ unsigned long long hc_word(float v, uint32_t tag) {
+    return (unsigned long long)__float_as_uint(v) | ((unsigned long long)tag << 32);
+}
+
 // Norm + X8 + down/inject GEMV in one launch. grid (rows / RB, T), 1024
 // threads: block b owns weight rows RB b .. RB b + RB - 1 (down rows first,
 // then the inject rows), the 16-byte steps of each row dealt round-robin to
@@ -102,12 +127,17 @@ k_gemv_i8x8(GemvBatch b, const int8_t *__restrict__ xq, const float *__restrict_
 // partial dots run against the LDS codes and are summed in wave order. The
 // fused inject's updated residual is not stored here (other blocks still read
 // R): k_hc_up_combine stores it.
-template <int NV, int RB>
-__global__ void __launch_bounds__(1024)
-k_hc_norm_down(const float *__restrict__ R, const uint16_t *__restrict__ wn, const float *__restrict__ y_prev,
-               const float *__restrict__ inj_prev, const int8_t *__restrict__ Wd, const float *__restrict__ Sd,
-               const int8_t *__restrict__ Wi, const float *__restrict__ Si, float *__restrict__ hc_d,
-               float *__restrict__ inj, float *__restrict__ normed, int8_t *__restrict__ q, float *__restrict__ sc) {
+//
+// With PUB (the one-launch pre-mixer, T = 1) the block also publishes what the
+// up blocks of the same launch read: its rows' values (hc_d, and the inject
+// values when pub_inj) and, in block 0, normed, as tagged words in A.
+template <int NV, int RB, bool PUB>
+__device__ __forceinline__ void
+hc_norm_down_body(int bx, const float *__restrict__ R, const uint16_t *__restrict__ wn,
+                  const float *__restrict__ y_prev, const float *__restrict__ inj_prev, const int8_t *__restrict__ Wd,
+                  const float *__restrict__ Sd, const int8_t *__restrict__ Wi, const float *__restrict__ Si,
+                  float *__restrict__ hc_d, float *__restrict__ inj, float *__restrict__ normed,
+                  int8_t *__restrict__ q, float *__restrict__ sc, HcArea *A, bool pub_inj) {
     constexpr int H = NV * 256, RS = 4 * H, NST = RS / 1024;
     __shared__ __align__(16) int8_t s_q[RS];
     __shared__ float s_s[RS / 32];
@@ -115,11 +145,14 @@ k_hc_norm_down(const float *__restrict__ R, const uint16_t *__restrict__ wn, con
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = tid >> 8, t256 = tid & 255;                  // stream, thread within the stream
     const size_t t = blockIdx.y;
+    // the call's tag (first: it is needed last and then has long arrived)
+    uint32_t tag = 0u;
+    if constexpr (PUB) tag = next_tag(__hip_atomic_load(&A->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     // RB rows per block, each row's 16-byte steps dealt round-robin to WPR waves
     constexpr int WPR = 16 / RB;
     constexpr int NSQ = (NST + WPR - 1) / WPR;                 // steps per wave (the last may be short)
     const int kq = wave % WPR, rloc = wave / WPR;
-    const int row = blockIdx.x * RB + rloc;
+    const int row = bx * RB + rloc;
     const int nrow = QF8_HCL + (Wi ? QF8_HCC : 0);
     const bool live = row < nrow;
     const bool is_inj = row >= QF8_HCL;
@@ -164,10 +197,11 @@ k_hc_norm_down(const float *__restrict__ R, const uint16_t *__restrict__ wn, con
         const int qi = x8_code(nv, s1);
         s_q[e] = (int8_t)qi;
         if ((tid & 31) == 0) s_s[e >> 5] = s1;
-        if (blockIdx.x == 0) {
+        if (bx == 0) {
             normed[t * RS + e] = nv;
             q[t * RS + e] = (int8_t)qi;
             if ((tid & 31) == 0) sc[(t * RS + e) >> 5] = s1;
+            if constexpr (PUB) st_agent_u64(&A->w[kHcNormed + e], hc_word(nv, tag));
         }
     }
     __syncthreads();
@@ -184,14 +218,32 @@ k_hc_norm_down(const float *__restrict__ R, const uint16_t *__restrict__ wn, con
     __shared__ float part[RB][WPR];
     if (lane == 0) part[rloc][kq] = a;
     __syncthreads();
-    if (tid < RB && blockIdx.x * RB + tid < nrow) {            // one lane per row: its WPR parts in order
-        const int r = blockIdx.x * RB + tid;
+    if (tid < RB && bx * RB + tid < nrow) {                    // one lane per row: its WPR parts in order
+        const int r = bx * RB + tid;
         float sum = part[tid][0];
 #pragma unroll
         for (int q = 1; q < WPR; q++) sum += part[tid][q];
-        if (r >= QF8_HCL) inj[t * QF8_HCC + r - QF8_HCL] = gemv_act(sum * Si[r - QF8_HCL], 2);
-        else hc_d[t * QF8_HCL + r] = gemv_act(sum * Sd[r], 1);
+        if (r >= QF8_HCL) {
+            const float v = gemv_act(sum * Si[r - QF8_HCL], 2);
+            inj[t * QF8_HCC + r - QF8_HCL] = v;
+            if constexpr (PUB)
+                if (pub_inj) st_agent_u64(&A->w[r], hc_word(v, tag));
+        } else {
+            const float v = gemv_act(sum * Sd[r], 1);
+            hc_d[t * QF8_HCL + r] = v;
+            if constexpr (PUB) st_agent_u64(&A->w[r], hc_word(v, tag));
+        }
     }
+}
+
+template <int NV, int RB>
+__global__ void __launch_bounds__(1024)
+k_hc_norm_down(const float *__restrict__ R, const uint16_t *__restrict__ wn, const float *__restrict__ y_prev,
+               const float *__restrict__ inj_prev, const int8_t *__restrict__ Wd, const float *__restrict__ Sd,
+               const int8_t *__restrict__ Wi, const float *__restrict__ Si, float *__restrict__ hc_d,
+               float *__restrict__ inj, float *__restrict__ normed, int8_t *__restrict__ q, float *__restrict__ sc) {
+    hc_norm_down_body<NV, RB, false>((int)blockIdx.x, R, wn, y_prev, inj_prev, Wd, Sd, Wi, Si, hc_d, inj, normed, q,
+                                     sc, nullptr, false);
 }
 
 // grid (H / 32, T), 512 threads: 8 waves x 16 row groups of 4 lanes = 128 up rows
@@ -271,6 +323,152 @@ k_hc_up_combine(const int8_t *__restrict__ Wu, const float *__restrict__ Su, con
     }
 }
 
+// The up / combine role of the one-launch pre-mixer: up block u owns the 64
+// outputs j0 = 64 u .. j0 + 63 (up rows {c*H + j}, 4 lanes per row over the
+// 320 codes, 1024 threads). It requests its weights and the residual inject's
+// operands, then waits for the words of the down blocks: hc_d (waves 0-4),
+// the inject values (wave 5, when the residual is updated here: once they
+// carry the call's tag every down block has read R), and its 4 x 64 normed
+// values (waves 6-9). The arithmetic is k_hc_up_combine's, value for value.
+template <int H>
+__device__ __forceinline__ void
+hc_up_body(int u, int nup, const int8_t *__restrict__ Wu, const float *__restrict__ Su, float *__restrict__ hcy,
+           float *__restrict__ mixed, int8_t *__restrict__ xq_out, float *__restrict__ xs_out,
+           int8_t *__restrict__ d8q, float *__restrict__ d8s, float *__restrict__ R, const float *__restrict__ y_prev,
+           const float *__restrict__ inj_prev, uint16_t *__restrict__ xb_out, HcArea *A, bool pub_inj) {
+    constexpr int L = QF8_HCL;
+    __shared__ __align__(16) int8_t s_q[L];
+    __shared__ float s_s[L / 32];
+    __shared__ float s_h[4][64], s_n[4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l = lane & 3;
+    const int j0 = u * 64;
+    const uint32_t tag = next_tag(__hip_atomic_load(&A->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const int li = tid >> 2, c = li >> 6, jj = li & 63;
+    const size_t row = (size_t)c * H + j0 + jj;
+    const int8_t *wr = Wu + row * L + l * 16;
+    i32x4 wv[L / 64];
+#pragma unroll
+    for (int st = 0; st < L / 64; st++) wv[st] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(wr + st * 64));
+    const float su = Su[row];
+    // the previous mixer's inject into R[rc][rj] (stored once the down blocks are done with R)
+    const bool rup = y_prev && tid < 256;
+    const int rc = tid >> 6, rj = j0 + lane;
+    float rv = 0.0f, iv = 0.0f, yv = 0.0f;
+    if (rup) {
+        rv = R[(size_t)rc * H + rj];
+        iv = inj_prev[rc];
+        yv = y_prev[rj];
+    }
+    int wi = -1;                                               // the word this thread waits for
+    if (wave < 5) wi = tid;
+    else if (wave == 5) wi = pub_inj && lane < QF8_HCC ? L + lane : -1;
+    else if (wave < 10) wi = kHcNormed + (tid / 64 - 6) * H + j0 + lane;
+    unsigned long long x = 0ull;
+    if (wi >= 0) x = ld_agent_u64(&A->w[wi]);
+    bool pend = wi >= 0 && (uint32_t)(x >> 32) != tag;
+    for (int it = 0; __builtin_amdgcn_ballot_w64(pend) != 0; it++) {
+        if (it == kTailSpinMax) {
+            if (pend) __hip_atomic_fetch_add(&A->timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        if (pend) {
+            x = ld_agent_u64(&A->w[wi]);
+            pend = (uint32_t)(x >> 32) != tag;
+        }
+    }
+    const float xv = __uint_as_float((uint32_t)x);
+    if (wave < 5) {                                            // X8(hc_d): five whole waves
+        float s1;
+        const int qi = x8_code(xv, s1);
+        s_q[tid] = (int8_t)qi;
+        if ((tid & 31) == 0) s_s[tid >> 5] = s1;
+        if (u == 0) {
+            d8q[tid] = (int8_t)qi;
+            if ((tid & 31) == 0) d8s[tid >> 5] = s1;
+        }
+    } else if (wave >= 6 && wave < 10) {
+        s_n[wave - 6][lane] = xv;
+    }
+    __syncthreads();
+    if (tid == 0) {                                            // every word of this block is read
+        const uint32_t old = __hip_atomic_fetch_add(&A->arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == (uint32_t)nup - 1u) {
+            __hip_atomic_store(&A->arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&A->epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int st = 0; st < L / 64; st++) {
+        const int e0 = st * 64 + l * 16;
+        acc = fmaf((float)dot16_i8i8(wv[st], *reinterpret_cast<const i32x4 *>(s_q + e0)), s_s[e0 >> 5], acc);
+    }
+    acc = group_sum<4>(acc);
+    if (l == 0) {
+        const float hv = acc * su;
+        hcy[row] = hv;
+        s_h[c][jj] = hv;
+    }
+    if (rup) R[(size_t)rc * H + rj] = fmaf(iv, yv, rv);
+    __syncthreads();
+    if (tid < 64) {
+        const int j = j0 + tid;
+        float sum = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            const float m = 1.0f / (1.0f + expf(-s_h[cc][tid]));
+            sum = fmaf(m, s_n[cc][tid], sum);
+        }
+        const float v = sum * 0.25f;
+        mixed[j] = v;
+        if (xb_out) xb_out[j] = f32_to_bf16(v);
+        float s1;
+        xq_out[j] = (int8_t)x8_code(v, s1);
+        if ((tid & 31) == 0) xs_out[j >> 5] = s1;
+    }
+}
+
+// The pre-mixer at T = 1 in one launch: grid (ndown + H / 64), 1024 threads;
+// blocks below ndown are k_hc_norm_down's blocks (publishing), the rest are
+// up blocks (last in the grid, so every down block is dispatched before any
+// up block waits; the waits are bounded either way).
+struct HcOneArgs {
+    const float *R;
+    const uint16_t *wn;
+    const float *y_prev, *inj_prev;
+    const int8_t *Wd;
+    const float *Sd;
+    const int8_t *Wi;
+    const float *Si;
+    float *hc_d, *inj, *normed;
+    int8_t *n8q;
+    float *n8s;
+    const int8_t *Wu;
+    const float *Su;
+    float *hcy, *mixed;
+    int8_t *xq_out;
+    float *xs_out;
+    int8_t *d8q;
+    float *d8s;
+    float *Rw;
+    uint16_t *xb_out;
+    HcArea *A;
+    int ndown;
+};
+
+template <int NV, int RB>
+__global__ void __launch_bounds__(1024) k_hc_one(HcOneArgs a) {
+    const int bx = (int)blockIdx.x;
+    const bool pub_inj = a.y_prev && a.Wi;
+    if (bx < a.ndown)
+        hc_norm_down_body<NV, RB, true>(bx, a.R, a.wn, a.y_prev, a.inj_prev, a.Wd, a.Sd, a.Wi, a.Si, a.hc_d, a.inj,
+                                        a.normed, a.n8q, a.n8s, a.A, pub_inj);
+    else
+        hc_up_body<NV * 256>(bx - a.ndown, (int)gridDim.x - a.ndown, a.Wu, a.Su, a.hcy, a.mixed, a.xq_out, a.xs_out,
+                             a.d8q, a.d8s, a.Rw, a.y_prev, a.inj_prev, a.xb_out, a.A, pub_inj);
+}
+
 __global__ void __launch_bounds__(256) k_stream_inject(float *__restrict__ R, const float *__restrict__ y,
                                                        const float *__restrict__ inj, int H) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -278,6 +476,40 @@ __global__ void __launch_bounds__(256) k_stream_inject(float *__restrict__ R, co
 }
 
 // ---- host side -------------------------------------------------------------------
+// Device address of this device's hand-off area (hipGetSymbolAddress once per
+// device, with that device current; host code never passes the array's name
+// to a kernel). nullptr and an error latched on failure.
+constexpr int kHcMaxDevices = 64;
+static HcArea *g_hc_area[kHcMaxDevices];
+static std::mutex g_hc_mu;
+
+static HcArea *hc_area_for_current_device(const char *who, bool latch = true) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kHcMaxDevices) {
+        if (latch) set_error(-5, "%s: no current device (or device index >= %d)", who, kHcMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_hc_mu);
+    if (!g_hc_area[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(hc_area));
+        if (e != hipSuccess || !p) {
+            if (latch) set_error(-5, "%s: hipGetSymbolAddress: %s", who, hipGetErrorString(e));
+            return nullptr;
+        }
+        g_hc_area[dev] = static_cast<HcArea *>(p);
+    }
+    return g_hc_area[dev];
+}
+
+// set-up from qfm_init: resolve the current device's area now (nothing done
+// when the host has no device)
+void hc_prepare_current_device() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) return;
+    (void)hc_area_for_current_device("qfm_init", false);
+}
+
 static int fill_batch(const Qf8I8Multi *mm, GemvBatch *b, int *maxr, const char *who) {
     if (!mm || mm->n < 1 || mm->n > 4) { set_error(-1, "%s: 1..4 matrices", who); return -1; }
     *b = GemvBatch{};
@@ -342,11 +574,23 @@ static int hc_impl(float *normed, float *hc_d, float *mixed, float *inj, float *
     }
     const int nrow = QF8_HCL + (inject ? QF8_HCC : 0);
     // two rows per block (162 blocks at the 2048 shape): 10.6 us per layer
-    // against 10.8 with four rows (81 blocks) and 12.6 with one
+    // against 10.8 with four rows (81 blocks) and 12.6 with one (two launches)
     constexpr int RB = 2;
-    const dim3 g1((unsigned)((nrow + RB - 1) / RB), (unsigned)T);
+    const int ndown = (nrow + RB - 1) / RB;
     const int8_t *wi = inject ? inject->w : nullptr;
     const float *si = inject ? inject->s : nullptr;
+    if (T == 1) {                                              // one launch, the up blocks last
+        HcArea *A = hc_area_for_current_device(who);
+        if (!A) return -5;
+        const HcOneArgs a{R,   wn,     y_prev, inj_prev, down->w, down->s, wi,     si, hc_d, inj,  normed, n8q,
+                          n8s, up->w,  up->s,  hcy,      mixed,   xq_out,  xs_out, d8q, d8s,  R,   xb_out, A,
+                          ndown};
+        const dim3 g((unsigned)(ndown + H / 64));
+        if (H == 2048) hipLaunchKernelGGL((k_hc_one<8, RB>), g, dim3(1024), 0, s, a);
+        else hipLaunchKernelGGL((k_hc_one<10, RB>), g, dim3(1024), 0, s, a);
+        return check_launch(who) ? -3 : 0;
+    }
+    const dim3 g1((unsigned)ndown, (unsigned)T);
     if (H == 2048)
         hipLaunchKernelGGL((k_hc_norm_down<8, RB>), g1, dim3(1024), 0, s, R, wn, y_prev, inj_prev, down->w, down->s, wi, si,
                            hc_d, inj, normed, n8q, n8s);
@@ -418,6 +662,17 @@ int qfm_hc_premix(float *normed, float *hc_d, float *mixed, float *inj, float *R
     if (T < 1 || T > 65535 || !x_bf16) { set_error(-1, "qfm_hc_premix: T = %d or no bf16 output", T); return -1; }
     return hc_impl(normed, hc_d, mixed, inj, R, wn, down, inject, up, n8q, n8s, d8q, d8s, hcy, y_prev, inj_prev,
                    xq_out, xs_out, T, s, "qfm_hc_premix", x_bf16);
+}
+
+int qfm_hc_wait_timeouts(uint32_t *count) {
+    if (!count) { set_error(-1, "qfm_hc_wait_timeouts: null count"); return -1; }
+    HcArea *A = hc_area_for_current_device("qfm_hc_wait_timeouts");
+    if (!A) return -5;
+    if (hipMemcpy(count, &A->timeouts, sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess) {
+        set_error(-3, "qfm_hc_wait_timeouts: hipMemcpy failed");
+        return -3;
+    }
+    return 0;
 }
 
 int qf8_stream_inject_ex(float *R, const float *y, const float *inj, hipStream_t s) {

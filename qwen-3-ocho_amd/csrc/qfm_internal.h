@@ -111,6 +111,8 @@ int forward_on_workspace(const qfm_layer *L, const uint16_t *x, int M, uint16_t 
 
 // Resolve the no-allocation entry's device array for the current device (qfm_init).
 void noalloc_prepare_current_device();
+// Resolve the one-launch pre-mixer's hand-off area for the current device (qfm_init).
+void hc_prepare_current_device();
 
 // Prefill (T > 8 rows): MFMA router + exact candidate selection, grouped
 // MFMA gate/up and down over the routing inversion, owned-partial combine.

@@ -229,6 +229,7 @@ _SIGS = {
     "qf8_i8_hc_m1_ex": (C.c_int, [vp] * 6 + [C.POINTER(Qf8I8Mat)] * 3 + [vp] * 9 + [vp]),
     "qf8_i8_hc_rows": (C.c_int, [vp] * 6 + [C.POINTER(Qf8I8Mat)] * 3 + [vp] * 9 + [C.c_int, vp]),
     "qfm_hc_premix": (C.c_int, [vp] * 6 + [C.POINTER(Qf8I8Mat)] * 3 + [vp] * 10 + [C.c_int, vp]),
+    "qfm_hc_wait_timeouts": (C.c_int, [C.POINTER(C.c_uint32)]),
     "qf8_stream_inject": (None, [vp, vp, vp, vp]),
     "qf8_stream_inject_ex": (C.c_int, [vp, vp, vp, vp]),
     "qf8_shexp": (None, [C.POINTER(Qf8ShexpW), vp, vp, vp, vp, vp, vp, vp]),

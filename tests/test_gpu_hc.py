@@ -170,3 +170,104 @@ def test_hc_rejects_bad_shapes(lib):
     assert lib.qf8_i8_hc_m1_ex(*common, C.byref(down.m), None, C.byref(up.m), p, p, p, p, p, p, None, p, p,
                                None) == -1                      # y_prev without inj_prev
     lib.qfm_last_error()
+
+
+def _hc_bufs(T, H):
+    RS, L = 4 * H, 320
+    return {nm: qfm.DevBuf(T * n) for nm, n in (("normed", RS * 4), ("hc_d", L * 4), ("mixed", H * 4), ("inj", 16),
+                                                ("n8q", RS), ("n8s", RS // 32 * 4), ("d8q", L), ("d8s", L // 32 * 4),
+                                                ("hcy", RS * 4), ("xq", H), ("xs", H // 32 * 4), ("xb", H * 2))}
+
+
+def _hc_call(lib, b, dR, dwn, mats, dyp, dip, with_inject, T, st):
+    down, inject, up = mats
+    args = [b["normed"].ptr, b["hc_d"].ptr, b["mixed"].ptr, b["inj"].ptr if with_inject else None, dR.ptr, dwn.ptr,
+            C.byref(down.m), C.byref(inject.m) if with_inject else None, C.byref(up.m), b["n8q"].ptr, b["n8s"].ptr,
+            b["d8q"].ptr, b["d8s"].ptr, b["hcy"].ptr, dyp.ptr if dyp else None, dip.ptr if dip else None,
+            b["xq"].ptr, b["xs"].ptr, b["xb"].ptr, T, st.h]
+    rc = lib.qfm_hc_premix(*args)
+    assert rc == 0, lib.qfm_last_error().decode()
+
+
+def _hc_bytes(b, T):
+    return {nm: buf.download(np.uint8, (T, buf.nbytes // T)) for nm, buf in b.items()}
+
+
+@pytest.mark.parametrize("H,with_inject,fused", [(2048, True, True), (2560, True, True), (2048, False, True),
+                                                 (2560, True, False), (2048, False, False)])
+def test_hc_one_launch_matches_two_launches(lib, H, with_inject, fused):
+    """One row runs as one launch (up blocks wait for the down blocks' tagged
+    words); T rows run as two launches. Both give the same bits for every
+    output and the updated residual, over consecutive calls (the hand-off tag
+    advancing) and over graph replays with eager calls between them; no
+    bounded wait runs out."""
+    _say("hc one launch vs two: H", H, "inject", with_inject, "fused inject", fused)
+    qfm.init(H, H // 4, 512, 10, 1, 1)
+    rng = np.random.default_rng(7 * H + with_inject + 2 * fused)
+    RS, L = 4 * H, 320
+    mats = (_Mat(rng, L, RS, 0.004), _Mat(rng, 4, RS, 0.004), _Mat(rng, RS, L, 0.02))
+    wn = (rng.uniform(-0.2, 0.2, RS).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    dwn = qfm.DevBuf.from_array(wn)
+    st = qfm.Stream()
+    before = C.c_uint32(0)
+    assert lib.qfm_hc_wait_timeouts(C.byref(before)) == 0, lib.qfm_last_error().decode()
+    one, two = _hc_bufs(1, H), _hc_bufs(2, H)
+    results = []
+    for k in range(3):
+        R0 = rng.standard_normal(RS).astype(np.float32)
+        yp = rng.standard_normal(H).astype(np.float32)
+        ip = rng.uniform(0, 2, 4).astype(np.float32)
+        dyp = qfm.DevBuf.from_array(yp) if fused else None
+        dip = qfm.DevBuf.from_array(ip) if fused else None
+        dyp2 = qfm.DevBuf.from_array(np.stack([yp, yp])) if fused else None
+        dip2 = qfm.DevBuf.from_array(np.stack([ip, ip])) if fused else None
+        dR1, dR2 = qfm.DevBuf.from_array(R0), qfm.DevBuf.from_array(np.stack([R0, R0]))
+        _hc_call(lib, one, dR1, dwn, mats, dyp, dip, with_inject, 1, st)
+        _hc_call(lib, two, dR2, dwn, mats, dyp2, dip2, with_inject, 2, st)
+        st.sync()
+        a, b = _hc_bytes(one, 1), _hc_bytes(two, 2)
+        for nm in one:
+            if nm == "inj" and not with_inject:
+                continue
+            assert np.array_equal(a[nm][0], b[nm][0]) and np.array_equal(b[nm][0], b[nm][1]), (k, nm)
+        r1, r2 = dR1.download(np.float32, (RS,)), dR2.download(np.float32, (2, RS))
+        assert np.array_equal(r1.view(np.uint32), r2[0].view(np.uint32)), k
+        if fused:
+            assert np.array_equal(r1.view(np.uint32), orc.stream_inject(R0, yp, ip).view(np.uint32)), k
+        results.append((R0, dyp, dip, a))
+    # graph: two one-row calls captured, replayed three times with eager calls between
+    R0, dyp, dip, ref = results[-1]
+    dRg = qfm.DevBuf.from_array(R0)
+    g_out = [_hc_bufs(1, H), _hc_bufs(1, H)]
+    qfm.check(lib.qfm_graph_capture_begin(st.h), "capture")
+    for bo in g_out:
+        _hc_call(lib, bo, dRg, dwn, mats, None, None, with_inject, 1, st)
+    g = lib.qfm_graph_capture_end(st.h)
+    assert g, lib.qfm_last_error().decode()
+    dRe = qfm.DevBuf.from_array(R0)
+    eager = _hc_bufs(1, H)
+    _hc_call(lib, eager, dRe, dwn, mats, None, None, with_inject, 1, st)
+    st.sync()
+    want = _hc_bytes(eager, 1)
+    for rep in range(3):
+        for bo in g_out:
+            for buf in bo.values():
+                buf.zero()
+        qfm.check(lib.qfm_graph_launch(g, st.h), "launch")
+        st.sync()
+        for bo in g_out:
+            got = _hc_bytes(bo, 1)
+            for nm in got:
+                if nm == "inj" and not with_inject:
+                    continue
+                assert np.array_equal(got[nm], want[nm]), (rep, nm)
+        _hc_call(lib, eager, dRe, dwn, mats, None, None, with_inject, 1, st)
+        st.sync()
+        again = _hc_bytes(eager, 1)
+        assert all(np.array_equal(again[nm], want[nm]) for nm in want if nm != "inj" or with_inject), rep
+    assert lib.qfm_graph_destroy(g) == 0
+    after = C.c_uint32(0)
+    assert lib.qfm_hc_wait_timeouts(C.byref(after)) == 0
+    assert after.value == before.value, (before.value, after.value)
+    st.destroy()
+    qfm.init(2560, 640, 512, 10, 1, 1)
