@@ -7,10 +7,12 @@
 // tile. Block dots are exact int32 (sdot4), scaled by the 32-value block
 // scale and accumulated in fp32, then summed over the LPR lanes with DPP.
 //
-// One row (T = 1) runs in one launch, k_hc_one: k_hc_norm_down's blocks, which
-// also publish hc_d, the inject values and normed as tagged words, followed by
-// up blocks of 64 outputs that wait for those words (hc_up_body). T rows run
-// in two launches:
+// One row (T = 1) runs in one launch, k_hc_one: slice blocks, each of which
+// norms one stream, X8-codes one 512-value K slice of it and publishes the
+// partial dots of 32 down / inject rows over that slice (and, in the first
+// row group, the slice's normed values) as tagged words, followed by up blocks
+// of 64 outputs that wait for those words, sum the partials in slice order and
+// run k_hc_up_combine's arithmetic (hc_up_body). T rows run in two launches:
 //   k_hc_norm_down  one wave per down (silu(v/4)) or inject (2 sigmoid(v/4))
 //                   row, 2 rows per block; every block recomputes the fused
 //                   inject of the previous mixer, the zero-centred RMS norm
@@ -95,14 +97,17 @@ k_gemv_i8x8(GemvBatch b, const int8_t *__restrict__ xq, const float *__restrict_
 }
 
 // ---- hand-off area of the one-launch pre-mixer (T = 1) -----------------------------
-// 64-bit words (fp32 bits | tag << 32, agent-scope stores): [0, 320) hc_d,
-// [320, 324) the inject values, [324, 324 + 4H) normed. The call's tag is
+// 64-bit words (fp32 bits | tag << 32, agent-scope stores): [0, 20 * 324) the
+// partial dots of the down / inject rows, slice s of row r at s * 324 + r
+// (slices 0 .. NS - 1, NS = 4H / 512), then normed [4H]. The call's tag is
 // next_tag(epoch): every block reads epoch at its start and the last up block
 // to finish reading its words advances it (arrivals counts them), so the next
 // call, stream-ordered after this one, uses the next tag and no word needs
 // clearing. The array starts zeroed (epoch 0, no live tag); timeouts counts
 // the words whose bounded wait ran out (0 unless something is badly wrong).
-constexpr int kHcNormed = QF8_HCL + QF8_HCC;
+constexpr int kHcSlice = 512;                               // K slice of a down block
+constexpr int kHcRows = QF8_HCL + QF8_HCC;                 // partial words per slice
+constexpr int kHcNormed = kHcRows * (4 * 2560 / kHcSlice);
 constexpr int kHcWordsMax = kHcNormed + 4 * 2560;
 struct HcArea {
     uint32_t epoch, arrivals, timeouts, pad[61];
@@ -127,17 +132,13 @@ __device__ __forceinline__ unsigned long long hc_word(float v, uint32_t tag) {
 // partial dots run against the LDS codes and are summed in wave order. The
 // fused inject's updated residual is not stored here (other blocks still read
 // R): k_hc_up_combine stores it.
-//
-// With PUB (the one-launch pre-mixer, T = 1) the block also publishes what the
-// up blocks of the same launch read: its rows' values (hc_d, and the inject
-// values when pub_inj) and, in block 0, normed, as tagged words in A.
-template <int NV, int RB, bool PUB>
-__device__ __forceinline__ void
-hc_norm_down_body(int bx, const float *__restrict__ R, const uint16_t *__restrict__ wn,
-                  const float *__restrict__ y_prev, const float *__restrict__ inj_prev, const int8_t *__restrict__ Wd,
-                  const float *__restrict__ Sd, const int8_t *__restrict__ Wi, const float *__restrict__ Si,
-                  float *__restrict__ hc_d, float *__restrict__ inj, float *__restrict__ normed,
-                  int8_t *__restrict__ q, float *__restrict__ sc, HcArea *A, bool pub_inj) {
+
+template <int NV, int RB>
+__global__ void __launch_bounds__(1024)
+k_hc_norm_down(const float *__restrict__ R, const uint16_t *__restrict__ wn, const float *__restrict__ y_prev,
+               const float *__restrict__ inj_prev, const int8_t *__restrict__ Wd, const float *__restrict__ Sd,
+               const int8_t *__restrict__ Wi, const float *__restrict__ Si, float *__restrict__ hc_d,
+               float *__restrict__ inj, float *__restrict__ normed, int8_t *__restrict__ q, float *__restrict__ sc) {
     constexpr int H = NV * 256, RS = 4 * H, NST = RS / 1024;
     __shared__ __align__(16) int8_t s_q[RS];
     __shared__ float s_s[RS / 32];
@@ -145,14 +146,11 @@ hc_norm_down_body(int bx, const float *__restrict__ R, const uint16_t *__restric
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = tid >> 8, t256 = tid & 255;                  // stream, thread within the stream
     const size_t t = blockIdx.y;
-    // the call's tag (first: it is needed last and then has long arrived)
-    uint32_t tag = 0u;
-    if constexpr (PUB) tag = next_tag(__hip_atomic_load(&A->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     // RB rows per block, each row's 16-byte steps dealt round-robin to WPR waves
     constexpr int WPR = 16 / RB;
     constexpr int NSQ = (NST + WPR - 1) / WPR;                 // steps per wave (the last may be short)
     const int kq = wave % WPR, rloc = wave / WPR;
-    const int row = bx * RB + rloc;
+    const int row = blockIdx.x * RB + rloc;
     const int nrow = QF8_HCL + (Wi ? QF8_HCC : 0);
     const bool live = row < nrow;
     const bool is_inj = row >= QF8_HCL;
@@ -197,11 +195,10 @@ hc_norm_down_body(int bx, const float *__restrict__ R, const uint16_t *__restric
         const int qi = x8_code(nv, s1);
         s_q[e] = (int8_t)qi;
         if ((tid & 31) == 0) s_s[e >> 5] = s1;
-        if (bx == 0) {
+        if (blockIdx.x == 0) {
             normed[t * RS + e] = nv;
             q[t * RS + e] = (int8_t)qi;
             if ((tid & 31) == 0) sc[(t * RS + e) >> 5] = s1;
-            if constexpr (PUB) st_agent_u64(&A->w[kHcNormed + e], hc_word(nv, tag));
         }
     }
     __syncthreads();
@@ -218,32 +215,14 @@ hc_norm_down_body(int bx, const float *__restrict__ R, const uint16_t *__restric
     __shared__ float part[RB][WPR];
     if (lane == 0) part[rloc][kq] = a;
     __syncthreads();
-    if (tid < RB && bx * RB + tid < nrow) {                    // one lane per row: its WPR parts in order
-        const int r = bx * RB + tid;
+    if (tid < RB && blockIdx.x * RB + tid < nrow) {            // one lane per row: its WPR parts in order
+        const int r = blockIdx.x * RB + tid;
         float sum = part[tid][0];
 #pragma unroll
         for (int q = 1; q < WPR; q++) sum += part[tid][q];
-        if (r >= QF8_HCL) {
-            const float v = gemv_act(sum * Si[r - QF8_HCL], 2);
-            inj[t * QF8_HCC + r - QF8_HCL] = v;
-            if constexpr (PUB)
-                if (pub_inj) st_agent_u64(&A->w[r], hc_word(v, tag));
-        } else {
-            const float v = gemv_act(sum * Sd[r], 1);
-            hc_d[t * QF8_HCL + r] = v;
-            if constexpr (PUB) st_agent_u64(&A->w[r], hc_word(v, tag));
-        }
+        if (r >= QF8_HCL) inj[t * QF8_HCC + r - QF8_HCL] = gemv_act(sum * Si[r - QF8_HCL], 2);
+        else hc_d[t * QF8_HCL + r] = gemv_act(sum * Sd[r], 1);
     }
-}
-
-template <int NV, int RB>
-__global__ void __launch_bounds__(1024)
-k_hc_norm_down(const float *__restrict__ R, const uint16_t *__restrict__ wn, const float *__restrict__ y_prev,
-               const float *__restrict__ inj_prev, const int8_t *__restrict__ Wd, const float *__restrict__ Sd,
-               const int8_t *__restrict__ Wi, const float *__restrict__ Si, float *__restrict__ hc_d,
-               float *__restrict__ inj, float *__restrict__ normed, int8_t *__restrict__ q, float *__restrict__ sc) {
-    hc_norm_down_body<NV, RB, false>((int)blockIdx.x, R, wn, y_prev, inj_prev, Wd, Sd, Wi, Si, hc_d, inj, normed, q,
-                                     sc, nullptr, false);
 }
 
 // grid (H / 32, T), 512 threads: 8 waves x 16 row groups of 4 lanes = 128 up rows
@@ -323,20 +302,111 @@ k_hc_up_combine(const int8_t *__restrict__ Wu, const float *__restrict__ Su, con
     }
 }
 
+// The down / inject role of the one-launch pre-mixer: block b owns K slice
+// s = b % NS (the 512 values 512 k .. 512 k + 511 of stream c, s = c * H / 512
+// + k) of the row group g = b / NS (rows 32 g .. 32 g + 31 of the 320 down rows
+// followed by the 4 inject rows). Threads 0..255 hold stream c as
+// k_hc_norm_down's stream threads do (thread t: elements i * 256 + t, with the
+// previous mixer's inject), so the sum of squares, rstd and the slice's normed
+// values and X8 codes are theirs bit for bit; X8 runs over the slice only
+// (two values per thread). Each half-wave then dots one row's 512 codes (16
+// bytes a lane, one exact int32 block dot scaled by its X8 scale) and
+// publishes the row's partial for slice s. Row group 0 stores the slice's
+// normed, X8 codes and scales and publishes normed.
+template <int NV>
+__device__ __forceinline__ void hc_slice_body(int b, const float *__restrict__ R, const uint16_t *__restrict__ wn,
+                                              const float *__restrict__ y_prev, const float *__restrict__ inj_prev,
+                                              const int8_t *__restrict__ Wd, const int8_t *__restrict__ Wi,
+                                              float *__restrict__ normed, int8_t *__restrict__ q,
+                                              float *__restrict__ sc, HcArea *A) {
+    constexpr int H = NV * 256, RS = 4 * H, SPS = H / kHcSlice, NS = 4 * SPS;
+    __shared__ __align__(16) int8_t s_q[kHcSlice];
+    __shared__ float s_s[kHcSlice / 32];
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int s = b % NS, g = b / NS;
+    const int c = s / SPS, k = s - c * SPS;                    // stream, slice within the stream
+    const uint32_t tag = next_tag(__hip_atomic_load(&A->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const int rloc = tid >> 5, l = tid & 31;
+    const int row = g * 32 + rloc;
+    const int nrow = QF8_HCL + (Wi ? QF8_HCC : 0);
+    const bool live = row < nrow;
+    const int8_t *wr = (row < QF8_HCL ? Wd + (size_t)row * RS : live ? Wi + (size_t)(row - QF8_HCL) * RS : Wd) +
+                       s * kHcSlice + l * 16;
+    // the stream's values and the slice's norm weights first (the norm waits
+    // only for these), then the weights, which stream meanwhile
+    const bool own = tid < 256;
+    float v[NV], yv[NV];
+    uint16_t wb0 = 0, wb1 = 0;
+    if (own) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = R[(size_t)c * H + i * 256 + tid];
+        wb0 = wn[(size_t)c * H + 2 * k * 256 + tid];
+        wb1 = wn[(size_t)c * H + (2 * k + 1) * 256 + tid];
+    }
+    const float sj = y_prev ? inj_prev[c] : 0.0f;
+    if (own && y_prev)
+#pragma unroll
+        for (int i = 0; i < NV; i++) yv[i] = y_prev[i * 256 + tid];
+    const i32x4 w = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(wr));
+    if (own) {                                                 // waves 0..3
+        if (y_prev)
+#pragma unroll
+            for (int i = 0; i < NV; i++) v[i] = fmaf(sj, yv[i], v[i]);
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NV; i++) acc = fmaf(v[i], v[i], acc);
+        acc = group_sum<64>(acc);
+        if (lane == 0) red[wave] = acc;
+    }
+    __syncthreads();
+    if (own) {
+        const float rstd = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + 1e-6f);
+        float v0 = v[0], v1 = v[1];
+#pragma unroll
+        for (int i = 1; i < NV / 2; i++)
+            if (k == i) { v0 = v[2 * i]; v1 = v[2 * i + 1]; }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int m = h * 256 + tid;                       // element of the slice
+            const float nv = (h ? v1 : v0) * rstd * (1.0f + bf16_to_f32(h ? wb1 : wb0));
+            float s1;
+            const int qi = x8_code(nv, s1);
+            s_q[m] = (int8_t)qi;
+            if ((tid & 31) == 0) s_s[m >> 5] = s1;
+            if (g == 0) {
+                const int e = c * H + k * kHcSlice + m;
+                normed[e] = nv;
+                q[e] = (int8_t)qi;
+                if ((tid & 31) == 0) sc[e >> 5] = s1;
+                st_agent_u64(&A->w[kHcNormed + e], hc_word(nv, tag));
+            }
+        }
+    }
+    __syncthreads();
+    float a = (float)dot16_i8i8(w, *reinterpret_cast<const i32x4 *>(s_q + l * 16)) * s_s[l >> 1];
+    a = group_sum<32>(a);
+    if (l == 0 && live) st_agent_u64(&A->w[s * kHcRows + row], hc_word(a, tag));
+}
+
 // The up / combine role of the one-launch pre-mixer: up block u owns the 64
 // outputs j0 = 64 u .. j0 + 63 (up rows {c*H + j}, 4 lanes per row over the
-// 320 codes, 1024 threads). It requests its weights and the residual inject's
-// operands, then waits for the words of the down blocks: hc_d (waves 0-4),
-// the inject values (wave 5, when the residual is updated here: once they
-// carry the call's tag every down block has read R), and its 4 x 64 normed
-// values (waves 6-9). The arithmetic is k_hc_up_combine's, value for value.
+// 320 codes, 1024 threads). It requests its weights, the row scales and the
+// residual inject's operands, then waits for the words of the down blocks:
+// the NS partials of down row tid (waves 0-4), of the inject rows (wave 5;
+// once every partial carries the call's tag every down block has read R), and
+// its 4 x 64 normed values (waves 6-9). hc_d / inject values are the
+// partials summed in slice order, scaled and activated; from there on the
+// arithmetic is k_hc_up_combine's, value for value.
 template <int H>
 __device__ __forceinline__ void
-hc_up_body(int u, int nup, const int8_t *__restrict__ Wu, const float *__restrict__ Su, float *__restrict__ hcy,
-           float *__restrict__ mixed, int8_t *__restrict__ xq_out, float *__restrict__ xs_out,
-           int8_t *__restrict__ d8q, float *__restrict__ d8s, float *__restrict__ R, const float *__restrict__ y_prev,
-           const float *__restrict__ inj_prev, uint16_t *__restrict__ xb_out, HcArea *A, bool pub_inj) {
-    constexpr int L = QF8_HCL;
+hc_up_body(int u, int nup, const float *__restrict__ Sd, const float *__restrict__ Si, bool has_inj,
+           const int8_t *__restrict__ Wu, const float *__restrict__ Su, float *__restrict__ hc_d,
+           float *__restrict__ inj, float *__restrict__ hcy, float *__restrict__ mixed, int8_t *__restrict__ xq_out,
+           float *__restrict__ xs_out, int8_t *__restrict__ d8q, float *__restrict__ d8s, float *__restrict__ R,
+           const float *__restrict__ y_prev, const float *__restrict__ inj_prev, uint16_t *__restrict__ xb_out,
+           HcArea *A) {
+    constexpr int L = QF8_HCL, NS = 4 * H / kHcSlice;
     __shared__ __align__(16) int8_t s_q[L];
     __shared__ float s_s[L / 32];
     __shared__ float s_h[4][64], s_n[4][64];
@@ -350,6 +420,9 @@ hc_up_body(int u, int nup, const int8_t *__restrict__ Wu, const float *__restric
 #pragma unroll
     for (int st = 0; st < L / 64; st++) wv[st] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(wr + st * 64));
     const float su = Su[row];
+    // the row whose partials this thread sums (down rows, then inject rows), or -1
+    const int dr = wave < 5 ? tid : wave == 5 && has_inj && lane < QF8_HCC ? L + lane : -1;
+    const float rsc = dr < 0 ? 0.0f : dr < L ? Sd[dr] : Si[dr - L];
     // the previous mixer's inject into R[rc][rj] (stored once the down blocks are done with R)
     const bool rup = y_prev && tid < 256;
     const int rc = tid >> 6, rj = j0 + lane;
@@ -359,45 +432,61 @@ hc_up_body(int u, int nup, const int8_t *__restrict__ Wu, const float *__restric
         iv = inj_prev[rc];
         yv = y_prev[rj];
     }
-    int wi = -1;                                               // the word this thread waits for
-    if (wave < 5) wi = tid;
-    else if (wave == 5) wi = pub_inj && lane < QF8_HCC ? L + lane : -1;
-    else if (wave < 10) wi = kHcNormed + (tid / 64 - 6) * H + j0 + lane;
-    unsigned long long x = 0ull;
-    if (wi >= 0) x = ld_agent_u64(&A->w[wi]);
-    bool pend = wi >= 0 && (uint32_t)(x >> 32) != tag;
-    for (int it = 0; __builtin_amdgcn_ballot_w64(pend) != 0; it++) {
-        if (it == kTailSpinMax) {
-            if (pend) __hip_atomic_fetch_add(&A->timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
+    // the words: waves 0-5 the NS partials of row dr (lanes with dr < 0 read
+    // row 0's and ignore them), all requested together and requested again
+    // until every one carries the call's tag (by the time the loads above
+    // have returned the slice blocks have mostly published); waves 6-9 one
+    // normed value each
+    float sum = 0.0f, w0 = 0.0f;
+    uint32_t bad = 0u;
+    if (wave < 6) {
+        const uint32_t off = (uint32_t)(dr < 0 ? 0 : dr);
+        unsigned long long x[NS];
+        for (int it = 0;;) {
+            uint32_t o = off;
+            asm volatile("" : "+v"(o));                        // addresses formed anew each pass, not kept live
+            const unsigned long long *wp = A->w + o;
+#pragma unroll
+            for (int i = 0; i < NS; i++) x[i] = ld_agent_u64(wp + i * kHcRows);
+            bad = 0u;
+#pragma unroll
+            for (int i = 0; i < NS; i++)
+                if (dr >= 0 && (uint32_t)(x[i] >> 32) != tag) bad |= 1u << i;
+            if (__builtin_amdgcn_ballot_w64(bad != 0u) == 0 || ++it >= kTailSpinMax) break;
+            __builtin_amdgcn_s_sleep(2);
         }
-        __builtin_amdgcn_s_sleep(2);
-        if (pend) {
-            x = ld_agent_u64(&A->w[wi]);
-            pend = (uint32_t)(x >> 32) != tag;
+        sum = __uint_as_float((uint32_t)x[0]);
+#pragma unroll
+        for (int i = 1; i < NS; i++) sum += __uint_as_float((uint32_t)x[i]);
+    } else if (wave < 10) {
+        const unsigned long long *wp = &A->w[kHcNormed + (wave - 6) * H + j0 + lane];
+        unsigned long long x = ld_agent_u64(wp);
+        for (int it = 0; (uint32_t)(x >> 32) != tag; it++) {   // (per lane; the wave leaves when all have)
+            if (it == kTailSpinMax) { bad = 1u; break; }
+            __builtin_amdgcn_s_sleep(2);
+            x = ld_agent_u64(wp);
         }
+        w0 = __uint_as_float((uint32_t)x);
     }
-    const float xv = __uint_as_float((uint32_t)x);
-    if (wave < 5) {                                            // X8(hc_d): five whole waves
+    if (bad) __hip_atomic_fetch_add(&A->timeouts, (uint32_t)__builtin_popcount(bad), __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    if (wave < 5) {                                            // hc_d and X8(hc_d): five whole waves
+        const float hv = gemv_act(sum * rsc, 1);
         float s1;
-        const int qi = x8_code(xv, s1);
+        const int qi = x8_code(hv, s1);
         s_q[tid] = (int8_t)qi;
         if ((tid & 31) == 0) s_s[tid >> 5] = s1;
         if (u == 0) {
+            hc_d[tid] = hv;
             d8q[tid] = (int8_t)qi;
             if ((tid & 31) == 0) d8s[tid >> 5] = s1;
         }
-    } else if (wave >= 6 && wave < 10) {
-        s_n[wave - 6][lane] = xv;
+    } else if (wave == 5) {
+        if (u == 0 && dr >= 0) inj[dr - L] = gemv_act(sum * rsc, 2);
+    } else if (wave < 10) {
+        s_n[wave - 6][lane] = w0;
     }
     __syncthreads();
-    if (tid == 0) {                                            // every word of this block is read
-        const uint32_t old = __hip_atomic_fetch_add(&A->arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == (uint32_t)nup - 1u) {
-            __hip_atomic_store(&A->arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&A->epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
     float acc = 0.0f;
 #pragma unroll
     for (int st = 0; st < L / 64; st++) {
@@ -412,15 +501,23 @@ hc_up_body(int u, int nup, const int8_t *__restrict__ Wu, const float *__restric
     }
     if (rup) R[(size_t)rc * H + rj] = fmaf(iv, yv, rv);
     __syncthreads();
+    if (tid == 64) {                                           // every word of this block is read (wave 1: no
+                                                               // combine work waits on the round trip)
+        const uint32_t old = __hip_atomic_fetch_add(&A->arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == (uint32_t)nup - 1u) {
+            __hip_atomic_store(&A->arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&A->epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
     if (tid < 64) {
         const int j = j0 + tid;
-        float sum = 0.0f;
+        float sm = 0.0f;
 #pragma unroll
         for (int cc = 0; cc < 4; cc++) {
             const float m = 1.0f / (1.0f + expf(-s_h[cc][tid]));
-            sum = fmaf(m, s_n[cc][tid], sum);
+            sm = fmaf(m, s_n[cc][tid], sm);
         }
-        const float v = sum * 0.25f;
+        const float v = sm * 0.25f;
         mixed[j] = v;
         if (xb_out) xb_out[j] = f32_to_bf16(v);
         float s1;
@@ -430,9 +527,9 @@ hc_up_body(int u, int nup, const int8_t *__restrict__ Wu, const float *__restric
 }
 
 // The pre-mixer at T = 1 in one launch: grid (ndown + H / 64), 1024 threads;
-// blocks below ndown are k_hc_norm_down's blocks (publishing), the rest are
-// up blocks (last in the grid, so every down block is dispatched before any
-// up block waits; the waits are bounded either way).
+// blocks below ndown = NS * ceil(rows / 32) are slice blocks (hc_slice_body),
+// the rest up blocks (last in the grid, so every slice block is dispatched
+// before any up block waits; the waits are bounded either way).
 struct HcOneArgs {
     const float *R;
     const uint16_t *wn;
@@ -457,16 +554,15 @@ struct HcOneArgs {
     int ndown;
 };
 
-template <int NV, int RB>
+template <int NV>
 __global__ void __launch_bounds__(1024) k_hc_one(HcOneArgs a) {
     const int bx = (int)blockIdx.x;
-    const bool pub_inj = a.y_prev && a.Wi;
     if (bx < a.ndown)
-        hc_norm_down_body<NV, RB, true>(bx, a.R, a.wn, a.y_prev, a.inj_prev, a.Wd, a.Sd, a.Wi, a.Si, a.hc_d, a.inj,
-                                        a.normed, a.n8q, a.n8s, a.A, pub_inj);
+        hc_slice_body<NV>(bx, a.R, a.wn, a.y_prev, a.inj_prev, a.Wd, a.Wi, a.normed, a.n8q, a.n8s, a.A);
     else
-        hc_up_body<NV * 256>(bx - a.ndown, (int)gridDim.x - a.ndown, a.Wu, a.Su, a.hcy, a.mixed, a.xq_out, a.xs_out,
-                             a.d8q, a.d8s, a.Rw, a.y_prev, a.inj_prev, a.xb_out, a.A, pub_inj);
+        hc_up_body<NV * 256>(bx - a.ndown, (int)gridDim.x - a.ndown, a.Sd, a.Si, a.Wi != nullptr, a.Wu, a.Su,
+                             a.hc_d, a.inj, a.hcy, a.mixed, a.xq_out, a.xs_out, a.d8q, a.d8s, a.Rw, a.y_prev,
+                             a.inj_prev, a.xb_out, a.A);
 }
 
 __global__ void __launch_bounds__(256) k_stream_inject(float *__restrict__ R, const float *__restrict__ y,
@@ -582,12 +678,13 @@ static int hc_impl(float *normed, float *hc_d, float *mixed, float *inj, float *
     if (T == 1) {                                              // one launch, the up blocks last
         HcArea *A = hc_area_for_current_device(who);
         if (!A) return -5;
+        const int nslice = (4 * H / kHcSlice) * ((nrow + 31) / 32);
         const HcOneArgs a{R,   wn,     y_prev, inj_prev, down->w, down->s, wi,     si, hc_d, inj,  normed, n8q,
                           n8s, up->w,  up->s,  hcy,      mixed,   xq_out,  xs_out, d8q, d8s,  R,   xb_out, A,
-                          ndown};
-        const dim3 g((unsigned)(ndown + H / 64));
-        if (H == 2048) hipLaunchKernelGGL((k_hc_one<8, RB>), g, dim3(1024), 0, s, a);
-        else hipLaunchKernelGGL((k_hc_one<10, RB>), g, dim3(1024), 0, s, a);
+                          nslice};
+        const dim3 g((unsigned)(nslice + H / 64));
+        if (H == 2048) hipLaunchKernelGGL(k_hc_one<8>, g, dim3(1024), 0, s, a);
+        else hipLaunchKernelGGL(k_hc_one<10>, g, dim3(1024), 0, s, a);
         return check_launch(who) ? -3 : 0;
     }
     const dim3 g1((unsigned)ndown, (unsigned)T);

@@ -94,6 +94,42 @@ def test_stream_inject_bit_exact(lib):
     s.destroy()
 
 
+def _check_mixer(g, R1, R0, wn, mats, y_prev, inj_prev, fused, with_inject, H):
+    """Every stage of T pre-mixer rows against the oracle on the GPU's own
+    inputs to that stage; returns the worst end-to-end error of mixed."""
+    down, inject, up = mats
+    T = R0.shape[0]
+    worst_e2e = 0.0
+    for t in range(T):
+        # fused inject: one fma per element, bit-exact
+        Rt = orc.stream_inject(R0[t], y_prev[t], inj_prev[t]) if fused else R0[t]
+        assert np.array_equal(R1[t].view(np.uint32), Rt.view(np.uint32))
+        # norm on the GPU's residual, X8 of the GPU's normed
+        nref = np.concatenate([orc.hc_norm(Rt[c * H:(c + 1) * H], wn[c * H:(c + 1) * H]) for c in range(4)])
+        assert _rel(g["normed"][t], nref) <= STAGE
+        q, sc = orc.x8_quant(g["normed"][t])
+        assert np.array_equal(g["n8q"][t], q) and np.array_equal(g["n8s"][t].view(np.uint32), sc.view(np.uint32))
+        # down / inject on the GPU's X8(normed)
+        assert _rel(g["hc_d"][t], orc.i8_gemv(down.q, down.s, q, sc, 1)) <= STAGE
+        if with_inject:
+            assert _rel(g["inj"][t][:4], orc.i8_gemv(inject.q, inject.s, q, sc, 2)) <= STAGE
+        dq, ds = orc.x8_quant(g["hc_d"][t])
+        assert np.array_equal(g["d8q"][t], dq) and np.array_equal(g["d8s"][t].view(np.uint32), ds.view(np.uint32))
+        assert _rel(g["hcy"][t], orc.i8_gemv(up.q, up.s, dq, ds, 0)) <= STAGE
+        assert _rel(g["mixed"][t], orc.hc_combine(g["hcy"][t], g["normed"][t], H)) <= STAGE
+        xq, xs = orc.x8_quant(g["mixed"][t])
+        assert np.array_equal(g["xq"][t], xq) and np.array_equal(g["xs"][t].view(np.uint32), xs.view(np.uint32))
+        # the whole mixer from the residual alone (the oracle's own X8 roundings between stages)
+        n32 = nref.astype(np.float32)
+        q2, s2 = orc.x8_quant(n32)
+        h32 = orc.i8_gemv(down.q, down.s, q2, s2, 1).astype(np.float32)
+        dq2, ds2 = orc.x8_quant(h32)
+        hy = orc.i8_gemv(up.q, up.s, dq2, ds2, 0).astype(np.float32)
+        e2e = _rel(g["mixed"][t], orc.hc_combine(hy, n32, H))
+        worst_e2e = max(worst_e2e, e2e)
+    return worst_e2e
+
+
 @pytest.mark.parametrize("H,T,fused,with_inject", [(2560, 1, False, True), (2560, 1, True, True), (2048, 1, True, False),
                                                    (2560, 3, True, True), (2048, 4, False, True)])
 def test_hc_premixer(lib, H, T, fused, with_inject):
@@ -124,34 +160,7 @@ def test_hc_premixer(lib, H, T, fused, with_inject):
          zip(out.items(), (np.float32, np.float32, np.float32, np.float32, np.int8, np.float32, np.int8, np.float32,
                            np.float32, np.int8, np.float32))}
     R1 = dR.download(np.float32, (T, RS))
-    worst_e2e = 0.0
-    for t in range(T):
-        # fused inject: one fma per element, bit-exact
-        Rt = orc.stream_inject(R0[t], y_prev[t], inj_prev[t]) if fused else R0[t]
-        assert np.array_equal(R1[t].view(np.uint32), Rt.view(np.uint32))
-        # norm on the GPU's residual, X8 of the GPU's normed
-        nref = np.concatenate([orc.hc_norm(Rt[c * H:(c + 1) * H], wn[c * H:(c + 1) * H]) for c in range(4)])
-        assert _rel(g["normed"][t], nref) <= STAGE
-        q, sc = orc.x8_quant(g["normed"][t])
-        assert np.array_equal(g["n8q"][t], q) and np.array_equal(g["n8s"][t].view(np.uint32), sc.view(np.uint32))
-        # down / inject on the GPU's X8(normed)
-        assert _rel(g["hc_d"][t], orc.i8_gemv(down.q, down.s, q, sc, 1)) <= STAGE
-        if with_inject:
-            assert _rel(g["inj"][t][:4], orc.i8_gemv(inject.q, inject.s, q, sc, 2)) <= STAGE
-        dq, ds = orc.x8_quant(g["hc_d"][t])
-        assert np.array_equal(g["d8q"][t], dq) and np.array_equal(g["d8s"][t].view(np.uint32), ds.view(np.uint32))
-        assert _rel(g["hcy"][t], orc.i8_gemv(up.q, up.s, dq, ds, 0)) <= STAGE
-        assert _rel(g["mixed"][t], orc.hc_combine(g["hcy"][t], g["normed"][t], H)) <= STAGE
-        xq, xs = orc.x8_quant(g["mixed"][t])
-        assert np.array_equal(g["xq"][t], xq) and np.array_equal(g["xs"][t].view(np.uint32), xs.view(np.uint32))
-        # the whole mixer from the residual alone (the oracle's own X8 roundings between stages)
-        n32 = nref.astype(np.float32)
-        q2, s2 = orc.x8_quant(n32)
-        h32 = orc.i8_gemv(down.q, down.s, q2, s2, 1).astype(np.float32)
-        dq2, ds2 = orc.x8_quant(h32)
-        hy = orc.i8_gemv(up.q, up.s, dq2, ds2, 0).astype(np.float32)
-        e2e = _rel(g["mixed"][t], orc.hc_combine(hy, n32, H))
-        worst_e2e = max(worst_e2e, e2e)
+    worst_e2e = _check_mixer(g, R1, R0, wn, (down, inject, up), y_prev, inj_prev, fused, with_inject, H)
     _say("  end-to-end mixed rel err", worst_e2e)
     assert worst_e2e <= 1e-2
     s.destroy()
@@ -193,15 +202,26 @@ def _hc_bytes(b, T):
     return {nm: buf.download(np.uint8, (T, buf.nbytes // T)) for nm, buf in b.items()}
 
 
+_HC_TYPES = {"normed": np.float32, "hc_d": np.float32, "mixed": np.float32, "inj": np.float32, "n8q": np.int8,
+             "n8s": np.float32, "d8q": np.int8, "d8s": np.float32, "hcy": np.float32, "xq": np.int8, "xs": np.float32,
+             "xb": np.uint16}
+
+
+def _hc_typed(b, T):
+    return {nm: buf.download(_HC_TYPES[nm], (T, buf.nbytes // T // np.dtype(_HC_TYPES[nm]).itemsize))
+            for nm, buf in b.items()}
+
+
 @pytest.mark.parametrize("H,with_inject,fused", [(2048, True, True), (2560, True, True), (2048, False, True),
                                                  (2560, True, False), (2048, False, False)])
-def test_hc_one_launch_matches_two_launches(lib, H, with_inject, fused):
-    """One row runs as one launch (up blocks wait for the down blocks' tagged
-    words); T rows run as two launches. Both give the same bits for every
-    output and the updated residual, over consecutive calls (the hand-off tag
-    advancing) and over graph replays with eager calls between them; no
-    bounded wait runs out."""
-    _say("hc one launch vs two: H", H, "inject", with_inject, "fused inject", fused)
+def test_hc_one_launch_consecutive_and_graph(lib, H, with_inject, fused):
+    """One row runs as one launch (slice blocks publish partial dots and normed
+    as tagged words, up blocks wait for them); T rows run as two launches.
+    Over consecutive one-row calls (the hand-off tag advancing) every stage
+    matches the oracle, and normed, its X8 codes and the updated residual are
+    the two-launch form's bits (the same norm partition); graph replays with
+    eager calls between them give the eager bits; no bounded wait runs out."""
+    _say("hc one launch: H", H, "inject", with_inject, "fused inject", fused)
     qfm.init(H, H // 4, 512, 10, 1, 1)
     rng = np.random.default_rng(7 * H + with_inject + 2 * fused)
     RS, L = 4 * H, 320
@@ -212,7 +232,6 @@ def test_hc_one_launch_matches_two_launches(lib, H, with_inject, fused):
     before = C.c_uint32(0)
     assert lib.qfm_hc_wait_timeouts(C.byref(before)) == 0, lib.qfm_last_error().decode()
     one, two = _hc_bufs(1, H), _hc_bufs(2, H)
-    results = []
     for k in range(3):
         R0 = rng.standard_normal(RS).astype(np.float32)
         yp = rng.standard_normal(H).astype(np.float32)
@@ -225,18 +244,19 @@ def test_hc_one_launch_matches_two_launches(lib, H, with_inject, fused):
         _hc_call(lib, one, dR1, dwn, mats, dyp, dip, with_inject, 1, st)
         _hc_call(lib, two, dR2, dwn, mats, dyp2, dip2, with_inject, 2, st)
         st.sync()
-        a, b = _hc_bytes(one, 1), _hc_bytes(two, 2)
-        for nm in one:
-            if nm == "inj" and not with_inject:
-                continue
-            assert np.array_equal(a[nm][0], b[nm][0]) and np.array_equal(b[nm][0], b[nm][1]), (k, nm)
-        r1, r2 = dR1.download(np.float32, (RS,)), dR2.download(np.float32, (2, RS))
-        assert np.array_equal(r1.view(np.uint32), r2[0].view(np.uint32)), k
-        if fused:
-            assert np.array_equal(r1.view(np.uint32), orc.stream_inject(R0, yp, ip).view(np.uint32)), k
-        results.append((R0, dyp, dip, a))
+        a, b = _hc_typed(one, 1), _hc_typed(two, 2)
+        r1, r2 = dR1.download(np.float32, (1, RS)), dR2.download(np.float32, (2, RS))
+        e2e = _check_mixer(a, r1, R0[None], wn, mats, yp[None], ip[None], fused, with_inject, H)
+        _say("  call", k, "end-to-end mixed rel err", e2e)
+        assert e2e <= 1e-2
+        for nm in ("normed", "n8q", "n8s"):
+            assert np.array_equal(a[nm][0].view(np.uint8), b[nm][0].view(np.uint8)), (k, nm)
+        assert np.array_equal(r1[0].view(np.uint32), r2[0].view(np.uint32)), k
+        # the down / inject values differ from the two-launch form's by the summation order only
+        for nm in ("hc_d",) + (("inj",) if with_inject else ()):
+            assert _rel(a[nm][0][:4] if nm == "inj" else a[nm][0], (b[nm][0][:4] if nm == "inj" else b[nm][0])
+                        .astype(np.float64)) <= STAGE, (k, nm)
     # graph: two one-row calls captured, replayed three times with eager calls between
-    R0, dyp, dip, ref = results[-1]
     dRg = qfm.DevBuf.from_array(R0)
     g_out = [_hc_bufs(1, H), _hc_bufs(1, H)]
     qfm.check(lib.qfm_graph_capture_begin(st.h), "capture")
