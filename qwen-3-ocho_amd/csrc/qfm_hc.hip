@@ -308,8 +308,9 @@ k_hc_up_combine(const int8_t *__restrict__ Wu, const float *__restrict__ Su, con
 // followed by the 4 inject rows). Threads 0..255 hold stream c as
 // k_hc_norm_down's stream threads do (thread t: elements i * 256 + t, with the
 // previous mixer's inject), so the sum of squares, rstd and the slice's normed
-// values and X8 codes are theirs bit for bit; X8 runs over the slice only
-// (two values per thread). Each half-wave then dots one row's 512 codes (16
+// values and X8 codes are theirs bit for bit; X8 runs over the slice only,
+// one value per thread of waves 0..7 (threads 256..511 load the slice's
+// second half themselves). Each half-wave then dots one row's 512 codes (16
 // bytes a lane, one exact int32 block dot scaled by its X8 scale) and
 // publishes the row's partial for slice s. Row group 0 stores the slice's
 // normed, X8 codes and scales and publishes normed.
@@ -333,21 +334,30 @@ __device__ __forceinline__ void hc_slice_body(int b, const float *__restrict__ R
     const bool live = row < nrow;
     const int8_t *wr = (row < QF8_HCL ? Wd + (size_t)row * RS : live ? Wi + (size_t)(row - QF8_HCL) * RS : Wd) +
                        s * kHcSlice + l * 16;
-    // the stream's values and the slice's norm weights first (the norm waits
-    // only for these), then the weights, which stream meanwhile
-    const bool own = tid < 256;
-    float v[NV], yv[NV];
-    uint16_t wb0 = 0, wb1 = 0;
+    // the stream's values (threads 0..255) and the slice's second half
+    // (threads 256..511: element 256 + t of the slice, with the same inject
+    // fma) and norm weights first (the norm waits only for these), then the
+    // weights, which stream meanwhile
+    const bool own = tid < 256, half2 = tid >= 256 && tid < 512;
+    const int m = tid;                                         // element of the slice (tid < 512)
+    const size_t e_own = (size_t)c * H + (size_t)k * kHcSlice + (tid & 511);
+    float v[NV], yv[NV], v2 = 0.0f, y2 = 0.0f;
+    uint16_t wb = 0;
     if (own) {
 #pragma unroll
         for (int i = 0; i < NV; i++) v[i] = R[(size_t)c * H + i * 256 + tid];
-        wb0 = wn[(size_t)c * H + 2 * k * 256 + tid];
-        wb1 = wn[(size_t)c * H + (2 * k + 1) * 256 + tid];
+    } else if (half2) {
+        v2 = R[e_own];
     }
+    if (tid < 512) wb = wn[e_own];
     const float sj = y_prev ? inj_prev[c] : 0.0f;
-    if (own && y_prev)
+    if (y_prev) {
+        if (own)
 #pragma unroll
-        for (int i = 0; i < NV; i++) yv[i] = y_prev[i * 256 + tid];
+            for (int i = 0; i < NV; i++) yv[i] = y_prev[i * 256 + tid];
+        else if (half2)
+            y2 = y_prev[e_own - (size_t)c * H];
+    }
     const i32x4 w = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(wr));
     if (own) {                                                 // waves 0..3
         if (y_prev)
@@ -358,29 +368,26 @@ __device__ __forceinline__ void hc_slice_body(int b, const float *__restrict__ R
         for (int i = 0; i < NV; i++) acc = fmaf(v[i], v[i], acc);
         acc = group_sum<64>(acc);
         if (lane == 0) red[wave] = acc;
+    } else if (half2 && y_prev) {
+        v2 = fmaf(sj, y2, v2);
     }
     __syncthreads();
-    if (own) {
+    if (tid < 512) {                                           // waves 0..7, one slice value each
         const float rstd = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + 1e-6f);
-        float v0 = v[0], v1 = v[1];
+        float v0 = v[0];
 #pragma unroll
         for (int i = 1; i < NV / 2; i++)
-            if (k == i) { v0 = v[2 * i]; v1 = v[2 * i + 1]; }
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int m = h * 256 + tid;                       // element of the slice
-            const float nv = (h ? v1 : v0) * rstd * (1.0f + bf16_to_f32(h ? wb1 : wb0));
-            float s1;
-            const int qi = x8_code(nv, s1);
-            s_q[m] = (int8_t)qi;
-            if ((tid & 31) == 0) s_s[m >> 5] = s1;
-            if (g == 0) {
-                const int e = c * H + k * kHcSlice + m;
-                normed[e] = nv;
-                q[e] = (int8_t)qi;
-                if ((tid & 31) == 0) sc[e >> 5] = s1;
-                st_agent_u64(&A->w[kHcNormed + e], hc_word(nv, tag));
-            }
+            if (k == i) v0 = v[2 * i];
+        const float nv = (own ? v0 : v2) * rstd * (1.0f + bf16_to_f32(wb));
+        float s1;
+        const int qi = x8_code(nv, s1);
+        s_q[m] = (int8_t)qi;
+        if ((tid & 31) == 0) s_s[m >> 5] = s1;
+        if (g == 0) {
+            normed[e_own] = nv;
+            q[e_own] = (int8_t)qi;
+            if ((tid & 31) == 0) sc[e_own >> 5] = s1;
+            st_agent_u64(&A->w[kHcNormed + e_own], hc_word(nv, tag));
         }
     }
     __syncthreads();
@@ -397,7 +404,8 @@ __device__ __forceinline__ void hc_slice_body(int b, const float *__restrict__ R
 // once every partial carries the call's tag every down block has read R), and
 // its 4 x 64 normed values (waves 6-9). hc_d / inject values are the
 // partials summed in slice order, scaled and activated; from there on the
-// arithmetic is k_hc_up_combine's, value for value.
+// arithmetic is k_hc_up_combine's, except that silu and the combine's sigmoid
+// use the hardware exp and reciprocal (within 1e-6 of the IEEE forms).
 template <int H>
 __device__ __forceinline__ void
 hc_up_body(int u, int nup, const float *__restrict__ Sd, const float *__restrict__ Si, bool has_inj,
@@ -471,7 +479,8 @@ hc_up_body(int u, int nup, const float *__restrict__ Sd, const float *__restrict
     if (bad) __hip_atomic_fetch_add(&A->timeouts, (uint32_t)__builtin_popcount(bad), __ATOMIC_RELAXED,
                                     __HIP_MEMORY_SCOPE_AGENT);
     if (wave < 5) {                                            // hc_d and X8(hc_d): five whole waves
-        const float hv = gemv_act(sum * rsc, 1);
+        const float q4 = sum * rsc * 0.25f;                    // silu(v / 4), hardware exp and reciprocal
+        const float hv = q4 * __builtin_amdgcn_rcpf(1.0f + __expf(-q4));
         float s1;
         const int qi = x8_code(hv, s1);
         s_q[tid] = (int8_t)qi;
@@ -514,7 +523,7 @@ hc_up_body(int u, int nup, const float *__restrict__ Sd, const float *__restrict
         float sm = 0.0f;
 #pragma unroll
         for (int cc = 0; cc < 4; cc++) {
-            const float m = 1.0f / (1.0f + expf(-s_h[cc][tid]));
+            const float m = __builtin_amdgcn_rcpf(1.0f + __expf(-s_h[cc][tid]));
             sm = fmaf(m, s_n[cc][tid], sm);
         }
         const float v = sm * 0.25f;
