@@ -145,6 +145,7 @@ def test_validated_twins_reject_without_launching(built):
         "qf8_fp8_downacc_ex": (None,) * 7,
         "qf8_i8_gemv_multi_ex": (None, None, None, None),
         "qf8_i8_hc_m1_ex": (None,) * 19,
+        "qfm_hc_wait_timeouts": (None,),
         "qf8_stream_inject_ex": (None, None, None, None),
     }
     for name, args in calls.items():
