@@ -12,7 +12,8 @@
 // partial dots of 32 down / inject rows over that slice (and, in the first
 // row group, the slice's normed values) as tagged words, followed by up blocks
 // of 64 outputs that wait for those words, sum the partials in slice order and
-// run k_hc_up_combine's arithmetic (hc_up_body). T rows run in two launches:
+// run the up GEMV, the combine and X8(mixed) (hc_up_body). T rows run in two
+// launches:
 //   k_hc_norm_down  one wave per down (silu(v/4)) or inject (2 sigmoid(v/4))
 //                   row, 2 rows per block; every block recomputes the fused
 //                   inject of the previous mixer, the zero-centred RMS norm
