@@ -448,6 +448,10 @@ hc_up_body(int u, int nup, const float *__restrict__ Sd, const float *__restrict
     // normed value each
     float sum = 0.0f, w0 = 0.0f;
     uint32_t bad = 0u;
+    // the first request only once the loads above have returned: one that
+    // went out now would sample the words long before the slice blocks
+    // publish, and its (useless) traffic would meet theirs
+    __builtin_amdgcn_s_waitcnt(0);
     if (wave < 6) {
         const uint32_t off = (uint32_t)(dr < 0 ? 0 : dr);
         unsigned long long x[NS];
