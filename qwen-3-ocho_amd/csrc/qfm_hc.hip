@@ -8,8 +8,9 @@
 // scale and accumulated in fp32, then summed over the LPR lanes with DPP.
 //
 // One row (T = 1) runs in one launch, k_hc_one: slice blocks, each of which
-// norms one stream, X8-codes one 512-value K slice of it and publishes the
-// partial dots of 32 down / inject rows over that slice (and, in the first
+// norms one stream, X8-codes one K slice of it (1024 values, 512 at H = 2560)
+// and publishes the partial dots of 16 (32) down / inject rows over that
+// slice (and, in the first
 // row group, the slice's normed values) as tagged words, followed by up blocks
 // of 64 outputs that wait for those words, sum the partials in slice order and
 // run the up GEMV, the combine and X8(mixed) (hc_up_body). T rows run in two
@@ -100,15 +101,16 @@ k_gemv_i8x8(GemvBatch b, const int8_t *__restrict__ xq, const float *__restrict_
 // ---- hand-off area of the one-launch pre-mixer (T = 1) -----------------------------
 // 64-bit words (fp32 bits | tag << 32, agent-scope stores): [0, 20 * 324) the
 // partial dots of the down / inject rows, slice s of row r at s * 324 + r
-// (slices 0 .. NS - 1, NS = 4H / 512), then normed [4H]. The call's tag is
+// (slices 0 .. NS - 1, NS = 4H / KS, at most 20), then normed [4H]. The call's tag is
 // next_tag(epoch): every block reads epoch at its start and the last up block
 // to finish reading its words advances it (arrivals counts them), so the next
 // call, stream-ordered after this one, uses the next tag and no word needs
 // clearing. The array starts zeroed (epoch 0, no live tag); timeouts counts
 // the words whose bounded wait ran out (0 unless something is badly wrong).
-constexpr int kHcSlice = 512;                               // K slice of a down block
+// K slice of a slice block: 1024 values where H allows, else 512 (H = 2560)
+__host__ __device__ constexpr int hc_slice_of(int H) { return H % 1024 == 0 ? 1024 : 512; }
 constexpr int kHcRows = QF8_HCL + QF8_HCC;                 // partial words per slice
-constexpr int kHcNormed = kHcRows * (4 * 2560 / kHcSlice);
+constexpr int kHcNormed = kHcRows * (4 * 2560 / 512);      // the most slices (H = 2560)
 constexpr int kHcWordsMax = kHcNormed + 4 * 2560;
 struct HcArea {
     uint32_t epoch, arrivals, timeouts, pad[61];
@@ -304,44 +306,47 @@ k_hc_up_combine(const int8_t *__restrict__ Wu, const float *__restrict__ Su, con
 }
 
 // The down / inject role of the one-launch pre-mixer: block b owns K slice
-// s = b % NS (the 512 values 512 k .. 512 k + 511 of stream c, s = c * H / 512
-// + k) of the row group g = b / NS (rows 32 g .. 32 g + 31 of the 320 down rows
-// followed by the 4 inject rows). Threads 0..255 hold stream c as
-// k_hc_norm_down's stream threads do (thread t: elements i * 256 + t, with the
-// previous mixer's inject), so the sum of squares, rstd and the slice's normed
-// values and X8 codes are theirs bit for bit; X8 runs over the slice only,
-// one value per thread of waves 0..7 (threads 256..511 load the slice's
-// second half themselves). Each half-wave then dots one row's 512 codes (16
-// bytes a lane, one exact int32 block dot scaled by its X8 scale) and
-// publishes the row's partial for slice s. Row group 0 stores the slice's
-// normed, X8 codes and scales and publishes normed.
+// s = b % NS (the KS values KS k .. KS k + KS - 1 of stream c, s = c * H / KS
+// + k; KS = 1024, or 512 at H = 2560) of the row group g = b / NS (RPB =
+// 16384 / KS rows, RPB g .. RPB g + RPB - 1 of the 320 down rows followed by
+// the 4 inject rows). Threads 0..255 hold stream c as k_hc_norm_down's stream
+// threads do (thread t: elements i * 256 + t, with the previous mixer's
+// inject), so the sum of squares, rstd and the slice's normed values and X8
+// codes are theirs bit for bit; X8 runs over the slice only, one value per
+// thread (threads 256..KS-1 load their slice element themselves). Each group
+// of KS / 16 lanes then dots one row's KS codes (16 bytes a lane, one exact
+// int32 block dot scaled by its X8 scale) and publishes the row's partial for
+// slice s. Row group 0 stores the slice's normed, X8 codes and scales and
+// publishes normed.
 template <int NV>
 __device__ __forceinline__ void hc_slice_body(int b, const float *__restrict__ R, const uint16_t *__restrict__ wn,
                                               const float *__restrict__ y_prev, const float *__restrict__ inj_prev,
                                               const int8_t *__restrict__ Wd, const int8_t *__restrict__ Wi,
                                               float *__restrict__ normed, int8_t *__restrict__ q,
                                               float *__restrict__ sc, HcArea *A) {
-    constexpr int H = NV * 256, RS = 4 * H, SPS = H / kHcSlice, NS = 4 * SPS;
-    __shared__ __align__(16) int8_t s_q[kHcSlice];
-    __shared__ float s_s[kHcSlice / 32];
+    constexpr int H = NV * 256, RS = 4 * H, KS = hc_slice_of(H), SPS = H / KS, NS = 4 * SPS;
+    constexpr int LPR = KS / 16, RPB = 1024 / LPR;      // lanes per row, rows per block
+    constexpr int SQ = KS / 256;                         // slice values per stream thread's i range
+    __shared__ __align__(16) int8_t s_q[KS];
+    __shared__ float s_s[KS / 32];
     __shared__ float red[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int s = b % NS, g = b / NS;
     const int c = s / SPS, k = s - c * SPS;                    // stream, slice within the stream
     const uint32_t tag = next_tag(__hip_atomic_load(&A->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    const int rloc = tid >> 5, l = tid & 31;
-    const int row = g * 32 + rloc;
+    const int rloc = tid / LPR, l = tid % LPR;
+    const int row = g * RPB + rloc;
     const int nrow = QF8_HCL + (Wi ? QF8_HCC : 0);
     const bool live = row < nrow;
     const int8_t *wr = (row < QF8_HCL ? Wd + (size_t)row * RS : live ? Wi + (size_t)(row - QF8_HCL) * RS : Wd) +
-                       s * kHcSlice + l * 16;
-    // the stream's values (threads 0..255) and the slice's second half
-    // (threads 256..511: element 256 + t of the slice, with the same inject
-    // fma) and norm weights first (the norm waits only for these), then the
+                       s * KS + l * 16;
+    // the stream's values (threads 0..255) and the slice's other elements
+    // (threads 256..KS-1: element t of the slice, with the same inject fma)
+    // and norm weights first (the norm waits only for these), then the
     // weights, which stream meanwhile
-    const bool own = tid < 256, half2 = tid >= 256 && tid < 512;
-    const int m = tid;                                         // element of the slice (tid < 512)
-    const size_t e_own = (size_t)c * H + (size_t)k * kHcSlice + (tid & 511);
+    const bool own = tid < 256, half2 = tid >= 256 && tid < KS;
+    const int m = tid;                                         // element of the slice (tid < KS)
+    const size_t e_own = (size_t)c * H + (size_t)k * KS + (tid & (KS - 1));
     float v[NV], yv[NV], v2 = 0.0f, y2 = 0.0f;
     uint16_t wb = 0;
     if (own) {
@@ -350,7 +355,7 @@ __device__ __forceinline__ void hc_slice_body(int b, const float *__restrict__ R
     } else if (half2) {
         v2 = R[e_own];
     }
-    if (tid < 512) wb = wn[e_own];
+    if (tid < KS) wb = wn[e_own];
     const float sj = y_prev ? inj_prev[c] : 0.0f;
     if (y_prev) {
         if (own)
@@ -373,12 +378,12 @@ __device__ __forceinline__ void hc_slice_body(int b, const float *__restrict__ R
         v2 = fmaf(sj, y2, v2);
     }
     __syncthreads();
-    if (tid < 512) {                                           // waves 0..7, one slice value each
+    if (tid < KS) {                                      // one slice value per thread
         const float rstd = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + 1e-6f);
         float v0 = v[0];
 #pragma unroll
-        for (int i = 1; i < NV / 2; i++)
-            if (k == i) v0 = v[2 * i];
+        for (int i = 1; i < NV / SQ; i++)
+            if (k == i) v0 = v[SQ * i];
         const float nv = (own ? v0 : v2) * rstd * (1.0f + bf16_to_f32(wb));
         float s1;
         const int qi = x8_code(nv, s1);
@@ -393,7 +398,7 @@ __device__ __forceinline__ void hc_slice_body(int b, const float *__restrict__ R
     }
     __syncthreads();
     float a = (float)dot16_i8i8(w, *reinterpret_cast<const i32x4 *>(s_q + l * 16)) * s_s[l >> 1];
-    a = group_sum<32>(a);
+    a = group_sum<LPR>(a);
     if (l == 0 && live) st_agent_u64(&A->w[s * kHcRows + row], hc_word(a, tag));
 }
 
@@ -415,7 +420,7 @@ hc_up_body(int u, int nup, const float *__restrict__ Sd, const float *__restrict
            float *__restrict__ xs_out, int8_t *__restrict__ d8q, float *__restrict__ d8s, float *__restrict__ R,
            const float *__restrict__ y_prev, const float *__restrict__ inj_prev, uint16_t *__restrict__ xb_out,
            HcArea *A) {
-    constexpr int L = QF8_HCL, NS = 4 * H / kHcSlice;
+    constexpr int L = QF8_HCL, NS = 4 * H / hc_slice_of(H);
     __shared__ __align__(16) int8_t s_q[L];
     __shared__ float s_s[L / 32];
     __shared__ float s_h[4][64], s_n[4][64];
@@ -692,7 +697,8 @@ static int hc_impl(float *normed, float *hc_d, float *mixed, float *inj, float *
     if (T == 1) {                                              // one launch, the up blocks last
         HcArea *A = hc_area_for_current_device(who);
         if (!A) return -5;
-        const int nslice = (4 * H / kHcSlice) * ((nrow + 31) / 32);
+        const int ks = hc_slice_of(H), rpb = 16384 / ks;   // slice values, rows per slice block
+        const int nslice = (4 * H / ks) * ((nrow + rpb - 1) / rpb);
         const HcOneArgs a{R,   wn,     y_prev, inj_prev, down->w, down->s, wi,     si, hc_d, inj,  normed, n8q,
                           n8s, up->w,  up->s,  hcy,      mixed,   xq_out,  xs_out, d8q, d8s,  R,   xb_out, A,
                           nslice};
